@@ -1,0 +1,366 @@
+// Flash attention forward for the DiT's joint / self / cross attention on CDNA4 matrix cores.
+//
+// out = softmax(q k^T * scale [+ mask]) v with head_dim 128, bf16 or fp16 inputs, fp32 softmax
+// statistics and accumulation, one pass over K/V (online softmax), O(S) memory.
+//
+// Work split: a 256-thread workgroup (4 wavefronts) owns 128 query rows of one (batch, head);
+// each wavefront owns 32 of them. K/V stream through LDS in tiles of 64 keys, double-buffered.
+//
+// Operand roles. Scores are computed transposed, S^T = K Q^T (MFMA 32x32x16, first operand a K
+// fragment, second a Q fragment held in registers for the whole kernel), so accumulator lane l
+// holds query l % 32 and its registers run over keys. Every softmax statistic of a query then
+// lives in two lanes (l and l ^ 32): row max and row sum need one cross-lane exchange, and the
+// rescale of the output accumulator is a per-lane multiply. The output is also accumulated
+// transposed, O^T += V^T P^T: the P^T operand is the lane's own probabilities (the 8 keys a
+// lane holds for a 16-key MFMA step are {4g..4g+3, 8+4g..8+4g+3}, g = l / 32, and the V^T
+// operand is read in that same key order), so P never leaves registers.
+//
+// LDS: K tile row-major [64 keys][128 dims] with 16-byte chunks XOR-swizzled by key; V tile
+// stored transposed [128 dims][64 keys] with a 136-byte row pitch, so the V^T fragment reads of
+// 16 lanes (16 dims, one key offset) cover all 32 banks. Both are written from registers
+// (V transposed in the write), one barrier per K/V tile.
+//
+// Masking follows the reference: masked scores become the lowest finite float (so a fully
+// masked row averages V, as softmax over equal finfo.min scores does); keys past seq_k do not
+// exist and take -inf.
+#include "common.hpp"
+#include <float.h>
+
+namespace dlt {
+
+constexpr int HD = 128;
+constexpr int BLOCK_M = 128;
+constexpr int BLOCK_N = 64;
+constexpr int VT_PITCH = BLOCK_N * 2 + 8;  // bytes per V^T row
+constexpr float LOG2E = 1.4426950408889634f;
+
+struct AttnArgs {
+  const uint8_t* q;
+  const uint8_t* k;
+  const uint8_t* v;
+  uint8_t* o;
+  int64_t qs[3], ks[3], vs[3], os[3];  // element strides: batch, head, seq
+  int heads, seq_q, seq_k;
+  int q_tiles, total;
+  float scale_log2;
+  int causal;
+  const void* mask;
+  int mask_dtype;
+  int64_t ms[4];
+  const int32_t* bmin;
+  const int32_t* bmax;
+  int64_t bs[3];
+};
+
+template <typename T> struct MfmaT;
+template <> struct MfmaT<bf16> {
+  typedef bf16x8 frag;
+  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    bf16x2 v = {(bf16)a, (bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+template <> struct MfmaT<f16> {
+  typedef f16x8 frag;
+  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    f16x2 v = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+__device__ __forceinline__ int k_off(int row, int chunk) {  // K tile: 256-byte rows
+  return row * (HD * 2) + ((chunk ^ (row & 7)) << 4);
+}
+
+template <typename T, bool MASKED>
+__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
+  typedef typename MfmaT<T>::frag frag;
+  __shared__ __attribute__((aligned(16))) uint8_t sk[2][BLOCK_N * HD * 2];
+  __shared__ __attribute__((aligned(16))) uint8_t sv[2][HD * VT_PITCH];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 31, g = lane >> 5;
+
+  // XCD-aware order: each XCD (ids round-robin over 8) gets a contiguous run of tiles, i.e.
+  // whole heads, so one head's K/V stays in one L2.
+  int bid = blockIdx.x;
+  if ((a.total & 7) == 0) bid = (bid & 7) * (a.total >> 3) + (bid >> 3);
+  const int bh = bid / a.q_tiles;
+  const int qt = bid % a.q_tiles;
+  const int b = bh / a.heads, h = bh % a.heads;
+  const int q0 = qt * BLOCK_M + wave * 32;
+  const int my_q = q0 + col;
+
+  const uint8_t* qp = a.q + (b * a.qs[0] + h * a.qs[1]) * 2;
+  const uint8_t* kp = a.k + (b * a.ks[0] + h * a.ks[1]) * 2;
+  const uint8_t* vp = a.v + (b * a.vs[0] + h * a.vs[1]) * 2;
+  const int64_t qrow = a.qs[2] * 2, krow = a.ks[2] * 2, vrow = a.vs[2] * 2;
+
+  // ---- Q fragments (second MFMA operand): lane holds q row my_q, dims 16c + 8g .. +8
+  frag qf[8];
+  {
+    const __amdgpu_buffer_rsrc_t rq =
+        make_rsrc(qp, (uint32_t)min((int64_t)a.seq_q * qrow, (int64_t)0xffffffff));
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      // rows past seq_q lie past the resource's range and read zero
+      qf[c] = __builtin_bit_cast(frag, buf_load16(rq, (uint32_t)(my_q * qrow) + (c * 16 + g * 8) * 2));
+    }
+  }
+
+  const __amdgpu_buffer_rsrc_t rk =
+      make_rsrc(kp, (uint32_t)min((int64_t)a.seq_k * krow, (int64_t)0xffffffff));
+  const __amdgpu_buffer_rsrc_t rv =
+      make_rsrc(vp, (uint32_t)min((int64_t)a.seq_k * vrow, (int64_t)0xffffffff));
+
+  // staging: K rows (t/16 + 16 i), chunk t % 16; V keys 4 (t % 16) + i, dims 8 (t / 16) .. +8
+  const int kr = tid >> 4, kc = tid & 15;
+  const int vkg = tid & 15, vdg = tid >> 4;
+  u32x4 gk[4], gv[4];
+  auto load_tile = [&](int j0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = j0 + kr + 16 * i;
+      gk[i] = buf_load16(rk, (uint32_t)(key * krow) + kc * 16);
+      const int vkey = j0 + vkg * 4 + i;
+      gv[i] = buf_load16(rv, (uint32_t)(vkey * vrow) + vdg * 16);
+    }
+  };
+  auto store_tile = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<u32x4*>(&sk[st][k_off(kr + 16 * i, kc)]) = gk[i];
+    // transpose: for each of the 8 dims, the 4 keys' 16-bit values side by side
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const int w = d >> 1, sh = (d & 1) * 16;
+      const uint32_t k0 = (gv[0][w] >> sh) & 0xffffu, k1 = (gv[1][w] >> sh) & 0xffffu;
+      const uint32_t k2 = (gv[2][w] >> sh) & 0xffffu, k3 = (gv[3][w] >> sh) & 0xffffu;
+      u32x2 pk;
+      pk[0] = k0 | (k1 << 16);
+      pk[1] = k2 | (k3 << 16);
+      *reinterpret_cast<u32x2*>(&sv[st][(vdg * 8 + d) * VT_PITCH + vkg * 8]) = pk;
+    }
+  };
+
+  f32x16 acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = f32x16{};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  int bmin = 0, bmax = a.seq_k;
+  if (MASKED && a.bmin && my_q < a.seq_q) {
+    bmin = a.bmin[b * a.bs[0] + h * a.bs[1] + (int64_t)my_q * a.bs[2]];
+    bmax = a.bmax[b * a.bs[0] + h * a.bs[1] + (int64_t)my_q * a.bs[2]];
+  }
+
+  const int ntiles = (a.seq_k + BLOCK_N - 1) / BLOCK_N;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  for (int jt = 0; jt < ntiles; ++jt) {
+    const int st = jt & 1;
+    const int j0 = jt * BLOCK_N;
+    if (jt + 1 < ntiles) load_tile(j0 + BLOCK_N);
+
+    // ---- S^T = K Q^T for 2 x 32 keys
+    f32x16 s[2];
+#pragma unroll
+    for (int kt2 = 0; kt2 < 2; ++kt2) {
+      s[kt2] = f32x16{};
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const frag kf =
+            *reinterpret_cast<const frag*>(&sk[st][k_off(kt2 * 32 + col, c * 2 + g)]);
+        s[kt2] = MfmaT<T>::mma(kf, qf[c], s[kt2]);
+      }
+    }
+
+    // ---- scale, mask, online softmax (this lane: query my_q, 32 of the tile's keys)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int key = j0 + kt2 * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+        float x = s[kt2][v] * a.scale_log2;
+        if (MASKED) {
+          bool masked = key < bmin || key >= bmax || (a.causal && key > my_q);
+          if (a.mask && !masked && key < a.seq_k && my_q < a.seq_q) {
+            const int64_t mo = b * a.ms[0] + h * a.ms[1] + (int64_t)my_q * a.ms[2] +
+                               (int64_t)key * a.ms[3];
+            if (a.mask_dtype == DIFFLET_BOOL) {
+              masked = reinterpret_cast<const uint8_t*>(a.mask)[mo] == 0;
+            } else if (a.mask_dtype == DIFFLET_F32) {
+              x += reinterpret_cast<const float*>(a.mask)[mo] * LOG2E;
+            } else if (a.mask_dtype == DIFFLET_BF16) {
+              x += bf16_to_f32(reinterpret_cast<const bf16*>(a.mask)[mo]) * LOG2E;
+            } else {
+              x += (float)reinterpret_cast<const f16*>(a.mask)[mo] * LOG2E;
+            }
+          }
+          if (masked) x = -FLT_MAX;
+        }
+        if (key >= a.seq_k) x = -INFINITY;
+        s[kt2][v] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    m_run = m_new;
+    float ls = 0.f;
+    uint32_t pp[2][8];  // P as packed 16-bit pairs, in register order
+#pragma unroll
+    for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+      for (int v = 0; v < 16; v += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(s[kt2][v] - m_use);
+        const float p1 = __builtin_amdgcn_exp2f(s[kt2][v + 1] - m_use);
+        ls += p0 + p1;
+        pp[kt2][v >> 1] = MfmaT<T>::pack2(p0, p1);
+      }
+    l_run = l_run * alpha + ls;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][v] *= alpha;
+
+    // ---- O^T += V^T P^T, 16 keys per MFMA: keys base + {4g..4g+3, 8+4g..8+4g+3}
+#pragma unroll
+    for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int base = kt2 * 32 + hh * 16;
+        u32x4 pb;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) pb[u] = pp[kt2][hh * 4 + u];
+        const frag pf = __builtin_bit_cast(frag, pb);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const uint8_t* rowp = &sv[st][(dt * 32 + col) * VT_PITCH];
+          const u32x2 lo = *reinterpret_cast<const u32x2*>(rowp + (base + g * 4) * 2);
+          const u32x2 hi = *reinterpret_cast<const u32x2*>(rowp + (base + 8 + g * 4) * 2);
+          const u32x4 vv = {lo[0], lo[1], hi[0], hi[1]};
+          acc[dt] = MfmaT<T>::mma(__builtin_bit_cast(frag, vv), pf, acc[dt]);
+        }
+      }
+
+    if (jt + 1 < ntiles) store_tile(st ^ 1);
+    __syncthreads();
+  }
+
+  // ---- normalize and write: lane holds query my_q, dims dt*32 + (v/4)*8 + 4g + v%4
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = 1.0f / l_tot;
+  if (my_q < a.seq_q) {
+    T* op = reinterpret_cast<T*>(a.o) + b * a.os[0] + h * a.os[1] + (int64_t)my_q * a.os[2];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        u32x2 w;
+        w[0] = MfmaT<T>::pack2(acc[dt][q4 * 4 + 0] * inv, acc[dt][q4 * 4 + 1] * inv);
+        w[1] = MfmaT<T>::pack2(acc[dt][q4 * 4 + 2] * inv, acc[dt][q4 * 4 + 3] * inv);
+        *reinterpret_cast<u32x2*>(op + dt * 32 + q4 * 8 + g * 4) = w;
+      }
+  }
+}
+
+}  // namespace dlt
+
+using namespace dlt;
+
+extern "C" int difflet_rocm_attention(const void* q, const void* k, const void* v, void* o,
+                                      int dtype, int64_t batch, int64_t heads, int64_t seq_q,
+                                      int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
+                                      const int64_t* k_strides, const int64_t* v_strides,
+                                      const int64_t* o_strides, float scale, int causal,
+                                      const void* mask, int mask_dtype,
+                                      const int64_t* mask_strides, const int32_t* bound_min,
+                                      const int32_t* bound_max, const int64_t* bound_strides,
+                                      difflet_stream_t stream) {
+  DLT_REQUIRE(q && k && v && o && q_strides && k_strides && v_strides && o_strides,
+              DIFFLET_EINVAL, "attention: null pointer");
+  DLT_REQUIRE(dtype == DIFFLET_BF16 || dtype == DIFFLET_F16, DIFFLET_EUNSUPPORTED,
+              "attention: dtype %d unsupported (bf16 and fp16 only)", dtype);
+  DLT_REQUIRE(head_dim == HD, DIFFLET_EUNSUPPORTED, "attention: head_dim %lld unsupported (128)",
+              (long long)head_dim);
+  DLT_REQUIRE(batch >= 0 && heads >= 0 && seq_q >= 0 && seq_k >= 0, DIFFLET_EINVAL,
+              "attention: negative size");
+  DLT_REQUIRE(seq_q < (1 << 24) && seq_k < (1 << 24) && batch * heads < (1 << 24),
+              DIFFLET_EUNSUPPORTED, "attention: sizes too large");
+  DLT_REQUIRE(!bound_min == !bound_max, DIFFLET_EINVAL,
+              "attention: bound_min and bound_max must both be provided");
+  DLT_REQUIRE(!(bound_min && mask), DIFFLET_EINVAL,
+              "attention: attention_mask and bounds are mutually exclusive");
+  DLT_REQUIRE(!bound_min || bound_strides, DIFFLET_EINVAL, "attention: bound strides missing");
+  DLT_REQUIRE(!mask || (mask_strides && (mask_dtype == DIFFLET_BOOL || mask_dtype == DIFFLET_F32 ||
+                                         mask_dtype == DIFFLET_BF16 || mask_dtype == DIFFLET_F16)),
+              DIFFLET_EINVAL, "attention: bad mask");
+  const int64_t* ss[4] = {q_strides, k_strides, v_strides, o_strides};
+  const void* ps[4] = {q, k, v, o};
+  for (int i = 0; i < 4; ++i) {
+    DLT_REQUIRE(ss[i][2] % 8 == 0 && ss[i][1] % 8 == 0 && ss[i][0] % 8 == 0 &&
+                    ((uintptr_t)ps[i] & 15) == 0,
+                DIFFLET_EINVAL, "attention: rows must be 16-byte aligned (strides %% 8 == 0)");
+  }
+  // keys / queries up to one tile past the end are addressed (and read as zero through the
+  // buffer range check), so the byte offsets of seq + 128 rows must fit 32 bits
+  DLT_REQUIRE((seq_q + 128) * q_strides[2] * 2 < (1LL << 32) &&
+                  (seq_k + 128) * k_strides[2] * 2 < (1LL << 32) &&
+                  (seq_k + 128) * v_strides[2] * 2 < (1LL << 32),
+              DIFFLET_EUNSUPPORTED, "attention: one head's sequence exceeds 4 GiB");
+  if (batch * heads * seq_q == 0) return DIFFLET_OK;
+  DLT_REQUIRE(seq_k > 0, DIFFLET_EUNSUPPORTED, "attention: seq_k must be positive");
+
+  AttnArgs args = {};
+  args.q = (const uint8_t*)q;
+  args.k = (const uint8_t*)k;
+  args.v = (const uint8_t*)v;
+  args.o = (uint8_t*)o;
+  for (int i = 0; i < 3; ++i) {
+    args.qs[i] = q_strides[i];
+    args.ks[i] = k_strides[i];
+    args.vs[i] = v_strides[i];
+    args.os[i] = o_strides[i];
+  }
+  args.heads = (int)heads;
+  args.seq_q = (int)seq_q;
+  args.seq_k = (int)seq_k;
+  args.q_tiles = (int)((seq_q + BLOCK_M - 1) / BLOCK_M);
+  const int64_t total = (int64_t)args.q_tiles * batch * heads;
+  DLT_REQUIRE(total < (1LL << 31), DIFFLET_EUNSUPPORTED, "attention: too many tiles");
+  args.total = (int)total;
+  args.scale_log2 = scale * LOG2E;
+  args.causal = causal;
+  args.mask = mask;
+  args.mask_dtype = mask_dtype;
+  if (mask)
+    for (int i = 0; i < 4; ++i) args.ms[i] = mask_strides[i];
+  args.bmin = bound_min;
+  args.bmax = bound_max;
+  if (bound_min)
+    for (int i = 0; i < 3; ++i) args.bs[i] = bound_strides[i];
+  const bool masked = causal || mask || bound_min;
+  hipStream_t s = (hipStream_t)stream;
+  dim3 grid((unsigned)total), block(256);
+  if (dtype == DIFFLET_BF16) {
+    if (masked) hipLaunchKernelGGL((attn_fwd_kernel<bf16, true>), grid, block, 0, s, args);
+    else hipLaunchKernelGGL((attn_fwd_kernel<bf16, false>), grid, block, 0, s, args);
+  } else {
+    if (masked) hipLaunchKernelGGL((attn_fwd_kernel<f16, true>), grid, block, 0, s, args);
+    else hipLaunchKernelGGL((attn_fwd_kernel<f16, false>), grid, block, 0, s, args);
+  }
+  return dlt_check_launch("attention");
+}

@@ -1,0 +1,165 @@
+// Shared device helpers for the gfx950 (CDNA4) kernels of the DiT denoise step.
+//
+// Everything here is written for 64-lane wavefronts. Types are the compiler's native vector
+// types so MFMA builtins take them directly.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/difflet_rocm.h"
+
+namespace dlt {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// ------------------------------------------------------------------ bf16 conversions
+// Round-to-nearest-even fp32 -> bf16 on the bit pattern (NaN kept quiet), the same rounding
+// torch uses for `.to(torch.bfloat16)`.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ bf16 f32_to_bf16(float f) {
+  return __builtin_bit_cast(bf16, f32_to_bf16_bits(f));
+}
+__device__ __forceinline__ float bf16_to_f32(bf16 h) {
+  return __builtin_bit_cast(float, ((uint32_t)__builtin_bit_cast(uint16_t, h)) << 16);
+}
+__device__ __forceinline__ float bf16bits_to_f32(uint32_t bits16) {
+  return __builtin_bit_cast(float, bits16 << 16);
+}
+// Two bf16 packed in one dword (low half = first element).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+}
+
+// Element loaders/storers for the activation dtypes the kernels accept.
+template <typename T> struct Elt;
+template <> struct Elt<bf16> {
+  static __device__ __forceinline__ float load(const bf16* p) { return bf16_to_f32(*p); }
+  static __device__ __forceinline__ void store(bf16* p, float v) { *p = f32_to_bf16(v); }
+};
+template <> struct Elt<f16> {
+  static __device__ __forceinline__ float load(const f16* p) { return (float)*p; }
+  static __device__ __forceinline__ void store(f16* p, float v) { *p = (f16)v; }
+};
+template <> struct Elt<float> {
+  static __device__ __forceinline__ float load(const float* p) { return *p; }
+  static __device__ __forceinline__ void store(float* p, float v) { *p = v; }
+};
+
+// ------------------------------------------------------------------ fp8 e4m3fn encode
+// Round-to-nearest-even fp32 -> OCP float8_e4m3fn code. The caller clamps to [-448, 448]
+// first (both quantizer laws do), so no input reaches the NaN code except NaN itself.
+// Written on the integer bit pattern so CPU and GPU agree bit for bit.
+__device__ __forceinline__ uint32_t f32_to_e4m3fn(float x) {
+  uint32_t u = __builtin_bit_cast(uint32_t, x);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;          // NaN
+  if (a >= 0x43e00000u) return sign | 0x7eu;         // >= 448: saturate (inputs are clamped)
+  if (a < 0x3c800000u) {                             // below 2^-6: subnormal grid of 2^-9
+    float m = __builtin_rintf(__builtin_bit_cast(float, a) * 512.0f);
+    return sign | (uint32_t)m;                       // 8 rounds up into the smallest normal
+  }
+  uint32_t r = (a + 0x7ffffu + ((a >> 20) & 1u)) >> 20;  // RNE on the 3 kept mantissa bits
+  return sign | (r - (120u << 3));                   // rebias 127 -> 7
+}
+
+// ------------------------------------------------------------------ wave reductions
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Block-wide sum over `nwaves` waves through a small LDS scratch (one slot per wave).
+template <int NWAVES>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  if (NWAVES == 1) return v;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < NWAVES; ++i) t += red[i];
+  return t;
+}
+template <int NWAVES>
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  if (NWAVES == 1) return v;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float t = red[0];
+#pragma unroll
+  for (int i = 1; i < NWAVES; ++i) t = fmaxf(t, red[i]);
+  return t;
+}
+
+// ------------------------------------------------------------------ math
+// GELU with the tanh approximation, 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), with tanh
+// written through exp: tanh(u) = 1 - 2 / (exp(2u) + 1), which saturates cleanly at +-1.
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
+  const float k1 = 0.044715f;
+  float u = k0 * (x + k1 * x * x * x);
+  float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(__expf(2.0f * u) + 1.0f);
+  return 0.5f * x * (1.0f + t);
+}
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+// ------------------------------------------------------------------ buffer resources
+// Raw buffer loads: an out-of-range offset reads zero, which is how GEMM and attention tiles
+// handle ragged M / N / sequence edges without branches.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ u32x2 buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+
+}  // namespace dlt
+
+// Error plumbing shared by every entry point: a status code plus a message readable through
+// difflet_rocm_last_error().
+void dlt_set_error(const char* fmt, ...);
+int dlt_check_launch(const char* what);
+
+#define DLT_REQUIRE(cond, code, ...)   \
+  do {                                 \
+    if (!(cond)) {                     \
+      dlt_set_error(__VA_ARGS__);      \
+      return (code);                   \
+    }                                  \
+  } while (0)

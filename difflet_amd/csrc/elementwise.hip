@@ -1,0 +1,697 @@
+// Bandwidth-bound kernels of the DiT block: LayerNorm + adaLN modulation, RMSNorm, fused
+// per-head q/k RMSNorm + rotary embedding, rotary embedding alone, GELU-tanh, gate/residual,
+// the small-M GEMV of the modulation linears, and the sinusoidal timestep embedding.
+//
+// Layout: activations are token-major rows ([rows, dim], innermost contiguous). One wavefront
+// owns one row, so every statistic is a wavefront reduction with no LDS and no barrier, and
+// each lane moves 16-byte vectors (8 bf16) so HBM traffic is fully coalesced.
+#include "common.hpp"
+
+namespace dlt {
+
+// ------------------------------------------------------------------ vector load/store of 8
+template <typename T> struct V8;
+template <> struct V8<bf16> {
+  static __device__ __forceinline__ void load(const bf16* p, float* v) {
+    u32x4 r = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = bf16bits_to_f32(r[i] & 0xffffu);
+      v[2 * i + 1] = bf16bits_to_f32(r[i] >> 16);
+    }
+  }
+  static __device__ __forceinline__ void store(bf16* p, const float* v) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+    *reinterpret_cast<u32x4*>(p) = r;
+  }
+};
+template <> struct V8<f16> {
+  static __device__ __forceinline__ void load(const f16* p, float* v) {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    h8 r = *reinterpret_cast<const h8*>(p);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (float)r[i];
+  }
+  static __device__ __forceinline__ void store(f16* p, const float* v) {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    h8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = (_Float16)v[i];
+    *reinterpret_cast<h8*>(p) = r;
+  }
+};
+template <> struct V8<float> {
+  static __device__ __forceinline__ void load(const float* p, float* v) {
+    f32x4 a = *reinterpret_cast<const f32x4*>(p);
+    f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = a[i];
+      v[4 + i] = b[i];
+    }
+  }
+  static __device__ __forceinline__ void store(float* p, const float* v) {
+    f32x4 a, b;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[i] = v[i];
+      b[i] = v[4 + i];
+    }
+    *reinterpret_cast<f32x4*>(p) = a;
+    *reinterpret_cast<f32x4*>(p + 4) = b;
+  }
+};
+
+// ------------------------------------------------------------------ LayerNorm + modulation
+// NV = 16-byte vectors per lane; dim <= 64 * 8 * NV and dim % 8 == 0.
+template <typename TX, typename TY, typename TM, int NV>
+__global__ __launch_bounds__(256) void layernorm_modulate_kernel(
+    const TX* __restrict__ x, int64_t ldx, TY* __restrict__ y, int64_t ldy, int64_t rows,
+    int dim, const TM* __restrict__ mul, const TM* __restrict__ add, int64_t mod_stride,
+    int64_t rows_per_batch, int one_plus, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const TX* xr = x + row * ldx;
+  float v[NV][8];
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 8;
+    if (c < dim) {
+      V8<TX>::load(xr + c, v[j]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s += v[j][i];
+    }
+  }
+  const float mean = wave_sum(s) / (float)dim;
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 8;
+    if (c < dim) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float d = v[j][i] - mean;
+        q += d * d;
+      }
+    }
+  }
+  const float rstd = 1.0f / __builtin_sqrtf(wave_sum(q) / (float)dim + eps);
+  const int64_t b = row / rows_per_batch;
+  const TM* mb = mul ? mul + b * mod_stride : nullptr;
+  const TM* ab = add ? add + b * mod_stride : nullptr;
+  TY* yr = y + row * ldy;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 8;
+    if (c < dim) {
+      float m8[8], a8[8], o[8];
+      if (mb) {
+        V8<TM>::load(mb + c, m8);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m8[i] = one_plus ? 0.f : 1.f;
+      }
+      if (ab) {
+        V8<TM>::load(ab + c, a8);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a8[i] = 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float mm = one_plus ? 1.0f + m8[i] : m8[i];
+        o[i] = (v[j][i] - mean) * rstd * mm + a8[i];
+      }
+      V8<TY>::store(yr + c, o);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ RMSNorm (fp32 law)
+template <typename T, typename TW, int NV>
+__global__ __launch_bounds__(256) void rms_norm_kernel(const T* __restrict__ x, int64_t ldx,
+                                                       T* __restrict__ y, int64_t ldy,
+                                                       int64_t rows, int dim,
+                                                       const TW* __restrict__ w, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * ldx;
+  float v[NV][8];
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 8;
+    if (c < dim) {
+      V8<T>::load(xr + c, v[j]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s += v[j][i] * v[j][i];
+    }
+  }
+  const float r = 1.0f / __builtin_sqrtf(wave_sum(s) / (float)dim + eps);
+  T* yr = y + row * ldy;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 8;
+    if (c < dim) {
+      float w8[8], o[8];
+      if (w) {
+        V8<TW>::load(w + c, w8);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w8[i] = 1.f;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = v[j][i] * r * w8[i];
+      V8<T>::store(yr + c, o);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ rotary helpers
+// Rotates 8 consecutive head-dim elements starting at dim index d0 (even) in place.
+// law 0 (fp32 interleaved, apply_rotary_emb_fp32): out[2i] = x[2i] c[2i] - x[2i+1] s[2i],
+//                                                  out[2i+1] = x[2i+1] c[2i+1] + x[2i] s[2i+1]
+// law 1 (stride-2, apply_rotary_emb): out[2i] = x[2i] c[2i] - x[2i+1] s[2i+1],
+//                                     out[2i+1] = x[2i] s[2i+1] + x[2i+1] c[2i]
+__device__ __forceinline__ void rope8(float* v, const float* cs, const float* sn, int law) {
+  float c[8], s[8];
+  *reinterpret_cast<f32x4*>(c) = *reinterpret_cast<const f32x4*>(cs);
+  *reinterpret_cast<f32x4*>(c + 4) = *reinterpret_cast<const f32x4*>(cs + 4);
+  *reinterpret_cast<f32x4*>(s) = *reinterpret_cast<const f32x4*>(sn);
+  *reinterpret_cast<f32x4*>(s + 4) = *reinterpret_cast<const f32x4*>(sn + 4);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a = v[2 * i], b = v[2 * i + 1];
+    if (law == 0) {
+      v[2 * i] = a * c[2 * i] - b * s[2 * i];
+      v[2 * i + 1] = b * c[2 * i + 1] + a * s[2 * i + 1];
+    } else {
+      v[2 * i] = a * c[2 * i] - b * s[2 * i + 1];
+      v[2 * i + 1] = a * s[2 * i + 1] + b * c[2 * i];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ q/k RMSNorm + RoPE
+// One wavefront per row; LPH = lanes per head (head_dim / 8); a wave covers 64 / LPH heads
+// per step. Statistics reduce over the LPH lanes of one head with xor shuffles.
+template <typename T, typename TW, int LPH>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(
+    T* __restrict__ buf, int64_t ld, int64_t rows, int heads, int64_t q_off, int64_t k_off,
+    int do_norm, const TW* __restrict__ wq, const TW* __restrict__ wk, float eps,
+    const float* __restrict__ cosb, const float* __restrict__ sinb, int64_t rope_rows,
+    int law) {
+  constexpr int HD = LPH * 8;
+  constexpr int HPS = 64 / LPH;  // heads per step
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int sub = lane % LPH;  // which 8-wide slice of the head
+  const int hl = lane / LPH;   // which head of the step
+  const int d0 = sub * 8;
+  const float* cr = cosb ? cosb + (row % rope_rows) * HD + d0 : nullptr;
+  const float* sr = sinb ? sinb + (row % rope_rows) * HD + d0 : nullptr;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int64_t off = t == 0 ? q_off : k_off;
+    if (off < 0) continue;
+    const TW* w = t == 0 ? wq : wk;
+    T* base = buf + row * ld + off;
+    for (int h0 = 0; h0 < heads; h0 += HPS) {
+      const int h = h0 + hl;
+      if (h < heads) {
+        T* p = base + (int64_t)h * HD + d0;
+        float v[8];
+        V8<T>::load(p, v);
+        if (do_norm) {
+          float s = 0.f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) s += v[i] * v[i];
+#pragma unroll
+          for (int o = LPH / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+          const float r = 1.0f / __builtin_sqrtf(s / (float)HD + eps);
+          float w8[8];
+          if (w) {
+            V8<TW>::load(w + d0, w8);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w8[i] = 1.f;
+          }
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[i] = v[i] * r * w8[i];
+        }
+        if (cr) rope8(v, cr, sr, law);
+        V8<T>::store(p, v);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ RoPE, out of place
+template <typename T, int LPH>
+__global__ __launch_bounds__(256) void rope_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                   int64_t outer, int64_t seq,
+                                                   int64_t xos, int64_t xss, int64_t yos,
+                                                   int64_t yss, const float* __restrict__ cosb,
+                                                   const float* __restrict__ sinb,
+                                                   int64_t rope_rows, int law) {
+  constexpr int HD = LPH * 8;
+  constexpr int RPW = 64 / LPH;  // rows per wave
+  const int lane = threadIdx.x & 63;
+  const int64_t total = outer * seq;
+  const int64_t r = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / LPH;
+  if (r >= total) return;
+  const int64_t o = r / seq, s = r % seq;
+  const int d0 = (lane % LPH) * 8;
+  float v[8];
+  V8<T>::load(x + o * xos + s * xss + d0, v);
+  rope8(v, cosb + (s % rope_rows) * HD + d0, sinb + (s % rope_rows) * HD + d0, law);
+  V8<T>::store(y + o * yos + s * yss + d0, v);
+}
+
+// ------------------------------------------------------------------ GELU-tanh
+template <typename T>
+__global__ __launch_bounds__(256) void gelu_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                   int64_t n) {
+  const int64_t nv = n / 8;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nv;
+       i += (int64_t)gridDim.x * 256) {
+    float v[8];
+    V8<T>::load(x + i * 8, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = gelu_tanh(v[j]);
+    V8<T>::store(y + i * 8, v);
+  }
+  for (int64_t i = nv * 8 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * 256)
+    Elt<T>::store(y + i, gelu_tanh(Elt<T>::load(x + i)));
+}
+
+// ------------------------------------------------------------------ gate * x + residual
+template <typename T, typename TG>
+__global__ __launch_bounds__(256) void gate_residual_kernel(
+    const T* __restrict__ res, const T* __restrict__ x, const TG* __restrict__ gate,
+    T* __restrict__ y, int64_t rows, int64_t dim, int64_t gate_stride, int64_t rpb) {
+  const int64_t nvr = dim / 8;
+  const int64_t nv = rows * nvr;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nv;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / nvr, c = (i % nvr) * 8;
+    float a[8], b[8], g[8];
+    V8<T>::load(res + r * dim + c, a);
+    V8<T>::load(x + r * dim + c, b);
+    V8<TG>::load(gate + (r / rpb) * gate_stride + c, g);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a[j] = a[j] + g[j] * b[j];
+    V8<T>::store(y + r * dim + c, a);
+  }
+}
+
+// ------------------------------------------------------------------ small-M GEMV
+// One wavefront per output column n; the activated input rows sit in LDS as fp32 (rounded to
+// the input dtype first, as the reference's `silu(emb)` tensor is). W is read once, 16 bytes
+// per lane per step, so the kernel runs at HBM speed. M is a compile-time bound on the rows;
+// rows m..M-1 of the LDS stage are zero and never stored.
+template <typename T, int M>
+__global__ __launch_bounds__(256) void gemv_kernel(const T* __restrict__ x, int m, int64_t k,
+                                                   int64_t ldx, const bf16* __restrict__ w,
+                                                   int64_t ldw, int64_t n,
+                                                   const T* __restrict__ bias,
+                                                   T* __restrict__ y, int64_t ldy, int act) {
+  extern __shared__ float xs[];  // [M][k]
+  for (int64_t i = threadIdx.x; i < (int64_t)M * k; i += 256) {
+    const int64_t r = i / k, kk = i % k;
+    float v = 0.f;
+    if (r < m) {
+      v = Elt<T>::load(x + r * ldx + kk);
+      if (act == 1) {
+        T t;
+        Elt<T>::store(&t, silu(v));
+        v = Elt<T>::load(&t);
+      }
+    }
+    xs[i] = v;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int64_t waves = (int64_t)gridDim.x * 4;
+  for (int64_t col = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); col < n; col += waves) {
+    const bf16* wr = w + col * ldw;
+    float acc[M];
+#pragma unroll
+    for (int r = 0; r < M; ++r) acc[r] = 0.f;
+    constexpr int U = 4;
+    int64_t c0 = 0;
+    for (; c0 + (int64_t)U * 512 <= k; c0 += U * 512) {
+      u32x4 wv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        wv[u] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(wr + c0 + u * 512 + lane * 8));
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t c = c0 + u * 512 + lane * 8;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float w0 = bf16bits_to_f32(wv[u][i] & 0xffffu);
+          const float w1 = bf16bits_to_f32(wv[u][i] >> 16);
+#pragma unroll
+          for (int r = 0; r < M; ++r)
+            acc[r] += w0 * xs[r * k + c + 2 * i] + w1 * xs[r * k + c + 2 * i + 1];
+        }
+      }
+    }
+    for (int64_t c = c0 + lane * 8; c < k; c += 512) {
+      const u32x4 wv = *reinterpret_cast<const u32x4*>(wr + c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float w0 = bf16bits_to_f32(wv[i] & 0xffffu);
+        const float w1 = bf16bits_to_f32(wv[i] >> 16);
+#pragma unroll
+        for (int r = 0; r < M; ++r)
+          acc[r] += w0 * xs[r * k + c + 2 * i] + w1 * xs[r * k + c + 2 * i + 1];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < M; ++r) {
+      const float t = wave_sum(acc[r]);
+      if (lane == 0 && r < m) {
+        const float bv = bias ? Elt<T>::load(bias + col) : 0.f;
+        Elt<T>::store(y + r * ldy + col, t + bv);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ timestep embedding
+template <typename T>
+__global__ void timestep_embedding_kernel(const float* __restrict__ t, T* __restrict__ y,
+                                          int64_t m, int dim, int flip, float shift,
+                                          float scale, float neg_log_period) {
+  const int half = dim / 2;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < m * dim;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / dim;
+    const int c = (int)(i % dim);
+    float v = 0.f;
+    if (c < 2 * half) {
+      const int j = c < half ? c : c - half;
+      // exponent = -ln(max_period) * j / (half - shift) in fp32, emb = exp(exponent), as torch
+      const float e = (neg_log_period * (float)j) / ((float)half - shift);
+      const float arg = scale * (t[r] * expf(e));
+      const bool first = c < half;
+      // unflipped order is [sin, cos]; flip_sin_to_cos swaps the halves
+      const bool is_sin = flip ? !first : first;
+      v = is_sin ? sinf(arg) : cosf(arg);
+    }
+    Elt<T>::store(y + i, v);
+  }
+}
+
+}  // namespace dlt
+
+using namespace dlt;
+
+// ======================================================================== dispatch helpers
+#define DLT_DISPATCH_FLOAT(dt, T, ...)                                          \
+  switch (dt) {                                                                \
+    case DIFFLET_BF16: { typedef bf16 T; __VA_ARGS__; break; }                 \
+    case DIFFLET_F16: { typedef f16 T; __VA_ARGS__; break; }                   \
+    case DIFFLET_F32: { typedef float T; __VA_ARGS__; break; }                 \
+    default: dlt_set_error("unsupported dtype %d", (int)(dt)); return DIFFLET_EINVAL; \
+  }
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+template <typename TX, typename TY, typename TM>
+static int launch_ln(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
+                     int64_t dim, const void* mul, const void* add, int64_t mod_stride,
+                     int64_t rpb, int one_plus, float eps, hipStream_t s) {
+  const int nv = (int)((dim + 511) / 512);
+  dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+#define DLT_LN(NV)                                                                      \
+  hipLaunchKernelGGL((layernorm_modulate_kernel<TX, TY, TM, NV>), grid, block, 0, s,  \
+                     (const TX*)x, ldx, (TY*)y, ldy, rows, (int)dim, (const TM*)mul,   \
+                     (const TM*)add, mod_stride, rpb, one_plus, eps)
+  if (nv <= 2) DLT_LN(2);
+  else if (nv <= 4) DLT_LN(4);
+  else if (nv <= 6) DLT_LN(6);
+  else if (nv <= 8) DLT_LN(8);
+  else if (nv <= 10) DLT_LN(10);
+  else if (nv <= 16) DLT_LN(16);
+  else { dlt_set_error("layernorm: dim %lld exceeds 8192", (long long)dim); return DIFFLET_EUNSUPPORTED; }
+#undef DLT_LN
+  return dlt_check_launch("layernorm_modulate");
+}
+
+extern "C" int difflet_rocm_layernorm_modulate(const void* x, int64_t ldx, void* y,
+                                               int64_t ldy, int dtype, int out_dtype,
+                                               int64_t rows, int64_t dim, const void* mul,
+                                               const void* add, int mod_dtype,
+                                               int64_t mod_stride, int64_t rows_per_batch,
+                                               int one_plus, float eps,
+                                               difflet_stream_t stream) {
+  DLT_REQUIRE(x && y, DIFFLET_EINVAL, "layernorm: null pointer");
+  DLT_REQUIRE(rows >= 0 && dim > 0 && dim % 8 == 0, DIFFLET_EINVAL,
+              "layernorm: dim %lld must be a positive multiple of 8", (long long)dim);
+  DLT_REQUIRE(ldx % 8 == 0 && ldy % 8 == 0 && (mod_stride % 8 == 0 || (!mul && !add)),
+              DIFFLET_EINVAL, "layernorm: strides must be multiples of 8 elements");
+  DLT_REQUIRE(aligned16(x) && aligned16(y) && (!mul || aligned16(mul)) &&
+                  (!add || aligned16(add)),
+              DIFFLET_EINVAL, "layernorm: pointers must be 16-byte aligned");
+  if (rows == 0) return DIFFLET_OK;
+  if (rows_per_batch <= 0) rows_per_batch = rows;
+  hipStream_t s = (hipStream_t)stream;
+  DLT_DISPATCH_FLOAT(dtype, TX,
+    DLT_DISPATCH_FLOAT(out_dtype, TY,
+      DLT_DISPATCH_FLOAT(mod_dtype, TM,
+        return launch_ln<TX, TY, TM>(x, ldx, y, ldy, rows, dim, mul, add, mod_stride,
+                                     rows_per_batch, one_plus, eps, s))));
+  return DIFFLET_OK;
+}
+
+template <typename T, typename TW>
+static int launch_rms(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
+                      int64_t dim, const void* w, float eps, hipStream_t s) {
+  const int nv = (int)((dim + 511) / 512);
+  dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+#define DLT_RMS(NV)                                                                         \
+  hipLaunchKernelGGL((rms_norm_kernel<T, TW, NV>), grid, block, 0, s, (const T*)x, ldx,     \
+                     (T*)y, ldy, rows, (int)dim, (const TW*)w, eps)
+  if (nv <= 1) DLT_RMS(1);
+  else if (nv <= 2) DLT_RMS(2);
+  else if (nv <= 4) DLT_RMS(4);
+  else if (nv <= 8) DLT_RMS(8);
+  else if (nv <= 10) DLT_RMS(10);
+  else if (nv <= 16) DLT_RMS(16);
+  else { dlt_set_error("rms_norm: dim %lld exceeds 8192", (long long)dim); return DIFFLET_EUNSUPPORTED; }
+#undef DLT_RMS
+  return dlt_check_launch("rms_norm");
+}
+
+extern "C" int difflet_rocm_rms_norm(const void* x, int64_t ldx, void* y, int64_t ldy,
+                                     int dtype, int64_t rows, int64_t dim, const void* weight,
+                                     int wdtype, float eps, difflet_stream_t stream) {
+  DLT_REQUIRE(x && y, DIFFLET_EINVAL, "rms_norm: null pointer");
+  DLT_REQUIRE(rows >= 0 && dim > 0 && dim % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0,
+              DIFFLET_EINVAL, "rms_norm: dim and strides must be multiples of 8");
+  DLT_REQUIRE(aligned16(x) && aligned16(y) && (!weight || aligned16(weight)), DIFFLET_EINVAL,
+              "rms_norm: pointers must be 16-byte aligned");
+  if (rows == 0) return DIFFLET_OK;
+  hipStream_t s = (hipStream_t)stream;
+  DLT_DISPATCH_FLOAT(dtype, T,
+    DLT_DISPATCH_FLOAT(wdtype, TW,
+      return launch_rms<T, TW>(x, ldx, y, ldy, rows, dim, weight, eps, s)));
+  return DIFFLET_OK;
+}
+
+template <typename T, typename TW>
+static int launch_qk(void* buf, int64_t ld, int64_t rows, int64_t heads, int64_t hd,
+                     int64_t q_off, int64_t k_off, int do_norm, const void* wq,
+                     const void* wk, float eps, const float* c, const float* sn,
+                     int64_t rope_rows, int law, hipStream_t s) {
+  dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+#define DLT_QK(LPH)                                                                        \
+  hipLaunchKernelGGL((qk_norm_rope_kernel<T, TW, LPH>), grid, block, 0, s, (T*)buf, ld,    \
+                     rows, (int)heads, q_off, k_off, do_norm, (const TW*)wq,                \
+                     (const TW*)wk, eps, c, sn, rope_rows, law)
+  switch (hd) {
+    case 32: DLT_QK(4); break;
+    case 64: DLT_QK(8); break;
+    case 128: DLT_QK(16); break;
+    case 256: DLT_QK(32); break;
+    default: dlt_set_error("qk_norm_rope: head_dim %lld not in {32,64,128,256}", (long long)hd);
+      return DIFFLET_EUNSUPPORTED;
+  }
+#undef DLT_QK
+  return dlt_check_launch("qk_norm_rope");
+}
+
+extern "C" int difflet_rocm_qk_norm_rope(void* buf, int64_t ld, int dtype, int64_t rows,
+                                         int64_t heads, int64_t head_dim, int64_t q_off,
+                                         int64_t k_off, int do_norm, const void* wq,
+                                         const void* wk, int wdtype, float eps,
+                                         const float* cos, const float* sin,
+                                         int64_t rope_rows, int law,
+                                         difflet_stream_t stream) {
+  DLT_REQUIRE(buf, DIFFLET_EINVAL, "qk_norm_rope: null buffer");
+  DLT_REQUIRE(rows >= 0 && heads > 0 && ld % 8 == 0 && (q_off < 0 || q_off % 8 == 0) &&
+                  (k_off < 0 || k_off % 8 == 0),
+              DIFFLET_EINVAL, "qk_norm_rope: strides and offsets must be multiples of 8");
+  DLT_REQUIRE(!cos == !sin, DIFFLET_EINVAL, "qk_norm_rope: cos and sin go together");
+  DLT_REQUIRE(!cos || rope_rows > 0, DIFFLET_EINVAL, "qk_norm_rope: rope_rows must be > 0");
+  DLT_REQUIRE(law == 0 || law == 1, DIFFLET_EINVAL, "qk_norm_rope: law must be 0 or 1");
+  DLT_REQUIRE(aligned16(buf) && (!cos || (aligned16(cos) && aligned16(sin))), DIFFLET_EINVAL,
+              "qk_norm_rope: pointers must be 16-byte aligned");
+  if (rows == 0) return DIFFLET_OK;
+  hipStream_t s = (hipStream_t)stream;
+  DLT_DISPATCH_FLOAT(dtype, T,
+    DLT_DISPATCH_FLOAT(wdtype, TW,
+      return launch_qk<T, TW>(buf, ld, rows, heads, head_dim, q_off, k_off, do_norm, wq, wk,
+                              eps, cos, sin, rope_rows, law, s)));
+  return DIFFLET_OK;
+}
+
+template <typename T>
+static int launch_rope(const void* x, void* y, int64_t outer, int64_t seq, int64_t head_dim,
+                       int64_t xos, int64_t xss, int64_t yos, int64_t yss, const float* cos,
+                       const float* sin, int64_t rope_rows, int law, hipStream_t s) {
+  const int64_t total = outer * seq;
+  int lph;
+  switch (head_dim) {
+    case 32: lph = 4; break;
+    case 64: lph = 8; break;
+    case 128: lph = 16; break;
+    case 256: lph = 32; break;
+    default:
+      dlt_set_error("rope: head_dim %lld not in {32,64,128,256}", (long long)head_dim);
+      return DIFFLET_EUNSUPPORTED;
+  }
+  const int64_t rows_per_block = 4 * (64 / lph);
+  dim3 grid((unsigned)((total + rows_per_block - 1) / rows_per_block)), block(256);
+#define DLT_ROPE(LPH)                                                                         \
+  hipLaunchKernelGGL((rope_kernel<T, LPH>), grid, block, 0, s, (const T*)x, (T*)y, outer, seq, \
+                     xos, xss, yos, yss, cos, sin, rope_rows, law)
+  if (lph == 4) DLT_ROPE(4);
+  else if (lph == 8) DLT_ROPE(8);
+  else if (lph == 16) DLT_ROPE(16);
+  else DLT_ROPE(32);
+#undef DLT_ROPE
+  return dlt_check_launch("rope");
+}
+
+extern "C" int difflet_rocm_rope(const void* x, void* y, int dtype, int64_t outer,
+                                 int64_t seq, int64_t head_dim, int64_t xos, int64_t xss,
+                                 int64_t yos, int64_t yss, const float* cos, const float* sin,
+                                 int64_t rope_rows, int law, difflet_stream_t stream) {
+  DLT_REQUIRE(x && y && cos && sin, DIFFLET_EINVAL, "rope: null pointer");
+  DLT_REQUIRE(outer >= 0 && seq >= 0 && rope_rows > 0 && (law == 0 || law == 1),
+              DIFFLET_EINVAL, "rope: bad shape or law");
+  DLT_REQUIRE(xos % 8 == 0 && xss % 8 == 0 && yos % 8 == 0 && yss % 8 == 0 && aligned16(x) &&
+                  aligned16(y) && aligned16(cos) && aligned16(sin),
+              DIFFLET_EINVAL, "rope: strides must be multiples of 8 and pointers aligned");
+  if (outer * seq == 0) return DIFFLET_OK;
+  hipStream_t s = (hipStream_t)stream;
+  DLT_DISPATCH_FLOAT(dtype, T,
+    return launch_rope<T>(x, y, outer, seq, head_dim, xos, xss, yos, yss, cos, sin, rope_rows,
+                          law, s));
+  return DIFFLET_OK;
+}
+
+extern "C" int difflet_rocm_gelu_tanh(const void* x, void* y, int dtype, int64_t n,
+                                      difflet_stream_t stream) {
+  DLT_REQUIRE(x && y && n >= 0, DIFFLET_EINVAL, "gelu: bad arguments");
+  DLT_REQUIRE(aligned16(x) && aligned16(y), DIFFLET_EINVAL, "gelu: pointers must be aligned");
+  if (n == 0) return DIFFLET_OK;
+  hipStream_t s = (hipStream_t)stream;
+  int64_t blocks = (n / 8 + 255) / 256;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 65536) blocks = 65536;
+  DLT_DISPATCH_FLOAT(dtype, T,
+    hipLaunchKernelGGL((gelu_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, s,
+                       (const T*)x, (T*)y, n));
+  return dlt_check_launch("gelu_tanh");
+}
+
+extern "C" int difflet_rocm_gate_residual(const void* residual, const void* x,
+                                          const void* gate, void* y, int dtype,
+                                          int gate_dtype, int64_t rows, int64_t dim,
+                                          int64_t gate_stride, int64_t rows_per_batch,
+                                          difflet_stream_t stream) {
+  DLT_REQUIRE(residual && x && gate && y, DIFFLET_EINVAL, "gate_residual: null pointer");
+  DLT_REQUIRE(dim % 8 == 0 && gate_stride % 8 == 0 && aligned16(residual) && aligned16(x) &&
+                  aligned16(gate) && aligned16(y),
+              DIFFLET_EINVAL, "gate_residual: dim must be a multiple of 8, pointers aligned");
+  if (rows * dim == 0) return DIFFLET_OK;
+  if (rows_per_batch <= 0) rows_per_batch = rows;
+  hipStream_t s = (hipStream_t)stream;
+  int64_t blocks = (rows * dim / 8 + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  DLT_DISPATCH_FLOAT(dtype, T,
+    DLT_DISPATCH_FLOAT(gate_dtype, TG,
+      hipLaunchKernelGGL((gate_residual_kernel<T, TG>), dim3((unsigned)blocks), dim3(256), 0,
+                         s, (const T*)residual, (const T*)x, (const TG*)gate, (T*)y, rows,
+                         dim, gate_stride, rows_per_batch)));
+  return dlt_check_launch("gate_residual");
+}
+
+template <typename T>
+static int launch_gemv(const void* x, int64_t m, int mb, int64_t k, int64_t ldx, const void* w,
+                       int64_t ldw, int64_t n, const void* bias, void* y, int64_t ldy, int act,
+                       hipStream_t s) {
+  int64_t blocks = (n + 3) / 4;
+  if (blocks > 8192) blocks = 8192;
+  const size_t lds = (size_t)(mb * k * 4);
+#define DLT_GEMV(M)                                                                          \
+  hipLaunchKernelGGL((gemv_kernel<T, M>), dim3((unsigned)blocks), dim3(256), lds, s,         \
+                     (const T*)x, (int)m, k, ldx, (const bf16*)w, ldw, n, (const T*)bias,     \
+                     (T*)y, ldy, act)
+  switch (mb) {
+    case 1: DLT_GEMV(1); break;
+    case 2: DLT_GEMV(2); break;
+    case 4: DLT_GEMV(4); break;
+    default: DLT_GEMV(8); break;
+  }
+#undef DLT_GEMV
+  return dlt_check_launch("gemv");
+}
+
+extern "C" int difflet_rocm_gemv(const void* x, int dtype, int64_t m, int64_t k, int64_t ldx,
+                                 const void* w, int64_t ldw, int64_t n, const void* bias,
+                                 void* y, int64_t ldy, int act, difflet_stream_t stream) {
+  DLT_REQUIRE(x && w && y, DIFFLET_EINVAL, "gemv: null pointer");
+  DLT_REQUIRE(m >= 1 && m <= 8, DIFFLET_EUNSUPPORTED, "gemv: m = %lld not in [1, 8]",
+              (long long)m);
+  DLT_REQUIRE(k > 0 && k % 8 == 0 && ldw % 8 == 0 && aligned16(w), DIFFLET_EINVAL,
+              "gemv: k and ldw must be multiples of 8 and w 16-byte aligned");
+  const int mb = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
+  DLT_REQUIRE(mb * k * 4 <= 64 * 1024, DIFFLET_EUNSUPPORTED,
+              "gemv: m * k = %lld exceeds the 16384-element LDS stage", (long long)(mb * k));
+  DLT_REQUIRE(act == 0 || act == 1, DIFFLET_EINVAL, "gemv: act must be 0 or 1");
+  if (n == 0) return DIFFLET_OK;
+  hipStream_t s = (hipStream_t)stream;
+  DLT_DISPATCH_FLOAT(dtype, T,
+    return launch_gemv<T>(x, m, mb, k, ldx, w, ldw, n, bias, y, ldy, act, s));
+  return DIFFLET_OK;
+}
+
+extern "C" int difflet_rocm_timestep_embedding(const float* t, void* y, int dtype, int64_t m,
+                                               int64_t dim, int flip_sin_to_cos,
+                                               float downscale_freq_shift, float scale,
+                                               float max_period, difflet_stream_t stream) {
+  DLT_REQUIRE(t && y && m >= 0 && dim > 0, DIFFLET_EINVAL, "timestep_embedding: bad args");
+  if (m == 0) return DIFFLET_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t total = m * dim;
+  DLT_DISPATCH_FLOAT(dtype, T,
+    hipLaunchKernelGGL((timestep_embedding_kernel<T>),
+                       dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, t, (T*)y, m,
+                       (int)dim, flip_sin_to_cos, downscale_freq_shift, scale,
+                       (float)(-log((double)max_period))));
+  return dlt_check_launch("timestep_embedding");
+}

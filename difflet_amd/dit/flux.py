@@ -1,0 +1,317 @@
+"""FLUX.1 DiT denoise step on the gfx950 kernels: the fused, MI355X-first form of
+NeuronFluxTransformer2DModel.forward (difflet/models/flux/modeling_flux.py:364-613).
+
+This is the rocm backend's load-time module swap for FLUX (the reference's rule for a fusion of
+one model on one backend, docs/design/gpu_backend.md:36-40): same weights (diffusers names),
+same math, fewer HBM passes.
+
+HBM layout, batch 1, S = S_txt + S_img tokens, D = hidden:
+  h      [S, D] bf16     the residual stream, text rows first: the double blocks' two streams
+                         are its two row ranges, so the double -> single concat is free.
+  n      [S, D] bf16     LayerNorm + adaLN modulation output (the GEMM input).
+  qkv    [S, 3D] bf16    double blocks: [q | k | v] per row from one GEMM per stream (text and
+                         image grouped in one launch); q/k RMSNorm + RoPE in place; attention
+                         reads q/k/v through strides and writes its output over q.
+  big    [S, 7D] bf16    single blocks: [k | v | q | gelu(mlp)] from one GEMM (N = 7D, GELU
+                         on the last 4D columns); attention output over q, so [attn | mlp] is
+                         columns 2D..7D and proj_out is one K = 5D GEMM on that view with the
+                         gate * (x + bias) + residual epilogue writing h in place.
+  ff     [S, 4D] bf16    double blocks' MLP hidden (GELU fused into the up-projection).
+  mod    [344 D] bf16    every block's adaLN vectors from one GEMV per step (temb is shared).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Callable
+
+import torch
+
+from difflet_amd import _lib, kernels
+from difflet_amd.dit.linear import DeviceLinear, run
+from difflet_amd.dit.rope import flux_rope_tables
+
+EPS = 1e-6
+
+
+class FluxConfig:
+    def __init__(self, hidden=3072, heads=24, head_dim=128, mlp_ratio=4, n_double=19,
+                 n_single=38, in_channels=64, out_channels=64, txt_dim=4096, pooled_dim=768,
+                 axes=(16, 56, 56), guidance=True):
+        self.hidden, self.heads, self.head_dim = hidden, heads, head_dim
+        self.mlp = hidden * mlp_ratio
+        self.n_double, self.n_single = n_double, n_single
+        self.in_channels, self.out_channels = in_channels, out_channels
+        self.txt_dim, self.pooled_dim = txt_dim, pooled_dim
+        self.axes, self.guidance = tuple(axes), guidance
+        if heads * head_dim != hidden:
+            raise ValueError("heads * head_dim must equal hidden")
+
+
+class _Double:
+    def __init__(self, get: Callable[[str], torch.Tensor], pre: str, cfg: FluxConfig, kind: str):
+        W = lambda n: get(f"{pre}.{n}")  # noqa: E731
+        cat = lambda *ns: torch.cat([W(n) for n in ns], dim=0)  # noqa: E731
+        a = "attn."
+        self.qkv_img = DeviceLinear(cat(a + "to_q.weight", a + "to_k.weight", a + "to_v.weight"),
+                                    cat(a + "to_q.bias", a + "to_k.bias", a + "to_v.bias"), kind)
+        self.qkv_txt = DeviceLinear(
+            cat(a + "add_q_proj.weight", a + "add_k_proj.weight", a + "add_v_proj.weight"),
+            cat(a + "add_q_proj.bias", a + "add_k_proj.bias", a + "add_v_proj.bias"), kind)
+        self.out_img = DeviceLinear(W(a + "to_out.0.weight"), W(a + "to_out.0.bias"), kind)
+        self.out_txt = DeviceLinear(W(a + "to_add_out.weight"), W(a + "to_add_out.bias"), kind)
+        self.ff1_img = DeviceLinear(W("ff.net.0.proj.weight"), W("ff.net.0.proj.bias"), kind)
+        self.ff2_img = DeviceLinear(W("ff.net.2.weight"), W("ff.net.2.bias"), kind)
+        self.ff1_txt = DeviceLinear(W("ff_context.net.0.proj.weight"),
+                                    W("ff_context.net.0.proj.bias"), kind)
+        self.ff2_txt = DeviceLinear(W("ff_context.net.2.weight"), W("ff_context.net.2.bias"),
+                                    kind)
+        bf = lambda n: W(n).to(torch.bfloat16).contiguous()  # noqa: E731
+        self.nq, self.nk = bf(a + "norm_q.weight"), bf(a + "norm_k.weight")
+        self.naq, self.nak = bf(a + "norm_added_q.weight"), bf(a + "norm_added_k.weight")
+
+
+class _Single:
+    def __init__(self, get: Callable[[str], torch.Tensor], pre: str, cfg: FluxConfig, kind: str):
+        W = lambda n: get(f"{pre}.{n}")  # noqa: E731
+        a = "attn."
+        # column order [k | v | q | mlp]: attention writes over q, leaving [attn | mlp] adjacent
+        self.w1 = DeviceLinear(
+            torch.cat([W(a + "to_k.weight"), W(a + "to_v.weight"), W(a + "to_q.weight"),
+                       W("proj_mlp.weight")], dim=0),
+            torch.cat([W(a + "to_k.bias"), W(a + "to_v.bias"), W(a + "to_q.bias"),
+                       W("proj_mlp.bias")], dim=0), kind)
+        self.w2 = DeviceLinear(W("proj_out.weight"), W("proj_out.bias"), kind)
+        bf = lambda n: W(n).to(torch.bfloat16).contiguous()  # noqa: E731
+        self.nq, self.nk = bf(a + "norm_q.weight"), bf(a + "norm_k.weight")
+
+
+class FluxDiT:
+    """The FLUX transformer on the HIP kernels. `get(name)` returns a parameter by its diffusers
+    name (any dtype, on the target device); `kind` picks the block linears' format."""
+
+    def __init__(self, cfg: FluxConfig, get: Callable[[str], torch.Tensor], kind: str = "bf16",
+                 device: str | torch.device = "cuda"):
+        self.cfg, self.kind = cfg, kind
+        self.device = torch.device(device)
+        d = cfg.hidden
+        G = lambda n: get(n).to(self.device)  # noqa: E731
+        bf = lambda n: G(n).to(torch.bfloat16).contiguous()  # noqa: E731
+        # embedders and the final layer stay bf16 (difflet/quant/targets.py:174-184)
+        self.x_emb = DeviceLinear(G("x_embedder.weight"), G("x_embedder.bias"))
+        self.ctx_emb = DeviceLinear(G("context_embedder.weight"), G("context_embedder.bias"))
+        self.t_w1, self.t_b1 = bf("time_text_embed.timestep_embedder.linear_1.weight"), bf("time_text_embed.timestep_embedder.linear_1.bias")
+        self.t_w2, self.t_b2 = bf("time_text_embed.timestep_embedder.linear_2.weight"), bf("time_text_embed.timestep_embedder.linear_2.bias")
+        if cfg.guidance:
+            self.g_w1, self.g_b1 = bf("time_text_embed.guidance_embedder.linear_1.weight"), bf("time_text_embed.guidance_embedder.linear_1.bias")
+            self.g_w2, self.g_b2 = bf("time_text_embed.guidance_embedder.linear_2.weight"), bf("time_text_embed.guidance_embedder.linear_2.bias")
+        self.p_w1, self.p_b1 = bf("time_text_embed.text_embedder.linear_1.weight"), bf("time_text_embed.text_embedder.linear_1.bias")
+        self.p_w2, self.p_b2 = bf("time_text_embed.text_embedder.linear_2.weight"), bf("time_text_embed.text_embedder.linear_2.bias")
+        self.proj_out = DeviceLinear(G("proj_out.weight"), G("proj_out.bias"))
+
+        # every adaLN linear of the step in one [344 D, D] matrix: one GEMV per step
+        mod_w, mod_b, self.mod_off = [], [], {}
+        off = 0
+        for i in range(cfg.n_double):
+            for part in ("norm1", "norm1_context"):
+                mod_w.append(bf(f"transformer_blocks.{i}.{part}.linear.weight"))
+                mod_b.append(bf(f"transformer_blocks.{i}.{part}.linear.bias"))
+                self.mod_off[("d", i, part)] = off
+                off += 6 * d
+        for i in range(cfg.n_single):
+            mod_w.append(bf(f"single_transformer_blocks.{i}.norm.linear.weight"))
+            mod_b.append(bf(f"single_transformer_blocks.{i}.norm.linear.bias"))
+            self.mod_off[("s", i)] = off
+            off += 3 * d
+        mod_w.append(bf("norm_out.linear.weight"))
+        mod_b.append(bf("norm_out.linear.bias"))
+        self.mod_off["out"] = off
+        off += 2 * d
+        self.mod_w = torch.cat(mod_w, dim=0)
+        self.mod_b = torch.cat(mod_b, dim=0)
+        del mod_w, mod_b
+        self.double = [_Double(G, f"transformer_blocks.{i}", cfg, kind) for i in range(cfg.n_double)]
+        self.single = [_Single(G, f"single_transformer_blocks.{i}", cfg, kind)
+                       for i in range(cfg.n_single)]
+        self._bufs: dict = {}
+        self._rope: dict = {}
+
+    # -------------------------------------------------------------------------- helpers
+    def _buffers(self, st: int, si: int):
+        key = (st, si)
+        if key not in self._bufs:
+            s, d, dev = st + si, self.cfg.hidden, self.device
+            e = lambda *shape: torch.empty(shape, dtype=torch.bfloat16, device=dev)  # noqa: E731
+            self._bufs = {key: {"h": e(s, d), "n": e(s, d), "qkv": e(s, 3 * d),
+                                "big": e(s, 7 * d), "ff": e(s, self.cfg.mlp),
+                                "mod": e(1, self.mod_w.shape[0])}}
+        return self._bufs[key]
+
+    def rope_tables(self, st: int, img_hw: tuple[int, int]):
+        key = (st, tuple(img_hw))
+        if key not in self._rope:
+            self._rope = {key: flux_rope_tables(st, img_hw, self.cfg.axes, self.device)}
+        return self._rope[key]
+
+    def _mods(self, mod: torch.Tensor, off: int, n: int):
+        d = self.cfg.hidden
+        return [mod[:, off + j * d: off + (j + 1) * d] for j in range(n)]
+
+    def _qk(self, buf, rows: slice, q_off: int, k_off: int, wq, wk, cos, sin):
+        c = self.cfg
+        kernels.qk_norm_rope(buf[rows], heads=c.heads, head_dim=c.head_dim, q_off=q_off,
+                             k_off=k_off, wq=wq, wk=wk, eps=EPS, cos=cos[rows], sin=sin[rows],
+                             law=0)
+
+    def _attn(self, buf, q_off: int, k_off: int, v_off: int):
+        """Joint attention over all rows of `buf` [S, ld]; output written over q."""
+        c = self.cfg
+        s, ld = buf.shape
+        view = lambda off: buf.as_strided((1, c.heads, s, c.head_dim), (0, c.head_dim, ld, 1),  # noqa: E731
+                                          buf.storage_offset() + off)
+        q, k, v = view(q_off), view(k_off), view(v_off)
+        kernels.attention(q, k, v, scale=1.0 / math.sqrt(c.head_dim), out=q)
+
+    # -------------------------------------------------------------------------- blocks
+    def double_block(self, i: int, bufs, st: int, mod, cos, sin):
+        blk = self.double[i]
+        d = self.cfg.hidden
+        h, n, qkv, ff = bufs["h"], bufs["n"], bufs["qkv"], bufs["ff"]
+        s = h.shape[0]
+        T, I = slice(0, st), slice(st, s)
+        x_sh, x_sc, x_g, x_sh2, x_sc2, x_g2 = self._mods(mod, self.mod_off[("d", i, "norm1")], 6)
+        c_sh, c_sc, c_g, c_sh2, c_sc2, c_g2 = self._mods(mod, self.mod_off[("d", i, "norm1_context")], 6)
+        kernels.layernorm_modulate(h[T], c_sc, c_sh, eps=EPS, out=n[T])
+        kernels.layernorm_modulate(h[I], x_sc, x_sh, eps=EPS, out=n[I])
+        run([blk.qkv_txt.problem(n[T], qkv[T]), blk.qkv_img.problem(n[I], qkv[I])], self.kind)
+        self._qk(qkv, T, 0, d, blk.naq, blk.nak, cos, sin)
+        self._qk(qkv, I, 0, d, blk.nq, blk.nk, cos, sin)
+        self._attn(qkv, 0, d, 2 * d)
+        o = qkv[:, :d]
+        run([blk.out_txt.problem(o[T], h[T], gate=c_g, residual=h[T]),
+             blk.out_img.problem(o[I], h[I], gate=x_g, residual=h[I])], self.kind,
+            _lib.EPI_GATE_RESIDUAL)
+        kernels.layernorm_modulate(h[T], c_sc2, c_sh2, eps=EPS, out=n[T])
+        kernels.layernorm_modulate(h[I], x_sc2, x_sh2, eps=EPS, out=n[I])
+        run([blk.ff1_txt.problem(n[T], ff[T]), blk.ff1_img.problem(n[I], ff[I])], self.kind,
+            _lib.EPI_GELU)
+        run([blk.ff2_txt.problem(ff[T], h[T], gate=c_g2, residual=h[T]),
+             blk.ff2_img.problem(ff[I], h[I], gate=x_g2, residual=h[I])], self.kind,
+            _lib.EPI_GATE_RESIDUAL)
+
+    def single_block(self, i: int, bufs, mod, cos, sin):
+        blk = self.single[i]
+        d = self.cfg.hidden
+        h, n, big = bufs["h"], bufs["n"], bufs["big"]
+        sh, sc, g = self._mods(mod, self.mod_off[("s", i)], 3)
+        kernels.layernorm_modulate(h, sc, sh, eps=EPS, out=n)
+        run([blk.w1.problem(n, big)], self.kind, _lib.EPI_GELU, act_col_start=3 * d)
+        self._qk(big, slice(0, h.shape[0]), 2 * d, 0, blk.nq, blk.nk, cos, sin)
+        self._attn(big, 2 * d, 0, d)
+        run([blk.w2.problem(big[:, 2 * d:], h, gate=g, residual=h)], self.kind,
+            _lib.EPI_GATE_RESIDUAL)
+
+    # -------------------------------------------------------------------------- step
+    def embed(self, timestep, guidance, pooled):
+        """temb [1, D] (difflet/layers/embeddings.py:247-281)."""
+        dt = torch.bfloat16
+        # the model casts timestep and guidance to its dtype and scales them there
+        # (modeling_flux.py:453-456,477-479)
+        timestep = timestep.to(dt) * 1000
+        tp = kernels.timestep_embedding(timestep, 256, flip_sin_to_cos=True,
+                                        downscale_freq_shift=0.0, dtype=dt)
+        t = kernels.gemv(kernels.gemv(tp, self.t_w1, self.t_b1), self.t_w2, self.t_b2, act=1)
+        if self.cfg.guidance:
+            gp = kernels.timestep_embedding(guidance.to(dt) * 1000, 256, flip_sin_to_cos=True,
+                                            downscale_freq_shift=0.0, dtype=dt)
+            t = t + kernels.gemv(kernels.gemv(gp, self.g_w1, self.g_b1), self.g_w2, self.g_b2,
+                                 act=1)
+        p = kernels.gemv(kernels.gemv(pooled.to(dt), self.p_w1, self.p_b1), self.p_w2,
+                         self.p_b2, act=1)
+        return t + p
+
+    def forward(self, latents, text, pooled, timestep, guidance, img_hw):
+        """latents [1, S_img, in_ch], text [1, S_txt, txt_dim], pooled [1, pooled_dim],
+        timestep / guidance [1] (timestep in [0, 1]) -> [1, S_img, out_ch] bf16."""
+        if latents.shape[0] != 1:
+            raise NotImplementedError("the fused FLUX step runs batch 1 (one request per call)")
+        st, si = text.shape[1], latents.shape[1]
+        bufs = self._buffers(st, si)
+        cos, sin = self.rope_tables(st, img_hw)
+        h = bufs["h"]
+        dt = torch.bfloat16
+        self.ctx_emb(text[0].to(dt).contiguous(), out=h[:st])
+        self.x_emb(latents[0].to(dt).contiguous(), out=h[st:])
+        temb = self.embed(timestep.to(self.device).float(), guidance.to(self.device).float(),
+                          pooled.to(self.device))
+        mod = kernels.gemv(temb, self.mod_w, self.mod_b, act=1, out=bufs["mod"])
+        for i in range(self.cfg.n_double):
+            self.double_block(i, bufs, st, mod, cos, sin)
+        for i in range(self.cfg.n_single):
+            self.single_block(i, bufs, mod, cos, sin)
+        sc, sh = self._mods(mod, self.mod_off["out"], 2)  # AdaLN-Continuous: scale, shift
+        n = bufs["n"]
+        kernels.layernorm_modulate(h[st:], sc, sh, eps=EPS, out=n[st:])
+        return self.proj_out(n[st:]).unsqueeze(0)
+
+    __call__ = forward
+
+
+def random_param_source(cfg: FluxConfig, seed: int, device, std: float = 0.02):
+    """Parameters drawn on the device on demand, N(0, std) (RMSNorm weights ones), one
+    generator per parameter seeded from (seed, name): the full model is built without a host
+    copy. Not the oracle's draw (that one runs on the host); used where no CPU comparison of
+    the same weights is made (the full-size step benchmark)."""
+    import zlib
+
+    shapes = flux_param_shapes(cfg)
+
+    def get(name: str) -> torch.Tensor:
+        shp = shapes[name]
+        if ".norm_" in name and name.endswith(".weight") and len(shp) == 1:
+            return torch.ones(shp, dtype=torch.bfloat16, device=device)
+        g = torch.Generator(device=device).manual_seed(seed * 1_000_003 + zlib.crc32(name.encode()))
+        return (torch.randn(shp, generator=g, device=device, dtype=torch.float32) * std).to(torch.bfloat16)
+
+    return get
+
+
+def flux_param_shapes(cfg: FluxConfig) -> dict[str, tuple]:
+    d, f, hd = cfg.hidden, cfg.mlp, cfg.head_dim
+    out: dict[str, tuple] = {}
+
+    def lin(n, o, i):
+        out[f"{n}.weight"] = (o, i)
+        out[f"{n}.bias"] = (o,)
+
+    lin("x_embedder", d, cfg.in_channels)
+    lin("context_embedder", d, cfg.txt_dim)
+    for e, i in (("timestep_embedder", 256), ("guidance_embedder", 256),
+                 ("text_embedder", cfg.pooled_dim)):
+        lin(f"time_text_embed.{e}.linear_1", d, i)
+        lin(f"time_text_embed.{e}.linear_2", d, d)
+    lin("norm_out.linear", 2 * d, d)
+    lin("proj_out", cfg.out_channels, d)
+    for b in range(cfg.n_double):
+        p = f"transformer_blocks.{b}"
+        lin(f"{p}.norm1.linear", 6 * d, d)
+        lin(f"{p}.norm1_context.linear", 6 * d, d)
+        for n in ("to_q", "to_k", "to_v", "add_q_proj", "add_k_proj", "add_v_proj", "to_out.0",
+                  "to_add_out"):
+            lin(f"{p}.attn.{n}", d, d)
+        for n in ("norm_q", "norm_k", "norm_added_q", "norm_added_k"):
+            out[f"{p}.attn.{n}.weight"] = (hd,)
+        lin(f"{p}.ff.net.0.proj", f, d)
+        lin(f"{p}.ff.net.2", d, f)
+        lin(f"{p}.ff_context.net.0.proj", f, d)
+        lin(f"{p}.ff_context.net.2", d, f)
+    for b in range(cfg.n_single):
+        p = f"single_transformer_blocks.{b}"
+        lin(f"{p}.norm.linear", 3 * d, d)
+        lin(f"{p}.proj_mlp", f, d)
+        for n in ("to_q", "to_k", "to_v"):
+            lin(f"{p}.attn.{n}", d, d)
+        for n in ("norm_q", "norm_k"):
+            out[f"{p}.attn.{n}.weight"] = (hd,)
+        lin(f"{p}.proj_out", d, d + f)
+    return out

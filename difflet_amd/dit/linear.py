@@ -1,0 +1,65 @@
+"""Device linear layers of the fused DiT blocks: one weight in the layout its GEMM reads.
+
+kind "bf16": W bf16 [N, K].
+kind "fp8" : per-output-channel e4m3 codes [N, K] + fp32 scales [N]; activations are quantized
+             per token right before the GEMM (difflet_rocm_quantize_fp8_rowwise), and the GEMM
+             applies s_x[m] * s_w[n] in its epilogue.
+kind "mx"  : MXFP8, codes in swizzle order [N, K] + E8M0 scales [N, K/32] (the block law of
+             difflet/quant/mx.py:46-108); activations quantized per call in the same order.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from difflet_amd import kernels
+from difflet_amd.kernels import Problem
+
+KINDS = ("bf16", "fp8", "mx")
+
+
+class DeviceLinear:
+    __slots__ = ("kind", "w", "ws", "bias", "n", "k")
+
+    def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None, kind: str = "bf16"):
+        if kind not in KINDS:
+            raise ValueError(f"linear kind must be one of {KINDS}, got {kind!r}")
+        w = weight.to(torch.bfloat16).contiguous()
+        self.kind = kind
+        self.n, self.k = w.shape
+        self.bias = None if bias is None else bias.to(device=w.device, dtype=torch.bfloat16).contiguous()
+        if kind == "bf16":
+            self.w, self.ws = w, None
+        elif kind == "fp8":
+            self.w, self.ws = kernels.quantize_fp8_rowwise(w)
+        else:
+            self.w, self.ws = kernels.quantize_mxfp8(w, swizzled=True)
+
+    def prep(self, a: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor | None]:
+        """The GEMM's A operand for activations a [M, K] (quantized for the fp8 kinds)."""
+        if self.kind == "bf16":
+            return a, None
+        if self.kind == "fp8":
+            return kernels.quantize_fp8_rowwise(a)
+        return kernels.quantize_mxfp8(a, swizzled=True)
+
+    def problem(self, a: torch.Tensor, c: torch.Tensor, *, gate=None, residual=None,
+                prepared=None) -> Problem:
+        aq, asc = prepared if prepared is not None else self.prep(a)
+        return Problem(aq, self.w, c, self.bias, gate, residual, asc, self.ws)
+
+    def __call__(self, a: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        c = out if out is not None else torch.empty((a.shape[0], self.n), dtype=torch.bfloat16,
+                                                    device=a.device)
+        run([self.problem(a, c)], self.kind)
+        return c
+
+    def weight_bytes(self) -> int:
+        b = self.w.numel() * self.w.element_size()
+        if self.ws is not None:
+            b += self.ws.numel() * self.ws.element_size()
+        return b
+
+
+def run(problems, kind: str, epilogue: int = 0, act_col_start: int = 0) -> None:
+    kernels.gemm_grouped(problems, kind=kind, epilogue=epilogue, act_col_start=act_col_start)

@@ -1,0 +1,390 @@
+"""torch-facing wrappers of the C ABI: validate tensors, pick strides, call libdifflet_rocm.
+
+Every function here runs a HIP kernel on the tensors' device, on torch's current stream. There
+is no CPU or eager-torch path: a CPU tensor, an unsupported dtype or a missing library raises.
+Outputs are allocated with torch (the library never allocates).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Sequence
+
+import torch
+
+from difflet_amd import _lib
+from difflet_amd._lib import GemmProblem, check
+
+_DT = {
+    torch.float32: _lib.F32,
+    torch.bfloat16: _lib.BF16,
+    torch.float16: _lib.F16,
+    torch.uint8: _lib.U8,
+    torch.bool: _lib.BOOL,
+    torch.int32: _lib.I32,
+    torch.float8_e4m3fn: _lib.U8,
+}
+FLOAT_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def lib():
+    return _lib.load()
+
+
+def _dt(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise TypeError(f"dtype {t.dtype} is not supported by the rocm kernels") from None
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _on_gpu(*ts: torch.Tensor | None) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError(f"rocm kernels take device tensors, got one on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    if dev is None:
+        raise ValueError("no tensor given")
+    return dev
+
+
+def _arr(vals: Sequence[int]):
+    return (ctypes.c_int64 * len(vals))(*[int(v) for v in vals])
+
+
+def _rows2d(t: torch.Tensor, name: str) -> torch.Tensor:
+    """A [rows, cols] view with contiguous rows (copies only if the innermost dim is strided)."""
+    if t.dim() < 1:
+        raise ValueError(f"{name}: needs at least one dimension")
+    t2 = t.reshape(-1, t.shape[-1]) if t.dim() != 2 else t
+    if t2.stride(-1) != 1:
+        t2 = t2.contiguous()
+    return t2
+
+
+# ------------------------------------------------------------------------------- attention
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float,
+              causal: bool = False, attention_mask: torch.Tensor | None = None,
+              bound_min: torch.Tensor | None = None, bound_max: torch.Tensor | None = None,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """softmax(q k^T scale [+ mask]) v on [B, H, S, D] (or [B*H, S, D]) tensors."""
+    dev = _on_gpu(q, k, v)
+    folded = q.dim() == 3
+    scores_shape = tuple(q.shape[:-1]) + (k.shape[-2],)
+    if folded:
+        q, k, v = q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("attention takes [B, H, S, D] or [B*H, S, D] tensors")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError(f"q, k, v dtypes differ: {q.dtype}, {k.dtype}, {v.dtype}")
+    b, h, sq, d = q.shape
+    sk = k.shape[2]
+    if k.shape != (b, h, sk, d) or v.shape != (b, h, sk, d):
+        raise ValueError(f"shape mismatch: q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
+    q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+    if out is None:
+        out = torch.empty((b, h, sq, d), dtype=v.dtype, device=dev)
+        o = out
+        out = out[0] if folded else out
+    else:
+        o = out.unsqueeze(0) if folded else out
+    mask_ptr, mask_dt, mask_strides = None, 0, None
+    keep = []
+    if attention_mask is not None:
+        if bound_min is not None or bound_max is not None:
+            raise ValueError("attention_mask and bounds are mutually exclusive")
+        m = attention_mask.to(dev)
+        if m.dtype == torch.bool:
+            m, mask_dt = m.view(torch.uint8), _lib.BOOL
+        else:
+            if m.dtype not in FLOAT_DTYPES:
+                m = m.to(q.dtype)
+            mask_dt = _dt(m)
+        m = torch.broadcast_to(m, scores_shape)  # a view: broadcast dims get stride 0
+        m = m.unsqueeze(0) if folded else m
+        keep.append(m)
+        mask_ptr = ctypes.c_void_p(m.data_ptr())
+        mask_strides = _arr(m.stride())
+    bmin_ptr = bmax_ptr = bstr = None
+    if bound_min is not None or bound_max is not None:
+        if bound_min is None or bound_max is None:
+            raise ValueError("bound_min and bound_max must both be provided")
+        # bounds broadcast against the scores with a trailing key dim of 1
+        def _as_bhq(t):
+            t = torch.broadcast_to(t.to(device=dev, dtype=torch.int32), scores_shape[:-1] + (1,))
+            t = t[..., 0]
+            return (t.unsqueeze(0) if folded else t).contiguous()
+        bmn, bmx = _as_bhq(bound_min), _as_bhq(bound_max)
+        keep += [bmn, bmx]
+        bmin_ptr, bmax_ptr = _ptr(bmn), _ptr(bmx)
+        bstr = _arr(bmn.stride())
+    st = lib().difflet_rocm_attention(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(o), _dt(q), b, h, sq, sk, d,
+        _arr(q.stride()[:3]), _arr(k.stride()[:3]), _arr(v.stride()[:3]), _arr(o.stride()[:3]),
+        float(scale), int(bool(causal)), mask_ptr, mask_dt, mask_strides, bmin_ptr, bmax_ptr,
+        bstr, _stream(dev))
+    check(st, "attention")
+    return out
+
+
+# ------------------------------------------------------------------------------------ GEMM
+class Problem:
+    """One problem of a grouped GEMM: C = epilogue(A W^T + bias)."""
+
+    __slots__ = ("a", "w", "c", "bias", "gate", "residual", "a_scale", "w_scale",
+                 "rows_per_batch")
+
+    def __init__(self, a, w, c, bias=None, gate=None, residual=None, a_scale=None,
+                 w_scale=None, rows_per_batch=None):
+        self.a, self.w, self.c = a, w, c
+        self.bias, self.gate, self.residual = bias, gate, residual
+        self.a_scale, self.w_scale = a_scale, w_scale
+        self.rows_per_batch = rows_per_batch
+
+
+_GEMM_FN = {"bf16": "difflet_rocm_gemm_bf16", "fp8": "difflet_rocm_gemm_fp8_rowwise",
+            "mx": "difflet_rocm_gemm_mxfp8"}
+
+
+def gemm_grouped(problems: Sequence[Problem], *, kind: str = "bf16",
+                 epilogue: int = _lib.EPI_NONE, act_col_start: int = 0) -> None:
+    """Runs up to 4 GEMMs sharing N, K and the epilogue in one launch (writes each p.c)."""
+    if not problems:
+        return
+    dev = _on_gpu(*[p.a for p in problems], *[p.w for p in problems])
+    n, k = problems[0].w.shape[0], problems[0].w.shape[1]
+    arr = (GemmProblem * len(problems))()
+    for i, p in enumerate(problems):
+        for t in (p.a, p.w, p.c):
+            if t.dim() != 2 or t.stride(1) != 1:
+                raise ValueError("GEMM operands must be 2-D with contiguous rows")
+        if p.w.shape != (n, k) or p.a.shape[1] != k or p.c.shape != (p.a.shape[0], n):
+            raise ValueError(f"GEMM shapes: a {tuple(p.a.shape)} w {tuple(p.w.shape)} "
+                             f"c {tuple(p.c.shape)}")
+        if kind == "bf16" and (p.a.dtype != torch.bfloat16 or p.w.dtype != torch.bfloat16):
+            raise TypeError("bf16 GEMM takes bf16 operands")
+        if kind != "bf16" and (p.a.element_size() != 1 or p.w.element_size() != 1):
+            raise TypeError("fp8 GEMMs take e4m3 codes (uint8 or float8_e4m3fn)")
+        if p.c.dtype != torch.bfloat16:
+            raise TypeError("GEMM output is bf16")
+        q = arr[i]
+        q.a, q.lda = p.a.data_ptr(), p.a.stride(0)
+        q.w, q.ldw = p.w.data_ptr(), p.w.stride(0)
+        q.c, q.ldc = p.c.data_ptr(), p.c.stride(0)
+        q.bias = p.bias.data_ptr() if p.bias is not None else None
+        if p.gate is not None:
+            g = p.gate if p.gate.dim() == 2 else p.gate.reshape(1, -1)
+            q.gate, q.gate_stride = g.data_ptr(), g.stride(0)
+        if p.residual is not None:
+            q.residual, q.ldr = p.residual.data_ptr(), p.residual.stride(0)
+        q.a_scale = p.a_scale.data_ptr() if p.a_scale is not None else None
+        q.w_scale = p.w_scale.data_ptr() if p.w_scale is not None else None
+        q.m = p.a.shape[0]
+        q.rows_per_batch = p.rows_per_batch or p.a.shape[0]
+    fn = getattr(lib(), _GEMM_FN[kind])
+    check(fn(len(problems), arr, n, k, int(epilogue), int(act_col_start), _stream(dev)),
+          f"gemm_{kind}")
+
+
+def linear(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, *,
+           epilogue: int = _lib.EPI_NONE, gate: torch.Tensor | None = None,
+           residual: torch.Tensor | None = None, act_col_start: int = 0,
+           rows_per_batch: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16 ``x W^T + b`` over the last dim of x, with an optional fused epilogue."""
+    x2 = _rows2d(x, "linear")
+    n = w.shape[0]
+    c = out if out is not None else torch.empty((x2.shape[0], n), dtype=torch.bfloat16,
+                                                device=x.device)
+    res2 = _rows2d(residual, "residual") if residual is not None else None
+    gemm_grouped([Problem(x2, w, c, bias, gate, res2, rows_per_batch=rows_per_batch)],
+                 kind="bf16", epilogue=epilogue, act_col_start=act_col_start)
+    return c.reshape(*x.shape[:-1], n) if out is None else c
+
+
+# ------------------------------------------------------------------------------- quantizers
+def quantize_fp8_rowwise(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row e4m3 codes (float8_e4m3fn [rows, K]) and fp32 scales [rows]."""
+    dev = _on_gpu(x)
+    x2 = _rows2d(x, "quantize_fp8_rowwise")
+    rows, cols = x2.shape
+    q = torch.empty((rows, cols), dtype=torch.float8_e4m3fn, device=dev)
+    s = torch.empty((rows,), dtype=torch.float32, device=dev)
+    check(lib().difflet_rocm_quantize_fp8_rowwise(_ptr(x2), _dt(x2), rows, cols, x2.stride(0),
+                                                  _ptr(q), cols, _ptr(s), _stream(dev)),
+          "quantize_fp8_rowwise")
+    return q, s
+
+
+def quantize_mxfp8(x: torch.Tensor, *, swizzled: bool = False
+                   ) -> tuple[torch.Tensor, torch.Tensor]:
+    """MXFP8 codes (float8_e4m3fn [rows, K], logical or swizzle order) and uint8 E8M0 scales
+    [rows, K/32] in block order."""
+    dev = _on_gpu(x)
+    x2 = _rows2d(x, "quantize_mxfp8")
+    rows, cols = x2.shape
+    q = torch.empty((rows, cols), dtype=torch.float8_e4m3fn, device=dev)
+    s = torch.empty((rows, cols // 32), dtype=torch.uint8, device=dev)
+    check(lib().difflet_rocm_quantize_mxfp8(_ptr(x2), _dt(x2), rows, cols, x2.stride(0), _ptr(q),
+                                            cols, _ptr(s), cols // 32, int(swizzled),
+                                            _stream(dev)),
+          "quantize_mxfp8")
+    return q, s
+
+
+# ---------------------------------------------------------------------------- norms, rope
+def layernorm_modulate(x: torch.Tensor, mul: torch.Tensor | None, add: torch.Tensor | None, *,
+                       eps: float, one_plus: bool = True, out_dtype: torch.dtype | None = None,
+                       rows_per_batch: int | None = None,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
+    """LN(x) * (1 + mul) + add (one_plus) or LN(x) * mul + add, over the last dim.
+
+    mul / add: [dim] or [batches, dim], broadcast over the rows of each batch element."""
+    dev = _on_gpu(x)
+    x2 = _rows2d(x, "layernorm")
+    rows, dim = x2.shape
+    out_dtype = out_dtype or x.dtype
+    y = out if out is not None else torch.empty((rows, dim), dtype=out_dtype, device=dev)
+    mod = mul if mul is not None else add
+    mod_dt, mod_stride = _lib.F32, 0
+    if mod is not None:
+        if mul is not None and add is not None and mul.dtype != add.dtype:
+            add = add.to(mul.dtype)
+        mul2 = mul.reshape(-1, dim) if mul is not None else None
+        add2 = add.reshape(-1, dim) if add is not None else None
+        for t in (mul2, add2):
+            if t is not None and t.stride(-1) != 1:
+                raise ValueError("modulation vectors must have contiguous rows")
+        ref = mul2 if mul2 is not None else add2
+        if mul2 is not None and add2 is not None and mul2.stride(0) != add2.stride(0):
+            add2 = add2.contiguous()
+            mul2 = mul2.contiguous()
+        mod_dt, mod_stride = _dt(ref), ref.stride(0) if ref.shape[0] > 1 else 0
+        mul, add = mul2, add2
+    rpb = rows_per_batch or rows
+    check(lib().difflet_rocm_layernorm_modulate(
+        _ptr(x2), x2.stride(0), _ptr(y), y.stride(0), _dt(x2), _dt(y), rows, dim, _ptr(mul),
+        _ptr(add), mod_dt, mod_stride, rpb, int(one_plus), float(eps), _stream(dev)),
+        "layernorm_modulate")
+    return y.reshape(*x.shape[:-1], dim) if out is None else y
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float) -> torch.Tensor:
+    dev = _on_gpu(x)
+    x2 = _rows2d(x, "rms_norm")
+    rows, dim = x2.shape
+    y = torch.empty((rows, dim), dtype=x.dtype, device=dev)
+    wdt = _dt(weight) if weight is not None else _lib.F32
+    check(lib().difflet_rocm_rms_norm(_ptr(x2), x2.stride(0), _ptr(y), dim, _dt(x2), rows, dim,
+                                      _ptr(weight), wdt, float(eps), _stream(dev)), "rms_norm")
+    return y.reshape(x.shape)
+
+
+def qk_norm_rope(buf: torch.Tensor, *, heads: int, head_dim: int, q_off: int, k_off: int,
+                 wq: torch.Tensor | None, wk: torch.Tensor | None, eps: float,
+                 cos: torch.Tensor | None, sin: torch.Tensor | None, law: int = 0,
+                 do_norm: bool = True) -> None:
+    """In place on a [rows, ld] projection buffer: per-head RMSNorm of q (columns
+    q_off + h * head_dim ..) and k, then the rotary embedding with fp32 tables [S, head_dim]."""
+    dev = _on_gpu(buf)
+    if buf.dim() != 2 or buf.stride(1) != 1:
+        raise ValueError("qk_norm_rope: buf must be 2-D with contiguous rows")
+    rows = buf.shape[0]
+    wdt = _dt(wq) if wq is not None else (_dt(wk) if wk is not None else _lib.F32)
+    if cos is not None:
+        if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+            raise TypeError("rope tables must be fp32")
+        cos, sin = cos.contiguous(), sin.contiguous()
+    check(lib().difflet_rocm_qk_norm_rope(
+        _ptr(buf), buf.stride(0), _dt(buf), rows, heads, head_dim, q_off, k_off, int(do_norm),
+        _ptr(wq), _ptr(wk), wdt, float(eps), _ptr(cos), _ptr(sin),
+        cos.shape[0] if cos is not None else 0, law, _stream(dev)), "qk_norm_rope")
+
+
+def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *, law: int) -> torch.Tensor:
+    """Rotary embedding of x [..., S, D] with fp32 tables [S, D] (law 0: fp32 interleaved,
+    law 1: stride-2 with cos of the even and sin of the odd entries)."""
+    dev = _on_gpu(x, cos, sin)
+    s, d = x.shape[-2], x.shape[-1]
+    xv = x.reshape(-1, s, d)
+    if xv.stride(-1) != 1:
+        xv = xv.contiguous()
+    y = torch.empty(xv.shape, dtype=x.dtype, device=dev)
+    c = cos.reshape(-1, d).to(torch.float32).contiguous()
+    sn = sin.reshape(-1, d).to(torch.float32).contiguous()
+    check(lib().difflet_rocm_rope(_ptr(xv), _ptr(y), _dt(xv), xv.shape[0], s, d, xv.stride(0),
+                                  xv.stride(1), y.stride(0), y.stride(1), _ptr(c), _ptr(sn),
+                                  c.shape[0], law, _stream(dev)), "rope")
+    return y.reshape(x.shape)
+
+
+# ------------------------------------------------------------------------ small kernels
+def gelu_tanh(x: torch.Tensor) -> torch.Tensor:
+    dev = _on_gpu(x)
+    xc = x.contiguous()
+    y = torch.empty_like(xc)
+    check(lib().difflet_rocm_gelu_tanh(_ptr(xc), _ptr(y), _dt(xc), xc.numel(), _stream(dev)),
+          "gelu_tanh")
+    return y
+
+
+def gate_residual(residual: torch.Tensor, x: torch.Tensor, gate: torch.Tensor, *,
+                  rows_per_batch: int | None = None) -> torch.Tensor:
+    """residual + gate * x with gate [dim] or [batches, dim]."""
+    dev = _on_gpu(residual, x, gate)
+    r2 = residual.reshape(-1, residual.shape[-1]).contiguous()
+    x2 = x.reshape(-1, x.shape[-1]).contiguous()
+    g2 = gate.reshape(-1, gate.shape[-1]).contiguous()
+    y = torch.empty_like(r2)
+    check(lib().difflet_rocm_gate_residual(_ptr(r2), _ptr(x2), _ptr(g2), _ptr(y), _dt(r2),
+                                           _dt(g2), r2.shape[0], r2.shape[1],
+                                           g2.stride(0) if g2.shape[0] > 1 else 0,
+                                           rows_per_batch or r2.shape[0], _stream(dev)),
+          "gate_residual")
+    return y.reshape(residual.shape)
+
+
+def gemv(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, *,
+         act: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """act(x) W^T + b for x [m <= 8, K] (act 1 = SiLU on x), W bf16 [N, K]."""
+    dev = _on_gpu(x, w)
+    x2 = x.reshape(-1, x.shape[-1]).contiguous()
+    m, k = x2.shape
+    n = w.shape[0]
+    if w.dtype != torch.bfloat16 or w.stride(1) != 1:
+        raise TypeError("gemv weights must be bf16 with contiguous rows")
+    if bias is not None and bias.dtype != x2.dtype:
+        bias = bias.to(x2.dtype)
+    y = out if out is not None else torch.empty((m, n), dtype=x2.dtype, device=dev)
+    check(lib().difflet_rocm_gemv(_ptr(x2), _dt(x2), m, k, x2.stride(0), _ptr(w), w.stride(0), n,
+                                  _ptr(bias), _ptr(y), y.stride(0), int(act), _stream(dev)),
+          "gemv")
+    return y
+
+
+def timestep_embedding(t: torch.Tensor, dim: int, *, flip_sin_to_cos: bool,
+                       downscale_freq_shift: float, scale: float = 1.0,
+                       max_period: float = 10000.0, dtype: torch.dtype = torch.float32
+                       ) -> torch.Tensor:
+    dev = _on_gpu(t)
+    tt = t.reshape(-1).to(torch.float32).contiguous()
+    y = torch.empty((tt.shape[0], dim), dtype=dtype, device=dev)
+    check(lib().difflet_rocm_timestep_embedding(_ptr(tt), _ptr(y), _dt(y), tt.shape[0], dim,
+                                                int(flip_sin_to_cos),
+                                                float(downscale_freq_shift), float(scale),
+                                                float(max_period), _stream(dev)),
+          "timestep_embedding")
+    return y

@@ -1,0 +1,226 @@
+/*
+ * difflet_rocm.h -- the C ABI of the MI355X (gfx950) DiT denoise-step kernels.
+ *
+ * One shared library, libdifflet_rocm.so, exports these entry points. They are what the
+ * `rocm` backend of Difflet's backend-neutral op surface binds (through ctypes, from
+ * difflet_amd/backends/rocm/ops_impl/ *.py and difflet_amd/quant/), in place of the torch
+ * calls the CUDA backend makes. Each declaration names the reference interface it replaces.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers the caller allocated; no entry point allocates, frees or
+ *     synchronizes. Work is enqueued on `stream` (a hipStream_t; NULL is the null stream).
+ *   - Shapes and strides are int64 element counts. The innermost dimension is contiguous.
+ *   - Return value: DIFFLET_OK (0) or an error code; difflet_rocm_last_error() then holds a
+ *     message (thread-local).
+ *   - Inference only: there are no backward entry points.
+ */
+#ifndef DIFFLET_ROCM_H
+#define DIFFLET_ROCM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* difflet_stream_t;
+
+enum difflet_dtype {
+  DIFFLET_F32 = 0,
+  DIFFLET_BF16 = 1,
+  DIFFLET_F16 = 2,
+  DIFFLET_U8 = 3,   /* raw bytes: fp8 e4m3fn codes, E8M0 scales */
+  DIFFLET_BOOL = 4, /* one byte per element, nonzero = attend */
+  DIFFLET_I32 = 5
+};
+
+enum difflet_status {
+  DIFFLET_OK = 0,
+  DIFFLET_EINVAL = 1,       /* bad shape, stride, pointer or dtype */
+  DIFFLET_EUNSUPPORTED = 2, /* a valid request this build does not implement */
+  DIFFLET_ELAUNCH = 3       /* the HIP runtime refused the launch */
+};
+
+/* Library identity and error reporting. */
+const char* difflet_rocm_last_error(void);
+const char* difflet_rocm_version(void);
+int difflet_rocm_abi_version(void);
+/* Number of gfx950 devices the library can launch on (0 when none). */
+int difflet_rocm_device_count(void);
+
+/* ------------------------------------------------------------------------------------------
+ * Attention.
+ * Replaces difflet/backends/cuda/ops_impl/attention.py:41-86 (`attention` / `_sdpa`); the
+ * semantics are the CPU oracle's, difflet/backends/cpu/ops_impl/attention.py:8-48:
+ *   out = softmax(q k^T * scale [+ mask]) v, softmax in fp32, output in v's dtype.
+ * q: [batch, heads, seq_q, head_dim] addressed by strides {b, h, s}; k, v: [.., seq_k, ..];
+ * o: like q. head_dim must be 64 or 128; dtype BF16 or F16.
+ * causal: key j > query i is masked. mask: optional, [batch, heads, seq_q, seq_k] through
+ * strides (0 broadcasts); BOOL (nonzero attends) or F32/BF16/F16 additive. bound_min /
+ * bound_max: optional int32 [batch, heads, seq_q] through strides; keys in [min, max) attend
+ * (difflet/backends/cpu/ops_impl/attention.py:24-35). Masked scores take the dtype's lowest
+ * finite value, so a fully masked row averages v exactly as the reference does.
+ * ---------------------------------------------------------------------------------------- */
+int difflet_rocm_attention(const void* q, const void* k, const void* v, void* o, int dtype,
+                           int64_t batch, int64_t heads, int64_t seq_q, int64_t seq_k,
+                           int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
+                           const int64_t* v_strides, const int64_t* o_strides, float scale,
+                           int causal, const void* mask, int mask_dtype,
+                           const int64_t* mask_strides, const int32_t* bound_min,
+                           const int32_t* bound_max, const int64_t* bound_strides,
+                           difflet_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * GEMM with fused epilogues: for each problem p, C_p = epilogue(A_p W_p^T + bias_p).
+ * Replaces F.linear in difflet/backends/_torch_megatron/linear.py:120-126,189-202 (and the
+ * CPU twins difflet/backends/cpu/ops_impl/linear.py:9-41), plus the elementwise tails the
+ * FLUX blocks apply to linear outputs: GELU-tanh (difflet/layers/activations.py:59-65),
+ * gate * (x + bias) + residual (difflet/models/flux/modeling_flux.py:720-731,840-866).
+ * All problems of one call share n, k and the epilogue; each has its own A, W, C, M.
+ * ---------------------------------------------------------------------------------------- */
+enum difflet_epilogue {
+  DIFFLET_EPI_NONE = 0,          /* C = acc + bias */
+  DIFFLET_EPI_GELU = 1,          /* C = gelu_tanh(acc + bias) for columns >= act_col_start */
+  DIFFLET_EPI_GATE_RESIDUAL = 2  /* C = residual + gate[batch] * (acc + bias) */
+};
+
+typedef struct difflet_gemm_problem {
+  const void* a;        /* [m, k], row stride lda (bf16, or e4m3 codes for the fp8 GEMMs) */
+  int64_t lda;
+  const void* w;        /* [n, k], row stride ldw */
+  int64_t ldw;
+  void* c;              /* [m, n] bf16, row stride ldc */
+  int64_t ldc;
+  const void* bias;     /* [n] bf16 or NULL */
+  const void* gate;     /* GATE_RESIDUAL: [batches, n] bf16, batch stride gate_stride */
+  int64_t gate_stride;
+  const void* residual; /* GATE_RESIDUAL: [m, n] bf16, row stride ldr (may alias c) */
+  int64_t ldr;
+  const void* a_scale;  /* fp8 GEMMs: per-row scales of A (see each entry point) */
+  const void* w_scale;  /* fp8 GEMMs: per-column (per-row of W) scales */
+  int64_t m;
+  int64_t rows_per_batch; /* rows of A per batch element, for gate indexing (>= m for one) */
+} difflet_gemm_problem;
+
+/* bf16 x bf16 -> fp32 accumulate -> bf16. k % 64 == 0. */
+int difflet_rocm_gemm_bf16(int nproblems, const difflet_gemm_problem* problems, int64_t n,
+                           int64_t k, int epilogue, int64_t act_col_start,
+                           difflet_stream_t stream);
+
+/* fp8 e4m3 x e4m3 with per-row scales: acc * a_scale[m] * w_scale[n] (both fp32), then the
+ * epilogue. a_scale / w_scale come from difflet_rocm_quantize_fp8_rowwise. k % 128 == 0.
+ * New format, no reference counterpart (the reference's only fp8 recipe is MXFP8,
+ * difflet/quant/spec.py:22-33); it is the per-channel x per-token linear of the FLUX fp8 step. */
+int difflet_rocm_gemm_fp8_rowwise(int nproblems, const difflet_gemm_problem* problems,
+                                  int64_t n, int64_t k, int epilogue, int64_t act_col_start,
+                                  difflet_stream_t stream);
+
+/* MXFP8: e4m3 codes in swizzled K order with one E8M0 scale (uint8) per 32 values along K,
+ * a_scale [m, k/32] and w_scale [n, k/32] (row strides k/32). Replaces the nkilib
+ * `matmul_mxfp8` call of difflet/backends/neuron/ops_impl/fp8_kernels.py:30-71,101-125 and
+ * computes what difflet/quant/fake_linear.py:56-61 (FakeQuantMXLinear.forward) computes.
+ * k % 128 == 0. */
+int difflet_rocm_gemm_mxfp8(int nproblems, const difflet_gemm_problem* problems, int64_t n,
+                            int64_t k, int epilogue, int64_t act_col_start,
+                            difflet_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Quantizers (bit-exact with the CPU laws).
+ * ---------------------------------------------------------------------------------------- */
+/* Per-row e4m3: amax = max|x|, a = max(amax, 2^-126), scale = a / 448, inv = 448 / a,
+ * q = e4m3_rne(clamp(x * inv, -448, 448)) (IEEE fp32 ops). scale: fp32 [rows]. Used for
+ * per-token activations and per-output-channel weights. No reference counterpart (see
+ * difflet_rocm_gemm_fp8_rowwise). */
+int difflet_rocm_quantize_fp8_rowwise(const void* x, int dtype, int64_t rows, int64_t cols,
+                                      int64_t ldx, uint8_t* q, int64_t ldq, float* scale,
+                                      difflet_stream_t stream);
+
+/* MXFP8 block law of difflet/quant/mx.py:46-108 (`swizzle_perm`, `_block_scales`,
+ * `quantize_mx`): blocks are consecutive 32 values in swizzle order, scale_u8 =
+ * clamp(max exponent field - 7, 0, 255), q = e4m3_rne(clamp(x / 2^(scale_u8 - 127), +-448)).
+ * swizzled_out = 0 stores codes in logical K order (the reference's storage); 1 stores them in
+ * swizzle order, the operand order difflet_rocm_gemm_mxfp8 reads. scale: uint8 [rows, cols/32]
+ * row stride lds. cols % 128 == 0. */
+int difflet_rocm_quantize_mxfp8(const void* x, int dtype, int64_t rows, int64_t cols,
+                                int64_t ldx, uint8_t* q, int64_t ldq, uint8_t* scale,
+                                int64_t lds, int swizzled_out, difflet_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Normalization and modulation.
+ * ---------------------------------------------------------------------------------------- */
+/* LayerNorm over the last dim (fp32 statistics, biased variance) then an affine:
+ *   one_plus = 1: y = LN(x) * (1 + mul[b]) + add[b]   (adaLN: difflet/layers/normalization.py
+ *                 :81-84,141-147,185-190; Wan difflet/models/wan/modeling_wan.py:741-763)
+ *   one_plus = 0: y = LN(x) * mul + add               (nn.LayerNorm, difflet/backends/cpu/
+ *                 ops_impl/norm.py:9); mul / add may be NULL (no affine).
+ * mul / add: [batches, dim] of mod_dtype with batch stride mod_stride, batch = row /
+ * rows_per_batch. */
+int difflet_rocm_layernorm_modulate(const void* x, int64_t ldx, void* y, int64_t ldy,
+                                    int dtype, int out_dtype, int64_t rows, int64_t dim,
+                                    const void* mul, const void* add, int mod_dtype,
+                                    int64_t mod_stride, int64_t rows_per_batch, int one_plus,
+                                    float eps, difflet_stream_t stream);
+
+/* RMSNorm with fp32 statistics, normalisation and affine and one cast back to dtype: the
+ * law of rms_norm_fp32 (difflet/backends/_torch_megatron/norm.py:35-45) and of the CUDA
+ * backend's RMSNorm (difflet/backends/cuda/ops_impl/norm.py:24-44). weight may be NULL. */
+int difflet_rocm_rms_norm(const void* x, int64_t ldx, void* y, int64_t ldy, int dtype,
+                          int64_t rows, int64_t dim, const void* weight, int wdtype, float eps,
+                          difflet_stream_t stream);
+
+/* Fused per-head q/k RMSNorm + rotary embedding, in place, on rows of a projection buffer:
+ * for each row r and head h, x = buf[r * ld + off + h * head_dim .. +head_dim] for off in
+ * (q_off, k_off), x <- rope(rmsnorm_fp32(x) * w) with the rotary law
+ *   law 0: difflet/backends/_torch_megatron/embeddings.py:24-33 (apply_rotary_emb_fp32,
+ *          interleaved pairs, fp32, cast back);
+ *   law 1: difflet/backends/cpu/ops_impl/embeddings.py:6-14 (apply_rotary_emb: cos of the
+ *          even, sin of the odd table entries).
+ * Replaces the norm_q/norm_k + apply_rotary_emb sequence of difflet/models/flux/
+ * modeling_flux.py:1249-1252,1289-1294,1407-1411. cos / sin: fp32 [rope_rows, head_dim], row
+ * index r % rope_rows; NULL skips the rotation. wq / wk NULL skips that tensor's norm
+ * (do_norm = 0 skips both). */
+int difflet_rocm_qk_norm_rope(void* buf, int64_t ld, int dtype, int64_t rows, int64_t heads,
+                              int64_t head_dim, int64_t q_off, int64_t k_off, int do_norm,
+                              const void* wq, const void* wk, int wdtype, float eps,
+                              const float* cos, const float* sin, int64_t rope_rows, int law,
+                              difflet_stream_t stream);
+
+/* Rotary embedding out of place on a strided [batch*heads, seq, head_dim] tensor with tables
+ * [seq, head_dim] (row index s % rope_rows); laws as above. Replaces apply_rotary_emb /
+ * apply_rotary_emb_fp32 of the op surface (difflet/ops/embeddings.py:12-25). */
+int difflet_rocm_rope(const void* x, void* y, int dtype, int64_t outer, int64_t seq,
+                      int64_t head_dim, int64_t x_outer_stride, int64_t x_seq_stride,
+                      int64_t y_outer_stride, int64_t y_seq_stride, const float* cos,
+                      const float* sin, int64_t rope_rows, int law, difflet_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Elementwise and small-M kernels.
+ * ---------------------------------------------------------------------------------------- */
+/* y = gelu_tanh(x), n elements (difflet/layers/activations.py:59-65). */
+int difflet_rocm_gelu_tanh(const void* x, void* y, int dtype, int64_t n, difflet_stream_t stream);
+
+/* y[r, :] = residual[r, :] + gate[b, :] * x[r, :] (fp32 math, one rounding), [rows, dim]
+ * (the gate/residual tails of difflet/models/flux/modeling_flux.py:840-866). */
+int difflet_rocm_gate_residual(const void* residual, const void* x, const void* gate, void* y,
+                               int dtype, int gate_dtype, int64_t rows, int64_t dim,
+                               int64_t gate_stride, int64_t rows_per_batch,
+                               difflet_stream_t stream);
+
+/* y[i, n] = sum_k act(x[i, k]) w[n, k] + bias[n] for m <= 8 rows: the adaLN modulation
+ * linears `linear(silu(emb))` of difflet/layers/normalization.py:81,141,187 and the timestep
+ * MLPs, HBM-bound on W. act: 0 none, 1 SiLU. x, bias, y: dtype; w: bf16 [n, k] row stride ldw. */
+int difflet_rocm_gemv(const void* x, int dtype, int64_t m, int64_t k, int64_t ldx,
+                      const void* w, int64_t ldw, int64_t n, const void* bias, void* y,
+                      int64_t ldy, int act, difflet_stream_t stream);
+
+/* Sinusoidal timestep embedding of difflet/layers/embeddings.py:422-473
+ * (get_timestep_embedding): t fp32 [m] -> y [m, dim] in dtype. */
+int difflet_rocm_timestep_embedding(const float* t, void* y, int dtype, int64_t m,
+                                    int64_t dim, int flip_sin_to_cos, float downscale_freq_shift,
+                                    float scale, float max_period, difflet_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DIFFLET_ROCM_H */

@@ -1,0 +1,49 @@
+"""The per-row e4m3 law of the per-channel (weights) x per-token (activations) fp8 linear.
+Test infrastructure only (see oracle/__init__.py).
+
+There is no reference counterpart: the reference's only fp8 recipe is MXFP8
+(difflet/quant/spec.py:22-33). The law is this build's and is fixed in include/difflet_rocm.h
+(difflet_rocm_quantize_fp8_rowwise): amax = max |x|, a = max(amax, 2^-126), scale = a / 448,
+inv = 448 / a (IEEE fp32 divisions), q = e4m3_rne(clamp(x * inv, -448, 448)).
+
+Pins (tests/test_oracle_fp8.py): the e4m3 encoder is pinned in oracle/mx.py; the row law
+against its closed-form invariants (the row's amax encodes to +-448 = code 0x7e, dequantized
+rows are within e4m3's half-ulp of the input, a zero row gives zero codes) and against torch's
+own float8 cast of the same fp32 products.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from oracle.mx import e4m3_decode, e4m3_encode
+
+E4M3_MAX = np.float32(448.0)
+TINY = np.float32(2.0 ** -126)
+
+
+def quantize_rowwise(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """[R, K] -> (codes uint8 [R, K], fp32 scales [R])."""
+    x = np.asarray(x, dtype=np.float32)
+    amax = np.abs(x).max(axis=-1)
+    a = np.maximum(amax, TINY).astype(np.float32)
+    scale = (a / E4M3_MAX).astype(np.float32)
+    inv = (E4M3_MAX / a).astype(np.float32)
+    prod = (x * inv[..., None]).astype(np.float32)
+    q = e4m3_encode(np.clip(prod, -E4M3_MAX, E4M3_MAX))
+    return q, scale
+
+
+def dequantize_rowwise(q: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    return (e4m3_decode(q) * scale[..., None]).astype(np.float32)
+
+
+def fp8_linear(x: np.ndarray, wq: np.ndarray, ws: np.ndarray, bias=None) -> np.ndarray:
+    """y = (q_x q_w^T) * s_x[m] * s_w[n] + b, fp32 accumulate: what the fp8 GEMM computes."""
+    x2 = np.asarray(x, dtype=np.float32).reshape(-1, x.shape[-1])
+    xq, xs = quantize_rowwise(x2)
+    acc = e4m3_decode(xq).astype(np.float64) @ e4m3_decode(wq).astype(np.float64).T
+    y = (acc * xs[:, None].astype(np.float64) * ws[None, :].astype(np.float64)).astype(np.float32)
+    if bias is not None:
+        y = y + np.asarray(bias, dtype=np.float32)
+    return y.reshape(*x.shape[:-1], wq.shape[0])

@@ -1,0 +1,324 @@
+"""Kernel-level parity of the HIP path against the oracle, through the C ABI.
+
+Integer work (fp8 / E8M0 codes) must be bit-exact; floating-point results are compared by
+relative L2 against fp32 CPU math on the same (already bf16-rounded) inputs, with the tolerance
+written in each test.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from difflet_amd import _lib, kernels
+from oracle import fp8 as ofp8
+from oracle import mx as omx
+from oracle import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_l2(a, b):
+    a, b = a.detach().float().cpu(), b.detach().float().cpu()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+def rnd(g, *shape, std=1.0, dtype=torch.bfloat16):
+    return (torch.randn(*shape, generator=g) * std).to(dtype)
+
+
+# ------------------------------------------------------------------------------------ GEMM
+@pytest.mark.parametrize("m,n,k", [(256, 256, 64), (300, 200, 128), (1, 64, 64),
+                                   (513, 1028, 320), (4608, 3072, 3072)])
+def test_gemm_bf16_matches_fp32(gpu, m, n, k):
+    print(f"gemm_bf16 m={m} n={n} k={k}", flush=True)
+    g = torch.Generator().manual_seed(m * 7 + n)
+    a, w, b = rnd(g, m, k), rnd(g, n, k, std=0.05), rnd(g, n, std=0.1)
+    ref = ops.linear(a.float(), w.float(), b.float())
+    out = kernels.linear(a.to(gpu), w.to(gpu), b.to(gpu))
+    assert out.dtype == torch.bfloat16 and out.shape == (m, n)
+    assert rel_l2(out, ref) < 4e-3  # one bf16 rounding of the output (2^-9 relative)
+
+
+def test_gemm_bf16_no_bias_and_strided_views(gpu):
+    g = torch.Generator().manual_seed(1)
+    big = rnd(g, 320, 3 * 192)
+    a = big[:, 192:384]  # row stride 576, K = 192
+    w = rnd(g, 128, 192, std=0.05)
+    ref = ops.linear(a.float(), w.float())
+    c = torch.zeros(320, 2 * 128, dtype=torch.bfloat16, device=gpu)
+    out = c[:, 128:]
+    kernels.gemm_grouped([kernels.Problem(a.to(gpu), w.to(gpu), out)])
+    assert rel_l2(out, ref) < 4e-3
+    assert torch.count_nonzero(c[:, :128]) == 0  # nothing written outside the view
+
+
+def test_gemm_epilogues_gelu_and_gate_residual(gpu):
+    g = torch.Generator().manual_seed(2)
+    m, n, k = 700, 512, 256
+    a, w, b = rnd(g, m, k), rnd(g, n, k, std=0.05), rnd(g, n, std=0.1)
+    pre = ops.linear(a.float(), w.float(), b.float())
+    # GELU on columns >= 128 only
+    out = kernels.linear(a.to(gpu), w.to(gpu), b.to(gpu), epilogue=_lib.EPI_GELU,
+                         act_col_start=128)
+    ref = torch.cat([pre[:, :128], ops.gelu_tanh(pre[:, 128:])], dim=1)
+    assert rel_l2(out, ref) < 4e-3
+    # residual + gate * (acc + bias), written in place over the residual
+    gate, res = rnd(g, 1, n), rnd(g, m, n)
+    ref2 = res.float() + gate.float() * pre
+    r = res.to(gpu)
+    kernels.gemm_grouped([kernels.Problem(a.to(gpu), w.to(gpu), r, b.to(gpu), gate.to(gpu), r)],
+                         epilogue=_lib.EPI_GATE_RESIDUAL)
+    assert rel_l2(r, ref2) < 4e-3
+
+
+def test_gemm_grouped_problems_share_n_k(gpu):
+    g = torch.Generator().manual_seed(3)
+    n, k = 384, 192
+    ms = [512, 37, 1000, 256]
+    probs, refs = [], []
+    for m in ms:
+        a, w, b = rnd(g, m, k), rnd(g, n, k, std=0.05), rnd(g, n, std=0.1)
+        c = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+        probs.append(kernels.Problem(a.to(gpu), w.to(gpu), c, b.to(gpu)))
+        refs.append(ops.linear(a.float(), w.float(), b.float()))
+    kernels.gemm_grouped(probs)
+    for p, r in zip(probs, refs):
+        assert rel_l2(p.c, r) < 4e-3
+
+
+def test_gemm_rejects_bad_shapes(gpu):
+    a = torch.zeros(16, 100, dtype=torch.bfloat16, device=gpu)  # k not a multiple of 64
+    w = torch.zeros(32, 100, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError):
+        kernels.linear(a, w)
+    a = torch.zeros(16, 64, dtype=torch.bfloat16, device=gpu)
+    w = torch.zeros(30, 64, dtype=torch.bfloat16, device=gpu)  # n not a multiple of 4
+    with pytest.raises(ValueError):
+        kernels.linear(a, w)
+
+
+# ------------------------------------------------------------------------------ quantizers
+@pytest.mark.parametrize("rows,cols", [(7, 64), (300, 3072), (33, 15360)])
+def test_quantize_fp8_rowwise_bit_exact(gpu, rows, cols):
+    g = torch.Generator().manual_seed(rows + cols)
+    x = rnd(g, rows, cols) * torch.exp(torch.randn(rows, 1, generator=g) * 3).bfloat16()
+    x[0] = 0  # an all-zero row
+    q, s = kernels.quantize_fp8_rowwise(x.to(gpu))
+    q_ref, s_ref = ofp8.quantize_rowwise(x.float().numpy())
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("cols", [128, 384, 512, 896, 3072, 3456, 13824])
+@pytest.mark.parametrize("swizzled", [False, True])
+def test_quantize_mxfp8_bit_exact(gpu, cols, swizzled):
+    g = torch.Generator().manual_seed(cols)
+    rows = 19
+    x = rnd(g, rows, cols) * torch.exp(torch.randn(rows, cols, generator=g) * 2).bfloat16()
+    x[1, :] = 0
+    x[2, 5] = 1e4  # an outlier in one block
+    x[3, :32] = 1e-30  # tiny block (scale clamps at 0)
+    q, s = kernels.quantize_mxfp8(x.to(gpu), swizzled=swizzled)
+    q_ref, s_ref = omx.quantize_mx(x.float().numpy(), swizzled_out=swizzled)
+    assert np.array_equal(s.cpu().numpy(), s_ref)
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), q_ref)
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 128), (300, 520, 384), (4608, 3072, 3072)])
+def test_gemm_fp8_rowwise_matches_oracle(gpu, m, n, k):
+    print(f"gemm_fp8 m={m} n={n} k={k}", flush=True)
+    g = torch.Generator().manual_seed(m + n + k)
+    a, w, b = rnd(g, m, k), rnd(g, n, k, std=0.05), rnd(g, n, std=0.1)
+    wq, ws = kernels.quantize_fp8_rowwise(w.to(gpu))
+    aq, as_ = kernels.quantize_fp8_rowwise(a.to(gpu))
+    c = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+    kernels.gemm_grouped([kernels.Problem(aq, wq, c, b.to(gpu), a_scale=as_, w_scale=ws)],
+                         kind="fp8")
+    wq_ref, ws_ref = ofp8.quantize_rowwise(w.float().numpy())
+    ref = ofp8.fp8_linear(a.float().numpy(), wq_ref, ws_ref, b.float().numpy())
+    assert rel_l2(c, torch.from_numpy(ref)) < 4e-3  # same codes; fp32 sum order + bf16 out
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 128), (300, 520, 384), (1030, 1024, 3072)])
+def test_gemm_mxfp8_matches_fake_quant_linear(gpu, m, n, k):
+    print(f"gemm_mx m={m} n={n} k={k}", flush=True)
+    g = torch.Generator().manual_seed(m * 3 + k)
+    a, w, b = rnd(g, m, k), rnd(g, n, k, std=0.05), rnd(g, n, std=0.1)
+    a[0, 7] = 50.0  # an outlier block
+    wq, ws = kernels.quantize_mxfp8(w.to(gpu), swizzled=True)
+    aq, as_ = kernels.quantize_mxfp8(a.to(gpu), swizzled=True)
+    c = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+    kernels.gemm_grouped([kernels.Problem(aq, wq, c, b.to(gpu), a_scale=as_, w_scale=ws)],
+                         kind="mx")
+    wq_l, ws_l = omx.quantize_mx(w.float().numpy())
+    ref = omx.mx_linear(a.float().numpy(), wq_l, ws_l, b.float().numpy())
+    assert rel_l2(c, torch.from_numpy(ref)) < 4e-3
+
+
+# ------------------------------------------------------------------------------- attention
+def _attn_case(g, b, h, sq, sk, d=128, dtype=torch.bfloat16):
+    q, k, v = rnd(g, b, h, sq, d, dtype=dtype), rnd(g, b, h, sk, d, dtype=dtype), rnd(g, b, h, sk, d, dtype=dtype)
+    return q, k, v
+
+
+@pytest.mark.parametrize("b,h,sq,sk", [(1, 2, 128, 64), (1, 3, 200, 333), (2, 2, 77, 1000),
+                                       (1, 2, 4608, 4608)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_attention_matches_fp32(gpu, b, h, sq, sk, dtype):
+    print(f"attention b={b} h={h} sq={sq} sk={sk} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(sq + sk)
+    q, k, v = _attn_case(g, b, h, sq, sk, dtype=dtype)
+    scale = 1 / math.sqrt(128)
+    ref = ops.attention(q.float(), k.float(), v.float(), scale=scale)
+    out = kernels.attention(q.to(gpu), k.to(gpu), v.to(gpu), scale=scale)
+    assert out.dtype == dtype and out.shape == q.shape
+    assert rel_l2(out, ref) < 1e-2  # probabilities rounded to 16 bits before P V
+
+
+def test_attention_folded_heads_and_scale_one(gpu):
+    g = torch.Generator().manual_seed(5)
+    q, k, v = (rnd(g, 6, 96, 128, std=0.2) for _ in range(3))
+    ref = ops.attention(q.float(), k.float(), v.float(), scale=None)
+    out = kernels.attention(q.to(gpu), k.to(gpu), v.to(gpu), scale=1.0)
+    assert out.shape == (6, 96, 128)
+    assert rel_l2(out, ref) < 1e-2
+
+
+def test_attention_causal_bool_and_additive_masks(gpu):
+    g = torch.Generator().manual_seed(6)
+    q, k, v = _attn_case(g, 1, 2, 150, 150)
+    s = 0.1
+    qf, kf, vf = q.float(), k.float(), v.float()
+    ref = ops.attention(qf, kf, vf, scale=s, causal=True)
+    assert rel_l2(kernels.attention(q.to(gpu), k.to(gpu), v.to(gpu), scale=s, causal=True), ref) < 1e-2
+    mask = torch.rand(150, 150, generator=g) > 0.3
+    ref = ops.attention(qf, kf, vf, scale=s, attention_mask=mask)
+    out = kernels.attention(q.to(gpu), k.to(gpu), v.to(gpu), scale=s, attention_mask=mask.to(gpu))
+    assert rel_l2(out, ref) < 1e-2
+    add = torch.randn(1, 2, 150, 150, generator=g)
+    ref = ops.attention(qf, kf, vf, scale=s, attention_mask=add)
+    out = kernels.attention(q.to(gpu), k.to(gpu), v.to(gpu), scale=s, attention_mask=add.to(gpu))
+    assert rel_l2(out, ref) < 1e-2
+
+
+def test_attention_bounds_equal_mask_and_fully_masked_rows_average_v(gpu):
+    """tests/unit/backends/test_cpu_ops_impl.py:492-517: bounds are the contiguous key window;
+    a row with no valid key averages v (softmax over equal finfo.min scores)."""
+    g = torch.Generator().manual_seed(7)
+    bh, s = 4, 300
+    q, k, v = (rnd(g, bh, s, 128) for _ in range(3))
+    bmin = torch.randint(0, 100, (bh, s, 1), generator=g, dtype=torch.int32)
+    bmax = bmin + torch.randint(1, 200, (bh, s, 1), generator=g, dtype=torch.int32)
+    bmax[0, :10] = bmin[0, :10]  # empty window
+    ref = ops.attention(q.float(), k.float(), v.float(), scale=0.05, bound_min=bmin,
+                        bound_max=bmax)
+    out = kernels.attention(q.to(gpu), k.to(gpu), v.to(gpu), scale=0.05,
+                            bound_min=bmin.to(gpu), bound_max=bmax.to(gpu))
+    assert rel_l2(out, ref) < 1e-2
+    mean_v = v[0].float().mean(dim=0)
+    assert rel_l2(out[0, :10].float().cpu(), mean_v.expand(10, -1)) < 1e-2
+    with pytest.raises(ValueError):
+        kernels.attention(q.to(gpu), k.to(gpu), v.to(gpu), scale=1.0, bound_min=bmin.to(gpu))
+
+
+def test_attention_strided_inplace_over_q(gpu):
+    """The DiT layout: q/k/v are column ranges of one [S, 3D] buffer; output over q."""
+    g = torch.Generator().manual_seed(8)
+    s, hds = 333, 3
+    d = hds * 128
+    buf = rnd(g, s, 3 * d)
+    ref_q, ref_k, ref_v = (buf[:, i * d:(i + 1) * d].reshape(s, hds, 128).transpose(0, 1).float()
+                           for i in range(3))
+    ref = ops.attention(ref_q, ref_k, ref_v, scale=0.08).transpose(0, 1).reshape(s, d)
+    gb = buf.to(gpu)
+    view = lambda off: gb.as_strided((1, hds, s, 128), (0, 128, 3 * d, 1), off)  # noqa: E731
+    q = view(0)
+    kernels.attention(q, view(d), view(2 * d), scale=0.08, out=q)
+    assert rel_l2(gb[:, :d], ref) < 1e-2
+    assert torch.equal(gb[:, d:].cpu(), buf[:, d:])  # k, v untouched
+
+
+# --------------------------------------------------------------------- norms, rope, misc
+@pytest.mark.parametrize("rows,dim", [(5, 64), (4608, 3072), (130, 5120)])
+def test_layernorm_modulate(gpu, rows, dim):
+    g = torch.Generator().manual_seed(rows)
+    x = rnd(g, rows, dim, std=2.0) + 0.5
+    sc, sh = rnd(g, 1, dim, std=0.3), rnd(g, 1, dim, std=0.3)
+    ref = ops.ada_modulate(x.float()[None], sh.float(), sc.float())[0]
+    out = kernels.layernorm_modulate(x.to(gpu), sc.to(gpu), sh.to(gpu), eps=1e-6)
+    assert rel_l2(out, ref) < 4e-3
+    # plain affine LayerNorm and fp32 in / bf16 out
+    w, b = rnd(g, dim, dtype=torch.float32), rnd(g, dim, dtype=torch.float32)
+    ref = torch.nn.functional.layer_norm(x.float(), (dim,), w, b, eps=1e-5)
+    out = kernels.layernorm_modulate(x.float().to(gpu), w.to(gpu), b.to(gpu), eps=1e-5,
+                                     one_plus=False, out_dtype=torch.bfloat16)
+    assert out.dtype == torch.bfloat16 and rel_l2(out, ref) < 4e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rms_norm_fp32_law(gpu, dtype):
+    g = torch.Generator().manual_seed(9)
+    x = rnd(g, 37, 5120, dtype=dtype)
+    w = (torch.rand(5120, generator=g) + 0.5).to(dtype)
+    ref = ops.rms_norm_fp32(x, w, 1e-6)
+    out = kernels.rms_norm(x.to(gpu), w.to(gpu), 1e-6)
+    tol = 1e-6 if dtype == torch.float32 else 4e-3
+    assert rel_l2(out, ref) < tol
+
+
+def test_qk_norm_rope_in_place(gpu):
+    g = torch.Generator().manual_seed(10)
+    s, h = 520, 24
+    d = h * 128
+    buf = rnd(g, s, 3 * d)
+    wq = (1 + 0.1 * torch.randn(128, generator=g)).bfloat16()
+    wk = (1 + 0.1 * torch.randn(128, generator=g)).bfloat16()
+    ids = ops.flux_ids(8, 16, 32)
+    cos, sin = ops.flux_pos_embed(ids)
+    def ref_of(off, w):
+        x = buf[:, off:off + d].float().reshape(s, h, 128).transpose(0, 1)
+        x = ops.rms_norm_fp32(x, w.float(), 1e-6)
+        return ops.apply_rotary_emb_fp32(x, cos[None], sin[None]).transpose(0, 1).reshape(s, d)
+    rq, rk = ref_of(0, wq), ref_of(d, wk)
+    gb = buf.to(gpu)
+    kernels.qk_norm_rope(gb, heads=h, head_dim=128, q_off=0, k_off=d, wq=wq.to(gpu),
+                         wk=wk.to(gpu), eps=1e-6, cos=cos.to(gpu), sin=sin.to(gpu), law=0)
+    assert rel_l2(gb[:, :d], rq) < 4e-3
+    assert rel_l2(gb[:, d:2 * d], rk) < 4e-3
+    assert torch.equal(gb[:, 2 * d:].cpu(), buf[:, 2 * d:])
+
+
+@pytest.mark.parametrize("law", [0, 1])
+def test_rope_laws(gpu, law):
+    g = torch.Generator().manual_seed(11 + law)
+    x = rnd(g, 2, 3, 50, 128, dtype=torch.float32)
+    cos = torch.randn(50, 128, generator=g)
+    sin = torch.randn(50, 128, generator=g)  # not repeat-interleaved: the laws differ
+    fn = ops.apply_rotary_emb_fp32 if law == 0 else ops.apply_rotary_emb
+    ref = fn(x, cos, sin)
+    out = kernels.rope(x.to(gpu), cos.to(gpu), sin.to(gpu), law=law)
+    assert rel_l2(out, ref) < 1e-6
+
+
+def test_gelu_gate_residual_gemv_timestep(gpu):
+    g = torch.Generator().manual_seed(12)
+    x = rnd(g, 1001, dtype=torch.float32) * 4
+    assert rel_l2(kernels.gelu_tanh(x.to(gpu)), ops.gelu_tanh(x)) < 1e-5
+    r, y, gt = rnd(g, 64, 256), rnd(g, 64, 256), rnd(g, 256)
+    out = kernels.gate_residual(r.to(gpu), y.to(gpu), gt.to(gpu))
+    assert rel_l2(out, r.float() + gt.float() * y.float()) < 4e-3
+    for m in (1, 2, 3):
+        xv = rnd(g, m, 3072)
+        w = rnd(g, 1000, 3072, std=0.02)
+        b = rnd(g, 1000, std=0.1)
+        silu_x = torch.nn.functional.silu(xv.float()).bfloat16().float()
+        ref = ops.linear(silu_x, w.float(), b.float())
+        out = kernels.gemv(xv.to(gpu), w.to(gpu), b.to(gpu), act=1)
+        assert rel_l2(out, ref) < 4e-3
+    t = torch.tensor([0.0, 1.5, 999.0, 437.25])
+    ref = ops.timestep_embedding(t, 256, flip_sin_to_cos=True, downscale_freq_shift=0)
+    out = kernels.timestep_embedding(t.to(gpu), 256, flip_sin_to_cos=True,
+                                     downscale_freq_shift=0.0)
+    assert (out.cpu() - ref).abs().max().item() < 2e-4
