@@ -5,8 +5,8 @@
 //   bf16  : v_mfma_f32_32x32x16_bf16, 64 K-elements (128 bytes) per K tile;
 //   fp8   : v_mfma_f32_32x32x64_f8f6f4 (e4m3), 128 K-elements per K tile, per-row scales of A
 //           and W applied in the epilogue (acc * sa[m] * sw[n]);
-//   mxfp8 : v_mfma_scale_f32_32x32x64_f8f6f4 with one E8M0 scale per lane per 32 K, i.e. per
-//           32-element block of a row, 128 K-elements per K tile.
+//   mxfp8 : v_mfma_scale_f32_32x32x64_f8f6f4 with one E8M0 scale per 32-element block of a
+//           row (the block split over the two lane groups, see the K loop), 128 K per K tile.
 // A K tile is therefore always 128 bytes per row, and the LDS geometry is shared.
 //
 // Tiling: a 256-thread workgroup (4 wavefronts in a 2 x 2 grid) owns a 256 x 256 tile of C;
@@ -190,16 +190,21 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_kernel(const GemmArgs args) 
       }
     } else {
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {  // 64 K per step; a lane holds 32 consecutive K
-        const int chunk = ks * 4 + fhalf * 2;
+      for (int ks = 0; ks < 2; ++ks) {
+        // 64 K per step = two 32-K blocks b0 | b1 (chunks 4ks..4ks+1 | 4ks+2..4ks+3). The
+        // f8f6f4 MFMA takes K in lane-group halves: bytes 0-15 of both lane groups are one
+        // 32-K block (scaled by the group-0 lane's scale), bytes 16-31 the other (scaled by the
+        // group-1 lane's). So group g holds chunk g of b0 and chunk g of b1, and its scale is
+        // that of block 2 ks + g.
+        const int chunk = ks * 4 + fhalf;
         i32x8 fa[4], fw[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int ra_ = wm * 128 + i * 32 + frow, rw_ = wn * 128 + i * 32 + frow;
           const i32x4 a0 = *reinterpret_cast<const i32x4*>(sA + lds_off(ra_, chunk));
-          const i32x4 a1 = *reinterpret_cast<const i32x4*>(sA + lds_off(ra_, chunk + 1));
+          const i32x4 a1 = *reinterpret_cast<const i32x4*>(sA + lds_off(ra_, chunk + 2));
           const i32x4 w0 = *reinterpret_cast<const i32x4*>(sW + lds_off(rw_, chunk));
-          const i32x4 w1 = *reinterpret_cast<const i32x4*>(sW + lds_off(rw_, chunk + 1));
+          const i32x4 w1 = *reinterpret_cast<const i32x4*>(sW + lds_off(rw_, chunk + 2));
           fa[i] = i32x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
           fw[i] = i32x8{w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
         }
@@ -211,7 +216,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_kernel(const GemmArgs args) 
               acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
                   fw[j], fa[i], acc[i][j], 0, 0, 0, 0, 0, 0);
         } else {
-          const int sh = (ks * 2 + fhalf) * 8;  // this lane's block within the tile's 4
+          const int sh = (ks * 2 + fhalf) * 8;  // block 2 ks + g within the tile's 4
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll

@@ -22,6 +22,7 @@ HBM layout, batch 1, S = S_txt + S_img tokens, D = hidden:
 
 from __future__ import annotations
 
+import contextlib
 import math
 from typing import Callable
 
@@ -32,6 +33,7 @@ from difflet_amd.dit.linear import DeviceLinear, run
 from difflet_amd.dit.rope import flux_rope_tables
 
 EPS = 1e-6
+_NULL = contextlib.nullcontext()
 
 
 class FluxConfig:
@@ -135,6 +137,9 @@ class FluxDiT:
                        for i in range(cfg.n_single)]
         self._bufs: dict = {}
         self._rope: dict = {}
+        #: optional timing hook: probe(name) returns a context manager recording HIP events
+        #: around a launch on the current stream (used by the benchmark, None otherwise)
+        self.probe = None
 
     # -------------------------------------------------------------------------- helpers
     def _buffers(self, st: int, si: int):
@@ -170,7 +175,13 @@ class FluxDiT:
         view = lambda off: buf.as_strided((1, c.heads, s, c.head_dim), (0, c.head_dim, ld, 1),  # noqa: E731
                                           buf.storage_offset() + off)
         q, k, v = view(q_off), view(k_off), view(v_off)
-        kernels.attention(q, k, v, scale=1.0 / math.sqrt(c.head_dim), out=q)
+        with self._timed("attn"):
+            kernels.attention(q, k, v, scale=1.0 / math.sqrt(c.head_dim), out=q)
+
+    def _gemm(self, name: str, problems, epilogue: int = 0, act_col_start: int = 0):
+        """One grouped GEMM launch (activation quantization already done by problem())."""
+        with self._timed(name):
+            run(problems, self.kind, epilogue, act_col_start)
 
     # -------------------------------------------------------------------------- blocks
     def double_block(self, i: int, bufs, st: int, mod, cos, sin):
@@ -183,21 +194,25 @@ class FluxDiT:
         c_sh, c_sc, c_g, c_sh2, c_sc2, c_g2 = self._mods(mod, self.mod_off[("d", i, "norm1_context")], 6)
         kernels.layernorm_modulate(h[T], c_sc, c_sh, eps=EPS, out=n[T])
         kernels.layernorm_modulate(h[I], x_sc, x_sh, eps=EPS, out=n[I])
-        run([blk.qkv_txt.problem(n[T], qkv[T]), blk.qkv_img.problem(n[I], qkv[I])], self.kind)
+        self._gemm("gemm.double.qkv", [blk.qkv_txt.problem(n[T], qkv[T]),
+                                       blk.qkv_img.problem(n[I], qkv[I])])
         self._qk(qkv, T, 0, d, blk.naq, blk.nak, cos, sin)
         self._qk(qkv, I, 0, d, blk.nq, blk.nk, cos, sin)
         self._attn(qkv, 0, d, 2 * d)
         o = qkv[:, :d]
-        run([blk.out_txt.problem(o[T], h[T], gate=c_g, residual=h[T]),
-             blk.out_img.problem(o[I], h[I], gate=x_g, residual=h[I])], self.kind,
-            _lib.EPI_GATE_RESIDUAL)
+        self._gemm("gemm.double.out", [blk.out_txt.problem(o[T], h[T], gate=c_g, residual=h[T]),
+                                       blk.out_img.problem(o[I], h[I], gate=x_g, residual=h[I])],
+                   _lib.EPI_GATE_RESIDUAL)
         kernels.layernorm_modulate(h[T], c_sc2, c_sh2, eps=EPS, out=n[T])
         kernels.layernorm_modulate(h[I], x_sc2, x_sh2, eps=EPS, out=n[I])
-        run([blk.ff1_txt.problem(n[T], ff[T]), blk.ff1_img.problem(n[I], ff[I])], self.kind,
-            _lib.EPI_GELU)
-        run([blk.ff2_txt.problem(ff[T], h[T], gate=c_g2, residual=h[T]),
-             blk.ff2_img.problem(ff[I], h[I], gate=x_g2, residual=h[I])], self.kind,
-            _lib.EPI_GATE_RESIDUAL)
+        self._gemm("gemm.double.ff1", [blk.ff1_txt.problem(n[T], ff[T]),
+                                       blk.ff1_img.problem(n[I], ff[I])], _lib.EPI_GELU)
+        self._gemm("gemm.double.ff2", [blk.ff2_txt.problem(ff[T], h[T], gate=c_g2, residual=h[T]),
+                                       blk.ff2_img.problem(ff[I], h[I], gate=x_g2, residual=h[I])],
+                   _lib.EPI_GATE_RESIDUAL)
+
+    def _timed(self, name: str):
+        return self.probe(name) if self.probe is not None else _NULL
 
     def single_block(self, i: int, bufs, mod, cos, sin):
         blk = self.single[i]
@@ -205,11 +220,11 @@ class FluxDiT:
         h, n, big = bufs["h"], bufs["n"], bufs["big"]
         sh, sc, g = self._mods(mod, self.mod_off[("s", i)], 3)
         kernels.layernorm_modulate(h, sc, sh, eps=EPS, out=n)
-        run([blk.w1.problem(n, big)], self.kind, _lib.EPI_GELU, act_col_start=3 * d)
+        self._gemm("gemm.single.w1", [blk.w1.problem(n, big)], _lib.EPI_GELU, 3 * d)
         self._qk(big, slice(0, h.shape[0]), 2 * d, 0, blk.nq, blk.nk, cos, sin)
         self._attn(big, 2 * d, 0, d)
-        run([blk.w2.problem(big[:, 2 * d:], h, gate=g, residual=h)], self.kind,
-            _lib.EPI_GATE_RESIDUAL)
+        self._gemm("gemm.single.w2", [blk.w2.problem(big[:, 2 * d:], h, gate=g, residual=h)],
+                   _lib.EPI_GATE_RESIDUAL)
 
     # -------------------------------------------------------------------------- step
     def embed(self, timestep, guidance, pooled):

@@ -127,7 +127,7 @@ int difflet_rocm_gemm_mxfp8(int nproblems, const difflet_gemm_problem* problems,
 /* ------------------------------------------------------------------------------------------
  * Quantizers (bit-exact with the CPU laws).
  * ---------------------------------------------------------------------------------------- */
-/* Per-row e4m3: amax = max|x|, a = max(amax, 2^-126), scale = a / 448, inv = 448 / a,
+/* Per-row e4m3: amax = max|x|, a = max(amax, 2^-112), scale = a / 448, inv = 448 / a,
  * q = e4m3_rne(clamp(x * inv, -448, 448)) (IEEE fp32 ops). scale: fp32 [rows]. Used for
  * per-token activations and per-output-channel weights. No reference counterpart (see
  * difflet_rocm_gemm_fp8_rowwise). */

@@ -3,7 +3,7 @@ Test infrastructure only (see oracle/__init__.py).
 
 There is no reference counterpart: the reference's only fp8 recipe is MXFP8
 (difflet/quant/spec.py:22-33). The law is this build's and is fixed in include/difflet_rocm.h
-(difflet_rocm_quantize_fp8_rowwise): amax = max |x|, a = max(amax, 2^-126), scale = a / 448,
+(difflet_rocm_quantize_fp8_rowwise): amax = max |x|, a = max(amax, 2^-112), scale = a / 448,
 inv = 448 / a (IEEE fp32 divisions), q = e4m3_rne(clamp(x * inv, -448, 448)).
 
 Pins (tests/test_oracle_fp8.py): the e4m3 encoder is pinned in oracle/mx.py; the row law
@@ -19,7 +19,7 @@ import numpy as np
 from oracle.mx import e4m3_decode, e4m3_encode
 
 E4M3_MAX = np.float32(448.0)
-TINY = np.float32(2.0 ** -126)
+TINY = np.float32(2.0 ** -112)  # 448 / TINY is finite in fp32
 
 
 def quantize_rowwise(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
@@ -39,11 +39,14 @@ def dequantize_rowwise(q: np.ndarray, scale: np.ndarray) -> np.ndarray:
 
 
 def fp8_linear(x: np.ndarray, wq: np.ndarray, ws: np.ndarray, bias=None) -> np.ndarray:
-    """y = (q_x q_w^T) * s_x[m] * s_w[n] + b, fp32 accumulate: what the fp8 GEMM computes."""
+    """y = (q_x q_w^T) * s_x[m] * s_w[n] + b with an fp32 product: what the fp8 GEMM computes.
+    Products of two e4m3 values are exact in fp32; the sum is an fp32 matmul."""
+    import torch
+
     x2 = np.asarray(x, dtype=np.float32).reshape(-1, x.shape[-1])
     xq, xs = quantize_rowwise(x2)
-    acc = e4m3_decode(xq).astype(np.float64) @ e4m3_decode(wq).astype(np.float64).T
-    y = (acc * xs[:, None].astype(np.float64) * ws[None, :].astype(np.float64)).astype(np.float32)
+    acc = torch.from_numpy(e4m3_decode(xq)) @ torch.from_numpy(e4m3_decode(wq)).T
+    y = (acc * torch.from_numpy(xs)[:, None] * torch.from_numpy(ws)[None, :]).numpy()
     if bias is not None:
         y = y + np.asarray(bias, dtype=np.float32)
-    return y.reshape(*x.shape[:-1], wq.shape[0])
+    return y.reshape(*x.shape[:-1], wq.shape[0]).astype(np.float32)

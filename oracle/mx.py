@@ -35,15 +35,23 @@ def e4m3_encode(x: np.ndarray) -> np.ndarray:
     return (code | sign).astype(np.uint8)
 
 
-def e4m3_decode(code: np.ndarray) -> np.ndarray:
-    """float8_e4m3fn codes -> fp32 values (exact)."""
-    c = np.asarray(code, dtype=np.uint8).astype(np.int64)
+def _e4m3_table() -> np.ndarray:
+    c = np.arange(256, dtype=np.int64)
     s = np.where(c & 0x80, -1.0, 1.0)
     e = (c >> 3) & 0xF
     m = c & 7
     val = np.where(e == 0, m * 2.0 ** -9, (1 + m / 8.0) * 2.0 ** (e - 7))
     val = np.where((e == 15) & (m == 7), np.nan, val)
     return (s * val).astype(np.float32)
+
+
+_E4M3 = _e4m3_table()
+
+
+def e4m3_decode(code: np.ndarray) -> np.ndarray:
+    """float8_e4m3fn codes -> fp32 values (exact): sign * 2^(e-7) * (1 + m/8), subnormals
+    m * 2^-9, code 0x7f / 0xff NaN."""
+    return _E4M3[np.asarray(code, dtype=np.uint8)]
 
 
 def tile_sizes(k: int) -> list[int]:
@@ -113,9 +121,11 @@ def fake_quantize_mx(t: np.ndarray) -> np.ndarray:
 
 def mx_linear(x: np.ndarray, wq: np.ndarray, ws: np.ndarray, bias=None) -> np.ndarray:
     """FakeQuantMXLinear.forward (difflet/quant/fake_linear.py:56-61) in fp32:
-    mx(x) @ deq(W)^T + b."""
-    xq = fake_quantize_mx(x.reshape(-1, x.shape[-1]))
-    y = xq @ dequantize_mx(wq, ws).T
+    mx(x) @ deq(W)^T + b (dequantized values are exact in fp32; the product is an fp32 matmul)."""
+    import torch
+
+    xq = torch.from_numpy(fake_quantize_mx(x.reshape(-1, x.shape[-1])))
+    y = (xq @ torch.from_numpy(dequantize_mx(wq, ws)).T).numpy()
     if bias is not None:
         y = y + np.asarray(bias, dtype=np.float32)
     return y.reshape(*x.shape[:-1], wq.shape[0]).astype(np.float32)
