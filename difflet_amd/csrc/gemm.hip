@@ -27,7 +27,8 @@
 
 namespace dlt {
 
-constexpr int BM = 256, BN = 256, KT_BYTES = 128, NTHREADS = 256;
+constexpr int BM = 256, BN = 256, KT_BYTES = 64, NTHREADS = 256;
+constexpr int STAGES = 4;  // K stages in LDS: 4 x (16 KB A + 16 KB W) = 128 KB, 3 in flight
 constexpr int MAX_PROBLEMS = 4;
 constexpr int GROUP_M = 8;
 
@@ -55,19 +56,37 @@ struct GemmArgs {
 };
 
 template <Elem E> struct ElemTraits;
-template <> struct ElemTraits<Elem::BF16> { static constexpr int KT = 64, BYTES = 2; };
-template <> struct ElemTraits<Elem::FP8> { static constexpr int KT = 128, BYTES = 1; };
-template <> struct ElemTraits<Elem::MX> { static constexpr int KT = 128, BYTES = 1; };
+template <> struct ElemTraits<Elem::BF16> { static constexpr int KT = 32, BYTES = 2; };
+template <> struct ElemTraits<Elem::FP8> { static constexpr int KT = 64, BYTES = 1; };
+template <> struct ElemTraits<Elem::MX> { static constexpr int KT = 64, BYTES = 1; };
 
+// A stage row is 64 bytes = 4 chunks of 16. Chunk c of row r sits at c ^ swz(r), swz(r) =
+// ((r >> 1) ^ (r >> 2)) & 3: the rows an ds_read_b128 serves together (8 or 16 consecutive
+// rows, one logical chunk) then land in distinct bank groups whether the LDS serves 8 lanes
+// over 32 banks or 16 lanes over 64 banks per cycle.
+// Scheduling hint: NREAD LDS reads spread evenly among NMFMA MFMAs (the scheduler would otherwise
+// sink each read next to its first use and wait on it there).
+template <int NMFMA, int NREAD>
+__device__ __forceinline__ void interleave() {
+#pragma unroll
+  for (int r = 0; r < NREAD; ++r) {
+    __builtin_amdgcn_sched_group_barrier(0x008, NMFMA / NREAD, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);              // DS read
+  }
+}
+
+__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
 __device__ __forceinline__ int lds_off(int row, int chunk) {
-  return row * KT_BYTES + ((chunk ^ (row & 7)) << 4);
+  return row * KT_BYTES + ((chunk ^ swz(row)) << 4);
 }
 
 template <Elem E, int EPI>
 __global__ __launch_bounds__(NTHREADS, 1) void gemm_kernel(const GemmArgs args) {
   constexpr int KT = ElemTraits<E>::KT;
   constexpr int EB = ElemTraits<E>::BYTES;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2][2][BM * KT_BYTES];  // [stage][A|W]
+  __shared__ __attribute__((aligned(16))) uint8_t smem[STAGES][2][BM * KT_BYTES];  // [stage][A|W]
+  // MX: per stage and row, the dword of E8M0 scales holding the stage's two 32-K blocks
+  __shared__ __attribute__((aligned(16))) uint32_t smem_sc[E == Elem::MX ? STAGES : 1][2][BM];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -104,43 +123,47 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_kernel(const GemmArgs args) 
   const __amdgpu_buffer_rsrc_t rw =
       make_rsrc(P.w + n0 * w_row_bytes, (uint32_t)min(w_valid, (int64_t)0xffffffff));
 
-  // thread t stages chunks (row = t/8 + 32 i, chunk = t % 8), i = 0..7, of both tiles
-  const int srow = tid >> 3, schunk = tid & 7;
-  u32x4 ga[8], gw[8];
-  auto load_global = [&](int kt) {
-    const uint32_t kb = (uint32_t)kt * KT_BYTES + schunk * 16;
+  // Direct-to-LDS staging: a stage of one operand is 256 rows x 64 bytes = 16 KB = 16 slabs of
+  // 1 KB; wave w fills slabs 4 w .. 4 w + 3. Lane l of load i writes slot p = (4 w + i) * 64 + l,
+  // i.e. row p / 4, physical chunk p % 4, so it loads logical chunk (p % 4) ^ swz(row) of that
+  // row. Per-lane offsets are fixed; the stage's K offset goes in soffset.
+  typedef __attribute__((address_space(3))) void lds_void;
+  uint32_t a_off[4], w_off[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = srow + 32 * i;
-      ga[i] = buf_load16(ra, (uint32_t)(r * a_row_bytes) + kb);
-      gw[i] = buf_load16(rw, (uint32_t)(r * w_row_bytes) + kb);
-    }
-  };
-  auto store_lds = [&](int st) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = srow + 32 * i;
-      *reinterpret_cast<u32x4*>(&smem[st][0][lds_off(r, schunk)]) = ga[i];
-      *reinterpret_cast<u32x4*>(&smem[st][1][lds_off(r, schunk)]) = gw[i];
-    }
-  };
-
-  // ---- MX scales: one dword per row per K tile holds the tile's 4 block scales
+  for (int i = 0; i < 4; ++i) {
+    const int p = (wave * 4 + i) * 64 + lane;
+    const int r = p >> 2, ch = (p & 3) ^ swz(r);
+    a_off[i] = (uint32_t)(r * a_row_bytes) + ch * 16;
+    w_off[i] = (uint32_t)(r * w_row_bytes) + ch * 16;
+  }
+  // MX scales ride along with their stage: one DMA dword per row (scale bytes 4 q .. 4 q + 3,
+  // q = stage / 2, so the stage's two blocks are its half kt & 1), rows past M / N read zero.
   const int ksb = K / 32;  // scale row stride (blocks per row)
-  uint32_t sa_w[4], sw_w[4];
-  auto load_scales = [&](int kt) {
-    if constexpr (E == Elem::MX) {
-      const uint8_t* as = (const uint8_t*)P.a_scale;
-      const uint8_t* ws = (const uint8_t*)P.w_scale;
+  __amdgpu_buffer_rsrc_t rsa = rw, rsw = rw;
+  if constexpr (E == Elem::MX) {
+    rsa = make_rsrc((const uint8_t*)P.a_scale + m0 * ksb, (uint32_t)((M - m0) * ksb));
+    rsw = make_rsrc((const uint8_t*)P.w_scale + n0 * ksb, (uint32_t)((N - n0) * ksb));
+  }
+  auto issue_stage = [&](int kt, int st) {
+    const uint32_t kb = (uint32_t)kt * KT_BYTES;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t mr = m0 + wm * 128 + i * 32 + (lane & 31);
-        const int64_t nr = n0 + wn * 128 + i * 32 + (lane & 31);
-        sa_w[i] = mr < M ? *reinterpret_cast<const uint32_t*>(as + mr * ksb + kt * 4) : 0u;
-        sw_w[i] = nr < N ? *reinterpret_cast<const uint32_t*>(ws + nr * ksb + kt * 4) : 0u;
-      }
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ra, (lds_void*)&smem[st][0][(wave * 4 + i) * 1024], 16, a_off[i], kb, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rw, (lds_void*)&smem[st][1][(wave * 4 + i) * 1024], 16, w_off[i], kb, 0, 0);
+    }
+    if constexpr (E == Elem::MX) {
+      const uint32_t row = wave * 64 + lane;
+      const uint32_t so = (uint32_t)(kt & ~1) * 2;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)&smem_sc[st][0][wave * 64], 4,
+                                               row * ksb, so, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_void*)&smem_sc[st][1][wave * 64], 4,
+                                               row * ksb, so, 0, 0);
     }
   };
+  // vector-memory instructions one stage issues per wave (for s_waitcnt vmcnt)
+  constexpr int LOADS_PER_STAGE = E == Elem::MX ? 10 : 8;
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -148,93 +171,165 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_kernel(const GemmArgs args) 
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
-  const int nkt = K / KT;
-  load_global(0);
-  load_scales(0);
-  store_lds(0);
-  __syncthreads();
-
   const int frow = lane & 31;  // fragment row within a 32-row MFMA tile
   const int fhalf = lane >> 5;
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int st = kt & 1;
-    uint32_t cur_sa[4], cur_sw[4];
-    if constexpr (E == Elem::MX) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        cur_sa[i] = sa_w[i];
-        cur_sw[i] = sw_w[i];
-      }
-    }
-    if (kt + 1 < nkt) {
-      load_global(kt + 1);
-      load_scales(kt + 1);
-    }
+
+  // A stage (64 bytes of K per row) is computed in two halves of equal MFMA time:
+  //   bf16: MFMA K step h (16 K), all 16 tiles, fragments of chunk 2 h + g;
+  //   fp8 / mx: one 64-K MFMA step; half h covers W tiles j = 2 h, 2 h + 1. The f8f6f4 MFMA
+  //   takes K in lane-group halves: bytes 0-15 of both lane groups are one 32-K block (scaled by
+  //   the group-0 lane's scale), bytes 16-31 the other, so group g holds chunks g and 2 + g.
+  struct Frags {
+    i32x4 a[4][2], w[4][2];
+    uint32_t sa[4], sw[4];  // MX: this lane's scale bytes for its A rows / W rows
+  };
+  auto read_a = [&](int st, int kt, Frags& f) {
     const uint8_t* sA = smem[st][0];
+    const int h = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = wm * 128 + i * 32 + frow;
+      if constexpr (E == Elem::BF16) {
+        f.a[i][0] = *reinterpret_cast<const i32x4*>(sA + lds_off(r, h * 2 + fhalf));
+      } else {
+        f.a[i][0] = *reinterpret_cast<const i32x4*>(sA + lds_off(r, fhalf));
+        f.a[i][1] = *reinterpret_cast<const i32x4*>(sA + lds_off(r, 2 + fhalf));
+      }
+      if constexpr (E == Elem::MX)
+        f.sa[i] = (smem_sc[st][0][r] >> ((kt & 1) * 16 + fhalf * 8)) & 0xffu;
+    }
+  };
+  auto read_a1 = [&](int st, Frags& f) {  // bf16: the A fragments of half 1
+    const uint8_t* sA = smem[st][0];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      f.a[i][0] = *reinterpret_cast<const i32x4*>(sA + lds_off(wm * 128 + i * 32 + frow, 2 + fhalf));
+  };
+  auto read_w = [&](int st, int h, int kt, Frags& f) {
     const uint8_t* sW = smem[st][1];
     if constexpr (E == Elem::BF16) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {  // 16 K per step
-        const int chunk = ks * 2 + fhalf;
-        bf16x8 fa[4], fw[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          fa[i] = *reinterpret_cast<const bf16x8*>(sA + lds_off(wm * 128 + i * 32 + frow, chunk));
-          fw[i] = *reinterpret_cast<const bf16x8*>(sW + lds_off(wn * 128 + i * 32 + frow, chunk));
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[j], fa[i], acc[i][j], 0, 0, 0);
-      }
+      for (int j = 0; j < 4; ++j)
+        f.w[j][0] = *reinterpret_cast<const i32x4*>(sW + lds_off(wn * 128 + j * 32 + frow, h * 2 + fhalf));
     } else {
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        // 64 K per step = two 32-K blocks b0 | b1 (chunks 4ks..4ks+1 | 4ks+2..4ks+3). The
-        // f8f6f4 MFMA takes K in lane-group halves: bytes 0-15 of both lane groups are one
-        // 32-K block (scaled by the group-0 lane's scale), bytes 16-31 the other (scaled by the
-        // group-1 lane's). So group g holds chunk g of b0 and chunk g of b1, and its scale is
-        // that of block 2 ks + g.
-        const int chunk = ks * 4 + fhalf;
-        i32x8 fa[4], fw[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int ra_ = wm * 128 + i * 32 + frow, rw_ = wn * 128 + i * 32 + frow;
-          const i32x4 a0 = *reinterpret_cast<const i32x4*>(sA + lds_off(ra_, chunk));
-          const i32x4 a1 = *reinterpret_cast<const i32x4*>(sA + lds_off(ra_, chunk + 2));
-          const i32x4 w0 = *reinterpret_cast<const i32x4*>(sW + lds_off(rw_, chunk));
-          const i32x4 w1 = *reinterpret_cast<const i32x4*>(sW + lds_off(rw_, chunk + 2));
-          fa[i] = i32x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-          fw[i] = i32x8{w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
-        }
-        if constexpr (E == Elem::FP8) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                  fw[j], fa[i], acc[i][j], 0, 0, 0, 0, 0, 0);
-        } else {
-          const int sh = (ks * 2 + fhalf) * 8;  // block 2 ks + g within the tile's 4
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                  fw[j], fa[i], acc[i][j], 0, 0, 0, (int)((cur_sw[j] >> sh) & 0xffu), 0,
-                  (int)((cur_sa[i] >> sh) & 0xffu));
-        }
+      for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * h + jj;
+        const int r = wn * 128 + j * 32 + frow;
+        f.w[j][0] = *reinterpret_cast<const i32x4*>(sW + lds_off(r, fhalf));
+        f.w[j][1] = *reinterpret_cast<const i32x4*>(sW + lds_off(r, 2 + fhalf));
+        if constexpr (E == Elem::MX)
+          f.sw[j] = (smem_sc[st][1][r] >> ((kt & 1) * 16 + fhalf * 8)) & 0xffu;
       }
     }
-    if (kt + 1 < nkt) store_lds(st ^ 1);
+  };
+  auto mma_half = [&](const Frags& f, int h) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int jj = 0; jj < (E == Elem::BF16 ? 4 : 2); ++jj) {
+        const int j = E == Elem::BF16 ? jj : 2 * h + jj;
+        if constexpr (E == Elem::BF16) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8, f.w[j][0]), __builtin_bit_cast(bf16x8, f.a[i][0]),
+              acc[i][j], 0, 0, 0);
+        } else {
+          const i32x8 fw = {f.w[j][0][0], f.w[j][0][1], f.w[j][0][2], f.w[j][0][3],
+                            f.w[j][1][0], f.w[j][1][1], f.w[j][1][2], f.w[j][1][3]};
+          const i32x8 fa = {f.a[i][0][0], f.a[i][0][1], f.a[i][0][2], f.a[i][0][3],
+                            f.a[i][1][0], f.a[i][1][1], f.a[i][1][2], f.a[i][1][3]};
+          if constexpr (E == Elem::FP8) {
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw, fa, acc[i][j], 0, 0,
+                                                                        0, 0, 0, 0);
+          } else {
+            // group g scales block g of the stage
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                fw, fa, acc[i][j], 0, 0, 0, (int)f.sw[j], 0, (int)f.sa[i]);
+          }
+        }
+      }
+  };
+
+  const int nkt = K / KT;
+  // prologue: stages 0 .. STAGES-2 in flight, then wait for stage 0
+#pragma unroll
+  for (int s0 = 0; s0 < STAGES - 1; ++s0)
+    if (s0 < nkt) issue_stage(s0, s0);
+  if (nkt > 2) __builtin_amdgcn_s_waitcnt(0x0f70 | (2 * LOADS_PER_STAGE & 15) | ((2 * LOADS_PER_STAGE >> 4) << 14));
+  else __builtin_amdgcn_s_waitcnt(0x0f70);
+  __syncthreads();
+  Frags f0, f1;
+  read_a(0, 0, f0);
+  read_w(0, 0, 0, f0);
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int st = kt % STAGES;
+    // half 0 of stage kt; meanwhile read half 1's fragments
+    if constexpr (E == Elem::BF16) {
+      read_a1(st, f1);
+      read_w(st, 1, kt, f1);
+      mma_half(f0, 0);
+      interleave<16, 8>();
+    } else {
+      read_w(st, 1, kt, f1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f1.a[i][0] = f0.a[i][0];
+        f1.a[i][1] = f0.a[i][1];
+        f1.sa[i] = f0.sa[i];
+      }
+      mma_half(f0, 0);
+      interleave<8, 4>();
+    }
+    // stage kt + 1 must have landed (stage kt + 2 may still be in flight), then the barrier
+    // publishes it to every wave and frees stage kt - 1 for stage kt + STAGES - 1
+    if (kt + 2 < nkt) {
+      constexpr int c = LOADS_PER_STAGE;
+      __builtin_amdgcn_s_waitcnt(0x0f70 | (c & 15) | ((c >> 4) << 14));
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0f70);
+    }
     __syncthreads();
+    if (kt + STAGES - 1 < nkt) issue_stage(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+    // half 1 of stage kt; meanwhile read half 0 of stage kt + 1
+    const int nst = (kt + 1) % STAGES;
+    if (kt + 1 < nkt) {
+      read_a(nst, kt + 1, f0);
+      read_w(nst, 0, kt + 1, f0);
+    }
+    mma_half(f1, 1);
+    if (kt + 1 < nkt) {
+      if constexpr (E == Elem::BF16) interleave<16, 8>();
+      else interleave<8, 8>();
+    }
   }
 
-  // ---- epilogue: lane l holds row m = l % 32 of each MFMA tile, columns in runs of 4
+  // ---- epilogue: lane l holds row m = l % 32 of each MFMA tile; register 4 q + e of tile
+  // (i, j) is column n = n0 + wn * 128 + j * 32 + q * 8 + 4 g + e (N % 4 == 0, so a run of 4
+  // is all in or all out). Column vectors (bias, gate, W scales) are read once for the whole
+  // tile, and each row block's residual is read before any of its stores: the residual may
+  // alias C, so loads left between stores would each wait out a full memory latency.
   const int act_start = args.act_col_start;
   const float* ws = reinterpret_cast<const float*>(P.w_scale);
   const bf16* bias = P.bias;
+  u32x2 bias_v[4][4], gate_v[4][4];
+  f32x4 ws_v[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t n = n0 + wn * 128 + j * 32 + q * 8 + fhalf * 4;
+      const bool nok = n < N;
+      bias_v[j][q] = (bias && nok) ? *reinterpret_cast<const u32x2*>(bias + n) : u32x2{0u, 0u};
+      if constexpr (E == Elem::FP8)
+        ws_v[j][q] = nok ? *reinterpret_cast<const f32x4*>(ws + n) : f32x4{};
+      if constexpr (EPI == DIFFLET_EPI_GATE_RESIDUAL) {
+        // one gate row per batch element: a wave's 128 rows lie in one batch element, since
+        // the host requires rows_per_batch % 128 == 0 when a problem holds several
+        const int64_t b0 = (m0 + wm * 128) / P.rows_per_batch;
+        gate_v[j][q] = nok ? *reinterpret_cast<const u32x2*>(P.gate + b0 * P.gate_stride + n)
+                           : u32x2{0u, 0u};
+      }
+    }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t m = m0 + wm * 128 + i * 32 + frow;
@@ -242,58 +337,50 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_kernel(const GemmArgs args) 
     const int64_t mc = mok ? m : 0;  // clamped row for address formation
     float sa = 1.f;
     if constexpr (E == Elem::FP8) sa = mok ? reinterpret_cast<const float*>(P.a_scale)[mc] : 0.f;
-    const int64_t bidx = mc / P.rows_per_batch;
     bf16* crow = reinterpret_cast<bf16*>(P.c) + mc * P.ldc;
-    const bf16* rrow = EPI == DIFFLET_EPI_GATE_RESIDUAL ? P.res + mc * P.ldr : nullptr;
-    const bf16* grow = EPI == DIFFLET_EPI_GATE_RESIDUAL ? P.gate + bidx * P.gate_stride : nullptr;
+    u32x2 res_v[4][4];
+    if constexpr (EPI == DIFFLET_EPI_GATE_RESIDUAL) {
+      const bf16* rrow = P.res + mc * P.ldr;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t n = n0 + wn * 128 + j * 32 + q * 8 + fhalf * 4;
+          res_v[j][q] = (mok && n < N) ? *reinterpret_cast<const u32x2*>(rrow + n) : u32x2{0u, 0u};
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int64_t n = n0 + wn * 128 + j * 32 + q * 8 + fhalf * 4;
         float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][q * 4 + e];
-        if (mok && n < N) {  // N % 4 == 0, so a run of 4 is all in or all out
-          {
-            float sw4[4] = {1.f, 1.f, 1.f, 1.f}, bb[4] = {0.f, 0.f, 0.f, 0.f};
-            if constexpr (E == Elem::FP8) {
-              const f32x4 t4 = *reinterpret_cast<const f32x4*>(ws + n);
+        for (int e = 0; e < 4; ++e) {
+          v[e] = acc[i][j][q * 4 + e];
+          if constexpr (E == Elem::FP8) v[e] = v[e] * (sa * ws_v[j][q][e]);
+          v[e] += bf16bits_to_f32(e & 1 ? bias_v[j][q][e >> 1] >> 16
+                                        : bias_v[j][q][e >> 1] & 0xffffu);
+        }
+        if constexpr (EPI == DIFFLET_EPI_GELU) {
 #pragma unroll
-              for (int e = 0; e < 4; ++e) sw4[e] = t4[e];
-            }
-            if (bias) {
-              const u32x2 t = *reinterpret_cast<const u32x2*>(bias + n);
-              bb[0] = bf16bits_to_f32(t[0] & 0xffffu);
-              bb[1] = bf16bits_to_f32(t[0] >> 16);
-              bb[2] = bf16bits_to_f32(t[1] & 0xffffu);
-              bb[3] = bf16bits_to_f32(t[1] >> 16);
-            }
+          for (int e = 0; e < 4; ++e)
+            if (n + e >= act_start) v[e] = gelu_tanh(v[e]);
+        } else if constexpr (EPI == DIFFLET_EPI_GATE_RESIDUAL) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              if constexpr (E == Elem::FP8) v[e] = v[e] * (sa * sw4[e]);
-              v[e] += bb[e];
-            }
-            if constexpr (EPI == DIFFLET_EPI_GELU) {
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                if (n + e >= act_start) v[e] = gelu_tanh(v[e]);
-            } else if constexpr (EPI == DIFFLET_EPI_GATE_RESIDUAL) {
-              const u32x2 rt = *reinterpret_cast<const u32x2*>(rrow + n);
-              const u32x2 gt = *reinterpret_cast<const u32x2*>(grow + n);
-              v[0] = bf16bits_to_f32(rt[0] & 0xffffu) + bf16bits_to_f32(gt[0] & 0xffffu) * v[0];
-              v[1] = bf16bits_to_f32(rt[0] >> 16) + bf16bits_to_f32(gt[0] >> 16) * v[1];
-              v[2] = bf16bits_to_f32(rt[1] & 0xffffu) + bf16bits_to_f32(gt[1] & 0xffffu) * v[2];
-              v[3] = bf16bits_to_f32(rt[1] >> 16) + bf16bits_to_f32(gt[1] >> 16) * v[3];
-            }
-            u32x2 o;
-            o[0] = pack_bf16x2(v[0], v[1]);
-            o[1] = pack_bf16x2(v[2], v[3]);
-            *reinterpret_cast<u32x2*>(crow + n) = o;
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t rw_ = res_v[j][q][e >> 1], gw_ = gate_v[j][q][e >> 1];
+            v[e] = bf16bits_to_f32(e & 1 ? rw_ >> 16 : rw_ & 0xffffu) +
+                   bf16bits_to_f32(e & 1 ? gw_ >> 16 : gw_ & 0xffffu) * v[e];
           }
         }
+        if (mok && n < N) {
+          u32x2 o;
+          o[0] = pack_bf16x2(v[0], v[1]);
+          o[1] = pack_bf16x2(v[2], v[3]);
+          *reinterpret_cast<u32x2*>(crow + n) = o;
+        }
       }
-    }
   }
 }
 
@@ -364,6 +451,11 @@ static int gemm_launch(const char* name, int nproblems, const difflet_gemm_probl
     d.gate_stride = q.gate_stride;
     d.m = q.m;
     d.rows_per_batch = q.rows_per_batch > 0 ? q.rows_per_batch : (q.m > 0 ? q.m : 1);
+    DLT_REQUIRE(epilogue != DIFFLET_EPI_GATE_RESIDUAL || d.rows_per_batch >= q.m ||
+                    d.rows_per_batch % 128 == 0,
+                DIFFLET_EUNSUPPORTED,
+                "%s: with several batches per problem, rows_per_batch must be a multiple of 128",
+                name);
     d.tiles_m = (int)((q.m + BM - 1) / BM);
     d.tile_start = (int)tiles;
     tiles += (int64_t)d.tiles_m * args.tiles_n;

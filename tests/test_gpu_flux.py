@@ -59,13 +59,15 @@ def _gpu_mod(dit, temb, gpu):
     return kernels.gemv(temb.to(gpu, torch.bfloat16), dit.mod_w, dit.mod_b, act=1)
 
 
-# bf16: the device against the fp32 oracle (1e-2). fp8 / mx: (a) the device against the
-# oracle run with the same quantization law on activations rounded to bf16 where the device
-# keeps them in bf16, so both quantize (nearly) the same values; (b) the format's own error
-# against unquantized fp32. (b) is the e4m3 format on these random N(0, 0.02) weights: the CPU
-# oracle with the identical law shows the same ~4.8e-2 at FLUX width, above the 3e-2 the fp8
-# budget names, so (b) is bounded at 6e-2 and reported, and (a) is the kernels' check.
-CASES = [("bf16", None, 1e-2), ("fp8", "fp8", 1.5e-2), ("mx", "mx", 1.5e-2)]
+# bf16: the device against the fp32 oracle, rel L2 < 1e-2.
+# fp8 / mx: two inputs that differ by bf16 rounding (~0.4%) land in different e4m3 bins often
+# enough that two correct quantized computations differ by ~2-3% (each linear's kernels are
+# checked bit-exact / tight on equal inputs in test_gpu_kernels.py). The block-level checks are
+# therefore: (a) the device against the same-law oracle, rel L2 < 4e-2; (b) the device's error
+# against unquantized fp32 equals the oracle's own error with the same law (the format's error)
+# within 10% -- a wrong scale, block or rounding rule moves it far more; (c) that format error,
+# ~4.8e-2 at FLUX width on these random N(0, 0.02) weights for the CPU law itself, stays < 6e-2.
+CASES = [("bf16", None, 1e-2), ("fp8", "fp8", 4e-2), ("mx", "mx", 4e-2)]
 FORMAT_ERR = 6e-2
 
 
@@ -90,7 +92,10 @@ def test_double_block_matches_fp32_oracle(gpu, kind, quant, tol):
     if quant is not None:
         f_c, f_h = oflux.double_block(bw, hidden, context, temb, cos, sin, shape)
         q_c, q_h = rel_l2(bufs["h"][:st], f_c[0]), rel_l2(bufs["h"][st:], f_h[0])
-        print(f"{kind} format error vs fp32: context {q_c:.3e} hidden {q_h:.3e}", flush=True)
+        o_c, o_h = rel_l2(ref_c, f_c), rel_l2(ref_h, f_h)
+        print(f"{kind} format error vs fp32: device {q_c:.3e} / {q_h:.3e}, "
+              f"oracle {o_c:.3e} / {o_h:.3e}", flush=True)
+        assert abs(q_c - o_c) < 0.1 * o_c and abs(q_h - o_h) < 0.1 * o_h
         assert q_c < FORMAT_ERR and q_h < FORMAT_ERR
     assert e_c < tol and e_h < tol
 
@@ -114,8 +119,10 @@ def test_single_block_matches_fp32_oracle(gpu, kind, quant, tol):
     e = rel_l2(bufs["h"], ref[0])
     print(f"rel L2 vs same-law oracle {e:.3e}", flush=True)
     if quant is not None:
-        q = rel_l2(bufs["h"], oflux.single_block(bw, x, temb, cos, sin, shape)[0])
-        print(f"{kind} format error vs fp32: {q:.3e}", flush=True)
+        full = oflux.single_block(bw, x, temb, cos, sin, shape)
+        q, o = rel_l2(bufs["h"], full[0]), rel_l2(ref, full)
+        print(f"{kind} format error vs fp32: device {q:.3e}, oracle {o:.3e}", flush=True)
+        assert abs(q - o) < 0.1 * o
         assert q < FORMAT_ERR
     assert e < tol
 
