@@ -15,10 +15,17 @@
 // lane holds for a 16-key MFMA step are {4g..4g+3, 8+4g..8+4g+3}, g = l / 32, and the V^T
 // operand is read in that same key order), so P never leaves registers.
 //
-// LDS: K tile row-major [64 keys][128 dims] with 16-byte chunks XOR-swizzled by key; V tile
-// stored transposed [128 dims][64 keys] with a 136-byte row pitch, so the V^T fragment reads of
-// 16 lanes (16 dims, one key offset) cover all 32 banks. Both are written from registers
-// (V transposed in the write), one barrier per K/V tile.
+// LDS: K tile row-major [64 keys][128 dims] with a 272-byte row pitch (256 + 16): the K fragment
+// reads of 8 or 16 lanes (consecutive keys, one 16-byte chunk) land in distinct bank groups, and
+// every fragment address is the lane's base plus an immediate. V tile stored transposed
+// [128 dims][64 keys] with a 136-byte row pitch, so the V^T fragment reads of 16 lanes (16 dims,
+// one key offset) cover all banks. Both are written from registers (V transposed in the
+// write), one barrier per K/V tile.
+//
+// VALU budget: the softmax costs about as many instruction cycles as the MFMAs, so the fast
+// (unmasked) path folds the scale into one FMA ahead of exp2 (p = exp2(s c - m), the running
+// max kept in scaled units, c > 0), checks the key bound only on the last tile, and rescales
+// the output only when some lane's running max moved (wave-uniform branch).
 //
 // Masking follows the reference: masked scores become the lowest finite float (so a fully
 // masked row averages V, as softmax over equal finfo.min scores does); keys past seq_k do not
@@ -32,6 +39,7 @@ constexpr int HD = 128;
 constexpr int BLOCK_M = 128;
 constexpr int BLOCK_N = 64;
 constexpr int VT_PITCH = BLOCK_N * 2 + 8;  // bytes per V^T row
+constexpr int K_PITCH = HD * 2 + 16;         // bytes per K row
 constexpr float LOG2E = 1.4426950408889634f;
 
 struct AttnArgs {
@@ -76,14 +84,12 @@ template <> struct MfmaT<f16> {
   }
 };
 
-__device__ __forceinline__ int k_off(int row, int chunk) {  // K tile: 256-byte rows
-  return row * (HD * 2) + ((chunk ^ (row & 7)) << 4);
-}
+__device__ __forceinline__ int k_off(int row, int chunk) { return row * K_PITCH + (chunk << 4); }
 
 template <typename T, bool MASKED>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
   typedef typename MfmaT<T>::frag frag;
-  __shared__ __attribute__((aligned(16))) uint8_t sk[2][BLOCK_N * HD * 2];
+  __shared__ __attribute__((aligned(16))) uint8_t sk[2][BLOCK_N * K_PITCH];
   __shared__ __attribute__((aligned(16))) uint8_t sv[2][HD * VT_PITCH];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -186,14 +192,17 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
     }
 
     // ---- scale, mask, online softmax (this lane: query my_q, 32 of the tile's keys)
-    float mx = -INFINITY;
+    // Scores stay raw in the fast path (p = exp2(s * cmul - m)); the masked path scales them
+    // first (cmul = 1) so additive masks and finfo.min fills work in scaled units.
+    float cmul = a.scale_log2;
+    if (MASKED) {
+      cmul = 1.0f;
 #pragma unroll
-    for (int kt2 = 0; kt2 < 2; ++kt2)
+      for (int kt2 = 0; kt2 < 2; ++kt2)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int key = j0 + kt2 * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
-        float x = s[kt2][v] * a.scale_log2;
-        if (MASKED) {
+        for (int v = 0; v < 16; ++v) {
+          const int key = j0 + kt2 * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+          float x = s[kt2][v] * a.scale_log2;
           bool masked = key < bmin || key >= bmax || (a.causal && key > my_q);
           if (a.mask && !masked && key < a.seq_k && my_q < a.seq_q) {
             const int64_t mo = b * a.ms[0] + h * a.ms[1] + (int64_t)my_q * a.ms[2] +
@@ -208,14 +217,25 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
               x += (float)reinterpret_cast<const f16*>(a.mask)[mo] * LOG2E;
             }
           }
-          if (masked) x = -FLT_MAX;
+          s[kt2][v] = masked ? -FLT_MAX : x;
         }
-        if (key >= a.seq_k) x = -INFINITY;
-        s[kt2][v] = x;
-        mx = fmaxf(mx, x);
-      }
+    }
+    if (j0 + BLOCK_N > a.seq_k) {  // last tile: keys past seq_k do not exist
+#pragma unroll
+      for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = j0 + kt2 * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+          if (key >= a.seq_k) s[kt2][v] = -INFINITY;
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kt2][v]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
+    const float m_new = fmaxf(m_run, mx * cmul);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
     m_run = m_new;
@@ -225,16 +245,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
     for (int kt2 = 0; kt2 < 2; ++kt2)
 #pragma unroll
       for (int v = 0; v < 16; v += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(s[kt2][v] - m_use);
-        const float p1 = __builtin_amdgcn_exp2f(s[kt2][v + 1] - m_use);
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt2][v], cmul, -m_use));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt2][v + 1], cmul, -m_use));
         ls += p0 + p1;
         pp[kt2][v >> 1] = MfmaT<T>::pack2(p0, p1);
       }
     l_run = l_run * alpha + ls;
+    if (__any(alpha != 1.0f)) {  // the running max moved for some query of this wave
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][v] *= alpha;
+        for (int v = 0; v < 16; ++v) acc[i][v] *= alpha;
+    }
 
     // ---- O^T += V^T P^T, 16 keys per MFMA: keys base + {4g..4g+3, 8+4g..8+4g+3}
 #pragma unroll
@@ -352,7 +374,8 @@ extern "C" int difflet_rocm_attention(const void* q, const void* k, const void* 
   args.bmax = bound_max;
   if (bound_min)
     for (int i = 0; i < 3; ++i) args.bs[i] = bound_strides[i];
-  const bool masked = causal || mask || bound_min;
+  // the fast path keeps scores raw and scales inside exp2, which needs scale > 0
+  const bool masked = causal || mask || bound_min || !(scale > 0.0f);
   hipStream_t s = (hipStream_t)stream;
   dim3 grid((unsigned)total), block(256);
   if (dtype == DIFFLET_BF16) {
