@@ -1,0 +1,149 @@
+"""What is quantized and how, for the rocm backend. Torch-free.
+
+The rocm twin of difflet/quant/spec.py's QuantSpec (:46-176): the same fields, matching,
+serialisation and cache-key rules, plus
+
+* the ``rocm`` compute mode (the HIP fp8 GEMMs) next to ``dequant`` (weights dequantized once
+  to bf16, bf16 GEMM: memory-only);
+* a ``format`` field: ``mxfp8`` (the reference's one format: e4m3 with one E8M0 scale per 32
+  values along K, difflet/quant/mx.py) or ``fp8_rowwise`` (new in this build: e4m3 weights with
+  one fp32 scale per output channel, activations quantized per token at run time;
+  include/difflet_rocm.h difflet_rocm_quantize_fp8_rowwise states the law).
+
+For ``mxfp8`` the cache and weight identities are the reference's dicts unchanged (the format
+is not added), so keys of existing specs stay byte-identical; ``fp8_rowwise`` adds its format.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import hashlib
+import json
+import re
+from collections.abc import Iterable
+from typing import Any
+
+QUANT_SCHEMA = 3  # difflet/quant/spec.py:27
+FORMATS = ("mxfp8", "fp8_rowwise")
+COMPUTE_MODES = ("rocm", "dequant")
+DEFAULT_COMPUTE = "rocm"
+BLOCK = 32          # difflet/quant/spec.py:39
+LAYOUT_K = 128      # difflet/quant/spec.py:40
+STRIPPED_PREFIXES = ("transformer.",)
+
+
+def strip_prefix(name: str) -> str:
+    for prefix in STRIPPED_PREFIXES:
+        if name.startswith(prefix):
+            return name[len(prefix):]
+    return name
+
+
+@dataclasses.dataclass(frozen=True)
+class RocmQuantSpec:
+    targets: tuple[str, ...]
+    compute: str = DEFAULT_COMPUTE
+    tp_degree: int = 1
+    row_parallel: tuple[str, ...] = ()
+    split_linears: tuple[str, ...] = ()
+    schema: int = QUANT_SCHEMA
+    format: str = "mxfp8"
+
+    def __post_init__(self) -> None:
+        if int(self.tp_degree) != 1:
+            raise ValueError(f"the rocm backend runs tp = 1, got tp_degree={self.tp_degree}")
+        if self.compute not in COMPUTE_MODES:
+            raise ValueError(f"compute must be one of {COMPUTE_MODES}, got {self.compute!r}")
+        if self.format not in FORMATS:
+            raise ValueError(f"format must be one of {FORMATS}, got {self.format!r}")
+        if not self.targets or any(not t for t in self.targets):
+            raise ValueError("a QuantSpec needs at least one non-empty target pattern")
+        for pattern in (*self.targets, *self.row_parallel, *self.split_linears):
+            re.compile(pattern)
+
+    # ------------------------------------------------------------------ matching
+    def matches(self, name: str) -> bool:
+        bare = strip_prefix(name)
+        return any(re.fullmatch(p, bare) for p in self.targets)
+
+    def unmatched_targets(self, names: Iterable[str]) -> list[str]:
+        bare = [strip_prefix(n) for n in names]
+        return [p for p in self.targets if not any(re.fullmatch(p, n) for n in bare)]
+
+    def is_row_parallel(self, name: str) -> bool:
+        bare = strip_prefix(name)
+        return any(re.fullmatch(p, bare) for p in self.row_parallel)
+
+    def k_shards(self, name: str) -> int:
+        return 1  # tp = 1
+
+    def is_split(self, name: str) -> bool:
+        bare = strip_prefix(name)
+        return any(re.fullmatch(p, bare) for p in self.split_linears)
+
+    # ------------------------------------------------------------- serialisation
+    def to_dict(self) -> dict[str, Any]:
+        body = dataclasses.asdict(self)
+        body["targets"] = list(self.targets)
+        body["row_parallel"] = list(self.row_parallel)
+        if self.split_linears:
+            body["split_linears"] = list(self.split_linears)
+        else:
+            del body["split_linears"]
+        return body
+
+    @classmethod
+    def from_dict(cls, body: dict[str, Any]) -> "RocmQuantSpec":
+        body = dict(body)
+        body["targets"] = tuple(body["targets"])
+        body["row_parallel"] = tuple(body.get("row_parallel", ()))
+        body["split_linears"] = tuple(body.get("split_linears", ()))
+        body.setdefault("format", "mxfp8")
+        return cls(**body)
+
+    def targets_sha256(self) -> str:
+        return hashlib.sha256(json.dumps(list(self.targets)).encode()).hexdigest()[:16]
+
+    def cache_fields(self) -> dict[str, Any]:
+        """difflet/quant/spec.py:147-157, with the format named only when it is not mxfp8."""
+        fields = {
+            "quant": self.format,
+            "quant_schema": self.schema,
+            "quant_compute": self.compute,
+            "quant_targets_sha256": self.targets_sha256(),
+            "quant_tp_degree": int(self.tp_degree),
+        }
+        return fields
+
+    def weights_identity(self) -> dict[str, Any]:
+        identity = {
+            "quant": self.format,
+            "quant_schema": self.schema,
+            "quant_targets": list(self.targets),
+            "quant_row_parallel": list(self.row_parallel),
+            "quant_tp_degree": int(self.tp_degree),
+        }
+        if self.split_linears:
+            identity["quant_split_linears"] = list(self.split_linears)
+        return identity
+
+
+_BLOCK = r"transformer_blocks\.\d+"
+_SINGLE = r"single_transformer_blocks\.\d+"
+
+#: Every linear of the FLUX blocks but the adaLN ones (the "every block linear" fp8 step);
+#: diffusers' names, the single blocks' proj_out as the one fused [attn | mlp] linear.
+FLUX_ALL_BLOCK_LINEARS: tuple[str, ...] = (
+    rf"{_BLOCK}\.attn\.(to_q|to_k|to_v|add_q_proj|add_k_proj|add_v_proj|to_out\.0|to_add_out)",
+    rf"{_BLOCK}\.(ff|ff_context)\.net\.(0\.proj|2)",
+    rf"{_SINGLE}\.attn\.(to_q|to_k|to_v)",
+    rf"{_SINGLE}\.(proj_mlp|proj_out)",
+)
+
+#: difflet/quant/targets.py:117-121 (QWEN_IMAGE_TARGETS): q/k/v, the added q/k/v and both MLPs;
+#: the output projections stay bf16.
+QWEN_IMAGE_TARGETS: tuple[str, ...] = (
+    rf"{_BLOCK}\.attn\.(to_q|to_k|to_v|add_q_proj|add_k_proj|add_v_proj)",
+    rf"{_BLOCK}\.(img_mlp|txt_mlp)\.net\.0\.proj",
+    rf"{_BLOCK}\.(img_mlp|txt_mlp)\.net\.2",
+)
