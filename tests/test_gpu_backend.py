@@ -110,9 +110,9 @@ def test_quantized_linear_twins(gpu, fmt):
     g = torch.Generator().manual_seed(2)
     k, n = 384, 256
     m = torch.nn.Module()
-    m.to_q = L.ColumnParallelLinear(k, n, bias=True, dtype=torch.bfloat16)
-    m.to_k = L.ColumnParallelLinear(k, n, bias=True, dtype=torch.bfloat16)
-    m.to_v = L.ColumnParallelLinear(k, n, bias=True, dtype=torch.bfloat16)
+    m.to_q = L.ColumnParallelLinear(k, n, bias=True, gather_output=False, dtype=torch.bfloat16)
+    m.to_k = L.ColumnParallelLinear(k, n, bias=True, gather_output=False, dtype=torch.bfloat16)
+    m.to_v = L.ColumnParallelLinear(k, n, bias=True, gather_output=False, dtype=torch.bfloat16)
     with torch.no_grad():
         for mod in (m.to_q, m.to_k, m.to_v):
             mod.weight.copy_(torch.randn(n, k, generator=g) * 0.05)
