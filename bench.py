@@ -1,6 +1,7 @@
 """Benchmark: one FLUX.1-dev-shaped 1024^2 denoise step on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--kinds bf16,fp8] [--no-cpu]
+                    [--calibrate-copy]
 
 Workload: the full FLUX transformer forward of one denoise step, batch 1, 4096 image tokens
 (64 x 64 patch grid) + 512 text tokens, 19 double + 38 single blocks, hidden 3072, 24 x 128
@@ -35,6 +36,7 @@ HBM_PEAK = 8.0e12
 IMG_HW = (64, 64)
 TXT = 512
 SEED = 0
+COPY_BYTES = 256 << 20
 
 
 def parse():
@@ -44,6 +46,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--kinds", default="bf16,fp8")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run a plain 256 MiB bf16 elementwise copy (torch.neg) three "
+                         "times, as the known-size reference for HBM byte counters")
     return ap.parse_args()
 
 
@@ -216,6 +221,13 @@ def main():
 
     _lib.load()
     kinds = [k for k in args.kinds.split(",") if k]
+    if args.calibrate_copy:
+        src = torch.randn(COPY_BYTES // 2, device="cuda").bfloat16()
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     res = {k: run_kind(k, args.steps, args.warmup, torch, log) for k in kinds}
 
     out = {}

@@ -2,12 +2,12 @@
 //
 // A [M, K] and W [N, K] are both K-contiguous (activations and nn.Linear weights as stored).
 // One kernel skeleton serves three element types:
-//   bf16  : v_mfma_f32_32x32x16_bf16, 64 K-elements (128 bytes) per K tile;
-//   fp8   : v_mfma_f32_32x32x64_f8f6f4 (e4m3), 128 K-elements per K tile, per-row scales of A
+//   bf16  : v_mfma_f32_32x32x16_bf16, 32 K-elements (64 bytes) per K stage;
+//   fp8   : v_mfma_f32_32x32x64_f8f6f4 (e4m3), 64 K-elements per K stage, per-row scales of A
 //           and W applied in the epilogue (acc * sa[m] * sw[n]);
 //   mxfp8 : v_mfma_scale_f32_32x32x64_f8f6f4 with one E8M0 scale per 32-element block of a
-//           row (the block split over the two lane groups, see the K loop), 128 K per K tile.
-// A K tile is therefore always 128 bytes per row, and the LDS geometry is shared.
+//           row (the block split over the two lane groups, see the K loop), 64 K per K stage.
+// A K stage is therefore always 64 bytes per row, and the LDS geometry is shared.
 //
 // Tiling: a 256-thread workgroup (4 wavefronts in a 2 x 2 grid) owns a 256 x 256 tile of C;
 // each wavefront owns 128 x 128 = 4 x 4 MFMA tiles of 32 x 32, 256 fp32 accumulators per lane.
@@ -15,10 +15,15 @@
 // row m = l % 32 and registers run along n in groups of 4 consecutive columns: the epilogue
 // reads bias / gate / residual and writes C in 8-byte pieces.
 //
-// LDS: two stages of (A tile + W tile) = 2 x 64 KB. A row of a K tile is 8 chunks of 16 bytes;
-// chunk c of row r lives at chunk c ^ (r & 7), so the 8 lanes an ds_read_b128 serves together
-// (8 consecutive rows, one chunk) hit 8 different bank groups. Global loads are raw buffer
-// loads: rows past M (or N) read as zero, so ragged edges need no branches.
+// LDS: a ring of 4 stages of (A tile + W tile) = 4 x 32 KB, filled by direct-to-LDS buffer
+// loads (no register round trip), 3 stages in flight. Rows are XOR-swizzled in 16-byte chunks
+// (swz below) so fragment reads are free of bank conflicts. Global loads are raw buffer loads:
+// rows past M (or N) read as zero, so ragged edges need no branches.
+//
+// K loop: one straight-line body per stage, one barrier per stage. Half 0 of the stage's MFMAs
+// runs while half 1's fragments are read; half 1 runs in four parts, each interleaving one A
+// tile's MFMAs with the next stage's fragment reads and a quarter of the loads three stages
+// ahead, so no part of the memory pipe sees a burst.
 //
 // Tile order: workgroup ids are spread round-robin over the 8 XCDs, each with its own L2. The id
 // is remapped so each XCD gets a contiguous run of tiles, and tiles run in groups of 8 tile rows
@@ -75,6 +80,24 @@ __device__ __forceinline__ void interleave() {
   }
 }
 
+// NM MFMAs with ND LDS reads and NV vector-memory loads spread evenly among them.
+template <int NM, int ND, int NV, int R = 0>
+__device__ __forceinline__ void interleave3() {
+  if constexpr (R < NM) {
+    constexpr int d = (ND * (R + 1)) / NM - (ND * R) / NM;
+    constexpr int v = (NV * (R + 1)) / NM - (NV * R) / NM;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if constexpr (d > 0) __builtin_amdgcn_sched_group_barrier(0x100, d, 0);
+    if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x020, v, 0);
+    interleave3<NM, ND, NV, R + 1>();
+  }
+}
+
+// Workgroup barrier without the LDS drain __syncthreads implies. At each use the only LDS reads
+// still in flight are of the stage being computed, which no load of this iteration overwrites;
+// the memory clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 __device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
 __device__ __forceinline__ int lds_off(int row, int chunk) {
   return row * KT_BYTES + ((chunk ^ swz(row)) << 4);
@@ -90,7 +113,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_kernel(const GemmArgs args) 
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave-uniform, held in a scalar register: LDS-DMA destinations (M0) are then scalar math
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
   // ---- tile assignment: XCD-contiguous runs, then grouped raster
@@ -144,23 +168,27 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_kernel(const GemmArgs args) 
     rsa = make_rsrc((const uint8_t*)P.a_scale + m0 * ksb, (uint32_t)((M - m0) * ksb));
     rsw = make_rsrc((const uint8_t*)P.w_scale + n0 * ksb, (uint32_t)((N - n0) * ksb));
   }
-  auto issue_stage = [&](int kt, int st) {
+  // part i of a stage's loads: this wave's A slab i and W slab i (MX: the scale dwords of A
+  // with part 0, of W with part 1)
+  auto issue_part = [&](int kt, int st, int i) {
     const uint32_t kb = (uint32_t)kt * KT_BYTES;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          ra, (lds_void*)&smem[st][0][(wave * 4 + i) * 1024], 16, a_off[i], kb, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rw, (lds_void*)&smem[st][1][(wave * 4 + i) * 1024], 16, w_off[i], kb, 0, 0);
-    }
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        ra, (lds_void*)&smem[st][0][(wave * 4 + i) * 1024], 16, a_off[i], kb, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rw, (lds_void*)&smem[st][1][(wave * 4 + i) * 1024], 16, w_off[i], kb, 0, 0);
     if constexpr (E == Elem::MX) {
-      const uint32_t row = wave * 64 + lane;
-      const uint32_t so = (uint32_t)(kt & ~1) * 2;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)&smem_sc[st][0][wave * 64], 4,
-                                               row * ksb, so, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_void*)&smem_sc[st][1][wave * 64], 4,
-                                               row * ksb, so, 0, 0);
+      if (i < 2) {
+        const uint32_t row = wave * 64 + lane;
+        const uint32_t so = (uint32_t)(kt & ~1) * 2;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(i == 0 ? rsa : rsw,
+                                                 (lds_void*)&smem_sc[st][i][wave * 64], 4,
+                                                 row * ksb, so, 0, 0);
+      }
     }
+  };
+  auto issue_stage = [&](int kt, int st) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) issue_part(kt, st, i);
   };
   // vector-memory instructions one stage issues per wave (for s_waitcnt vmcnt)
   constexpr int LOADS_PER_STAGE = E == Elem::MX ? 10 : 8;
@@ -183,21 +211,21 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_kernel(const GemmArgs args) 
     i32x4 a[4][2], w[4][2];
     uint32_t sa[4], sw[4];  // MX: this lane's scale bytes for its A rows / W rows
   };
-  auto read_a = [&](int st, int kt, Frags& f) {
+  auto read_a_i = [&](int st, int kt, Frags& f, int i) {  // A fragment i of half 0
     const uint8_t* sA = smem[st][0];
-    const int h = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = wm * 128 + i * 32 + frow;
-      if constexpr (E == Elem::BF16) {
-        f.a[i][0] = *reinterpret_cast<const i32x4*>(sA + lds_off(r, h * 2 + fhalf));
-      } else {
-        f.a[i][0] = *reinterpret_cast<const i32x4*>(sA + lds_off(r, fhalf));
-        f.a[i][1] = *reinterpret_cast<const i32x4*>(sA + lds_off(r, 2 + fhalf));
-      }
-      if constexpr (E == Elem::MX)
-        f.sa[i] = (smem_sc[st][0][r] >> ((kt & 1) * 16 + fhalf * 8)) & 0xffu;
+    const int r = wm * 128 + i * 32 + frow;
+    if constexpr (E == Elem::BF16) {
+      f.a[i][0] = *reinterpret_cast<const i32x4*>(sA + lds_off(r, fhalf));
+    } else {
+      f.a[i][0] = *reinterpret_cast<const i32x4*>(sA + lds_off(r, fhalf));
+      f.a[i][1] = *reinterpret_cast<const i32x4*>(sA + lds_off(r, 2 + fhalf));
     }
+    if constexpr (E == Elem::MX)
+      f.sa[i] = (smem_sc[st][0][r] >> ((kt & 1) * 16 + fhalf * 8)) & 0xffu;
+  };
+  auto read_a = [&](int st, int kt, Frags& f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) read_a_i(st, kt, f, i);
   };
   auto read_a1 = [&](int st, Frags& f) {  // bf16: the A fragments of half 1
     const uint8_t* sA = smem[st][0];
@@ -205,58 +233,67 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_kernel(const GemmArgs args) 
     for (int i = 0; i < 4; ++i)
       f.a[i][0] = *reinterpret_cast<const i32x4*>(sA + lds_off(wm * 128 + i * 32 + frow, 2 + fhalf));
   };
-  auto read_w = [&](int st, int h, int kt, Frags& f) {
+  // W fragment j (bf16: K step h; fp8 / mx: tile j of the stage's one K step)
+  auto read_w_j = [&](int st, int h, int kt, Frags& f, int j) {
     const uint8_t* sW = smem[st][1];
+    const int r = wn * 128 + j * 32 + frow;
+    if constexpr (E == Elem::BF16) {
+      f.w[j][0] = *reinterpret_cast<const i32x4*>(sW + lds_off(r, h * 2 + fhalf));
+    } else {
+      f.w[j][0] = *reinterpret_cast<const i32x4*>(sW + lds_off(r, fhalf));
+      f.w[j][1] = *reinterpret_cast<const i32x4*>(sW + lds_off(r, 2 + fhalf));
+      if constexpr (E == Elem::MX)
+        f.sw[j] = (smem_sc[st][1][r] >> ((kt & 1) * 16 + fhalf * 8)) & 0xffu;
+    }
+  };
+  auto read_w = [&](int st, int h, int kt, Frags& f) {
     if constexpr (E == Elem::BF16) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        f.w[j][0] = *reinterpret_cast<const i32x4*>(sW + lds_off(wn * 128 + j * 32 + frow, h * 2 + fhalf));
+      for (int j = 0; j < 4; ++j) read_w_j(st, h, kt, f, j);
     } else {
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const int j = 2 * h + jj;
-        const int r = wn * 128 + j * 32 + frow;
-        f.w[j][0] = *reinterpret_cast<const i32x4*>(sW + lds_off(r, fhalf));
-        f.w[j][1] = *reinterpret_cast<const i32x4*>(sW + lds_off(r, 2 + fhalf));
-        if constexpr (E == Elem::MX)
-          f.sw[j] = (smem_sc[st][1][r] >> ((kt & 1) * 16 + fhalf * 8)) & 0xffu;
+      for (int jj = 0; jj < 2; ++jj) read_w_j(st, h, kt, f, 2 * h + jj);
+    }
+  };
+  auto mma_row = [&](const Frags& f, int h, int i) {  // the MFMAs of A tile i in half h
+#pragma unroll
+    for (int jj = 0; jj < (E == Elem::BF16 ? 4 : 2); ++jj) {
+      const int j = E == Elem::BF16 ? jj : 2 * h + jj;
+      if constexpr (E == Elem::BF16) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8, f.w[j][0]), __builtin_bit_cast(bf16x8, f.a[i][0]),
+            acc[i][j], 0, 0, 0);
+      } else {
+        const i32x8 fw = {f.w[j][0][0], f.w[j][0][1], f.w[j][0][2], f.w[j][0][3],
+                          f.w[j][1][0], f.w[j][1][1], f.w[j][1][2], f.w[j][1][3]};
+        const i32x8 fa = {f.a[i][0][0], f.a[i][0][1], f.a[i][0][2], f.a[i][0][3],
+                          f.a[i][1][0], f.a[i][1][1], f.a[i][1][2], f.a[i][1][3]};
+        if constexpr (E == Elem::FP8) {
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw, fa, acc[i][j], 0, 0,
+                                                                      0, 0, 0, 0);
+        } else {
+          // group g scales block g of the stage
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+              fw, fa, acc[i][j], 0, 0, 0, (int)f.sw[j], 0, (int)f.sa[i]);
+        }
       }
     }
   };
   auto mma_half = [&](const Frags& f, int h) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int jj = 0; jj < (E == Elem::BF16 ? 4 : 2); ++jj) {
-        const int j = E == Elem::BF16 ? jj : 2 * h + jj;
-        if constexpr (E == Elem::BF16) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              __builtin_bit_cast(bf16x8, f.w[j][0]), __builtin_bit_cast(bf16x8, f.a[i][0]),
-              acc[i][j], 0, 0, 0);
-        } else {
-          const i32x8 fw = {f.w[j][0][0], f.w[j][0][1], f.w[j][0][2], f.w[j][0][3],
-                            f.w[j][1][0], f.w[j][1][1], f.w[j][1][2], f.w[j][1][3]};
-          const i32x8 fa = {f.a[i][0][0], f.a[i][0][1], f.a[i][0][2], f.a[i][0][3],
-                            f.a[i][1][0], f.a[i][1][1], f.a[i][1][2], f.a[i][1][3]};
-          if constexpr (E == Elem::FP8) {
-            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw, fa, acc[i][j], 0, 0,
-                                                                        0, 0, 0, 0);
-          } else {
-            // group g scales block g of the stage
-            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                fw, fa, acc[i][j], 0, 0, 0, (int)f.sw[j], 0, (int)f.sa[i]);
-          }
-        }
-      }
+    for (int i = 0; i < 4; ++i) mma_row(f, h, i);
   };
 
   const int nkt = K / KT;
-  // prologue: stages 0 .. STAGES-2 in flight, then wait for stage 0
+  // prologue: stages 0 .. STAGES-2 in flight, then wait for stage 0. Past the last K stage the
+  // loads re-read the last stage (in bounds) into the free ring slot: every iteration then
+  // issues and waits alike, and the loop body is one straight-line block.
 #pragma unroll
-  for (int s0 = 0; s0 < STAGES - 1; ++s0)
-    if (s0 < nkt) issue_stage(s0, s0);
-  if (nkt > 2) __builtin_amdgcn_s_waitcnt(0x0f70 | (2 * LOADS_PER_STAGE & 15) | ((2 * LOADS_PER_STAGE >> 4) << 14));
-  else __builtin_amdgcn_s_waitcnt(0x0f70);
+  for (int s0 = 0; s0 < STAGES - 1; ++s0) issue_stage(min(s0, nkt - 1), s0);
+  {
+    constexpr int c = 2 * LOADS_PER_STAGE;
+    __builtin_amdgcn_s_waitcnt(0x0f70 | (c & 15) | ((c >> 4) << 14));
+  }
   __syncthreads();
   Frags f0, f1;
   read_a(0, 0, f0);
@@ -282,26 +319,27 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_kernel(const GemmArgs args) 
     }
     // stage kt + 1 must have landed (stage kt + 2 may still be in flight), then the barrier
     // publishes it to every wave and frees stage kt - 1 for stage kt + STAGES - 1
-    if (kt + 2 < nkt) {
+    {
       constexpr int c = LOADS_PER_STAGE;
       __builtin_amdgcn_s_waitcnt(0x0f70 | (c & 15) | ((c >> 4) << 14));
-    } else {
-      __builtin_amdgcn_s_waitcnt(0x0f70);
     }
-    __syncthreads();
-    if (kt + STAGES - 1 < nkt) issue_stage(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-    // half 1 of stage kt; meanwhile read half 0 of stage kt + 1
+    stage_barrier();
+    // half 1 of stage kt in four parts, each one A tile's MFMAs, that tile's fragments of
+    // stage kt + 1 (unused after the last stage) and a quarter of stage kt + 3's loads: the
+    // loads then trickle into the vector-memory pipe instead of arriving as one burst
     const int nst = (kt + 1) % STAGES;
-    if (kt + 1 < nkt) {
-      read_a(nst, kt + 1, f0);
-      read_w(nst, 0, kt + 1, f0);
-    }
-    mma_half(f1, 1);
-    if (kt + 1 < nkt) {
-      if constexpr (E == Elem::BF16) interleave<16, 8>();
-      else interleave<8, 8>();
+    const int lk = min(kt + STAGES - 1, nkt - 1), ls = (kt + STAGES - 1) % STAGES;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mma_row(f1, 1, i);
+      read_a_i(nst, kt + 1, f0, i);
+      if constexpr (E == Elem::BF16) read_w_j(nst, 0, kt + 1, f0, i);
+      else if (i < 2) read_w_j(nst, 0, kt + 1, f0, i);
+      issue_part(lk, ls, i);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // the trailing re-reads land before the workgroup ends
 
   // ---- epilogue: lane l holds row m = l % 32 of each MFMA tile; register 4 q + e of tile
   // (i, j) is column n = n0 + wn * 128 + j * 32 + q * 8 + 4 g + e (N % 4 == 0, so a run of 4

@@ -164,7 +164,7 @@ def _attn_case(g, b, h, sq, sk, d=128, dtype=torch.bfloat16):
 
 
 @pytest.mark.parametrize("b,h,sq,sk", [(1, 2, 128, 64), (1, 3, 200, 333), (2, 2, 77, 1000),
-                                       (1, 2, 4608, 4608)])
+                                       (1, 2, 4608, 4608), (1, 2, 3000, 512)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_attention_matches_fp32(gpu, b, h, sq, sk, dtype):
     print(f"attention b={b} h={h} sq={sq} sk={sk} {dtype}", flush=True)
