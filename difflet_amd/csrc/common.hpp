@@ -83,6 +83,29 @@ __device__ __forceinline__ uint32_t f32_to_e4m3fn(float x) {
   return sign | (r - (120u << 3));                   // rebias 127 -> 7
 }
 
+__device__ __forceinline__ float clamp448(float v) {
+  return __builtin_fminf(__builtin_fmaxf(v, -448.0f), 448.0f);
+}
+
+// The per-row fp8 law's row constants: a = max(amax, 2^-112) keeps 448 / a finite for all-zero
+// rows; scale = a / 448 and inv = 448 / a are IEEE fp32 divides.
+__device__ __forceinline__ float rowwise_inv(float amax) {
+  return __fdiv_rn(448.0f, __builtin_fmaxf(amax, 1.925929944387236e-34f));
+}
+__device__ __forceinline__ float rowwise_scale(float amax) {
+  return __fdiv_rn(__builtin_fmaxf(amax, 1.925929944387236e-34f), 448.0f);
+}
+// Eight codes e4m3(clamp(v * inv)), little-endian in two dwords.
+__device__ __forceinline__ u32x2 encode8_rowwise(const float* v, float inv) {
+  u32x2 o = {0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t code = f32_to_e4m3fn(clamp448(__fmul_rn(v[i], inv)));
+    o[i >> 2] |= code << (8 * (i & 3));
+  }
+  return o;
+}
+
 // ------------------------------------------------------------------ wave reductions
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -65,17 +65,12 @@ template <> struct V8<float> {
 };
 
 // ------------------------------------------------------------------ LayerNorm + modulation
-// NV = 16-byte vectors per lane; dim <= 64 * 8 * NV and dim % 8 == 0.
-template <typename TX, typename TY, typename TM, int NV>
-__global__ __launch_bounds__(256) void layernorm_modulate_kernel(
-    const TX* __restrict__ x, int64_t ldx, TY* __restrict__ y, int64_t ldy, int64_t rows,
-    int dim, const TM* __restrict__ mul, const TM* __restrict__ add, int64_t mod_stride,
-    int64_t rows_per_batch, int one_plus, float eps) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const TX* xr = x + row * ldx;
-  float v[NV][8];
+// NV = 16-byte vectors per lane; dim <= 64 * 8 * NV and dim % 8 == 0. One wavefront per row:
+// v[j] holds elements (lane + 64 j) * 8 .. + 8 of the row, replaced by the modulated output.
+template <typename TX, typename TM, int NV>
+__device__ __forceinline__ void ln_modulate_row(const TX* __restrict__ xr, int dim,
+                                                const TM* mb, const TM* ab, int one_plus,
+                                                float eps, int lane, float (&v)[NV][8]) {
   float s = 0.f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
@@ -100,15 +95,11 @@ __global__ __launch_bounds__(256) void layernorm_modulate_kernel(
     }
   }
   const float rstd = 1.0f / __builtin_sqrtf(wave_sum(q) / (float)dim + eps);
-  const int64_t b = row / rows_per_batch;
-  const TM* mb = mul ? mul + b * mod_stride : nullptr;
-  const TM* ab = add ? add + b * mod_stride : nullptr;
-  TY* yr = y + row * ldy;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = (lane + 64 * j) * 8;
     if (c < dim) {
-      float m8[8], a8[8], o[8];
+      float m8[8], a8[8];
       if (mb) {
         V8<TM>::load(mb + c, m8);
       } else {
@@ -124,10 +115,67 @@ __global__ __launch_bounds__(256) void layernorm_modulate_kernel(
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float mm = one_plus ? 1.0f + m8[i] : m8[i];
-        o[i] = (v[j][i] - mean) * rstd * mm + a8[i];
+        v[j][i] = (v[j][i] - mean) * rstd * mm + a8[i];
       }
-      V8<TY>::store(yr + c, o);
     }
+  }
+}
+
+template <typename TX, typename TY, typename TM, int NV>
+__global__ __launch_bounds__(256) void layernorm_modulate_kernel(
+    const TX* __restrict__ x, int64_t ldx, TY* __restrict__ y, int64_t ldy, int64_t rows,
+    int dim, const TM* __restrict__ mul, const TM* __restrict__ add, int64_t mod_stride,
+    int64_t rows_per_batch, int one_plus, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t b = row / rows_per_batch;
+  float v[NV][8];
+  ln_modulate_row<TX, TM, NV>(x + row * ldx, dim, mul ? mul + b * mod_stride : nullptr,
+                              add ? add + b * mod_stride : nullptr, one_plus, eps, lane, v);
+  TY* yr = y + row * ldy;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 8;
+    if (c < dim) V8<TY>::store(yr + c, v[j]);
+  }
+}
+
+// The same row, rounded to bf16, then quantized by the per-row fp8 law: the codes and scale
+// equal layernorm_modulate (bf16 out) followed by quantize_fp8_rowwise, without the round trip.
+template <typename TX, typename TM, int NV>
+__global__ __launch_bounds__(256) void layernorm_modulate_fp8_kernel(
+    const TX* __restrict__ x, int64_t ldx, uint8_t* __restrict__ q, int64_t ldq,
+    float* __restrict__ scale, int64_t rows, int dim, const TM* __restrict__ mul,
+    const TM* __restrict__ add, int64_t mod_stride, int64_t rows_per_batch, int one_plus,
+    float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t b = row / rows_per_batch;
+  float v[NV][8];
+  ln_modulate_row<TX, TM, NV>(x + row * ldx, dim, mul ? mul + b * mod_stride : nullptr,
+                              add ? add + b * mod_stride : nullptr, one_plus, eps, lane, v);
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 8;
+    if (c < dim) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        v[j][i] = bf16bits_to_f32(f32_to_bf16_bits(v[j][i]));
+        amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j][i]));
+      }
+    }
+  }
+  amax = wave_max(amax);
+  const float inv = rowwise_inv(amax);
+  if (lane == 0) scale[row] = rowwise_scale(amax);
+  uint8_t* qr = q + row * ldq;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 8;
+    if (c < dim) *reinterpret_cast<u32x2*>(qr + c) = encode8_rowwise(v[j], inv);
   }
 }
 
@@ -472,6 +520,54 @@ extern "C" int difflet_rocm_layernorm_modulate(const void* x, int64_t ldx, void*
       DLT_DISPATCH_FLOAT(mod_dtype, TM,
         return launch_ln<TX, TY, TM>(x, ldx, y, ldy, rows, dim, mul, add, mod_stride,
                                      rows_per_batch, one_plus, eps, s))));
+  return DIFFLET_OK;
+}
+
+template <typename TX, typename TM>
+static int launch_ln_fp8(const void* x, int64_t ldx, uint8_t* q, int64_t ldq, float* scale,
+                         int64_t rows, int64_t dim, const void* mul, const void* add,
+                         int64_t mod_stride, int64_t rpb, int one_plus, float eps,
+                         hipStream_t s) {
+  const int nv = (int)((dim + 511) / 512);
+  dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+#define DLT_LNQ(NV)                                                                     \
+  hipLaunchKernelGGL((layernorm_modulate_fp8_kernel<TX, TM, NV>), grid, block, 0, s,  \
+                     (const TX*)x, ldx, q, ldq, scale, rows, (int)dim, (const TM*)mul,  \
+                     (const TM*)add, mod_stride, rpb, one_plus, eps)
+  if (nv <= 2) DLT_LNQ(2);
+  else if (nv <= 4) DLT_LNQ(4);
+  else if (nv <= 6) DLT_LNQ(6);
+  else if (nv <= 8) DLT_LNQ(8);
+  else if (nv <= 10) DLT_LNQ(10);
+  else if (nv <= 16) DLT_LNQ(16);
+  else { dlt_set_error("layernorm_modulate_fp8: dim %lld exceeds 8192", (long long)dim); return DIFFLET_EUNSUPPORTED; }
+#undef DLT_LNQ
+  return dlt_check_launch("layernorm_modulate_fp8");
+}
+
+extern "C" int difflet_rocm_layernorm_modulate_fp8(const void* x, int64_t ldx, uint8_t* q,
+                                                   int64_t ldq, float* scale, int dtype,
+                                                   int64_t rows, int64_t dim, const void* mul,
+                                                   const void* add, int mod_dtype,
+                                                   int64_t mod_stride, int64_t rows_per_batch,
+                                                   int one_plus, float eps,
+                                                   difflet_stream_t stream) {
+  DLT_REQUIRE(x && q && scale, DIFFLET_EINVAL, "layernorm_modulate_fp8: null pointer");
+  DLT_REQUIRE(rows >= 0 && dim > 0 && dim % 8 == 0, DIFFLET_EINVAL,
+              "layernorm_modulate_fp8: dim %lld must be a positive multiple of 8",
+              (long long)dim);
+  DLT_REQUIRE(ldx % 8 == 0 && ldq % 8 == 0 && (mod_stride % 8 == 0 || (!mul && !add)),
+              DIFFLET_EINVAL, "layernorm_modulate_fp8: strides must be multiples of 8 elements");
+  DLT_REQUIRE(aligned16(x) && ((uintptr_t)q & 7) == 0 && (!mul || aligned16(mul)) &&
+                  (!add || aligned16(add)),
+              DIFFLET_EINVAL, "layernorm_modulate_fp8: misaligned pointers");
+  if (rows == 0) return DIFFLET_OK;
+  if (rows_per_batch <= 0) rows_per_batch = rows;
+  hipStream_t s = (hipStream_t)stream;
+  DLT_DISPATCH_FLOAT(dtype, TX,
+    DLT_DISPATCH_FLOAT(mod_dtype, TM,
+      return launch_ln_fp8<TX, TM>(x, ldx, q, ldq, scale, rows, dim, mul, add, mod_stride,
+                                   rows_per_batch, one_plus, eps, s)));
   return DIFFLET_OK;
 }
 

@@ -1,7 +1,8 @@
 // Activation / weight quantizers to fp8 e4m3fn, bit-exact with the CPU laws.
 //
-// Per-row (per-token activations, per-output-channel weights): one wavefront per row, a pass
-// for the absmax and a pass that writes codes (the second pass re-reads the row from L2).
+// Per-row (per-token activations, per-output-channel weights): 16-bit rows up to 16384 wide run
+// one workgroup per row holding the row in registers (one read of the row); wider or fp32 rows
+// run one wavefront per row in two passes (absmax, then codes).
 //
 // MXFP8 (difflet/quant/mx.py:46-108): one thread per 32-element block. A block is 32 consecutive
 // positions of the swizzle order; inside a K tile of width `tile` (512, or the remainder) with
@@ -42,8 +43,20 @@ template <> struct Load8<float> {
   }
 };
 
-__device__ __forceinline__ float clamp448(float v) {
-  return __builtin_fminf(__builtin_fmaxf(v, -448.0f), 448.0f);
+// Eight 16-bit values held in a 16-byte register vector, to fp32.
+template <typename T> __device__ __forceinline__ void decode8(u32x4 r, float* v);
+template <> __device__ __forceinline__ void decode8<bf16>(u32x4 r, float* v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = bf16bits_to_f32(r[i] & 0xffffu);
+    v[2 * i + 1] = bf16bits_to_f32(r[i] >> 16);
+  }
+}
+template <> __device__ __forceinline__ void decode8<f16>(u32x4 r, float* v) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  const h8 h = __builtin_bit_cast(h8, r);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (float)h[i];
 }
 
 // ------------------------------------------------------------------ per-row
@@ -65,21 +78,74 @@ __global__ __launch_bounds__(256) void quant_rowwise_kernel(const T* __restrict_
     for (int i = 0; i < 8; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
   }
   amax = wave_max(amax);
-  const float a = __builtin_fmaxf(amax, 1.925929944387236e-34f);  // 2^-112: 448 / a stays finite
-  const float inv = __fdiv_rn(448.0f, a);
-  if (lane == 0) scale[row] = __fdiv_rn(a, 448.0f);
+  const float inv = rowwise_inv(amax);
+  if (lane == 0) scale[row] = rowwise_scale(amax);
   uint8_t* qr = q + row * ldq;
   for (int64_t c = lane * 8; c < cols; c += 512) {
     float v[8];
     Load8<T>::f(xr + c, v);
-    u32x2 o = {0u, 0u};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t code = f32_to_e4m3fn(clamp448(__fmul_rn(v[i], inv)));
-      o[i >> 2] |= code << (8 * (i & 3));
-    }
-    *reinterpret_cast<u32x2*>(qr + c) = o;
+    *reinterpret_cast<u32x2*>(qr + c) = encode8_rowwise(v, inv);
   }
+}
+
+// Single pass for 16-bit rows up to 2048 NCH elements: one workgroup per row, each thread keeps
+// its NCH chunks of 8 as raw 16-byte vectors, so the row is read from memory once.
+template <typename T, int NCH>
+__global__ __launch_bounds__(256) void quant_rowwise_wg_kernel(const T* __restrict__ x,
+                                                               int64_t cols, int64_t ldx,
+                                                               uint8_t* __restrict__ q,
+                                                               int64_t ldq,
+                                                               float* __restrict__ scale) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const T* xr = x + row * ldx;
+  u32x4 raw[NCH];
+  float amax = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t col = ((int64_t)c * 256 + tid) * 8;
+    raw[c] = col < cols ? *reinterpret_cast<const u32x4*>(xr + col) : u32x4{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    float v[8];
+    decode8<T>(raw[c], v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
+  }
+  amax = block_max<4>(amax, red);
+  const float inv = rowwise_inv(amax);
+  if (tid == 0) scale[row] = rowwise_scale(amax);
+  uint8_t* qr = q + row * ldq;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t col = ((int64_t)c * 256 + tid) * 8;
+    if (col < cols) {
+      float v[8];
+      decode8<T>(raw[c], v);
+      *reinterpret_cast<u32x2*>(qr + col) = encode8_rowwise(v, inv);
+    }
+  }
+}
+
+template <typename T>
+static void launch_rowwise(const void* x, int64_t rows, int64_t cols, int64_t ldx, uint8_t* q,
+                           int64_t ldq, float* scale, hipStream_t s) {
+  const int64_t nch = (cols + 2047) / 2048;
+  const dim3 wg_grid((unsigned)rows), block(256);
+#define DLT_QWG(N)                                                                           \
+  hipLaunchKernelGGL((quant_rowwise_wg_kernel<T, N>), wg_grid, block, 0, s, (const T*)x, cols, \
+                     ldx, q, ldq, scale)
+  if (nch <= 1) DLT_QWG(1);
+  else if (nch <= 2) DLT_QWG(2);
+  else if (nch <= 4) DLT_QWG(4);
+  else if (nch <= 6) DLT_QWG(6);
+  else if (nch <= 8) DLT_QWG(8);
+  else
+    hipLaunchKernelGGL((quant_rowwise_kernel<T>), dim3((unsigned)((rows + 3) / 4)), block, 0, s,
+                       (const T*)x, rows, cols, ldx, q, ldq, scale);
+#undef DLT_QWG
 }
 
 // ------------------------------------------------------------------ MXFP8
@@ -169,12 +235,10 @@ extern "C" int difflet_rocm_quantize_fp8_rowwise(const void* x, int dtype, int64
   dim3 grid((unsigned)((rows + 3) / 4)), block(256);
   switch (dtype) {
     case DIFFLET_BF16:
-      hipLaunchKernelGGL((quant_rowwise_kernel<bf16>), grid, block, 0, s, (const bf16*)x, rows,
-                         cols, ldx, q, ldq, scale);
+      launch_rowwise<bf16>(x, rows, cols, ldx, q, ldq, scale, s);
       break;
     case DIFFLET_F16:
-      hipLaunchKernelGGL((quant_rowwise_kernel<f16>), grid, block, 0, s, (const f16*)x, rows,
-                         cols, ldx, q, ldq, scale);
+      launch_rowwise<f16>(x, rows, cols, ldx, q, ldq, scale, s);
       break;
     case DIFFLET_F32:
       hipLaunchKernelGGL((quant_rowwise_kernel<float>), grid, block, 0, s, (const float*)x,

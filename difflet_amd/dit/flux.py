@@ -150,6 +150,9 @@ class FluxDiT:
             self._bufs = {key: {"h": e(s, d), "n": e(s, d), "qkv": e(s, 3 * d),
                                 "big": e(s, 7 * d), "ff": e(s, self.cfg.mlp),
                                 "mod": e(1, self.mod_w.shape[0])}}
+            if self.kind == "fp8":  # LayerNorm output straight to per-token e4m3 + scales
+                self._bufs[key]["nq"] = torch.empty((s, d), dtype=torch.float8_e4m3fn, device=dev)
+                self._bufs[key]["ns"] = torch.empty((s,), dtype=torch.float32, device=dev)
         return self._bufs[key]
 
     def rope_tables(self, st: int, img_hw: tuple[int, int]):
@@ -161,6 +164,17 @@ class FluxDiT:
     def _mods(self, mod: torch.Tensor, off: int, n: int):
         d = self.cfg.hidden
         return [mod[:, off + j * d: off + (j + 1) * d] for j in range(n)]
+
+    def _ln(self, bufs, rows: slice, sc, sh):
+        """adaLN of h[rows] into the next GEMM's A operand: bf16 into n, or (fp8 step) per-token
+        e4m3 codes and scales in one pass. Returns the `prepared` operand (None for bf16)."""
+        h = bufs["h"]
+        if self.kind == "fp8":
+            nq, ns = bufs["nq"][rows], bufs["ns"][rows]
+            kernels.layernorm_modulate_fp8(h[rows], sc, sh, eps=EPS, out=(nq, ns))
+            return nq, ns
+        kernels.layernorm_modulate(h[rows], sc, sh, eps=EPS, out=bufs["n"][rows])
+        return None
 
     def _qk(self, buf, rows: slice, q_off: int, k_off: int, wq, wk, cos, sin):
         c = self.cfg
@@ -192,10 +206,9 @@ class FluxDiT:
         T, I = slice(0, st), slice(st, s)
         x_sh, x_sc, x_g, x_sh2, x_sc2, x_g2 = self._mods(mod, self.mod_off[("d", i, "norm1")], 6)
         c_sh, c_sc, c_g, c_sh2, c_sc2, c_g2 = self._mods(mod, self.mod_off[("d", i, "norm1_context")], 6)
-        kernels.layernorm_modulate(h[T], c_sc, c_sh, eps=EPS, out=n[T])
-        kernels.layernorm_modulate(h[I], x_sc, x_sh, eps=EPS, out=n[I])
-        self._gemm("gemm.double.qkv", [blk.qkv_txt.problem(n[T], qkv[T]),
-                                       blk.qkv_img.problem(n[I], qkv[I])])
+        pt, pi = self._ln(bufs, T, c_sc, c_sh), self._ln(bufs, I, x_sc, x_sh)
+        self._gemm("gemm.double.qkv", [blk.qkv_txt.problem(n[T], qkv[T], prepared=pt),
+                                       blk.qkv_img.problem(n[I], qkv[I], prepared=pi)])
         self._qk(qkv, T, 0, d, blk.naq, blk.nak, cos, sin)
         self._qk(qkv, I, 0, d, blk.nq, blk.nk, cos, sin)
         self._attn(qkv, 0, d, 2 * d)
@@ -203,10 +216,10 @@ class FluxDiT:
         self._gemm("gemm.double.out", [blk.out_txt.problem(o[T], h[T], gate=c_g, residual=h[T]),
                                        blk.out_img.problem(o[I], h[I], gate=x_g, residual=h[I])],
                    _lib.EPI_GATE_RESIDUAL)
-        kernels.layernorm_modulate(h[T], c_sc2, c_sh2, eps=EPS, out=n[T])
-        kernels.layernorm_modulate(h[I], x_sc2, x_sh2, eps=EPS, out=n[I])
-        self._gemm("gemm.double.ff1", [blk.ff1_txt.problem(n[T], ff[T]),
-                                       blk.ff1_img.problem(n[I], ff[I])], _lib.EPI_GELU)
+        pt, pi = self._ln(bufs, T, c_sc2, c_sh2), self._ln(bufs, I, x_sc2, x_sh2)
+        self._gemm("gemm.double.ff1", [blk.ff1_txt.problem(n[T], ff[T], prepared=pt),
+                                       blk.ff1_img.problem(n[I], ff[I], prepared=pi)],
+                   _lib.EPI_GELU)
         self._gemm("gemm.double.ff2", [blk.ff2_txt.problem(ff[T], h[T], gate=c_g2, residual=h[T]),
                                        blk.ff2_img.problem(ff[I], h[I], gate=x_g2, residual=h[I])],
                    _lib.EPI_GATE_RESIDUAL)
@@ -219,8 +232,8 @@ class FluxDiT:
         d = self.cfg.hidden
         h, n, big = bufs["h"], bufs["n"], bufs["big"]
         sh, sc, g = self._mods(mod, self.mod_off[("s", i)], 3)
-        kernels.layernorm_modulate(h, sc, sh, eps=EPS, out=n)
-        self._gemm("gemm.single.w1", [blk.w1.problem(n, big)], _lib.EPI_GELU, 3 * d)
+        p = self._ln(bufs, slice(0, h.shape[0]), sc, sh)
+        self._gemm("gemm.single.w1", [blk.w1.problem(n, big, prepared=p)], _lib.EPI_GELU, 3 * d)
         self._qk(big, slice(0, h.shape[0]), 2 * d, 0, blk.nq, blk.nk, cos, sin)
         self._attn(big, 2 * d, 0, d)
         self._gemm("gemm.single.w2", [blk.w2.problem(big[:, 2 * d:], h, gate=g, residual=h)],

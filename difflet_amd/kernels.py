@@ -258,28 +258,60 @@ def layernorm_modulate(x: torch.Tensor, mul: torch.Tensor | None, add: torch.Ten
     rows, dim = x2.shape
     out_dtype = out_dtype or x.dtype
     y = out if out is not None else torch.empty((rows, dim), dtype=out_dtype, device=dev)
-    mod = mul if mul is not None else add
-    mod_dt, mod_stride = _lib.F32, 0
-    if mod is not None:
-        if mul is not None and add is not None and mul.dtype != add.dtype:
-            add = add.to(mul.dtype)
-        mul2 = mul.reshape(-1, dim) if mul is not None else None
-        add2 = add.reshape(-1, dim) if add is not None else None
-        for t in (mul2, add2):
-            if t is not None and t.stride(-1) != 1:
-                raise ValueError("modulation vectors must have contiguous rows")
-        ref = mul2 if mul2 is not None else add2
-        if mul2 is not None and add2 is not None and mul2.stride(0) != add2.stride(0):
-            add2 = add2.contiguous()
-            mul2 = mul2.contiguous()
-        mod_dt, mod_stride = _dt(ref), ref.stride(0) if ref.shape[0] > 1 else 0
-        mul, add = mul2, add2
+    mul, add, mod_dt, mod_stride = _mod_vectors(mul, add, dim)
     rpb = rows_per_batch or rows
     check(lib().difflet_rocm_layernorm_modulate(
         _ptr(x2), x2.stride(0), _ptr(y), y.stride(0), _dt(x2), _dt(y), rows, dim, _ptr(mul),
         _ptr(add), mod_dt, mod_stride, rpb, int(one_plus), float(eps), _stream(dev)),
         "layernorm_modulate")
     return y.reshape(*x.shape[:-1], dim) if out is None else y
+
+
+def _mod_vectors(mul, add, dim):
+    """Modulation vectors as [batches, dim] rows sharing one batch stride, and their dtype."""
+    mod = mul if mul is not None else add
+    if mod is None:
+        return None, None, _lib.F32, 0
+    if mul is not None and add is not None and mul.dtype != add.dtype:
+        add = add.to(mul.dtype)
+    mul2 = mul.reshape(-1, dim) if mul is not None else None
+    add2 = add.reshape(-1, dim) if add is not None else None
+    for t in (mul2, add2):
+        if t is not None and t.stride(-1) != 1:
+            raise ValueError("modulation vectors must have contiguous rows")
+    if mul2 is not None and add2 is not None and mul2.stride(0) != add2.stride(0):
+        add2 = add2.contiguous()
+        mul2 = mul2.contiguous()
+    ref = mul2 if mul2 is not None else add2
+    return mul2, add2, _dt(ref), (ref.stride(0) if ref.shape[0] > 1 else 0)
+
+
+def layernorm_modulate_fp8(x: torch.Tensor, mul: torch.Tensor | None,
+                           add: torch.Tensor | None, *, eps: float, one_plus: bool = True,
+                           rows_per_batch: int | None = None,
+                           out: tuple[torch.Tensor, torch.Tensor] | None = None):
+    """layernorm_modulate rounded to bf16 and quantized per row to e4m3 in one pass:
+    (codes float8_e4m3fn [rows, dim], scales fp32 [rows]), equal to quantize_fp8_rowwise of the
+    bf16 layernorm_modulate output."""
+    dev = _on_gpu(x)
+    x2 = _rows2d(x, "layernorm_modulate_fp8")
+    rows, dim = x2.shape
+    if out is None:
+        q = torch.empty((rows, dim), dtype=torch.float8_e4m3fn, device=dev)
+        sc = torch.empty((rows,), dtype=torch.float32, device=dev)
+    else:
+        q, sc = out
+        if q.element_size() != 1 or sc.dtype != torch.float32 or q.shape[0] != rows or \
+                q.shape[-1] < dim or sc.numel() < rows or not sc.is_contiguous():
+            raise ValueError("layernorm_modulate_fp8: out must be (8-bit [rows, >=dim], "
+                             "contiguous fp32 [rows])")
+    mul, add, mod_dt, mod_stride = _mod_vectors(mul, add, dim)
+    rpb = rows_per_batch or rows
+    check(lib().difflet_rocm_layernorm_modulate_fp8(
+        _ptr(x2), x2.stride(0), _ptr(q), q.stride(0), _ptr(sc), _dt(x2), rows, dim, _ptr(mul),
+        _ptr(add), mod_dt, mod_stride, rpb, int(one_plus), float(eps), _stream(dev)),
+        "layernorm_modulate_fp8")
+    return q, sc
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float) -> torch.Tensor:

@@ -161,6 +161,17 @@ int difflet_rocm_layernorm_modulate(const void* x, int64_t ldx, void* y, int64_t
                                     int64_t mod_stride, int64_t rows_per_batch, int one_plus,
                                     float eps, difflet_stream_t stream);
 
+/* difflet_rocm_layernorm_modulate with bf16 output followed by difflet_rocm_quantize_fp8_rowwise,
+ * in one pass and bit-identical with that pair: the modulated row is rounded to bf16, then
+ * q[row] = e4m3(clamp(y * 448 / a)), scale[row] = a / 448, a = max(max|y|, 2^-112). It feeds
+ * the per-token fp8 linears that follow an adaLN (the q/k/v and MLP-in projections of
+ * difflet/models/flux/modeling_flux.py:840-866; the per-row fp8 format is this library's). */
+int difflet_rocm_layernorm_modulate_fp8(const void* x, int64_t ldx, uint8_t* q, int64_t ldq,
+                                        float* scale, int dtype, int64_t rows, int64_t dim,
+                                        const void* mul, const void* add, int mod_dtype,
+                                        int64_t mod_stride, int64_t rows_per_batch,
+                                        int one_plus, float eps, difflet_stream_t stream);
+
 /* RMSNorm with fp32 statistics, normalisation and affine and one cast back to dtype: the
  * law of rms_norm_fp32 (difflet/backends/_torch_megatron/norm.py:35-45) and of the CUDA
  * backend's RMSNorm (difflet/backends/cuda/ops_impl/norm.py:24-44). weight may be NULL. */

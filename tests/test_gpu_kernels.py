@@ -100,15 +100,43 @@ def test_gemm_rejects_bad_shapes(gpu):
 
 
 # ------------------------------------------------------------------------------ quantizers
-@pytest.mark.parametrize("rows,cols", [(7, 64), (300, 3072), (33, 15360)])
-def test_quantize_fp8_rowwise_bit_exact(gpu, rows, cols):
+# widths cover every register-resident path (one chunk of 2048 per thread up to 8) and the
+# two-pass path beyond 16384 columns; fp32 rows always take the two-pass path
+@pytest.mark.parametrize("rows,cols,dtype", [(7, 64, torch.bfloat16), (300, 3072, torch.bfloat16),
+                                             (33, 15360, torch.bfloat16),
+                                             (20, 12288, torch.float16),
+                                             (9, 16384, torch.bfloat16),
+                                             (5, 16400, torch.bfloat16),
+                                             (6, 3000, torch.float32)])
+def test_quantize_fp8_rowwise_bit_exact(gpu, rows, cols, dtype):
+    print(f"quantize_fp8_rowwise rows={rows} cols={cols} {dtype}", flush=True)
     g = torch.Generator().manual_seed(rows + cols)
-    x = rnd(g, rows, cols) * torch.exp(torch.randn(rows, 1, generator=g) * 3).bfloat16()
+    x = (rnd(g, rows, cols) * torch.exp(torch.randn(rows, 1, generator=g) * 3).bfloat16()).to(dtype)
     x[0] = 0  # an all-zero row
     q, s = kernels.quantize_fp8_rowwise(x.to(gpu))
     q_ref, s_ref = ofp8.quantize_rowwise(x.float().numpy())
     assert np.array_equal(q.view(torch.uint8).cpu().numpy(), q_ref)
     assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,dim", [(5, 64), (512, 3072), (77, 5120)])
+def test_layernorm_modulate_fp8_equals_layernorm_then_quantize(gpu, rows, dim):
+    g = torch.Generator().manual_seed(rows * 3 + dim)
+    x = rnd(g, rows, dim, std=2.0) + 0.5
+    x[1] = 0.25  # a constant row: LN output is the shift alone
+    sc, sh = rnd(g, 1, dim, std=0.3), rnd(g, 1, dim, std=0.3)
+    q, s = kernels.layernorm_modulate_fp8(x.to(gpu), sc.to(gpu), sh.to(gpu), eps=1e-6)
+    y = kernels.layernorm_modulate(x.to(gpu), sc.to(gpu), sh.to(gpu), eps=1e-6)
+    q2, s2 = kernels.quantize_fp8_rowwise(y)
+    assert q.dtype == q2.dtype == torch.float8_e4m3fn
+    assert torch.equal(q.view(torch.uint8), q2.view(torch.uint8)) and torch.equal(s, s2)
+    # and the per-row law of the oracle applied to the bf16 LayerNorm output
+    q_ref, s_ref = ofp8.quantize_rowwise(y.float().cpu().numpy())
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    # the bf16 LayerNorm output itself against the fp32 closed form
+    ref = ops.ada_modulate(x.float()[None], sh.float(), sc.float())[0]
+    assert rel_l2(y, ref) < 4e-3
 
 
 @pytest.mark.parametrize("cols", [128, 384, 512, 896, 3072, 3456, 13824])
