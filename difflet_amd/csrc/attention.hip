@@ -18,8 +18,9 @@
 // LDS: K tile row-major [64 keys][128 dims] with a 272-byte row pitch (256 + 16): the K fragment
 // reads of 8 or 16 lanes (consecutive keys, one 16-byte chunk) land in distinct bank groups, and
 // every fragment address is the lane's base plus an immediate. V tile stored transposed
-// [128 dims][64 keys] with a 136-byte row pitch, so the V^T fragment reads of 16 lanes (16 dims,
-// one key offset) cover all banks. Both are written from registers (V transposed in the
+// [128 dims][64 keys] with a 144-byte row pitch and the key quads of each 16-key group in the
+// order 0, 2, 1, 3 (vt_quad_pos): a lane's 8 keys of an MFMA step are one 16-byte read, and the
+// reads of 16 lanes (16 dims) cover all banks. Both are written from registers (V transposed in the
 // write), one barrier per K/V tile.
 //
 // VALU budget: the softmax costs about as many instruction cycles as the MFMAs, so the fast
@@ -38,7 +39,7 @@ namespace dlt {
 constexpr int HD = 128;
 constexpr int BLOCK_M = 128;
 constexpr int BLOCK_N = 64;
-constexpr int VT_PITCH = BLOCK_N * 2 + 8;  // bytes per V^T row
+constexpr int VT_PITCH = BLOCK_N * 2 + 16;  // bytes per V^T row
 constexpr int K_PITCH = HD * 2 + 16;         // bytes per K row
 constexpr float LOG2E = 1.4426950408889634f;
 
@@ -86,6 +87,14 @@ template <> struct MfmaT<f16> {
 
 __device__ __forceinline__ int k_off(int row, int chunk) { return row * K_PITCH + (chunk << 4); }
 
+// Position of key quad q (keys 4q .. 4q + 3 of a tile) in a V^T row: inside each 16-key group the
+// middle quads swap, so the 8 keys a lane group feeds one 16-key MFMA step, {4g .. 4g + 3,
+// 8 + 4g .. 8 + 4g + 3}, sit side by side and load as one 16-byte read.
+__device__ __forceinline__ int vt_quad_pos(int q) {
+  const int r = q & 3;
+  return (q & ~3) | (r == 1 ? 2 : r == 2 ? 1 : r);
+}
+
 template <typename T, bool MASKED>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
   typedef typename MfmaT<T>::frag frag;
@@ -130,6 +139,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
   // staging: K rows (t/16 + 16 i), chunk t % 16; V keys 4 (t % 16) + i, dims 8 (t / 16) .. +8
   const int kr = tid >> 4, kc = tid & 15;
   const int vkg = tid & 15, vdg = tid >> 4;
+  const int vt_pos = vt_quad_pos(vkg) * 8;  // byte offset of this thread's key quad in a V^T row
   u32x4 gk[4], gv[4];
   auto load_tile = [&](int j0) {
 #pragma unroll
@@ -153,7 +163,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
       u32x2 pk;
       pk[0] = k0 | (k1 << 16);
       pk[1] = k2 | (k3 << 16);
-      *reinterpret_cast<u32x2*>(&sv[st][(vdg * 8 + d) * VT_PITCH + vkg * 8]) = pk;
+      *reinterpret_cast<u32x2*>(&sv[st][(vdg * 8 + d) * VT_PITCH + vt_pos]) = pk;
     }
   };
 
@@ -270,11 +280,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
         const frag pf = __builtin_bit_cast(frag, pb);
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
-          const uint8_t* rowp = &sv[st][(dt * 32 + col) * VT_PITCH];
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(rowp + (base + g * 4) * 2);
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(rowp + (base + 8 + g * 4) * 2);
-          const u32x4 vv = {lo[0], lo[1], hi[0], hi[1]};
-          acc[dt] = MfmaT<T>::mma(__builtin_bit_cast(frag, vv), pf, acc[dt]);
+          const frag vf = *reinterpret_cast<const frag*>(
+              &sv[st][(dt * 32 + col) * VT_PITCH + (base + g * 8) * 2]);
+          acc[dt] = MfmaT<T>::mma(vf, pf, acc[dt]);
         }
       }
 
