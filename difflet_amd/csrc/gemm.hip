@@ -384,8 +384,10 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
         ws_v[j][q] = nok ? *reinterpret_cast<const f32x4*>(ws + n) : f32x4{};
       if constexpr (EPI == DIFFLET_EPI_GATE_RESIDUAL) {
         // one gate row per batch element: a wave's 128 rows lie in one batch element, since
-        // the host requires rows_per_batch % 128 == 0 when a problem holds several
-        const int64_t b0 = (m0 + wm * 128) / P.rows_per_batch;
+        // the host requires rows_per_batch % 128 == 0 when a problem holds several. A wave whose
+        // rows all lie past M stores nothing; its row is clamped to M - 1 so the gate read stays
+        // within the ceil(M / rows_per_batch) rows the gate holds.
+        const int64_t b0 = min(m0 + wm * 128, (int64_t)M - 1) / P.rows_per_batch;
         gate_v[j][q] = nok ? *reinterpret_cast<const u32x2*>(P.gate + b0 * P.gate_stride + n)
                            : u32x2{0u, 0u};
       }

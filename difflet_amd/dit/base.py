@@ -1,0 +1,113 @@
+"""Launch helpers shared by the fused DiT steps, and the joint (dual-stream) block they share.
+
+The FLUX double-stream block (difflet/models/flux/modeling_flux.py:796-867) and the Qwen-Image
+block (difflet/models/qwen_image/modeling_qwen.py:107-285) run the same sequence: per stream
+LayerNorm + modulation (shift, scale, gate twice), q/k/v projections, per-head q/k RMSNorm and
+RoPE, one joint attention over [text | image], output projections with gate * (x + bias) +
+residual, then per stream LayerNorm + modulation and a GELU-tanh MLP with the same gated
+residual. On the device each step is one launch for both streams (grouped GEMMs over the text
+and image row ranges of one [S, ...] buffer).
+
+Buffers (batch 1, S = S_txt + S_img, D = hidden, text rows first):
+  h [S, D] residual stream, n [S, D] modulated LayerNorm output, qkv [S, 3D], ff [S, mlp];
+  fp8 steps add nq [S, D] e4m3 codes and ns [S] scales written by the fused LayerNorm.
+"""
+
+from __future__ import annotations
+
+import contextlib
+import math
+
+import torch
+
+from difflet_amd import _lib, kernels
+from difflet_amd.dit.linear import run
+
+EPS = 1e-6
+_NULL = contextlib.nullcontext()
+
+
+class JointDiT:
+    """Mixin: needs self.cfg (hidden, heads, head_dim, mlp), self.kind, self.device and
+    self.probe (None, or probe(name) -> context manager timing one launch)."""
+
+    def _mods(self, mod: torch.Tensor, off: int, n: int):
+        d = self.cfg.hidden
+        return [mod[:, off + j * d: off + (j + 1) * d] for j in range(n)]
+
+    def _timed(self, name: str):
+        return self.probe(name) if self.probe is not None else _NULL
+
+    def _new_buffers(self, s: int, extra: dict | None = None) -> dict:
+        d, dev = self.cfg.hidden, self.device
+        e = lambda *shape: torch.empty(shape, dtype=torch.bfloat16, device=dev)  # noqa: E731
+        bufs = {"h": e(s, d), "n": e(s, d), "qkv": e(s, 3 * d), "ff": e(s, self.cfg.mlp)}
+        if self.kind == "fp8":  # LayerNorm output straight to per-token e4m3 + scales
+            bufs["nq"] = torch.empty((s, d), dtype=torch.float8_e4m3fn, device=dev)
+            bufs["ns"] = torch.empty((s,), dtype=torch.float32, device=dev)
+        for k, shape in (extra or {}).items():
+            bufs[k] = e(*shape)
+        return bufs
+
+    def _ln(self, bufs, rows: slice, sc, sh, fused: bool = True):
+        """adaLN of h[rows] into the next GEMM's A operand: bf16 into n, or (fp8 step) per-token
+        e4m3 codes and scales in one pass. Returns the `prepared` operand (None for bf16)."""
+        h = bufs["h"]
+        if fused and self.kind == "fp8":
+            nq, ns = bufs["nq"][rows], bufs["ns"][rows]
+            kernels.layernorm_modulate_fp8(h[rows], sc, sh, eps=EPS, out=(nq, ns))
+            return nq, ns
+        kernels.layernorm_modulate(h[rows], sc, sh, eps=EPS, out=bufs["n"][rows])
+        return None
+
+    def _qk(self, buf, rows: slice, q_off: int, k_off: int, wq, wk, cos, sin):
+        c = self.cfg
+        kernels.qk_norm_rope(buf[rows], heads=c.heads, head_dim=c.head_dim, q_off=q_off,
+                             k_off=k_off, wq=wq, wk=wk, eps=EPS, cos=cos[rows], sin=sin[rows],
+                             law=0)
+
+    def _attn(self, buf, q_off: int, k_off: int, v_off: int):
+        """Joint attention over all rows of `buf` [S, ld]; output written over q."""
+        c = self.cfg
+        s, ld = buf.shape
+        view = lambda off: buf.as_strided((1, c.heads, s, c.head_dim), (0, c.head_dim, ld, 1),  # noqa: E731
+                                          buf.storage_offset() + off)
+        q, k, v = view(q_off), view(k_off), view(v_off)
+        with self._timed("attn"):
+            kernels.attention(q, k, v, scale=1.0 / math.sqrt(c.head_dim), out=q)
+
+    def _gemm(self, name: str, problems, kind: str, epilogue: int = 0, act_col_start: int = 0):
+        """One grouped GEMM launch (activation quantization already done by problem())."""
+        with self._timed(name):
+            run(problems, kind, epilogue, act_col_start)
+
+    def joint_block(self, blk, bufs, st: int, img_mods, txt_mods, cos, sin, tag: str):
+        """One joint block over h (text rows [0, st), image rows [st, S)). blk holds the device
+        linears qkv_{txt,img} ([q|k|v] rows), out_{txt,img}, ff1_{txt,img}, ff2_{txt,img} and the
+        bf16 RMSNorm weights nq, nk (image) and naq, nak (text)."""
+        d = self.cfg.hidden
+        h, n, qkv, ff = bufs["h"], bufs["n"], bufs["qkv"], bufs["ff"]
+        s = h.shape[0]
+        T, I = slice(0, st), slice(st, s)
+        x_sh, x_sc, x_g, x_sh2, x_sc2, x_g2 = img_mods
+        c_sh, c_sc, c_g, c_sh2, c_sc2, c_g2 = txt_mods
+        fq = blk.qkv_img.kind == "fp8"
+        pt, pi = self._ln(bufs, T, c_sc, c_sh, fq), self._ln(bufs, I, x_sc, x_sh, fq)
+        self._gemm(f"gemm.{tag}.qkv", [blk.qkv_txt.problem(n[T], qkv[T], prepared=pt),
+                                       blk.qkv_img.problem(n[I], qkv[I], prepared=pi)],
+                   blk.qkv_img.kind)
+        self._qk(qkv, T, 0, d, blk.naq, blk.nak, cos, sin)
+        self._qk(qkv, I, 0, d, blk.nq, blk.nk, cos, sin)
+        self._attn(qkv, 0, d, 2 * d)
+        o = qkv[:, :d]
+        self._gemm(f"gemm.{tag}.out", [blk.out_txt.problem(o[T], h[T], gate=c_g, residual=h[T]),
+                                       blk.out_img.problem(o[I], h[I], gate=x_g, residual=h[I])],
+                   blk.out_img.kind, _lib.EPI_GATE_RESIDUAL)
+        fq = blk.ff1_img.kind == "fp8"
+        pt, pi = self._ln(bufs, T, c_sc2, c_sh2, fq), self._ln(bufs, I, x_sc2, x_sh2, fq)
+        self._gemm(f"gemm.{tag}.ff1", [blk.ff1_txt.problem(n[T], ff[T], prepared=pt),
+                                       blk.ff1_img.problem(n[I], ff[I], prepared=pi)],
+                   blk.ff1_img.kind, _lib.EPI_GELU)
+        self._gemm(f"gemm.{tag}.ff2", [blk.ff2_txt.problem(ff[T], h[T], gate=c_g2, residual=h[T]),
+                                       blk.ff2_img.problem(ff[I], h[I], gate=x_g2, residual=h[I])],
+                   blk.ff2_img.kind, _lib.EPI_GATE_RESIDUAL)

@@ -22,18 +22,14 @@ HBM layout, batch 1, S = S_txt + S_img tokens, D = hidden:
 
 from __future__ import annotations
 
-import contextlib
-import math
 from typing import Callable
 
 import torch
 
 from difflet_amd import _lib, kernels
-from difflet_amd.dit.linear import DeviceLinear, run
+from difflet_amd.dit.base import EPS, JointDiT
+from difflet_amd.dit.linear import DeviceLinear
 from difflet_amd.dit.rope import flux_rope_tables
-
-EPS = 1e-6
-_NULL = contextlib.nullcontext()
 
 
 class FluxConfig:
@@ -88,7 +84,7 @@ class _Single:
         self.nq, self.nk = bf(a + "norm_q.weight"), bf(a + "norm_k.weight")
 
 
-class FluxDiT:
+class FluxDiT(JointDiT):
     """The FLUX transformer on the HIP kernels. `get(name)` returns a parameter by its diffusers
     name (any dtype, on the target device); `kind` picks the block linears' format."""
 
@@ -145,14 +141,9 @@ class FluxDiT:
     def _buffers(self, st: int, si: int):
         key = (st, si)
         if key not in self._bufs:
-            s, d, dev = st + si, self.cfg.hidden, self.device
-            e = lambda *shape: torch.empty(shape, dtype=torch.bfloat16, device=dev)  # noqa: E731
-            self._bufs = {key: {"h": e(s, d), "n": e(s, d), "qkv": e(s, 3 * d),
-                                "big": e(s, 7 * d), "ff": e(s, self.cfg.mlp),
-                                "mod": e(1, self.mod_w.shape[0])}}
-            if self.kind == "fp8":  # LayerNorm output straight to per-token e4m3 + scales
-                self._bufs[key]["nq"] = torch.empty((s, d), dtype=torch.float8_e4m3fn, device=dev)
-                self._bufs[key]["ns"] = torch.empty((s,), dtype=torch.float32, device=dev)
+            s, d = st + si, self.cfg.hidden
+            self._bufs = {key: self._new_buffers(s, {"big": (s, 7 * d),
+                                                     "mod": (1, self.mod_w.shape[0])})}
         return self._bufs[key]
 
     def rope_tables(self, st: int, img_hw: tuple[int, int]):
@@ -161,71 +152,12 @@ class FluxDiT:
             self._rope = {key: flux_rope_tables(st, img_hw, self.cfg.axes, self.device)}
         return self._rope[key]
 
-    def _mods(self, mod: torch.Tensor, off: int, n: int):
-        d = self.cfg.hidden
-        return [mod[:, off + j * d: off + (j + 1) * d] for j in range(n)]
-
-    def _ln(self, bufs, rows: slice, sc, sh):
-        """adaLN of h[rows] into the next GEMM's A operand: bf16 into n, or (fp8 step) per-token
-        e4m3 codes and scales in one pass. Returns the `prepared` operand (None for bf16)."""
-        h = bufs["h"]
-        if self.kind == "fp8":
-            nq, ns = bufs["nq"][rows], bufs["ns"][rows]
-            kernels.layernorm_modulate_fp8(h[rows], sc, sh, eps=EPS, out=(nq, ns))
-            return nq, ns
-        kernels.layernorm_modulate(h[rows], sc, sh, eps=EPS, out=bufs["n"][rows])
-        return None
-
-    def _qk(self, buf, rows: slice, q_off: int, k_off: int, wq, wk, cos, sin):
-        c = self.cfg
-        kernels.qk_norm_rope(buf[rows], heads=c.heads, head_dim=c.head_dim, q_off=q_off,
-                             k_off=k_off, wq=wq, wk=wk, eps=EPS, cos=cos[rows], sin=sin[rows],
-                             law=0)
-
-    def _attn(self, buf, q_off: int, k_off: int, v_off: int):
-        """Joint attention over all rows of `buf` [S, ld]; output written over q."""
-        c = self.cfg
-        s, ld = buf.shape
-        view = lambda off: buf.as_strided((1, c.heads, s, c.head_dim), (0, c.head_dim, ld, 1),  # noqa: E731
-                                          buf.storage_offset() + off)
-        q, k, v = view(q_off), view(k_off), view(v_off)
-        with self._timed("attn"):
-            kernels.attention(q, k, v, scale=1.0 / math.sqrt(c.head_dim), out=q)
-
-    def _gemm(self, name: str, problems, epilogue: int = 0, act_col_start: int = 0):
-        """One grouped GEMM launch (activation quantization already done by problem())."""
-        with self._timed(name):
-            run(problems, self.kind, epilogue, act_col_start)
-
     # -------------------------------------------------------------------------- blocks
     def double_block(self, i: int, bufs, st: int, mod, cos, sin):
-        blk = self.double[i]
-        d = self.cfg.hidden
-        h, n, qkv, ff = bufs["h"], bufs["n"], bufs["qkv"], bufs["ff"]
-        s = h.shape[0]
-        T, I = slice(0, st), slice(st, s)
-        x_sh, x_sc, x_g, x_sh2, x_sc2, x_g2 = self._mods(mod, self.mod_off[("d", i, "norm1")], 6)
-        c_sh, c_sc, c_g, c_sh2, c_sc2, c_g2 = self._mods(mod, self.mod_off[("d", i, "norm1_context")], 6)
-        pt, pi = self._ln(bufs, T, c_sc, c_sh), self._ln(bufs, I, x_sc, x_sh)
-        self._gemm("gemm.double.qkv", [blk.qkv_txt.problem(n[T], qkv[T], prepared=pt),
-                                       blk.qkv_img.problem(n[I], qkv[I], prepared=pi)])
-        self._qk(qkv, T, 0, d, blk.naq, blk.nak, cos, sin)
-        self._qk(qkv, I, 0, d, blk.nq, blk.nk, cos, sin)
-        self._attn(qkv, 0, d, 2 * d)
-        o = qkv[:, :d]
-        self._gemm("gemm.double.out", [blk.out_txt.problem(o[T], h[T], gate=c_g, residual=h[T]),
-                                       blk.out_img.problem(o[I], h[I], gate=x_g, residual=h[I])],
-                   _lib.EPI_GATE_RESIDUAL)
-        pt, pi = self._ln(bufs, T, c_sc2, c_sh2), self._ln(bufs, I, x_sc2, x_sh2)
-        self._gemm("gemm.double.ff1", [blk.ff1_txt.problem(n[T], ff[T], prepared=pt),
-                                       blk.ff1_img.problem(n[I], ff[I], prepared=pi)],
-                   _lib.EPI_GELU)
-        self._gemm("gemm.double.ff2", [blk.ff2_txt.problem(ff[T], h[T], gate=c_g2, residual=h[T]),
-                                       blk.ff2_img.problem(ff[I], h[I], gate=x_g2, residual=h[I])],
-                   _lib.EPI_GATE_RESIDUAL)
-
-    def _timed(self, name: str):
-        return self.probe(name) if self.probe is not None else _NULL
+        self.joint_block(self.double[i], bufs, st,
+                         self._mods(mod, self.mod_off[("d", i, "norm1")], 6),
+                         self._mods(mod, self.mod_off[("d", i, "norm1_context")], 6),
+                         cos, sin, "double")
 
     def single_block(self, i: int, bufs, mod, cos, sin):
         blk = self.single[i]
@@ -233,11 +165,12 @@ class FluxDiT:
         h, n, big = bufs["h"], bufs["n"], bufs["big"]
         sh, sc, g = self._mods(mod, self.mod_off[("s", i)], 3)
         p = self._ln(bufs, slice(0, h.shape[0]), sc, sh)
-        self._gemm("gemm.single.w1", [blk.w1.problem(n, big, prepared=p)], _lib.EPI_GELU, 3 * d)
+        self._gemm("gemm.single.w1", [blk.w1.problem(n, big, prepared=p)], self.kind,
+                   _lib.EPI_GELU, 3 * d)
         self._qk(big, slice(0, h.shape[0]), 2 * d, 0, blk.nq, blk.nk, cos, sin)
         self._attn(big, 2 * d, 0, d)
         self._gemm("gemm.single.w2", [blk.w2.problem(big[:, 2 * d:], h, gate=g, residual=h)],
-                   _lib.EPI_GATE_RESIDUAL)
+                   self.kind, _lib.EPI_GATE_RESIDUAL)
 
     # -------------------------------------------------------------------------- step
     def embed(self, timestep, guidance, pooled):

@@ -4,6 +4,12 @@ the device as fp32 [S, head_dim] cos / sin (the kernels read them per row).
 FLUX: FluxPosEmbed (difflet/layers/embeddings.py:148-176) with get_1d_rotary_pos_embed
 (:178-244, float64 frequencies, repeat-interleaved) over ids (0, 0, 0) for text tokens and
 (0, i, j) for image patch (i, j), text first.
+
+Qwen-Image: the QwenEmbedRope table diffusers' QwenImageTransformer2DModel builds (the
+reference converts its complex form to this real one, difflet/models/qwen_image/
+modeling_qwen_image.py:46-49,643-651): axes (16, 56, 56), theta 10000, angles in fp32; with
+scale_rope the image height / width positions run -(n - n // 2) .. n // 2 - 1 (frame 0), and
+text token j takes position max(h // 2, w // 2) + j on all three axes; text first.
 """
 
 from __future__ import annotations
@@ -30,4 +36,32 @@ def flux_rope_tables(txt_len: int, img_hw: tuple[int, int], axes=(16, 56, 56),
     cos, sin = zip(*[_axis(d, ids[:, i], theta) for i, d in enumerate(axes)])
     cos = torch.cat(cos, dim=-1).to(torch.float32)
     sin = torch.cat(sin, dim=-1).to(torch.float32)
+    return cos.to(device).contiguous(), sin.to(device).contiguous()
+
+
+def _qwen_axis(pos: torch.Tensor, dim: int, theta: float) -> torch.Tensor:
+    inv = 1.0 / torch.pow(torch.tensor(float(theta)),
+                          torch.arange(0, dim, 2, dtype=torch.float32).div(dim))
+    return torch.outer(pos.to(torch.float32), inv)
+
+
+def _centred(n: int) -> torch.Tensor:
+    return torch.cat([torch.arange(-(n - n // 2), 0), torch.arange(0, n // 2)])
+
+
+def qwen_rope_tables(txt_len: int, img_hw: tuple[int, int], axes=(16, 56, 56),
+                     device="cuda", theta: float = 10000.0):
+    h, w = img_hw
+    a0, a1, a2 = axes
+    hh, ww = torch.meshgrid(_centred(h), _centred(w), indexing="ij")
+    img = torch.cat([_qwen_axis(torch.zeros(h * w), a0, theta),
+                     _qwen_axis(hh.reshape(-1), a1, theta),
+                     _qwen_axis(ww.reshape(-1), a2, theta)], dim=1)
+    start = max(h // 2, w // 2)
+    p = torch.arange(start, start + txt_len)
+    txt = torch.cat([_qwen_axis(p, a0, theta), _qwen_axis(p, a1, theta),
+                     _qwen_axis(p, a2, theta)], dim=1)
+    ang = torch.cat([txt, img], dim=0)
+    cos = torch.cos(ang).repeat_interleave(2, dim=-1)
+    sin = torch.sin(ang).repeat_interleave(2, dim=-1)
     return cos.to(device).contiguous(), sin.to(device).contiguous()

@@ -188,7 +188,7 @@ def gemm_grouped(problems: Sequence[Problem], *, kind: str = "bf16",
         q.bias = p.bias.data_ptr() if p.bias is not None else None
         if p.gate is not None:
             g = p.gate if p.gate.dim() == 2 else p.gate.reshape(1, -1)
-            q.gate, q.gate_stride = g.data_ptr(), g.stride(0)
+            q.gate, q.gate_stride = g.data_ptr(), (g.stride(0) if g.shape[0] > 1 else 0)
         if p.residual is not None:
             q.residual, q.ldr = p.residual.data_ptr(), p.residual.stride(0)
         q.a_scale = p.a_scale.data_ptr() if p.a_scale is not None else None

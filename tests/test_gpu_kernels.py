@@ -154,6 +154,36 @@ def test_quantize_mxfp8_bit_exact(gpu, cols, swizzled):
     assert np.array_equal(q.view(torch.uint8).cpu().numpy(), q_ref)
 
 
+@pytest.mark.parametrize("kind", ["bf16", "mx"])
+def test_gemm_gate_residual_short_problems_read_only_their_gate_row(gpu, kind):
+    """Problems of 64 and 255 rows (one batch each) whose gate is one row of a much wider
+    modulation buffer: every wave, including those whose rows lie past M, reads that row only."""
+    print(f"gemm gate/residual short problems {kind}", flush=True)
+    g = torch.Generator().manual_seed(77)
+    n, k = 512, 256
+    wide = rnd(g, 1, 40 * n, std=0.5)  # like the stacked adaLN vectors: gate = a [1, n] slice
+    w, b = rnd(g, n, k, std=0.05), rnd(g, n, std=0.1)
+    gate = wide.to(gpu)[:, 3 * n:4 * n]
+    probs, refs = [], []
+    for m in (64, 255):
+        a, res = rnd(g, m, k), rnd(g, m, n)
+        c = res.to(gpu).clone()
+        if kind == "mx":
+            aq, asc = kernels.quantize_mxfp8(a.to(gpu), swizzled=True)
+            wq, ws = kernels.quantize_mxfp8(w.to(gpu), swizzled=True)
+            wq_l, ws_l = omx.quantize_mx(w.float().numpy())
+            y = torch.from_numpy(omx.mx_linear(a.float().numpy(), wq_l, ws_l, b.float().numpy()))
+            probs.append(kernels.Problem(aq, wq, c, b.to(gpu), gate, c, a_scale=asc, w_scale=ws))
+        else:
+            y = a.float() @ w.float().T + b.float()
+            probs.append(kernels.Problem(a.to(gpu), w.to(gpu), c, b.to(gpu), gate, c))
+        refs.append((c, res.float() + gate.float().cpu() * y))
+    kernels.gemm_grouped(probs, kind=kind, epilogue=_lib.EPI_GATE_RESIDUAL)
+    torch.cuda.synchronize()
+    for c, ref in refs:
+        assert rel_l2(c, ref) < 4e-3
+
+
 @pytest.mark.parametrize("m,n,k", [(256, 256, 128), (300, 520, 384), (4608, 3072, 3072)])
 def test_gemm_fp8_rowwise_matches_oracle(gpu, m, n, k):
     print(f"gemm_fp8 m={m} n={n} k={k}", flush=True)

@@ -1,0 +1,91 @@
+"""Qwen-Image joint blocks and a reduced-depth Qwen-Image step on the HIP path against the fp32
+oracle (bf16: rel L2 <= 1e-2; MXFP8 targets: the same-law and format-error checks the FLUX
+tests explain)."""
+
+import pytest
+import torch
+
+from difflet_amd import kernels
+from difflet_amd.dit.qwen import QwenConfig, QwenImageDiT
+from oracle import qwen as oqwen
+
+pytestmark = pytest.mark.gpu
+
+SEED = 4321
+FORMAT_ERR = 6e-2
+
+
+def rel_l2(a, b):
+    a, b = a.detach().float().cpu(), b.detach().float().cpu()
+    return ((a - b).norm() / b.norm()).item()
+
+
+def _source(shape, n_blocks, seed=SEED):
+    w = dict(oqwen.embed_weights(shape, seed))
+    for i in range(n_blocks):
+        for k, v in oqwen.block_weights(shape, seed, i).items():
+            w[f"transformer_blocks.{i}.{k}"] = v
+    return w
+
+
+@pytest.mark.parametrize("kind,tol", [("bf16", 1e-2), ("mx", 4e-2)])
+def test_qwen_block_matches_fp32_oracle(gpu, kind, tol):
+    print(f"qwen block {kind}", flush=True)
+    st, img_hw = (256, (32, 32)) if kind == "bf16" else (128, (16, 16))
+    shape = oqwen.QwenShape(n_blocks=1)
+    w = _source(shape, 1)
+    dit = QwenImageDiT(QwenConfig(n_blocks=1), lambda n: w[n], kind=kind, device=gpu)
+    g = torch.Generator().manual_seed(SEED)
+    si = img_hw[0] * img_hw[1]
+    hidden = torch.randn(1, si, shape.hidden, generator=g).bfloat16().float()
+    context = torch.randn(1, st, shape.hidden, generator=g).bfloat16().float()
+    temb = torch.randn(1, shape.hidden, generator=g).bfloat16().float()
+    cos, sin = oqwen.pos_embed(img_hw[0], img_hw[1], st)
+    bw = {k[len("transformer_blocks.0."):]: v for k, v in w.items()
+          if k.startswith("transformer_blocks.0.")}
+    quant = "mx" if kind == "mx" else None
+    ref_c, ref_h = oqwen.block(bw, hidden, context, temb, cos, sin, shape, quant=quant,
+                               act_dtype=torch.bfloat16 if quant else None)
+    bufs = dit._buffers(st, si)
+    bufs["h"][:st] = context[0].to(gpu, torch.bfloat16)
+    bufs["h"][st:] = hidden[0].to(gpu, torch.bfloat16)
+    mod = kernels.gemv(temb.to(gpu, torch.bfloat16), dit.mod_w, dit.mod_b, act=1)
+    gcos, gsin = dit.rope_tables(st, img_hw)
+    dit.block(0, bufs, st, mod, gcos, gsin)
+    torch.cuda.synchronize()
+    e_c, e_h = rel_l2(bufs["h"][:st], ref_c[0]), rel_l2(bufs["h"][st:], ref_h[0])
+    print(f"rel L2 vs same-law oracle: text {e_c:.3e} image {e_h:.3e}", flush=True)
+    if quant:
+        f_c, f_h = oqwen.block(bw, hidden, context, temb, cos, sin, shape)
+        q_c, q_h = rel_l2(bufs["h"][:st], f_c[0]), rel_l2(bufs["h"][st:], f_h[0])
+        o_c, o_h = rel_l2(ref_c, f_c), rel_l2(ref_h, f_h)
+        print(f"mx format error vs fp32: device {q_c:.3e} / {q_h:.3e}, oracle {o_c:.3e} / "
+              f"{o_h:.3e}", flush=True)
+        assert abs(q_c - o_c) < 0.1 * o_c and abs(q_h - o_h) < 0.1 * o_h
+        assert q_c < FORMAT_ERR and q_h < FORMAT_ERR
+    assert e_c < tol and e_h < tol
+
+
+@pytest.mark.parametrize("kind,tol", [("bf16", 1e-2), ("mx", 4e-2)])
+def test_qwen_reduced_depth_step_matches_fp32_oracle(gpu, kind, tol):
+    """img_in, txt_norm + txt_in, the timestep embedder, 2 joint blocks and norm_out / proj_out
+    at Qwen-Image width on an odd 15 x 17 patch grid (centred RoPE positions) + 64 text tokens."""
+    print(f"qwen reduced step {kind}", flush=True)
+    shape = oqwen.QwenShape(n_blocks=2)
+    w = _source(shape, 2)
+    img_hw, st = (15, 17), 64
+    inp = oqwen.synthetic_inputs(shape, SEED, img_hw, st)
+    lat, txt = inp["latents"].bfloat16().float(), inp["text"].bfloat16().float()
+    quant = "mx" if kind == "mx" else None
+    ref = oqwen.forward(shape, SEED, lat, txt, inp["timestep"], img_hw,
+                        weights=(oqwen.embed_weights(shape, SEED),
+                                 [oqwen.block_weights(shape, SEED, i) for i in range(2)]),
+                        model_dtype=torch.bfloat16, quant=quant,
+                        act_dtype=torch.bfloat16 if quant else None)
+    dit = QwenImageDiT(QwenConfig(n_blocks=2), lambda n: w[n], kind=kind, device=gpu)
+    out = dit.forward(lat.to(gpu), txt.to(gpu), inp["timestep"].to(gpu), img_hw)
+    torch.cuda.synchronize()
+    e = rel_l2(out, ref)
+    print(f"step rel L2 {e:.3e}", flush=True)
+    assert out.shape == (1, 255, 64)
+    assert e < tol
