@@ -1,42 +1,50 @@
-"""Benchmark: one FLUX.1-dev-shaped 1024^2 denoise step on one MI355X.
+"""Benchmark: one DiT denoise step on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--kinds bf16,fp8] [--no-cpu]
-                    [--calibrate-copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload flux|qwen]
+                    [--kinds bf16,fp8] [--no-cpu] [--calibrate-copy]
 
-Workload: the full FLUX transformer forward of one denoise step, batch 1, 4096 image tokens
-(64 x 64 patch grid) + 512 text tokens, 19 double + 38 single blocks, hidden 3072, 24 x 128
-heads, random-init N(0, 0.02) weights drawn on the device, latents / text / pooled N(0, 1),
-guidance 3.5. `value` is the bf16 step time; the fp8 step (every block linear per-channel e4m3
-with per-token activations) is reported beside it.
+flux (default): the full FLUX.1-dev-shaped transformer forward of one denoise step, batch 1,
+4096 image tokens (64 x 64 patch grid) + 512 text tokens, 19 double + 38 single blocks, hidden
+3072, 24 x 128 heads, guidance 3.5. `value` is the bf16 step time; the fp8 step (every block
+linear per-channel e4m3 with per-token activations) is reported beside it.
+qwen: the Qwen-Image-shaped step, 60 joint blocks, 83 x 83 = 6889 image tokens (1328^2) + 256
+text tokens (3584-wide encoder states), hidden 3072, 24 x 128 heads, MLP 12288; kinds "mx"
+(MXFP8 on the QWEN_IMAGE_TARGETS linears) and "bf16".
+Weights are random N(0, 0.02) drawn on the device (RMSNorm weights ones); inputs N(0, 1).
 
 Each step starts with its inputs resident in HBM. W untimed warmup steps, then K steps
 bracketed by torch.cuda.synchronize(); per-step times from HIP events on the step stream.
 
-roofline: the dominant kernel is the single-block input GEMM (M 4608, N 7 x 3072, K 3072, GELU on
-the MLP columns; 2 M N K = 608.8 GFLOP per launch, 38 launches per step). Its average duration
-comes from HIP events recorded around each of its launches inside the timed steps.
+roofline: the dominant kernel of the workload (flux: the single-block input GEMM, M 4608, N 7 x
+3072, K 3072, GELU on the MLP columns, 2 M N K = 608.8 GFLOP per launch, 38 per step; qwen: the
+joint attention, 24 heads x 7145^2 keys x 128, 4 H S^2 d = 627.3 GFLOP per launch, 60 per step).
+Its average duration comes from HIP events recorded around each of its launches inside the timed
+steps, on the stream it runs on. traffic: HBM bytes per launch of that kernel from rocprofv3
+read / write request counters (null when not measured for this kernel and shape).
 attn_gemm: one extra probed step times every GEMM and attention launch; the fraction is the
 roofline time of their algorithmic FLOPs at MFMA peak over their summed measured time.
-cpu_baseline: the oracle (fp32 torch restatement of the reference's CPU path) on one double and
-one single block at the real shape, on this host's cores, extrapolated to 19 + 38 blocks.
+cpu_baseline (flux, N = 1): the oracle (fp32 torch restatement of the reference's CPU path) on
+one double and one single block at the real shape, on this host's cores, extrapolated to the
+19 + 38 blocks.
 """
 
 from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
 import sys
 import time
 
 METRIC = ("FLUX 1024² denoise step ms (bf16, fp8) at 1 GPU; attn+GEMM % of MFMA peak")
 PEAK = {"bf16": 2.5e15, "fp8": 5.0e15, "mx": 5.0e15}  # dense MFMA, MI355X
-HBM_PEAK = 8.0e12
-IMG_HW = (64, 64)
-TXT = 512
 SEED = 0
 COPY_BYTES = 256 << 20
+
+# HBM bytes per launch of the dominant kernel (read + write), from rocprofv3 --pmc runs of this
+# script: TCC_EA0_RDREQ_{32B,64B,128B} and TCC_EA0_WRREQ{,_64B} request counts times their sizes.
+# Keyed by (workload, kind); absent -> null.
+TRAFFIC: dict = {}
 
 
 def parse():
@@ -44,23 +52,14 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--kinds", default="bf16,fp8")
+    ap.add_argument("--workload", default="flux", choices=("flux", "qwen"))
+    ap.add_argument("--kinds", default=None,
+                    help="comma list (flux: bf16,fp8 by default; qwen: mx,bf16)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain 256 MiB bf16 elementwise copy (torch.neg) three "
                          "times, as the known-size reference for HBM byte counters")
     return ap.parse_args()
-
-
-def flops_per_step(cfg, st, si):
-    """Algorithmic FLOPs: GEMMs 2 M N K, attention 4 H S^2 d (QK^T and PV)."""
-    d, f, s = cfg.hidden, cfg.mlp, st + si
-    dbl = 2 * s * d * 3 * d + 2 * s * d * d + 2 * (2 * s * d * f)
-    sgl = 2 * s * d * (3 * d + f) + 2 * s * (d + f) * d
-    attn = 4 * cfg.heads * s * s * cfg.head_dim
-    gemm = cfg.n_double * dbl + cfg.n_single * sgl
-    emb = 2 * si * cfg.in_channels * d + 2 * st * cfg.txt_dim * d + 2 * si * d * cfg.out_channels
-    return gemm, attn * (cfg.n_double + cfg.n_single), emb
 
 
 class Probe:
@@ -97,48 +96,130 @@ class Probe:
         return {k: [s.elapsed_time(e) for s, e in v] for k, v in self.events.items()}
 
 
-def gemm_flops_by_name(cfg, st, si):
-    d, f, s = cfg.hidden, cfg.mlp, st + si
-    return {
-        "gemm.double.qkv": 2 * s * d * 3 * d,
-        "gemm.double.out": 2 * s * d * d,
-        "gemm.double.ff1": 2 * s * d * f,
-        "gemm.double.ff2": 2 * s * f * d,
-        "gemm.single.w1": 2 * s * d * (3 * d + f),
-        "gemm.single.w2": 2 * s * (d + f) * d,
-        "attn": 4 * cfg.heads * s * s * cfg.head_dim,
-    }
+# ----------------------------------------------------------------------------------- workloads
+class Flux:
+    name = "flux"
+    kinds = ("bf16", "fp8")
+    img_hw, txt = (64, 64), 512
+    dominant = "gemm.single.w1"
+    dominant_desc = "single-block input GEMM (4608 x 21504 x 3072, GELU epilogue)"
+    config = {"workload": "FLUX.1-dev-shaped DiT denoise step, 1024x1024 image (64x64 patches "
+                          "= 4096 tokens) + 512 text tokens, 19 double + 38 single blocks, "
+                          "hidden 3072, 24 x 128 heads",
+              "global_batch": 1, "seq_len": 4608, "parallelism": "single GPU"}
+    data = ("synthetic: random-init N(0, 0.02) weights drawn on the device; latents, text, pooled "
+            "N(0, 1); timestep U[0, 1); guidance 3.5")
+
+    def __init__(self):
+        from difflet_amd.dit.flux import FluxConfig
+
+        self.cfg = FluxConfig()
+        self.si = self.img_hw[0] * self.img_hw[1]
+
+    def build(self, kind, torch, dev):
+        from difflet_amd.dit.flux import FluxDiT, random_param_source
+
+        model = FluxDiT(self.cfg, random_param_source(self.cfg, SEED, dev), kind=kind, device=dev)
+        g = torch.Generator(device=dev).manual_seed(SEED + 1)
+        c = self.cfg
+        lat = torch.randn(1, self.si, c.in_channels, generator=g, device=dev)
+        text = torch.randn(1, self.txt, c.txt_dim, generator=g, device=dev)
+        pooled = torch.randn(1, c.pooled_dim, generator=g, device=dev)
+        t = torch.rand(1, generator=g, device=dev)
+        guid = torch.full((1,), 3.5, device=dev)
+        return model, lambda: model.forward(lat, text, pooled, t, guid, self.img_hw)
+
+    def flops(self):
+        """Algorithmic FLOPs per launch by probe name: GEMM 2 M N K, attention 4 H S^2 d."""
+        c, s = self.cfg, self.txt + self.si
+        d, f = c.hidden, c.mlp
+        return {"gemm.double.qkv": 2 * s * d * 3 * d, "gemm.double.out": 2 * s * d * d,
+                "gemm.double.ff1": 2 * s * d * f, "gemm.double.ff2": 2 * s * f * d,
+                "gemm.single.w1": 2 * s * d * (3 * d + f), "gemm.single.w2": 2 * s * (d + f) * d,
+                "attn": 4 * c.heads * s * s * c.head_dim}
+
+    def step_flops(self):
+        c, fl = self.cfg, self.flops()
+        blocks = c.n_double * sum(fl[k] for k in fl if k.startswith("gemm.double")) + \
+            c.n_single * sum(fl[k] for k in fl if k.startswith("gemm.single")) + \
+            (c.n_double + c.n_single) * fl["attn"]
+        emb = 2 * self.si * c.in_channels * c.hidden + 2 * self.txt * c.txt_dim * c.hidden + \
+            2 * self.si * c.hidden * c.out_channels
+        return blocks + emb
+
+    def peak(self, name, kind):
+        return PEAK["bf16"] if name == "attn" else PEAK[kind]
 
 
-def run_kind(kind, steps, warmup, torch, log):
-    from difflet_amd.dit.flux import FluxConfig, FluxDiT, random_param_source
+class Qwen:
+    name = "qwen"
+    kinds = ("mx", "bf16")
+    img_hw, txt = (83, 83), 256
+    dominant = "attn"
+    dominant_desc = "joint attention (24 heads x 7145 queries x 7145 keys x 128, bf16)"
+    config = {"workload": "Qwen-Image-shaped MMDiT denoise step, 1328x1328 image (83x83 patches "
+                          "= 6889 tokens) + 256 text tokens, 60 joint blocks, hidden 3072, "
+                          "24 x 128 heads, MLP 12288",
+              "global_batch": 1, "seq_len": 7145, "parallelism": "single GPU"}
+    data = ("synthetic: random-init N(0, 0.02) weights drawn on the device; latents and text "
+            "encoder states N(0, 1); timestep U[0, 1)")
 
+    def __init__(self):
+        from difflet_amd.dit.qwen import QwenConfig
+
+        self.cfg = QwenConfig()
+        self.si = self.img_hw[0] * self.img_hw[1]
+
+    def build(self, kind, torch, dev):
+        from difflet_amd.dit.qwen import QwenImageDiT, random_param_source
+
+        model = QwenImageDiT(self.cfg, random_param_source(self.cfg, SEED, dev), kind=kind,
+                             device=dev)
+        g = torch.Generator(device=dev).manual_seed(SEED + 1)
+        c = self.cfg
+        lat = torch.randn(1, self.si, c.in_channels, generator=g, device=dev)
+        text = torch.randn(1, self.txt, c.txt_dim, generator=g, device=dev)
+        t = torch.rand(1, generator=g, device=dev)
+        return model, lambda: model.forward(lat, text, t, self.img_hw)
+
+    def flops(self):
+        c, s = self.cfg, self.txt + self.si
+        d, f = c.hidden, c.mlp
+        return {"gemm.joint.qkv": 2 * s * d * 3 * d, "gemm.joint.out": 2 * s * d * d,
+                "gemm.joint.ff1": 2 * s * d * f, "gemm.joint.ff2": 2 * s * f * d,
+                "attn": 4 * c.heads * s * s * c.head_dim}
+
+    def step_flops(self):
+        c, fl = self.cfg, self.flops()
+        emb = 2 * self.si * c.in_channels * c.hidden + 2 * self.txt * c.txt_dim * c.hidden + \
+            2 * self.si * c.hidden * c.out_channels
+        return c.n_blocks * sum(fl.values()) + emb
+
+    def peak(self, name, kind):
+        # the output projections are not MXFP8 targets: bf16 peak for them and attention
+        return PEAK["bf16"] if name in ("attn", "gemm.joint.out") else PEAK[kind]
+
+
+WORKLOADS = {"flux": Flux, "qwen": Qwen}
+
+
+# ----------------------------------------------------------------------------------- runs
+def run_kind(wl, kind, steps, warmup, torch, log):
     dev = torch.device("cuda", 0)
-    cfg = FluxConfig()
     t0 = time.time()
-    model = FluxDiT(cfg, random_param_source(cfg, SEED, dev), kind=kind, device=dev)
+    model, step = wl.build(kind, torch, dev)
     torch.cuda.synchronize()
-    log(f"[{kind}] model built in {time.time() - t0:.1f} s, "
+    log(f"[{wl.name}/{kind}] model built in {time.time() - t0:.1f} s, "
         f"{torch.cuda.memory_allocated() / 2**30:.1f} GiB allocated")
-    g = torch.Generator(device=dev).manual_seed(SEED + 1)
-    si = IMG_HW[0] * IMG_HW[1]
-    latents = torch.randn(1, si, cfg.in_channels, generator=g, device=dev)
-    text = torch.randn(1, TXT, cfg.txt_dim, generator=g, device=dev)
-    pooled = torch.randn(1, cfg.pooled_dim, generator=g, device=dev)
-    t = torch.rand(1, generator=g, device=dev)
-    guid = torch.full((1,), 3.5, device=dev)
-
-    def step():
-        return model.forward(latents, text, pooled, t, guid, IMG_HW)
-
+    out = None
     for _ in range(warmup):
         out = step()
     torch.cuda.synchronize()
-    if not torch.isfinite(out.float()).all():
-        raise RuntimeError(f"[{kind}] non-finite output")
-    log(f"[{kind}] warmup done")
+    if out is not None and not torch.isfinite(out.float()).all():
+        raise RuntimeError(f"[{wl.name}/{kind}] non-finite output")
+    log(f"[{wl.name}/{kind}] warmup done")
 
-    probe = Probe(only={"gemm.single.w1"})
+    probe = Probe(only={wl.dominant})
     model.probe = probe
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(steps)]
@@ -152,8 +233,9 @@ def run_kind(kind, steps, warmup, torch, log):
     wall_ms = (time.perf_counter() - t_wall) * 1e3 / steps
     model.probe = None
     per_step = sorted(s.elapsed_time(e) for s, e in evs)
-    dom = probe.times_ms()["gemm.single.w1"]
-    log(f"[{kind}] {steps} steps: mean {sum(per_step) / steps:.2f} ms, wall {wall_ms:.2f} ms")
+    dom = probe.times_ms()[wl.dominant]
+    log(f"[{wl.name}/{kind}] {steps} steps: mean {sum(per_step) / steps:.2f} ms, "
+        f"wall {wall_ms:.2f} ms")
 
     # one more step with every GEMM / attention launch probed
     full = Probe()
@@ -164,12 +246,40 @@ def run_kind(kind, steps, warmup, torch, log):
     by_name = full.times_ms()
     del model
     torch.cuda.empty_cache()
-    return {"per_step": per_step, "wall_ms": wall_ms, "dominant_ms": dom, "by_name": by_name,
-            "cfg": cfg, "si": si}
+    return {"per_step": per_step, "wall_ms": wall_ms, "dominant_ms": dom, "by_name": by_name}
 
 
-def cpu_baseline(log):
-    """The oracle's fp32 CPU path on one double + one single block at the real shape."""
+def summarize(wl, kind, r):
+    fl = wl.flops()
+    mean_ms = sum(r["per_step"]) / len(r["per_step"])
+    # attn+GEMM: roofline time of their FLOPs at MFMA peak / their measured kernel time
+    t_meas = sum(sum(v) for v in r["by_name"].values()) * 1e-3
+    t_roof = sum(fl[n] * len(v) / wl.peak(n, kind) for n, v in r["by_name"].items())
+    dom = r["dominant_ms"]
+    dom_avg = sum(dom) / len(dom)
+    peak = wl.peak(wl.dominant, kind)
+    achieved = fl[wl.dominant] / (dom_avg * 1e-3) / 1e12
+    per_kernel = {n: {"launches": len(v), "avg_ms": round(sum(v) / len(v), 4),
+                      "tflops": round(fl[n] / (sum(v) / len(v) * 1e-3) / 1e12, 1)}
+                  for n, v in sorted(r["by_name"].items())}
+    return {
+        "ms_per_step": round(mean_ms, 3),
+        "median_ms": round(r["per_step"][len(r["per_step"]) // 2], 3),
+        "p90_ms": round(r["per_step"][int(0.9 * (len(r["per_step"]) - 1))], 3),
+        "wall_ms_per_step": round(r["wall_ms"], 3),
+        "tflops_step": round(wl.step_flops() / (mean_ms * 1e-3) / 1e12, 1),
+        "attn_gemm_frac_of_mfma_peak": round(t_roof / t_meas, 4),
+        "attn_gemm_kernel_ms": round(t_meas * 1e3, 3),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak / 1e12,
+                     "unit": "TFLOP/s", "frac": round(achieved * 1e12 / peak, 4),
+                     "traffic": TRAFFIC.get((wl.name, kind)), "kernel": wl.dominant_desc,
+                     "avg_ms": round(dom_avg, 4), "launches_timed": len(dom)},
+        "kernels": per_kernel,
+    }
+
+
+def cpu_baseline(wl, log):
+    """The oracle's fp32 CPU path on one double + one single block at the real FLUX shape."""
     import torch
 
     from oracle import flux as oflux
@@ -179,11 +289,12 @@ def cpu_baseline(log):
     torch.set_num_threads(threads)
     shape = oflux.FluxShape()
     g = torch.Generator().manual_seed(SEED)
-    si = IMG_HW[0] * IMG_HW[1]
+    h, w = wl.img_hw
+    si, st = h * w, wl.txt
     hidden = torch.randn(1, si, shape.hidden, generator=g)
-    context = torch.randn(1, TXT, shape.hidden, generator=g)
+    context = torch.randn(1, st, shape.hidden, generator=g)
     temb = torch.randn(1, shape.hidden, generator=g)
-    cos, sin = ops.flux_pos_embed(ops.flux_ids(TXT, *IMG_HW))
+    cos, sin = ops.flux_pos_embed(ops.flux_ids(st, h, w))
     dw = oflux.double_block_weights(shape, SEED, 0)
     sw = oflux.single_block_weights(shape, SEED, 0)
     # warm the thread pool and allocator on a small slice
@@ -200,15 +311,14 @@ def cpu_baseline(log):
     return {"value": round(step_ms, 1), "unit": "ms/step (extrapolated)", "cores": threads,
             "kind": "port",
             "sample": (f"fp32 oracle, 1 double ({t_d:.2f} s) + 1 single ({t_s:.2f} s) block at "
-                       f"{TXT}+{si} tokens, extrapolated x{shape.n_double} + x{shape.n_single}")}
+                       f"{st}+{si} tokens, extrapolated x{shape.n_double} + x{shape.n_single}")}
 
 
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the step's sharding across GPUs is a design in DESIGN.md, not measured)",
-              file=sys.stderr)
+              "(sharding the step across GPUs is designed, not built)", file=sys.stderr)
         return 2
     import torch
 
@@ -220,7 +330,8 @@ def main():
     from difflet_amd import _lib
 
     _lib.load()
-    kinds = [k for k in args.kinds.split(",") if k]
+    wl = WORKLOADS[args.workload]()
+    kinds = [k for k in (args.kinds or ",".join(wl.kinds)).split(",") if k]
     if args.calibrate_copy:
         src = torch.randn(COPY_BYTES // 2, device="cuda").bfloat16()
         dst = torch.empty_like(src)
@@ -228,43 +339,13 @@ def main():
             torch.neg(src, out=dst)
         torch.cuda.synchronize()
         del src, dst
-    res = {k: run_kind(k, args.steps, args.warmup, torch, log) for k in kinds}
-
-    out = {}
-    for k, r in res.items():
-        cfg, si = r["cfg"], r["si"]
-        gemm_f, attn_f, emb_f = flops_per_step(cfg, TXT, si)
-        mean_ms = sum(r["per_step"]) / len(r["per_step"])
-        fl = gemm_flops_by_name(cfg, TXT, si)
-        # attn+GEMM: roofline time of their FLOPs at MFMA peak / their measured kernel time
-        t_meas = sum(sum(v) for n, v in r["by_name"].items()) * 1e-3
-        t_roof = sum(fl[n] * len(v) / (PEAK["bf16"] if n == "attn" else PEAK[k])
-                     for n, v in r["by_name"].items())
-        dom = r["dominant_ms"]
-        dom_avg = sum(dom) / len(dom)
-        dom_flops = fl["gemm.single.w1"]
-        achieved = dom_flops / (dom_avg * 1e-3) / 1e12
-        per_kernel = {n: {"launches": len(v), "avg_ms": round(sum(v) / len(v), 4),
-                          "tflops": round(fl[n] / (sum(v) / len(v) * 1e-3) / 1e12, 1)}
-                      for n, v in sorted(r["by_name"].items())}
-        out[k] = {
-            "ms_per_step": round(mean_ms, 3),
-            "median_ms": round(r["per_step"][len(r["per_step"]) // 2], 3),
-            "p90_ms": round(r["per_step"][int(0.9 * (len(r["per_step"]) - 1))], 3),
-            "wall_ms_per_step": round(r["wall_ms"], 3),
-            "tflops_step": round((gemm_f + attn_f + emb_f) / (mean_ms * 1e-3) / 1e12, 1),
-            "attn_gemm_frac_of_mfma_peak": round(t_roof / t_meas, 4),
-            "attn_gemm_kernel_ms": round(t_meas * 1e3, 3),
-            "roofline": {"bound": "mfma", "achieved": round(achieved, 1),
-                         "peak": PEAK[k] / 1e12, "unit": "TFLOP/s",
-                         "frac": round(achieved * 1e12 / PEAK[k], 4), "traffic": None,
-                         "kernel": "single-block input GEMM (4608 x 21504 x 3072, GELU epilogue)",
-                         "avg_ms": round(dom_avg, 4), "launches_timed": len(dom)},
-            "kernels": per_kernel,
-        }
+    out = {k: summarize(wl, k, run_kind(wl, k, args.steps, args.warmup, torch, log))
+           for k in kinds}
     head = kinds[0]
+    metric = METRIC if wl.name == "flux" else \
+        "Qwen-Image 1328² denoise step ms (MXFP8, bf16) at 1 GPU; attn+GEMM % of MFMA peak"
     line = {
-        "metric": METRIC,
+        "metric": metric,
         "value": out[head]["ms_per_step"],
         "unit": "ms",
         "n_gpus": 1,
@@ -275,19 +356,14 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": head,
-        "data": "synthetic: random-init N(0, 0.02) weights drawn on the device; latents, text, "
-                "pooled N(0, 1); timestep U[0, 1); guidance 3.5",
-        "config": {"workload": "FLUX.1-dev-shaped DiT denoise step, 1024x1024 image "
-                               "(64x64 patches = 4096 tokens) + 512 text tokens, 19 double + "
-                               "38 single blocks, hidden 3072, 24 x 128 heads",
-                   "global_batch": 1, "seq_len": TXT + IMG_HW[0] * IMG_HW[1],
-                   "parallelism": "single GPU"},
+        "data": wl.data,
+        "config": wl.config,
         "roofline": out[head]["roofline"],
         "attn_gemm_frac_of_mfma_peak": out[head]["attn_gemm_frac_of_mfma_peak"],
         "steps_by_dtype": out,
     }
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(log)
+    if not args.no_cpu and wl.name == "flux":
+        line["cpu_baseline"] = cpu_baseline(wl, log)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -116,10 +116,10 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
   constexpr int WN_WAVES = WN, NWAVES = 2 * WN;
   constexpr int WTN = BN / WN_WAVES, TJ = WTN / 32;  // wave tile 128 x WTN: 4 x TJ MFMA tiles
   constexpr int SLABS = 32 / NWAVES;  // 1 KB LDS slabs one wave loads per stage
-  constexpr int MXL = 8 / NWAVES;     // MX scale loads one wave issues per stage
   __shared__ __attribute__((aligned(16))) uint8_t smem[STAGES][2][BM * KT_BYTES];  // [stage][A|W]
-  // MX: per stage and row, the dword of E8M0 scales holding the stage's two 32-K blocks
-  __shared__ __attribute__((aligned(16))) uint32_t smem_sc[E == Elem::MX ? STAGES : 1][2][BM];
+  // MX: E8M0 scales of 8 stages (16 bytes) per row, a ring of 3 such blocks: [slot][A|W][row]
+  constexpr int SCB = E == Elem::MX ? 1 : 0;
+  __shared__ __attribute__((aligned(16))) uint32_t smem_sc[SCB ? 3 : 1][SCB ? 2 : 1][SCB ? BM : 1][4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -173,16 +173,27 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
     a_off[i] = (uint32_t)(r * a_row_bytes) + ch * 16;
     w_off[i] = (uint32_t)(r * w_row_bytes) + ch * 16;
   }
-  // MX scales ride along with their stage: one DMA dword per row (scale bytes 4 q .. 4 q + 3,
-  // q = stage / 2, so the stage's two blocks are its half kt & 1), rows past M / N read zero.
+  // MX scales: block q = the 16 scale bytes of stages 8 q .. 8 q + 7 of every row (K-blocks
+  // 16 q .. 16 q + 15), in ring slot q % 3. Block q + 1 is loaded in 8 parts of 64 rows while the
+  // stages of block q are issued: with stage s, wave s % 8 loads part s % 8 (A rows for parts
+  // 0-3, W rows for 4-7). A part lands before the stages that read it (it was issued with an
+  // earlier stage), and slot (q + 1) % 3 was last read by block q - 2. The whole offset goes in
+  // the per-lane offset so the resource's range check covers it: bytes past the scale array
+  // (rows past M / N, a last block shorter than 16 bytes) read zero.
   const int ksb = K / 32;  // scale row stride (blocks per row)
   __amdgpu_buffer_rsrc_t rsa = rw, rsw = rw;
   if constexpr (E == Elem::MX) {
     rsa = make_rsrc((const uint8_t*)P.a_scale + m0 * ksb, (uint32_t)((M - m0) * ksb));
     rsw = make_rsrc((const uint8_t*)P.w_scale + n0 * ksb, (uint32_t)((N - n0) * ksb));
   }
-  // part `part` (of 4) of a stage's loads: a quarter of this wave's slabs, A slabs first (MX:
-  // scale load v with part v; scale load u = wave * MXL + v covers 64 rows of A (u < 4) or W)
+  auto issue_scales = [&](int blk, int p) {  // MX: part p of scale block blk
+    const uint32_t row = (p & 3) * 64 + lane;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(p < 4 ? rsa : rsw,
+                                             (lds_void*)&smem_sc[blk % 3][p >> 2][(p & 3) * 64][0],
+                                             16, row * ksb + blk * 16, 0, 0, 0);
+  };
+  // part `part` (of 4) of stage kt's loads: a quarter of this wave's slabs, A slabs first (MX:
+  // with part 0, wave kt % 8 also loads part kt % 8 of the next scale block)
   auto issue_part = [&](int kt, int st, int part) {
     const uint32_t kb = (uint32_t)kt * KT_BYTES;
 #pragma unroll
@@ -195,22 +206,18 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
             rw, (lds_void*)&smem[st][1][(wave * SA + s - SA) * 1024], 16, w_off[s - SA], kb, 0, 0);
     }
     if constexpr (E == Elem::MX) {
-      if (part < MXL) {
-        const int u = wave * MXL + part;
-        const uint32_t row = (u & 3) * 64 + lane;
-        const uint32_t so = (uint32_t)(kt & ~1) * 2;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(u < 4 ? rsa : rsw,
-                                                 (lds_void*)&smem_sc[st][u >> 2][(u & 3) * 64], 4,
-                                                 row * ksb, so, 0, 0);
-      }
+      if (part == 0 && wave == (kt & 7) % NWAVES) issue_scales((kt >> 3) + 1, kt & 7);
     }
   };
   auto issue_stage = [&](int kt, int st) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) issue_part(kt, st, i);
   };
-  // vector-memory instructions one stage issues per wave (for s_waitcnt vmcnt)
-  constexpr int LOADS_PER_STAGE = SLABS + (E == Elem::MX ? MXL : 0);
+  // vector-memory instructions one stage issues per wave (for s_waitcnt vmcnt). A stage that
+  // also carries an MX scale part issues one more, which only makes a wait conservative: the
+  // waits allow the loads of the stages issued after the awaited one to stay in flight, and
+  // those are at least LOADS_PER_STAGE per stage.
+  constexpr int LOADS_PER_STAGE = SLABS;
 
   f32x16 acc[4][4];  // columns j < TJ used
 #pragma unroll
@@ -240,7 +247,7 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
       f.a[i][1] = *reinterpret_cast<const i32x4*>(sA + lds_off(r, 2 + fhalf));
     }
     if constexpr (E == Elem::MX)
-      f.sa[i] = (smem_sc[st][0][r] >> ((kt & 1) * 16 + fhalf * 8)) & 0xffu;
+      f.sa[i] = (smem_sc[(kt >> 3) % 3][0][r][(kt & 7) >> 1] >> ((kt & 1) * 16 + fhalf * 8)) & 0xffu;
   };
   auto read_a = [&](int st, int kt, Frags& f) {
 #pragma unroll
@@ -262,7 +269,7 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
       f.w[j][0] = *reinterpret_cast<const i32x4*>(sW + lds_off(r, fhalf));
       f.w[j][1] = *reinterpret_cast<const i32x4*>(sW + lds_off(r, 2 + fhalf));
       if constexpr (E == Elem::MX)
-        f.sw[j] = (smem_sc[st][1][r] >> ((kt & 1) * 16 + fhalf * 8)) & 0xffu;
+        f.sw[j] = (smem_sc[(kt >> 3) % 3][1][r][(kt & 7) >> 1] >> ((kt & 1) * 16 + fhalf * 8)) & 0xffu;
     }
   };
   auto read_w = [&](int st, int h, int kt, Frags& f) {
@@ -307,6 +314,10 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
   // prologue: stages 0 .. STAGES-2 in flight, then wait for stage 0. Past the last K stage the
   // loads re-read the last stage (in bounds) into the free ring slot: every iteration then
   // issues and waits alike, and the loop body is one straight-line block.
+  if constexpr (E == Elem::MX) {  // scale block 0, one part per wave, ahead of stage 0
+#pragma unroll
+    for (int p = wave; p < 8; p += NWAVES) issue_scales(0, p);
+  }
 #pragma unroll
   for (int s0 = 0; s0 < STAGES - 1; ++s0) issue_stage(min(s0, nkt - 1), s0);
   {
