@@ -1,6 +1,6 @@
 """Benchmark: one DiT denoise step on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload flux|qwen]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload flux|qwen|wan]
                     [--kinds bf16,fp8] [--no-cpu] [--calibrate-copy]
 
 flux (default): the full FLUX.1-dev-shaped transformer forward of one denoise step, batch 1,
@@ -10,7 +10,10 @@ linear per-channel e4m3 with per-token activations) is reported beside it.
 qwen: the Qwen-Image-shaped step, 60 joint blocks, 83 x 83 = 6889 image tokens (1328^2) + 256
 text tokens (3584-wide encoder states), hidden 3072, 24 x 128 heads, MLP 12288; kinds "mx"
 (MXFP8 on the QWEN_IMAGE_TARGETS linears) and "bf16".
-Weights are random N(0, 0.02) drawn on the device (RMSNorm weights ones); inputs N(0, 1).
+wan: the Wan-2.2-14B-shaped text-to-video step, 40 blocks, latent 21 x 60 x 104 with patch
+(1, 2, 2) = 32760 video tokens + 512 text tokens (4096-wide), hidden 5120, 40 x 128 heads, FFN
+13824, bf16.
+Weights are random N(0, 0.02) drawn on the device (norm weights ones); inputs N(0, 1).
 
 Each step starts with its inputs resident in HBM. W untimed warmup steps, then K steps
 bracketed by torch.cuda.synchronize(); per-step times from HIP events on the step stream.
@@ -52,7 +55,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="flux", choices=("flux", "qwen"))
+    ap.add_argument("--workload", default="flux", choices=("flux", "qwen", "wan"))
     ap.add_argument("--kinds", default=None,
                     help="comma list (flux: bf16,fp8 by default; qwen: mx,bf16)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -200,7 +203,58 @@ class Qwen:
         return PEAK["bf16"] if name in ("attn", "gemm.joint.out") else PEAK[kind]
 
 
-WORKLOADS = {"flux": Flux, "qwen": Qwen}
+class Wan:
+    name = "wan"
+    kinds = ("bf16",)
+    latent_fhw, txt = (21, 60, 104), 512
+    dominant = "attn.self"
+    dominant_desc = "self-attention (40 heads x 32760 queries x 32760 keys x 128, bf16)"
+    config = {"workload": "Wan-2.2-14B-shaped video DiT denoise step, 480x832x81 frames -> "
+                          "latent 21x60x104, patch (1, 2, 2) = 32760 video tokens + 512 text "
+                          "tokens, 40 blocks, hidden 5120, 40 x 128 heads, FFN 13824",
+              "global_batch": 1, "seq_len": 32760, "parallelism": "single GPU"}
+    data = ("synthetic: random-init N(0, 0.02) weights drawn on the device; latents and text "
+            "encoder states N(0, 1); timestep U[0, 1000)")
+
+    def __init__(self):
+        from difflet_amd.dit.wan import WanConfig
+
+        self.cfg = WanConfig()
+        f, h, w = self.latent_fhw
+        self.s = f * (h // 2) * (w // 2)
+
+    def build(self, kind, torch, dev):
+        from difflet_amd.dit.wan import WanDiT, random_param_source
+
+        model = WanDiT(self.cfg, random_param_source(self.cfg, SEED, dev), device=dev)
+        g = torch.Generator(device=dev).manual_seed(SEED + 1)
+        c = self.cfg
+        lat = torch.randn(1, c.in_channels, *self.latent_fhw, generator=g, device=dev)
+        text = torch.randn(1, self.txt, c.text_dim, generator=g, device=dev)
+        t = torch.rand(1, generator=g, device=dev) * 1000.0
+        return model, lambda: model.forward(lat, t, text)
+
+    def flops(self):
+        c, s, st = self.cfg, self.s, self.txt
+        d, f = c.hidden, c.ffn
+        return {"gemm.qkv": 2 * s * d * 3 * d, "gemm.out1": 2 * s * d * d,
+                "gemm.q2": 2 * s * d * d, "gemm.kv2": 2 * st * d * 2 * d,
+                "gemm.out2": 2 * s * d * d, "gemm.ffn_in": 2 * s * d * f,
+                "gemm.ffn_out": 2 * s * f * d,
+                "attn.self": 4 * c.heads * s * s * c.head_dim,
+                "attn.cross": 4 * c.heads * s * st * c.head_dim}
+
+    def step_flops(self):
+        c = self.cfg
+        emb = 2 * self.s * 64 * c.hidden + 2 * self.txt * (c.text_dim + c.hidden) * c.hidden + \
+            2 * self.s * c.hidden * 64
+        return c.n_blocks * sum(self.flops().values()) + emb
+
+    def peak(self, name, kind):
+        return PEAK["bf16"]
+
+
+WORKLOADS = {"flux": Flux, "qwen": Qwen, "wan": Wan}
 
 
 # ----------------------------------------------------------------------------------- runs
@@ -342,8 +396,11 @@ def main():
     out = {k: summarize(wl, k, run_kind(wl, k, args.steps, args.warmup, torch, log))
            for k in kinds}
     head = kinds[0]
-    metric = METRIC if wl.name == "flux" else \
-        "Qwen-Image 1328² denoise step ms (MXFP8, bf16) at 1 GPU; attn+GEMM % of MFMA peak"
+    metric = {"flux": METRIC,
+              "qwen": "Qwen-Image 1328² denoise step ms (MXFP8, bf16) at 1 GPU; attn+GEMM % of "
+                      "MFMA peak",
+              "wan": "Wan-2.2 480x832x81 denoise step ms (bf16) at 1 GPU; attn+GEMM % of MFMA "
+                     "peak"}[wl.name]
     line = {
         "metric": metric,
         "value": out[head]["ms_per_step"],

@@ -247,7 +247,9 @@ __device__ __forceinline__ void rope8(float* v, const float* cs, const float* sn
 
 // ------------------------------------------------------------------ q/k RMSNorm + RoPE
 // One wavefront per row; LPH = lanes per head (head_dim / 8); a wave covers 64 / LPH heads
-// per step. Statistics reduce over the LPH lanes of one head with xor shuffles.
+// per step. do_norm 1: per-head RMS, reduced over the LPH lanes of one head with xor shuffles,
+// weight [head_dim]. do_norm 2: one RMS over all heads of the tensor (a first pass over the
+// row, one wave reduction), weight [heads * head_dim].
 template <typename T, typename TW, int LPH>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     T* __restrict__ buf, int64_t ld, int64_t rows, int heads, int64_t q_off, int64_t k_off,
@@ -270,6 +272,20 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     if (off < 0) continue;
     const TW* w = t == 0 ? wq : wk;
     T* base = buf + row * ld + off;
+    float r_row = 1.f;
+    if (do_norm == 2) {
+      float s = 0.f;
+      for (int h0 = 0; h0 < heads; h0 += HPS) {
+        const int h = h0 + hl;
+        if (h < heads) {
+          float v[8];
+          V8<T>::load(base + (int64_t)h * HD + d0, v);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) s += v[i] * v[i];
+        }
+      }
+      r_row = 1.0f / __builtin_sqrtf(wave_sum(s) / (float)(heads * HD) + eps);
+    }
     for (int h0 = 0; h0 < heads; h0 += HPS) {
       const int h = h0 + hl;
       if (h < heads) {
@@ -277,15 +293,18 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
         float v[8];
         V8<T>::load(p, v);
         if (do_norm) {
-          float s = 0.f;
+          float r = r_row;
+          if (do_norm == 1) {
+            float s = 0.f;
 #pragma unroll
-          for (int i = 0; i < 8; ++i) s += v[i] * v[i];
+            for (int i = 0; i < 8; ++i) s += v[i] * v[i];
 #pragma unroll
-          for (int o = LPH / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-          const float r = 1.0f / __builtin_sqrtf(s / (float)HD + eps);
+            for (int o = LPH / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+            r = 1.0f / __builtin_sqrtf(s / (float)HD + eps);
+          }
           float w8[8];
           if (w) {
-            V8<TW>::load(w + d0, w8);
+            V8<TW>::load(w + (do_norm == 2 ? (int64_t)h * HD : 0) + d0, w8);
           } else {
 #pragma unroll
             for (int i = 0; i < 8; ++i) w8[i] = 1.f;
@@ -642,6 +661,7 @@ extern "C" int difflet_rocm_qk_norm_rope(void* buf, int64_t ld, int dtype, int64
   DLT_REQUIRE(!cos == !sin, DIFFLET_EINVAL, "qk_norm_rope: cos and sin go together");
   DLT_REQUIRE(!cos || rope_rows > 0, DIFFLET_EINVAL, "qk_norm_rope: rope_rows must be > 0");
   DLT_REQUIRE(law == 0 || law == 1, DIFFLET_EINVAL, "qk_norm_rope: law must be 0 or 1");
+  DLT_REQUIRE(do_norm >= 0 && do_norm <= 2, DIFFLET_EINVAL, "qk_norm_rope: do_norm must be 0, 1 or 2");
   DLT_REQUIRE(aligned16(buf) && (!cos || (aligned16(cos) && aligned16(sin))), DIFFLET_EINVAL,
               "qk_norm_rope: pointers must be 16-byte aligned");
   if (rows == 0) return DIFFLET_OK;

@@ -65,3 +65,22 @@ def qwen_rope_tables(txt_len: int, img_hw: tuple[int, int], axes=(16, 56, 56),
     cos = torch.cos(ang).repeat_interleave(2, dim=-1)
     sin = torch.sin(ang).repeat_interleave(2, dim=-1)
     return cos.to(device).contiguous(), sin.to(device).contiguous()
+
+
+def wan_rope_tables(grid: tuple[int, int, int], head_dim: int = 128, max_seq_len: int = 1024,
+                    device="cuda", theta: float = 10000.0):
+    """WanRotaryPosEmbed (difflet/models/wan/modeling_wan.py:209-296): axes of head_dim - 2 hw,
+    hw, hw dims (hw = 2 * (head_dim // 6)) over (frame, row, column) of the patch grid,
+    frame-major; float64 frequencies, repeat-interleaved, fp32 [F * H * W, head_dim]."""
+    f, h, w = grid
+    hw = 2 * (head_dim // 6)
+    dims = (head_dim - 2 * hw, hw, hw)
+    ff, yy, xx = torch.meshgrid(torch.arange(f), torch.arange(h), torch.arange(w), indexing="ij")
+    cos, sin = [], []
+    for d, pos in zip(dims, (ff.reshape(-1), yy.reshape(-1), xx.reshape(-1))):
+        freqs = 1.0 / (theta ** (torch.arange(0, d, 2, dtype=torch.float64)[: d // 2] / d))
+        table = torch.outer(torch.arange(max_seq_len, dtype=torch.float64), freqs)
+        cos.append(table.cos().repeat_interleave(2, dim=1).float()[pos])
+        sin.append(table.sin().repeat_interleave(2, dim=1).float()[pos])
+    return (torch.cat(cos, dim=1).to(device).contiguous(),
+            torch.cat(sin, dim=1).to(device).contiguous())

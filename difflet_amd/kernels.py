@@ -328,9 +328,10 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float) -> torch.
 def qk_norm_rope(buf: torch.Tensor, *, heads: int, head_dim: int, q_off: int, k_off: int,
                  wq: torch.Tensor | None, wk: torch.Tensor | None, eps: float,
                  cos: torch.Tensor | None, sin: torch.Tensor | None, law: int = 0,
-                 do_norm: bool = True) -> None:
-    """In place on a [rows, ld] projection buffer: per-head RMSNorm of q (columns
-    q_off + h * head_dim ..) and k, then the rotary embedding with fp32 tables [S, head_dim]."""
+                 do_norm: bool | int = True) -> None:
+    """In place on a [rows, ld] projection buffer: RMSNorm of q (columns q_off + h * head_dim ..;
+    q_off < 0 skips q) and k, per head (do_norm True / 1) or over all heads of the row (2), then
+    the rotary embedding with fp32 tables [S, head_dim] (cos None skips it)."""
     dev = _on_gpu(buf)
     if buf.dim() != 2 or buf.stride(1) != 1:
         raise ValueError("qk_norm_rope: buf must be 2-D with contiguous rows")

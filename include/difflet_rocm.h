@@ -179,17 +179,20 @@ int difflet_rocm_rms_norm(const void* x, int64_t ldx, void* y, int64_t ldy, int 
                           int64_t rows, int64_t dim, const void* weight, int wdtype, float eps,
                           difflet_stream_t stream);
 
-/* Fused per-head q/k RMSNorm + rotary embedding, in place, on rows of a projection buffer:
- * for each row r and head h, x = buf[r * ld + off + h * head_dim .. +head_dim] for off in
- * (q_off, k_off), x <- rope(rmsnorm_fp32(x) * w) with the rotary law
+/* Fused q/k RMSNorm + rotary embedding, in place, on rows of a projection buffer: for each
+ * row r and head h, x = buf[r * ld + off + h * head_dim .. +head_dim] for off in (q_off, k_off)
+ * (an offset < 0 skips that tensor), x <- rope(rmsnorm_fp32(x) * w) with
+ *   do_norm 0: no norm; 1: the RMS of each head, w [head_dim] (FLUX / Qwen-Image per-head
+ *   q/k norm); 2: one RMS over all heads * head_dim values of the row, w [heads * head_dim]
+ *   (Wan's rms_norm_across_heads, difflet/models/wan/modeling_wan.py:564-578 via
+ *   difflet/backends/_torch_megatron/norm.py:35-45), and the rotary law
  *   law 0: difflet/backends/_torch_megatron/embeddings.py:24-33 (apply_rotary_emb_fp32,
  *          interleaved pairs, fp32, cast back);
  *   law 1: difflet/backends/cpu/ops_impl/embeddings.py:6-14 (apply_rotary_emb: cos of the
  *          even, sin of the odd table entries).
  * Replaces the norm_q/norm_k + apply_rotary_emb sequence of difflet/models/flux/
  * modeling_flux.py:1249-1252,1289-1294,1407-1411. cos / sin: fp32 [rope_rows, head_dim], row
- * index r % rope_rows; NULL skips the rotation. wq / wk NULL skips that tensor's norm
- * (do_norm = 0 skips both). */
+ * index r % rope_rows; NULL skips the rotation. wq / wk NULL: unit weights. */
 int difflet_rocm_qk_norm_rope(void* buf, int64_t ld, int dtype, int64_t rows, int64_t heads,
                               int64_t head_dim, int64_t q_off, int64_t k_off, int do_norm,
                               const void* wq, const void* wk, int wdtype, float eps,
