@@ -44,10 +44,17 @@ PEAK = {"bf16": 2.5e15, "fp8": 5.0e15, "mx": 5.0e15}  # dense MFMA, MI355X
 SEED = 0
 COPY_BYTES = 256 << 20
 
-# HBM bytes per launch of the dominant kernel (read + write), from rocprofv3 --pmc runs of this
-# script: TCC_EA0_RDREQ_{32B,64B,128B} and TCC_EA0_WRREQ{,_64B} request counts times their sizes.
+# Bytes per launch of the dominant kernel between L2 and the memory fabric (read + write), from
+# two rocprofv3 --pmc runs of this script: TCC_EA0_RDREQ_{32B,64B,128B} and TCC_EA0_WRREQ{,_64B}
+# request counts times their sizes (the same counters read exactly 256 MiB each way for the
+# --calibrate-copy 256 MiB copy). MALL hits are counted too, so this bounds HBM bytes from above.
 # Keyed by (workload, kind); absent -> null.
-TRAFFIC: dict = {}
+TRAFFIC: dict = {
+    # 4608 x 21504 x 3072 GELU GEMM: 1139.1 MB read (A + W = 160 MB once) + 198.3 MB written
+    ("flux", "bf16"): 1_337_400_000,
+    # same GEMM, e4m3 operands: 581.5 MB read (80 MB once) + 203.0 MB written
+    ("flux", "fp8"): 784_500_000,
+}
 
 
 def parse():
