@@ -58,12 +58,15 @@ SIGNATURES: dict[str, tuple] = {
     "difflet_rocm_attention": (_i32, [
         _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64,
         _i64p, _i64p, _i64p, _i64p, _f32, _i32, _vp, _i32, _i64p, _vp, _vp, _i64p, _vp]),
+    "difflet_rocm_gemm_workspace_bytes": (_i64, []),
     "difflet_rocm_gemm_bf16": (_i32, [_i32, ctypes.POINTER(GemmProblem), _i64, _i64, _i32,
-                                      _i64, _vp]),
+                                      _i64, _vp, _i64, _vp]),
     "difflet_rocm_gemm_fp8_rowwise": (_i32, [_i32, ctypes.POINTER(GemmProblem), _i64, _i64,
-                                             _i32, _i64, _vp]),
+                                             _i32, _i64, _vp, _i64, _vp]),
     "difflet_rocm_gemm_mxfp8": (_i32, [_i32, ctypes.POINTER(GemmProblem), _i64, _i64, _i32,
-                                       _i64, _vp]),
+                                       _i64, _vp, _i64, _vp]),
+    "difflet_rocm_gemm_schedule_check": (_i32, [_i32, _i32, _i32, _i32, _i64,
+                                                ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
     "difflet_rocm_quantize_fp8_rowwise": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _vp,
                                                  _vp]),
     "difflet_rocm_quantize_mxfp8": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _vp, _i64,

@@ -9,9 +9,10 @@
 //           row (the block split over the two lane groups, see the K loop), 64 K per K stage.
 // A K stage is therefore always 64 bytes per row, and the LDS geometry is shared.
 //
-// Tiling: a workgroup owns a 256 x 256 tile of C. bf16: 4 wavefronts in a 2 x 2 grid, each
-// 128 x 128 = 4 x 4 MFMA tiles of 32 x 32 (256 fp32 accumulators per lane); fp8 / mx: 8
-// wavefronts in a 2 x 4 grid, each 128 x 64 (128 accumulators), two per SIMD.
+// Tiling: a workgroup owns a 256 x 256 tile of C: 8 wavefronts in a 2 x 4 grid, each 128 x 64 =
+// 4 x 2 MFMA tiles of 32 x 32 (128 fp32 accumulators per lane), two per SIMD, so one
+// wavefront's MFMAs cover the other's LDS waits. Launches whose last wave of tiles would be
+// poorly filled cut tiles along K over the compute units (the split schedule below).
 // The MFMA's first operand is the W tile and its second the A tile, so accumulator lane l holds
 // row m = l % 32 and registers run along n in groups of 4 consecutive columns: the epilogue
 // reads bias / gate / residual and writes C in 8-byte pieces.
@@ -29,6 +30,9 @@
 // Tile order: workgroup ids are spread round-robin over the 8 XCDs, each with its own L2. The id
 // is remapped so each XCD gets a contiguous run of tiles, and tiles run in groups of 8 tile rows
 // so the W and A panels of neighbouring tiles stay L2-resident.
+#include <algorithm>
+#include <vector>
+
 #include "common.hpp"
 
 namespace dlt {
@@ -54,18 +58,51 @@ struct GemmProblemDev {
   int tiles_m, tile_start;
 };
 
+// Split schedule (stream-K). Tiles [0, dp) run one per workgroup. The other S tiles are cut
+// along K: their S * nk (tile, K stage) units, tile-major, are dealt to `groups` workgroups in
+// contiguous ranges [lo(s), lo(s + 1)), lo(s) = s * units / groups, so every workgroup ends at
+// the same time whatever S is. A tile cut between workgroups c0 .. c1 is finished by the last of
+// them to arrive: each other one stores its fp32 accumulators to a workspace slot and counts
+// itself in the tile's counter; the last adds the slots in contributor order (a fixed order: the
+// result does not depend on which one arrives last) and runs the epilogue. Nobody waits.
+struct SkPlan {
+  int dp;         // data-parallel tiles (workgroups 0 .. dp - 1)
+  int groups;     // split workgroups after them (0: no split part)
+  int nu;         // units per tile: K stages in granules of `gran` (the last may be shorter)
+  int gran;       // K stages per unit (MX: 8, one block of E8M0 scales per row)
+  int64_t units;  // S * nu
+};
+__host__ __device__ inline int64_t sk_lo(const SkPlan& p, int s) {
+  return (int64_t)s * p.units / p.groups;
+}
+// the split workgroup whose range holds unit x (0 <= x < units)
+__host__ __device__ inline int sk_owner(const SkPlan& p, int64_t x) {
+  return (int)(((x + 1) * p.groups - 1) / p.units);
+}
+// workspace slot of workgroup c's part of split tile tl: 0 for the first tile of c's range,
+// 1 for its last (a range holds at most two cut tiles)
+__host__ __device__ inline int sk_slot(const SkPlan& p, int c, int tl) {
+  return 2 * c + (sk_lo(p, c) >= (int64_t)tl * p.nu ? 0 : 1);
+}
+constexpr int64_t SK_CTR_BYTES = 16384;        // one int counter per split tile
+constexpr int SK_MAX_TILES = (int)(SK_CTR_BYTES / 4);
+constexpr int64_t SK_SLOT_BYTES = 256 * 256 * 4;  // fp32 accumulators of one 256 x 256 tile
+constexpr int SK_MIN_STAGES = 8;               // shortest K range worth a workgroup
+
 struct GemmArgs {
   GemmProblemDev p[MAX_PROBLEMS];
   int nprob, total_tiles, tiles_n;
   int n, k;
   int act_col_start;
+  SkPlan sk;
+  uint8_t* ws;  // split workspace: counters, then 2 slots per split workgroup
 };
 
-// KT: K elements per stage. WN: wavefronts along N (two along M). bf16 runs 4 wavefronts of
-// 128 x 128; the 8-bit types run 8 of 128 x 64, two per SIMD, so one wavefront's MFMAs cover the
-// other's LDS waits (measured: +10-20 % for fp8, neutral for bf16).
+// KT: K elements per stage. WN: wavefronts along N (two along M). Every type runs 8 wavefronts
+// of 128 x 64 (measured against 4 of 128 x 128: +10-20 % for fp8, +0-6 % for bf16, and 128
+// accumulators leave room for the split-tile code without spills).
 template <Elem E> struct ElemTraits;
-template <> struct ElemTraits<Elem::BF16> { static constexpr int KT = 32, BYTES = 2, WN = 2; };
+template <> struct ElemTraits<Elem::BF16> { static constexpr int KT = 32, BYTES = 2, WN = 4; };
 template <> struct ElemTraits<Elem::FP8> { static constexpr int KT = 64, BYTES = 1, WN = 4; };
 template <> struct ElemTraits<Elem::MX> { static constexpr int KT = 64, BYTES = 1, WN = 4; };
 
@@ -116,10 +153,15 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
   constexpr int WN_WAVES = WN, NWAVES = 2 * WN;
   constexpr int WTN = BN / WN_WAVES, TJ = WTN / 32;  // wave tile 128 x WTN: 4 x TJ MFMA tiles
   constexpr int SLABS = 32 / NWAVES;  // 1 KB LDS slabs one wave loads per stage
-  __shared__ __attribute__((aligned(16))) uint8_t smem[STAGES][2][BM * KT_BYTES];  // [stage][A|W]
-  // MX: E8M0 scales of 8 stages (16 bytes) per row, a ring of 3 such blocks: [slot][A|W][row]
-  constexpr int SCB = E == Elem::MX ? 1 : 0;
-  __shared__ __attribute__((aligned(16))) uint32_t smem_sc[SCB ? 3 : 1][SCB ? 2 : 1][SCB ? BM : 1][4];
+  // LDS: the stage ring [stage][A|W] and (MX) the E8M0 scales of 8 stages (16 bytes) per row, a
+  // ring of 3 such blocks [slot][A|W][row]. One LDS variable: with two, the compiler gives their
+  // accesses alias scopes and then drains all loads (vmcnt(0)) before each LDS read that follows
+  // a direct-to-LDS load.
+  constexpr int RING_BYTES = STAGES * 2 * BM * KT_BYTES;
+  constexpr int SC_BYTES = E == Elem::MX ? 3 * 2 * BM * 16 : 0;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[RING_BYTES + SC_BYTES];
+  auto& smem = *reinterpret_cast<uint8_t(*)[STAGES][2][BM * KT_BYTES]>(lds);
+  auto& smem_sc = *reinterpret_cast<uint32_t(*)[3][2][BM][4]>(lds + RING_BYTES);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -127,16 +169,39 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN_WAVES, wn = wave % WN_WAVES;
 
-  // ---- tile assignment: XCD-contiguous runs, then grouped raster
+  // ---- work: one whole tile (data-parallel part), or a range of (tile, K stage) units
+  const SkPlan& plan = args.sk;
+  const int nk = args.k / KT, nu = plan.nu;
   int bid = blockIdx.x;
-  const int T = args.total_tiles;
-  if ((T & 7) == 0) bid = (bid & 7) * (T >> 3) + (bid >> 3);
+  int s_self = -1;  // split workgroup index
+  int64_t u_lo, u_hi;
+  if (bid < plan.dp) {  // XCD-contiguous runs of tiles
+    if ((plan.dp & 7) == 0) bid = (bid & 7) * (plan.dp >> 3) + (bid >> 3);
+    u_lo = (int64_t)bid * nu;
+    u_hi = u_lo + nu;
+  } else {
+    s_self = bid - plan.dp;
+    u_lo = (int64_t)plan.dp * nu + sk_lo(plan, s_self);
+    u_hi = (int64_t)plan.dp * nu + sk_lo(plan, s_self + 1);
+  }
+  // the split-tile flag lives in the LDS ring, idle when it is used (one LDS variable, above)
+  volatile int& sk_flag = *reinterpret_cast<volatile int*>(lds);
+
+  for (int64_t u = u_lo; u < u_hi;) {
+  const int tt = (int)(u / nu);  // tile
+  const int ub = (int)(u - (int64_t)tt * nu), ue = (int)(min(u_hi, (int64_t)(tt + 1) * nu) - (int64_t)tt * nu);
+  // its K stages [kbeg, kend) run here; the loop below counts them from 0
+  const int kbeg = ub * plan.gran, kend = min(ue * plan.gran, nk), nkt = kend - kbeg;
+  if (u != u_lo) __syncthreads();  // the previous tile's last LDS reads are done
+  u += ue - ub;
+
+  // ---- tile -> problem, grouped raster
   int p = 0;
 #pragma unroll
   for (int i = 1; i < MAX_PROBLEMS; ++i)
-    if (i < args.nprob && bid >= args.p[i].tile_start) p = i;
+    if (i < args.nprob && tt >= args.p[i].tile_start) p = i;
   const GemmProblemDev& P = args.p[p];
-  int t = bid - P.tile_start;
+  int t = tt - P.tile_start;
   const int tn_count = args.tiles_n;
   const int group_size = GROUP_M * tn_count;
   const int g = t / group_size;
@@ -186,16 +251,16 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
     rsa = make_rsrc((const uint8_t*)P.a_scale + m0 * ksb, (uint32_t)((M - m0) * ksb));
     rsw = make_rsrc((const uint8_t*)P.w_scale + n0 * ksb, (uint32_t)((N - n0) * ksb));
   }
-  auto issue_scales = [&](int blk, int p) {  // MX: part p of scale block blk
+  auto issue_scales = [&](int blk, int p) {  // MX: part p of scale block blk (of the range)
     const uint32_t row = (p & 3) * 64 + lane;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(p < 4 ? rsa : rsw,
                                              (lds_void*)&smem_sc[blk % 3][p >> 2][(p & 3) * 64][0],
-                                             16, row * ksb + blk * 16, 0, 0, 0);
+                                             16, row * ksb + ((kbeg >> 3) + blk) * 16, 0, 0, 0);
   };
   // part `part` (of 4) of stage kt's loads: a quarter of this wave's slabs, A slabs first (MX:
   // with part 0, wave kt % 8 also loads part kt % 8 of the next scale block)
   auto issue_part = [&](int kt, int st, int part) {
-    const uint32_t kb = (uint32_t)kt * KT_BYTES;
+    const uint32_t kb = (uint32_t)(kbeg + kt) * KT_BYTES;  // kt counts from the range start
 #pragma unroll
     for (int s = part * SLABS / 4; s < (part + 1) * SLABS / 4; ++s) {
       if (s < SA)
@@ -310,10 +375,11 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
     for (int i = 0; i < 4; ++i) mma_row(f, h, i);
   };
 
-  const int nkt = K / KT;
-  // prologue: stages 0 .. STAGES-2 in flight, then wait for stage 0. Past the last K stage the
-  // loads re-read the last stage (in bounds) into the free ring slot: every iteration then
-  // issues and waits alike, and the loop body is one straight-line block.
+  // prologue: stages 0 .. STAGES-2 of the range in flight, then wait for stage 0. Past the last
+  // K stage the loads re-read the last stage (in bounds) into the free ring slot: every
+  // iteration then issues and waits alike, and the loop body is one straight-line block.
+  // (Stage numbers count from the range start, which for MX is a multiple of 8 stages, so the
+  // scale blocks keep their alignment.)
   if constexpr (E == Elem::MX) {  // scale block 0, one part per wave, ahead of stage 0
 #pragma unroll
     for (int p = wave; p < 8; p += NWAVES) issue_scales(0, p);
@@ -373,6 +439,89 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
     }
   }
   __builtin_amdgcn_s_waitcnt(0x0f70);  // the trailing re-reads land before the workgroup ends
+
+  // ---- a tile cut between split workgroups c0 .. c1: the last to arrive finishes it.
+  // Partial sums move through the workspace with device-scope (sc1) loads and stores, which
+  // the L2 of another XCD cannot serve stale; a store is complete (vmcnt) before its workgroup
+  // counts itself, so a count read at device scope orders them without cache-wide fences.
+  if (kbeg != 0 || kend != nk) {
+    const int tl = tt - plan.dp;  // tile index within the split part
+    const int64_t x0 = (int64_t)tl * nu;
+    const int c0 = sk_owner(plan, x0), c1 = sk_owner(plan, x0 + nu - 1);
+    const int nc = c1 - c0 + 1;
+    int* ctr = reinterpret_cast<int*>(args.ws) + tl;
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(args.ws + SK_CTR_BYTES, (uint32_t)(2 * plan.groups * SK_SLOT_BYTES));
+    constexpr int SC1 = 16;  // cache policy: device scope
+    // lane-major slot layout: each store / load instruction moves 1 KB contiguous; only the
+    // lane's 16 bytes vary across the wave, the rest is a scalar offset
+    const uint32_t vo = (uint32_t)lane * 16;
+    auto soff = [&](int c, int i, int j, int q) {
+      return (uint32_t)(sk_slot(plan, c, tl) * SK_SLOT_BYTES) +
+             (uint32_t)(((wave * (4 * TJ) + i * TJ + j) * 4 + q) * 1024);
+    };
+    // With two contributors (a + b == b + a) or as the first one, this workgroup's own
+    // accumulators can stay in registers and still be summed in contributor order
+    const bool own_in_regs = nc == 2 || s_self == c0;
+    bool last = false;
+    __syncthreads();  // every wave's loads into the ring have landed (the flag is in slot 0)
+    if (own_in_regs) {
+      if (tid == 0)
+        sk_flag = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nc - 1;
+      __syncthreads();
+      last = sk_flag;
+      __syncthreads();
+    }
+    if (!last) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                             acc[i][j][4 * q + 3]};
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, vo,
+                                                   soff(s_self, i, j, q), SC1);
+          }
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the stores are complete
+      __syncthreads();
+      if (tid == 0)
+        sk_flag = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                  nc - 1;
+      __syncthreads();
+      last = sk_flag;
+    }
+    if (!last) continue;  // another contributor finishes the tile
+    if (!own_in_regs) {  // the own part is in its slot too: sum every slot from zero
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = f32x16{};
+    }
+    for (int c = c0; c <= c1; ++c) {
+      if (own_in_regs && c == s_self) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          // one MFMA tile's 16 values at a time: the accumulators already fill the registers
+          // (cast whole vectors: hipcc lowers a bit_cast of one vector element to a load of
+          // element 0)
+          f32x4 v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            v[q] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, vo, soff(c, i, j, q), SC1));
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += v[q][e];
+          __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    if (tid == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 
   // ---- epilogue: lane l holds row m = l % 32 of each MFMA tile; register 4 q + e of tile
   // (i, j) is column n = n0 + wn * WTN + j * 32 + q * 8 + 4 g + e (N % 4 == 0, so a run of 4
@@ -455,12 +604,53 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
         }
       }
   }
+  }  // tiles of this workgroup
+}
+
+// Compute units of the current device (one GEMM workgroup fits a CU: its LDS use is > 80 KB).
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    cached[dev] = v;
+  }
+  return cached[dev];
+}
+
+static int64_t sk_workspace_bytes(int groups) {
+  return SK_CTR_BYTES + 2 * (int64_t)groups * SK_SLOT_BYTES;
+}
+
+// The schedule of T tiles of nk K stages (cut in units of `gran` stages) on `cus` compute
+// units. Whole tiles while the last wave of workgroups would still be >= 92 % full; otherwise
+// all but one full wave run whole tiles and the remaining S tiles (one to two waves' worth) are
+// cut along K over `cus` workgroups, each taking at least SK_MIN_STAGES stages.
+static SkPlan sk_plan(int T, int nk, int gran, int cus, int64_t ws_bytes) {
+  const int nu = (nk + gran - 1) / gran;
+  SkPlan pl = {T, 0, nu, gran, 0};
+  if (cus <= 0 || T <= 0) return pl;
+  const int waves = (T + cus - 1) / cus;
+  if ((double)T >= 0.92 * (double)waves * cus) return pl;
+  const int dp = (T / cus > 1 ? T / cus - 1 : 0) * cus;
+  const int S = T - dp;
+  const int64_t units = (int64_t)S * nu;
+  const int64_t min_units = std::max(1, SK_MIN_STAGES / gran);
+  const int groups = (int)std::min<int64_t>(cus, units / min_units);
+  if (S > SK_MAX_TILES || groups < 2 || ws_bytes < sk_workspace_bytes(groups)) return pl;
+  pl.dp = dp;
+  pl.groups = groups;
+  pl.units = units;
+  return pl;
 }
 
 template <Elem E>
 static int gemm_launch(const char* name, int nproblems, const difflet_gemm_problem* problems,
                        int64_t n, int64_t k, int epilogue, int64_t act_col_start,
-                       hipStream_t stream) {
+                       void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   constexpr int KT = ElemTraits<E>::KT;
   constexpr int EB = ElemTraits<E>::BYTES;
   DLT_REQUIRE(problems && nproblems >= 1 && nproblems <= MAX_PROBLEMS, DIFFLET_EINVAL,
@@ -537,8 +727,13 @@ static int gemm_launch(const char* name, int nproblems, const difflet_gemm_probl
   if (tiles == 0) return DIFFLET_OK;
   DLT_REQUIRE(tiles < (1LL << 30), DIFFLET_EUNSUPPORTED, "%s: too many tiles", name);
   args.total_tiles = (int)tiles;
+  DLT_REQUIRE(workspace_bytes >= 0 && (workspace == nullptr || ((uintptr_t)workspace & 255) == 0),
+              DIFFLET_EINVAL, "%s: workspace must be 256-byte aligned", name);
+  args.sk = sk_plan((int)tiles, (int)(k / KT), E == Elem::MX ? 8 : 1,
+                    workspace ? device_cus() : 0, workspace ? workspace_bytes : 0);
+  args.ws = (uint8_t*)workspace;
   constexpr int NT = ElemTraits<E>::WN;
-  dim3 grid((unsigned)tiles), block(128 * NT);
+  dim3 grid((unsigned)(args.sk.dp + args.sk.groups)), block(128 * NT);
   switch (epilogue) {
     case DIFFLET_EPI_NONE:
       hipLaunchKernelGGL((gemm_kernel<E, DIFFLET_EPI_NONE, NT>), grid, block, 0, stream, args);
@@ -558,23 +753,79 @@ static int gemm_launch(const char* name, int nproblems, const difflet_gemm_probl
 
 using namespace dlt;
 
+extern "C" int64_t difflet_rocm_gemm_workspace_bytes(void) {
+  const int cus = device_cus();
+  return cus > 0 ? sk_workspace_bytes(cus) : 0;
+}
+
 extern "C" int difflet_rocm_gemm_bf16(int nproblems, const difflet_gemm_problem* problems,
                                       int64_t n, int64_t k, int epilogue,
-                                      int64_t act_col_start, difflet_stream_t stream) {
+                                      int64_t act_col_start, void* workspace,
+                                      int64_t workspace_bytes, difflet_stream_t stream) {
   return gemm_launch<Elem::BF16>("gemm_bf16", nproblems, problems, n, k, epilogue,
-                                 act_col_start, (hipStream_t)stream);
+                                 act_col_start, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 extern "C" int difflet_rocm_gemm_fp8_rowwise(int nproblems, const difflet_gemm_problem* problems,
                                              int64_t n, int64_t k, int epilogue,
-                                             int64_t act_col_start, difflet_stream_t stream) {
+                                             int64_t act_col_start, void* workspace,
+                                             int64_t workspace_bytes, difflet_stream_t stream) {
   return gemm_launch<Elem::FP8>("gemm_fp8_rowwise", nproblems, problems, n, k, epilogue,
-                                act_col_start, (hipStream_t)stream);
+                                act_col_start, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 extern "C" int difflet_rocm_gemm_mxfp8(int nproblems, const difflet_gemm_problem* problems,
                                        int64_t n, int64_t k, int epilogue, int64_t act_col_start,
+                                       void* workspace, int64_t workspace_bytes,
                                        difflet_stream_t stream) {
   return gemm_launch<Elem::MX>("gemm_mxfp8", nproblems, problems, n, k, epilogue,
-                               act_col_start, (hipStream_t)stream);
+                               act_col_start, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+// Host walk of the split schedule the kernels follow (same functions): every (tile, K stage)
+// runs on exactly one workgroup, each cut tile's contributors are the workgroups the kernels
+// sum, and no two cut tiles share a workspace slot. Returns 0, or the first violated check's
+// number; dp / groups receive the plan.
+extern "C" int difflet_rocm_gemm_schedule_check(int tiles, int k_stages, int gran, int cus,
+                                                int64_t workspace_bytes, int* dp, int* groups) {
+  if (tiles <= 0 || k_stages <= 0 || gran <= 0 || cus <= 0) return 1;
+  const SkPlan pl = sk_plan(tiles, k_stages, gran, cus, workspace_bytes);
+  if (dp) *dp = pl.dp;
+  if (groups) *groups = pl.groups;
+  if (pl.groups == 0) return pl.dp == tiles ? 0 : 2;
+  if (pl.dp % cus != 0 || pl.dp + (int64_t)pl.units / pl.nu != tiles) return 3;
+  const int S = tiles - pl.dp;
+  std::vector<int> covered((size_t)S * k_stages, 0);  // per (tile, K stage)
+  std::vector<int> slot_tile(2 * (size_t)pl.groups, -1);
+  for (int s = 0; s < pl.groups; ++s) {
+    const int64_t lo = sk_lo(pl, s), hi = sk_lo(pl, s + 1);
+    if (hi - lo < std::max(1, SK_MIN_STAGES / gran)) return 4;
+    for (int64_t u = lo; u < hi;) {  // the kernel's walk
+      const int tl = (int)(u / pl.nu);
+      const int ub = (int)(u - (int64_t)tl * pl.nu);
+      const int ue = (int)(std::min(hi, (int64_t)(tl + 1) * pl.nu) - (int64_t)tl * pl.nu);
+      const int kbeg = ub * gran, kend = std::min(ue * gran, k_stages);
+      if (kbeg >= kend) return 11;
+      for (int k = kbeg; k < kend; ++k) covered[(size_t)tl * k_stages + k] += 1;
+      if (kbeg != 0 || kend != k_stages) {  // a cut tile
+        const int c0 = sk_owner(pl, (int64_t)tl * pl.nu);
+        const int c1 = sk_owner(pl, (int64_t)(tl + 1) * pl.nu - 1);
+        if (s < c0 || s > c1 || c1 == c0) return 5;
+        const int slot = sk_slot(pl, s, tl);
+        if (slot < 2 * s || slot > 2 * s + 1) return 6;
+        if (slot_tile[slot] != -1) return 7;
+        slot_tile[slot] = tl;
+      }
+      u += ue - ub;
+    }
+  }
+  for (int v : covered)
+    if (v != 1) return 8;
+  for (int tl = 0; tl < S; ++tl) {  // contributors per the formula own exactly the tile's units
+    const int64_t x0 = (int64_t)tl * pl.nu, x1 = x0 + pl.nu;
+    const int c0 = sk_owner(pl, x0), c1 = sk_owner(pl, x1 - 1);
+    if (sk_lo(pl, c0) > x0 || sk_lo(pl, c1 + 1) < x1) return 9;
+    if (c0 < c1 && sk_lo(pl, c0 + 1) <= x0) return 10;
+  }
+  return 0;
 }

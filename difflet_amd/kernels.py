@@ -160,9 +160,31 @@ _GEMM_FN = {"bf16": "difflet_rocm_gemm_bf16", "fp8": "difflet_rocm_gemm_fp8_roww
             "mx": "difflet_rocm_gemm_mxfp8"}
 
 
+_WORKSPACE: dict[int, torch.Tensor] = {}
+
+
+def gemm_workspace(dev: torch.device) -> torch.Tensor:
+    """The device's shared split-GEMM workspace, zero-filled once on first use. It serves GEMMs
+    issued in order on one stream at a time; concurrent streams pass their own."""
+    i = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _WORKSPACE.get(i)
+    if ws is None:
+        with torch.cuda.device(i):
+            nbytes = int(lib().difflet_rocm_gemm_workspace_bytes())
+        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=torch.device("cuda", i))
+        _WORKSPACE[i] = ws
+    return ws
+
+
 def gemm_grouped(problems: Sequence[Problem], *, kind: str = "bf16",
-                 epilogue: int = _lib.EPI_NONE, act_col_start: int = 0) -> None:
-    """Runs up to 4 GEMMs sharing N, K and the epilogue in one launch (writes each p.c)."""
+                 epilogue: int = _lib.EPI_NONE, act_col_start: int = 0,
+                 workspace: torch.Tensor | None | str = None) -> None:
+    """Runs up to 4 GEMMs sharing N, K and the epilogue in one launch (writes each p.c).
+    workspace: None (every tile whole on one workgroup, the default), "shared" (the device's,
+    see gemm_workspace) or a zero-filled uint8 tensor of difflet_rocm_gemm_workspace_bytes()
+    bytes, which lets poorly filled launches cut tiles along K. On MI355X at the DiT shapes the
+    cut tiles measure slower than whole ones: workgroups that start mid-tile no longer share
+    K slices of A and W through their XCD's L2."""
     if not problems:
         return
     dev = _on_gpu(*[p.a for p in problems], *[p.w for p in problems])
@@ -195,9 +217,15 @@ def gemm_grouped(problems: Sequence[Problem], *, kind: str = "bf16",
         q.w_scale = p.w_scale.data_ptr() if p.w_scale is not None else None
         q.m = p.a.shape[0]
         q.rows_per_batch = p.rows_per_batch or p.a.shape[0]
+    if isinstance(workspace, str):
+        if workspace != "shared":
+            raise ValueError(f"workspace must be 'shared', a tensor or None, got {workspace!r}")
+        workspace = gemm_workspace(dev)
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
+                                                           workspace.numel())
     fn = getattr(lib(), _GEMM_FN[kind])
-    check(fn(len(problems), arr, n, k, int(epilogue), int(act_col_start), _stream(dev)),
-          f"gemm_{kind}")
+    check(fn(len(problems), arr, n, k, int(epilogue), int(act_col_start), ws_ptr, ws_bytes,
+             _stream(dev)), f"gemm_{kind}")
 
 
 def linear(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, *,

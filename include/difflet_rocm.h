@@ -102,10 +102,24 @@ typedef struct difflet_gemm_problem {
   int64_t rows_per_batch; /* rows of A per batch element, for gate indexing (>= m for one) */
 } difflet_gemm_problem;
 
+/* Workspace of the GEMMs below (all three take the same one). With a workspace, a launch whose
+ * output tiles would leave the last wave of workgroups less than 92 % full cuts part of its tiles
+ * along K over one workgroup per compute unit (stream-K); the workgroup finishing a cut tile
+ * adds the fp32 partial sums of the others in a fixed order, so results are deterministic for
+ * a given device. With workspace NULL (or too small) every tile runs whole on one workgroup.
+ * The workspace must be zero-filled once when allocated; the GEMMs leave it zeroed. Launches
+ * that may overlap in time (different streams) must not share one. Returns the bytes needed on
+ * the current device: 16 KiB of counters + 2 x 256 KiB per compute unit. Measured on MI355X at
+ * the DiT step's shapes, cut tiles run slower than whole ones (workgroups that start mid-tile
+ * stop sharing K slices of A and W through their XCD's L2), so the step passes NULL. No
+ * counterpart in the reference, whose linears call the vendor BLAS (torch.nn.functional.linear,
+ * difflet/backends/cpu/ops_impl/linear.py:9-41). */
+int64_t difflet_rocm_gemm_workspace_bytes(void);
+
 /* bf16 x bf16 -> fp32 accumulate -> bf16. k % 64 == 0. */
 int difflet_rocm_gemm_bf16(int nproblems, const difflet_gemm_problem* problems, int64_t n,
-                           int64_t k, int epilogue, int64_t act_col_start,
-                           difflet_stream_t stream);
+                           int64_t k, int epilogue, int64_t act_col_start, void* workspace,
+                           int64_t workspace_bytes, difflet_stream_t stream);
 
 /* fp8 e4m3 x e4m3 with per-row scales: acc * a_scale[m] * w_scale[n] (both fp32), then the
  * epilogue. a_scale / w_scale come from difflet_rocm_quantize_fp8_rowwise. k % 128 == 0.
@@ -113,6 +127,7 @@ int difflet_rocm_gemm_bf16(int nproblems, const difflet_gemm_problem* problems, 
  * difflet/quant/spec.py:22-33); it is the per-channel x per-token linear of the FLUX fp8 step. */
 int difflet_rocm_gemm_fp8_rowwise(int nproblems, const difflet_gemm_problem* problems,
                                   int64_t n, int64_t k, int epilogue, int64_t act_col_start,
+                                  void* workspace, int64_t workspace_bytes,
                                   difflet_stream_t stream);
 
 /* MXFP8: e4m3 codes in swizzled K order with one E8M0 scale (uint8) per 32 values along K,
@@ -121,8 +136,17 @@ int difflet_rocm_gemm_fp8_rowwise(int nproblems, const difflet_gemm_problem* pro
  * computes what difflet/quant/fake_linear.py:56-61 (FakeQuantMXLinear.forward) computes.
  * k % 128 == 0. */
 int difflet_rocm_gemm_mxfp8(int nproblems, const difflet_gemm_problem* problems, int64_t n,
-                            int64_t k, int epilogue, int64_t act_col_start,
-                            difflet_stream_t stream);
+                            int64_t k, int epilogue, int64_t act_col_start, void* workspace,
+                            int64_t workspace_bytes, difflet_stream_t stream);
+
+/* Host-side check of the split schedule the GEMMs use for `tiles` output tiles of `k_stages`
+ * K stages, cut in units of `gran` stages (1; 8 for MXFP8), on `cus` compute units with
+ * `workspace_bytes` of workspace: each (tile, stage) runs on exactly one workgroup, and cut
+ * tiles are summed from the right contributors and slots. Returns 0 or the number of the failed
+ * check; *dp / *groups receive the whole-tile count and the number of split workgroups. Runs on
+ * the CPU only (for tests). */
+int difflet_rocm_gemm_schedule_check(int tiles, int k_stages, int gran, int cus,
+                                     int64_t workspace_bytes, int* dp, int* groups);
 
 /* ------------------------------------------------------------------------------------------
  * Quantizers (bit-exact with the CPU laws).

@@ -30,7 +30,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     lib = _lib.load()
     for name in declared_symbols():
         assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
-    assert lib.difflet_rocm_abi_version() == 1
+    assert lib.difflet_rocm_abi_version() == 2
     assert b"gfx950" in lib.difflet_rocm_version()
 
 
@@ -39,7 +39,7 @@ def test_error_paths_report_without_a_gpu():
     from difflet_amd import _lib
 
     lib = _lib.load()
-    st = lib.difflet_rocm_gemm_bf16(0, None, 64, 64, 0, 0, None)
+    st = lib.difflet_rocm_gemm_bf16(0, None, 64, 64, 0, 0, None, 0, None)
     assert st == _lib.EINVAL
     assert b"nproblems" in lib.difflet_rocm_last_error()
     st = lib.difflet_rocm_attention(None, None, None, None, _lib.BF16, 1, 1, 1, 1, 128, None,
@@ -48,3 +48,51 @@ def test_error_paths_report_without_a_gpu():
     assert st == _lib.EINVAL
     with pytest.raises(ValueError):
         _lib.check(st, "attention")
+
+
+@pytest.mark.parametrize("cus", [256, 304, 80])
+def test_gemm_split_schedule_covers_every_stage_once(cus):
+    """The GEMMs' stream-K schedule, walked on the host with the kernels' own functions: every
+    (tile, K stage) runs exactly once, cut tiles are summed from their true contributors, and
+    no two cut tiles share a workspace slot."""
+    import ctypes
+
+    from difflet_amd import _lib
+
+    lib = _lib.load()
+    ws = 16384 + 2 * cus * 256 * 256 * 4
+    dp, groups = ctypes.c_int(), ctypes.c_int()
+    split = 0
+    for tiles in list(range(1, 40)) + [216, 255, 256, 257, 336, 392, 648, 864, 1008, 1344,
+                                       1512, 7 * cus + 5]:
+        for nk, gran in ((1, 1), (2, 1), (7, 1), (8, 1), (48, 1), (96, 1), (192, 1), (480, 1),
+                         (6, 8), (48, 8), (50, 8), (192, 8)):
+            r = lib.difflet_rocm_gemm_schedule_check(tiles, nk, gran, cus, ws, ctypes.byref(dp),
+                                                     ctypes.byref(groups))
+            assert r == 0, (tiles, nk, gran, r)
+            assert 0 <= dp.value <= tiles
+            if groups.value:
+                split += 1
+                assert dp.value % cus == 0 and groups.value <= cus
+    assert split > 50  # the split path is exercised
+
+
+def test_gemm_split_plan_at_the_step_shapes():
+    import ctypes
+
+    from difflet_amd import _lib
+
+    lib = _lib.load()
+    ws = 16384 + 2 * 256 * 256 * 256 * 4
+    dp, groups = ctypes.c_int(), ctypes.c_int()
+    # a 216-tile launch on 256 CUs splits all of its tiles; a 1512-tile one (98 % full) splits none
+    assert lib.difflet_rocm_gemm_schedule_check(216, 96, 1, 256, ws, ctypes.byref(dp),
+                                                ctypes.byref(groups)) == 0
+    assert (dp.value, groups.value) == (0, 256)
+    assert lib.difflet_rocm_gemm_schedule_check(1512, 96, 1, 256, ws, ctypes.byref(dp),
+                                                ctypes.byref(groups)) == 0
+    assert (dp.value, groups.value) == (1512, 0)
+    # without enough workspace nothing is split
+    assert lib.difflet_rocm_gemm_schedule_check(216, 96, 1, 256, 1 << 20, ctypes.byref(dp),
+                                                ctypes.byref(groups)) == 0
+    assert (dp.value, groups.value) == (216, 0)
