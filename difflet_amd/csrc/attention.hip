@@ -5,6 +5,8 @@
 //
 // Work split: a 256-thread workgroup (4 wavefronts) owns 128 query rows of one (batch, head);
 // each wavefront owns 32 of them. K/V stream through LDS in tiles of 64 keys, double-buffered.
+// Unmasked attention over more than 1024 keys runs the ping-pong variant (attn_pp_kernel,
+// below): 8 wavefronts, 256 queries, two groups alternating MFMA and softmax phases.
 //
 // Operand roles. Scores are computed transposed, S^T = K Q^T (MFMA 32x32x16, first operand a K
 // fragment, second a Q fragment held in registers for the whole kernel), so accumulator lane l
@@ -93,6 +95,22 @@ __device__ __forceinline__ int k_off(int row, int chunk) { return row * K_PITCH 
 __device__ __forceinline__ int vt_quad_pos(int q) {
   const int r = q & 3;
   return (q & ~3) | (r == 1 ? 2 : r == 2 ? 1 : r);
+}
+
+// max / sum of x over lanes l and l ^ 32 (the two lanes holding one query's statistics).
+// v_permlane32_swap exchanges the upper half of its first operand with the lower half of its
+// second: given x twice, the two results hold {x, x of lane l ^ 32} in every lane, so their max
+// or sum is the pair's. A VALU instruction, unlike ds_bpermute, so it neither uses the LDS nor
+// waits on it.
+__device__ __forceinline__ float pair_max(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
 }
 
 template <typename T, bool MASKED>
@@ -244,7 +262,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
     for (int kt2 = 0; kt2 < 2; ++kt2)
 #pragma unroll
       for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kt2][v]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = pair_max(mx);
     const float m_new = fmaxf(m_run, mx * cmul);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
@@ -291,8 +309,224 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
   }
 
   // ---- normalize and write: lane holds query my_q, dims dt*32 + (v/4)*8 + 4g + v%4
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float l_tot = pair_sum(l_run);
   const float inv = 1.0f / l_tot;
+  if (my_q < a.seq_q) {
+    T* op = reinterpret_cast<T*>(a.o) + b * a.os[0] + h * a.os[1] + (int64_t)my_q * a.os[2];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        u32x2 w;
+        w[0] = MfmaT<T>::pack2(acc[dt][q4 * 4 + 0] * inv, acc[dt][q4 * 4 + 1] * inv);
+        w[1] = MfmaT<T>::pack2(acc[dt][q4 * 4 + 2] * inv, acc[dt][q4 * 4 + 3] * inv);
+        *reinterpret_cast<u32x2*>(op + dt * 32 + q4 * 8 + g * 4) = w;
+      }
+  }
+}
+
+// Unmasked fast path: ping-pong between two wavefront groups. A 512-thread workgroup owns 256
+// queries; waves 0-3 (group A) and 4-7 (group B) each own 128, 32 per wave, and wave w shares
+// its SIMD with wave w ^ 4. Time is cut into phases separated by workgroup barriers; in every
+// phase one group runs MFMAs (the previous tile's P V and the next tile's scores) while the
+// other runs the softmax of its current tile on the VALU, then they swap, so each SIMD's matrix
+// core and VALU work on different waves at once. B trails A by one phase:
+//   phase 2j:     A: softmax(j), stores V(j), loads V(j + 1)  |  B: P V(j - 1), scores(j + 0)
+//   phase 2j + 1: A: P V(j), scores(j + 1)                    |  B: softmax(j), stores K(j + 2),
+//                                                                loads K(j + 3)
+// K(j) lives in sk[j & 1] (read in phases 2j - 1 and 2j, refilled in 2j + 1), V(j) in sv[j & 1]
+// (written in 2j, read in 2j + 1 and 2j + 2). The MFMA group raises its wave priority so the
+// SIMD issues its MFMAs first whenever the matrix core frees up.
+template <typename T>
+__global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
+  typedef typename MfmaT<T>::frag frag;
+  __shared__ __attribute__((aligned(16))) uint8_t sk[2][BLOCK_N * K_PITCH];
+  __shared__ __attribute__((aligned(16))) uint8_t sv[2][HD * VT_PITCH];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool grp_a = wave < 4;
+  const int gt = tid & 255;  // thread index within the group
+  const int col = lane & 31, g = lane >> 5;
+
+  int bid = blockIdx.x;  // XCD-contiguous runs of query tiles (whole heads share an L2)
+  if ((a.total & 7) == 0) bid = (bid & 7) * (a.total >> 3) + (bid >> 3);
+  const int bh = bid / a.q_tiles;
+  const int qt = bid % a.q_tiles;
+  const int b = bh / a.heads, h = bh % a.heads;
+  const int my_q = qt * (2 * BLOCK_M) + wave * 32 + col;
+
+  const uint8_t* qp = a.q + (b * a.qs[0] + h * a.qs[1]) * 2;
+  const uint8_t* kp = a.k + (b * a.ks[0] + h * a.ks[1]) * 2;
+  const uint8_t* vp = a.v + (b * a.vs[0] + h * a.vs[1]) * 2;
+  const int64_t qrow = a.qs[2] * 2, krow = a.ks[2] * 2, vrow = a.vs[2] * 2;
+
+  frag qf[8];  // Q fragments (second MFMA operand): row my_q, dims 16c + 8g .. +8
+  {
+    const __amdgpu_buffer_rsrc_t rq =
+        make_rsrc(qp, (uint32_t)min((int64_t)a.seq_q * qrow, (int64_t)0xffffffff));
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+      qf[c] = __builtin_bit_cast(frag, buf_load16(rq, (uint32_t)(my_q * qrow) + (c * 16 + g * 8) * 2));
+  }
+  const __amdgpu_buffer_rsrc_t rk =
+      make_rsrc(kp, (uint32_t)min((int64_t)a.seq_k * krow, (int64_t)0xffffffff));
+  const __amdgpu_buffer_rsrc_t rv =
+      make_rsrc(vp, (uint32_t)min((int64_t)a.seq_k * vrow, (int64_t)0xffffffff));
+
+  // staging, 256 threads per tile: group B moves K (rows gt / 16 + 16 i, chunk gt % 16),
+  // group A moves V (keys 4 (gt % 16) + i, dims 8 (gt / 16) .. +8, transposed into V^T)
+  const int kr = gt >> 4, kc = gt & 15;
+  const int vkg = gt & 15, vdg = gt >> 4;
+  const int vt_pos = vt_quad_pos(vkg) * 8;
+  u32x4 stg[4];
+  auto load_k = [&](int j0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) stg[i] = buf_load16(rk, (uint32_t)((j0 + kr + 16 * i) * krow) + kc * 16);
+  };
+  auto store_k = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(&sk[st][k_off(kr + 16 * i, kc)]) = stg[i];
+  };
+  auto load_v = [&](int j0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) stg[i] = buf_load16(rv, (uint32_t)((j0 + vkg * 4 + i) * vrow) + vdg * 16);
+  };
+  auto store_v = [&](int st) {
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const int w = d >> 1, sh = (d & 1) * 16;
+      const uint32_t k0 = (stg[0][w] >> sh) & 0xffffu, k1 = (stg[1][w] >> sh) & 0xffffu;
+      const uint32_t k2 = (stg[2][w] >> sh) & 0xffffu, k3 = (stg[3][w] >> sh) & 0xffffu;
+      u32x2 pk;
+      pk[0] = k0 | (k1 << 16);
+      pk[1] = k2 | (k3 << 16);
+      *reinterpret_cast<u32x2*>(&sv[st][(vdg * 8 + d) * VT_PITCH + vt_pos]) = pk;
+    }
+  };
+
+  f32x16 acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = f32x16{};
+  f32x16 s[2];          // scores of the tile being softmaxed next
+  uint32_t pp[2][8];    // P of the tile being multiplied next, packed 16-bit pairs
+  float m_run = -INFINITY, l_run = 0.f;
+  const float cmul = a.scale_log2;
+  const int ntiles = (a.seq_k + BLOCK_N - 1) / BLOCK_N;
+
+  auto scores = [&](int st) {  // S^T = K Q^T of the tile in sk[st]
+#pragma unroll
+    for (int kt2 = 0; kt2 < 2; ++kt2) {
+      s[kt2] = f32x16{};
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const frag kf = *reinterpret_cast<const frag*>(&sk[st][k_off(kt2 * 32 + col, c * 2 + g)]);
+        s[kt2] = MfmaT<T>::mma(kf, qf[c], s[kt2]);
+      }
+    }
+  };
+  auto pv = [&](int st) {  // O^T += V^T P^T of the tile in sv[st]
+#pragma unroll
+    for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int base = kt2 * 32 + hh * 16;
+        u32x4 pb;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) pb[u] = pp[kt2][hh * 4 + u];
+        const frag pf = __builtin_bit_cast(frag, pb);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const frag vf = *reinterpret_cast<const frag*>(
+              &sv[st][(dt * 32 + col) * VT_PITCH + (base + g * 8) * 2]);
+          acc[dt] = MfmaT<T>::mma(vf, pf, acc[dt]);
+        }
+      }
+  };
+  auto softmax = [&](int j0) {  // online softmax of s (keys j0 ..), P into pp
+    if (j0 + BLOCK_N > a.seq_k) {  // last tile: keys past seq_k do not exist
+#pragma unroll
+      for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = j0 + kt2 * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+          if (key >= a.seq_k) s[kt2][v] = -INFINITY;
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kt2][v]);
+    mx = pair_max(mx);
+    const float m_new = fmaxf(m_run, mx * cmul);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    m_run = m_new;
+    float ls = 0.f;
+#pragma unroll
+    for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+      for (int v = 0; v < 16; v += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt2][v], cmul, -m_use));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt2][v + 1], cmul, -m_use));
+        ls += p0 + p1;
+        pp[kt2][v >> 1] = MfmaT<T>::pack2(p0, p1);
+      }
+    l_run = l_run * alpha + ls;
+    if (__any(alpha != 1.0f)) {  // the running max moved for some query of this wave
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][v] *= alpha;
+    }
+  };
+
+  // The two groups run separate loops with the same barrier sequence (2 + 2 ntiles
+  // barriers), so each loop's registers are allocated for that group alone.
+  if (grp_a) {
+    load_v(0);
+    __syncthreads();  // prologue: B has K(0), K(1) in LDS
+    scores(0);
+    __syncthreads();
+    for (int jt = 0; jt < ntiles; ++jt) {
+      const int j0 = jt * BLOCK_N;
+      softmax(j0);  // phase 2j
+      store_v(jt & 1);
+      if (jt + 1 < ntiles) load_v(j0 + BLOCK_N);
+      __syncthreads();
+      __builtin_amdgcn_s_setprio(1);  // phase 2j + 1
+      pv(jt & 1);
+      if (jt + 1 < ntiles) scores((jt + 1) & 1);
+      __builtin_amdgcn_s_setprio(0);
+      __syncthreads();
+    }
+  } else {
+    load_k(0);
+    store_k(0);
+    if (ntiles > 1) {
+      load_k(BLOCK_N);
+      store_k(1);
+    }
+    if (ntiles > 2) load_k(2 * BLOCK_N);
+    __syncthreads();
+    __syncthreads();  // A scores tile 0
+    for (int jt = 0; jt < ntiles; ++jt) {
+      const int j0 = jt * BLOCK_N;
+      __builtin_amdgcn_s_setprio(1);  // phase 2j
+      if (jt > 0) pv((jt - 1) & 1);
+      scores(jt & 1);
+      __builtin_amdgcn_s_setprio(0);
+      __syncthreads();
+      softmax(j0);  // phase 2j + 1
+      if (jt + 2 < ntiles) store_k(jt & 1);
+      if (jt + 3 < ntiles) load_k(j0 + 3 * BLOCK_N);
+      __syncthreads();
+    }
+    pv((ntiles - 1) & 1);  // phase 2n
+  }
+
+  const float inv = 1.0f / pair_sum(l_run);
   if (my_q < a.seq_q) {
     T* op = reinterpret_cast<T*>(a.o) + b * a.os[0] + h * a.os[1] + (int64_t)my_q * a.os[2];
 #pragma unroll
@@ -345,9 +579,10 @@ extern "C" int difflet_rocm_attention(const void* q, const void* k, const void* 
                     ((uintptr_t)ps[i] & 15) == 0,
                 DIFFLET_EINVAL, "attention: rows must be 16-byte aligned (strides %% 8 == 0)");
   }
-  // keys / queries up to one tile past the end are addressed (and read as zero through the
-  // buffer range check), so the byte offsets of seq + 128 rows must fit 32 bits
-  DLT_REQUIRE((seq_q + 128) * q_strides[2] * 2 < (1LL << 32) &&
+  // queries up to one workgroup tile (256) and keys up to two K/V tiles past the end are
+  // addressed (and read as zero through the buffer range check), so those byte offsets must
+  // fit 32 bits
+  DLT_REQUIRE((seq_q + 256) * q_strides[2] * 2 < (1LL << 32) &&
                   (seq_k + 128) * k_strides[2] * 2 < (1LL << 32) &&
                   (seq_k + 128) * v_strides[2] * 2 < (1LL << 32),
               DIFFLET_EUNSUPPORTED, "attention: one head's sequence exceeds 4 GiB");
@@ -368,7 +603,13 @@ extern "C" int difflet_rocm_attention(const void* q, const void* k, const void* 
   args.heads = (int)heads;
   args.seq_q = (int)seq_q;
   args.seq_k = (int)seq_k;
-  args.q_tiles = (int)((seq_q + BLOCK_M - 1) / BLOCK_M);
+  // the fast paths need scale > 0 (scores stay raw and are scaled inside exp2); the ping-pong
+  // kernel pays a few tiles of pipeline fill, so short key sequences (cross-attention to text)
+  // run the single-group kernel
+  const bool masked = causal || mask || bound_min || !(scale > 0.0f);
+  const bool pingpong = !masked && seq_k > 1024;
+  const int qblock = pingpong ? 2 * BLOCK_M : BLOCK_M;  // queries per workgroup
+  args.q_tiles = (int)((seq_q + qblock - 1) / qblock);
   const int64_t total = (int64_t)args.q_tiles * batch * heads;
   DLT_REQUIRE(total < (1LL << 31), DIFFLET_EUNSUPPORTED, "attention: too many tiles");
   args.total = (int)total;
@@ -382,16 +623,16 @@ extern "C" int difflet_rocm_attention(const void* q, const void* k, const void* 
   args.bmax = bound_max;
   if (bound_min)
     for (int i = 0; i < 3; ++i) args.bs[i] = bound_strides[i];
-  // the fast path keeps scores raw and scales inside exp2, which needs scale > 0
-  const bool masked = causal || mask || bound_min || !(scale > 0.0f);
   hipStream_t s = (hipStream_t)stream;
-  dim3 grid((unsigned)total), block(256);
+  dim3 grid((unsigned)total);
   if (dtype == DIFFLET_BF16) {
-    if (masked) hipLaunchKernelGGL((attn_fwd_kernel<bf16, true>), grid, block, 0, s, args);
-    else hipLaunchKernelGGL((attn_fwd_kernel<bf16, false>), grid, block, 0, s, args);
+    if (pingpong) hipLaunchKernelGGL((attn_pp_kernel<bf16>), grid, dim3(512), 0, s, args);
+    else if (masked) hipLaunchKernelGGL((attn_fwd_kernel<bf16, true>), grid, dim3(256), 0, s, args);
+    else hipLaunchKernelGGL((attn_fwd_kernel<bf16, false>), grid, dim3(256), 0, s, args);
   } else {
-    if (masked) hipLaunchKernelGGL((attn_fwd_kernel<f16, true>), grid, block, 0, s, args);
-    else hipLaunchKernelGGL((attn_fwd_kernel<f16, false>), grid, block, 0, s, args);
+    if (pingpong) hipLaunchKernelGGL((attn_pp_kernel<f16>), grid, dim3(512), 0, s, args);
+    else if (masked) hipLaunchKernelGGL((attn_fwd_kernel<f16, true>), grid, dim3(256), 0, s, args);
+    else hipLaunchKernelGGL((attn_fwd_kernel<f16, false>), grid, dim3(256), 0, s, args);
   }
   return dlt_check_launch("attention");
 }

@@ -221,8 +221,11 @@ def _attn_case(g, b, h, sq, sk, d=128, dtype=torch.bfloat16):
     return q, k, v
 
 
+# seq_k > 1024 runs the ping-pong kernel (256 queries per workgroup): ragged query and key
+# counts, a single query, 17 / 18 / 32 key tiles, several batches and heads
 @pytest.mark.parametrize("b,h,sq,sk", [(1, 2, 128, 64), (1, 3, 200, 333), (2, 2, 77, 1000),
-                                       (1, 2, 4608, 4608), (1, 2, 3000, 512)])
+                                       (1, 2, 4608, 4608), (1, 2, 3000, 512), (1, 2, 300, 1025),
+                                       (2, 3, 777, 1100), (1, 1, 1, 2048), (1, 2, 513, 1088)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_attention_matches_fp32(gpu, b, h, sq, sk, dtype):
     print(f"attention b={b} h={h} sq={sq} sk={sk} {dtype}", flush=True)
@@ -281,10 +284,11 @@ def test_attention_bounds_equal_mask_and_fully_masked_rows_average_v(gpu):
         kernels.attention(q.to(gpu), k.to(gpu), v.to(gpu), scale=1.0, bound_min=bmin.to(gpu))
 
 
-def test_attention_strided_inplace_over_q(gpu):
+@pytest.mark.parametrize("s", [333, 1500])
+def test_attention_strided_inplace_over_q(gpu, s):
     """The DiT layout: q/k/v are column ranges of one [S, 3D] buffer; output over q."""
     g = torch.Generator().manual_seed(8)
-    s, hds = 333, 3
+    hds = 3
     d = hds * 128
     buf = rnd(g, s, 3 * d)
     ref_q, ref_k, ref_v = (buf[:, i * d:(i + 1) * d].reshape(s, hds, 128).transpose(0, 1).float()
