@@ -337,6 +337,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
 // K(j) lives in sk[j & 1] (read in phases 2j - 1 and 2j, refilled in 2j + 1), V(j) in sv[j & 1]
 // (written in 2j, read in 2j + 1 and 2j + 2). The MFMA group raises its wave priority so the
 // SIMD issues its MFMAs first whenever the matrix core frees up.
+// Workgroup barrier between ping-pong phases: this wave's LDS reads and writes are done
+// (lgkmcnt(0)), then s_barrier. Unlike __syncthreads it does not wait for the global loads in
+// flight: those feed the LDS only two phases later, and waiting here exposed their latency.
+__device__ __forceinline__ void phase_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt / expcnt untouched
+  asm volatile("s_barrier" ::: "memory");
+}
+
 template <typename T>
 __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
   typedef typename MfmaT<T>::frag frag;
@@ -409,12 +417,60 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) acc[i] = f32x16{};
   f32x16 s[2];          // scores of the tile being softmaxed next
-  uint32_t pp[2][8];    // P of the tile being multiplied next, packed 16-bit pairs
+  uint32_t pp[2][8] = {};  // P of the tile being multiplied next, packed 16-bit pairs
   float m_run = -INFINITY, l_run = 0.f;
   const float cmul = a.scale_log2;
   const int ntiles = (a.seq_k + BLOCK_N - 1) / BLOCK_N;
 
-  auto scores = [&](int st) {  // S^T = K Q^T of the tile in sk[st]
+  // One MFMA phase: O^T += V^T P^T of the tile in sv[vst] (4 groups of 4 MFMAs, one per
+  // 16 keys), then S^T = K Q^T of the tile in sk[kst] (4 groups: two d-chunks for both 32-key
+  // blocks, so consecutive MFMAs are independent). The fragments of group i + 1 are read
+  // while group i's MFMAs run; sched_barrier keeps the compiler from pulling each read down
+  // next to its MFMA, where every MFMA would wait out a full LDS latency.
+  auto mfma_phase = [&](int vst, int kst) {
+    frag fb[2][4];
+    auto load_group = [&](int gi, frag (&f)[4]) {
+      if (gi < 4) {
+        const int base = (gi >> 1) * 32 + (gi & 1) * 16;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+          f[dt] = *reinterpret_cast<const frag*>(
+              &sv[vst][(dt * 32 + col) * VT_PITCH + (base + g * 8) * 2]);
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int kt2 = u & 1, c = 2 * (gi - 4) + (u >> 1);
+          f[u] = *reinterpret_cast<const frag*>(&sk[kst][k_off(kt2 * 32 + col, c * 2 + g)]);
+        }
+      }
+    };
+    auto run_group = [&](int gi, const frag (&f)[4]) {
+      if (gi < 4) {
+        const int kt2 = gi >> 1, hh = gi & 1;
+        u32x4 pb;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) pb[u] = pp[kt2][hh * 4 + u];
+        const frag pf = __builtin_bit_cast(frag, pb);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) acc[dt] = MfmaT<T>::mma(f[dt], pf, acc[dt]);
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int kt2 = u & 1, c = 2 * (gi - 4) + (u >> 1);
+          s[kt2] = MfmaT<T>::mma(f[u], qf[c], c == 0 ? f32x16{} : s[kt2]);
+        }
+      }
+    };
+    load_group(0, fb[0]);
+#pragma unroll
+    for (int gi = 0; gi < 8; ++gi) {
+      if (gi < 7) load_group(gi + 1, fb[(gi + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      run_group(gi, fb[gi & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto scores_only = [&](int st) {  // the prologue's S^T = K Q^T of tile 0
 #pragma unroll
     for (int kt2 = 0; kt2 < 2; ++kt2) {
       s[kt2] = f32x16{};
@@ -424,24 +480,6 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
         s[kt2] = MfmaT<T>::mma(kf, qf[c], s[kt2]);
       }
     }
-  };
-  auto pv = [&](int st) {  // O^T += V^T P^T of the tile in sv[st]
-#pragma unroll
-    for (int kt2 = 0; kt2 < 2; ++kt2)
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int base = kt2 * 32 + hh * 16;
-        u32x4 pb;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) pb[u] = pp[kt2][hh * 4 + u];
-        const frag pf = __builtin_bit_cast(frag, pb);
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-          const frag vf = *reinterpret_cast<const frag*>(
-              &sv[st][(dt * 32 + col) * VT_PITCH + (base + g * 8) * 2]);
-          acc[dt] = MfmaT<T>::mma(vf, pf, acc[dt]);
-        }
-      }
   };
   auto softmax = [&](int j0) {  // online softmax of s (keys j0 ..), P into pp
     if (j0 + BLOCK_N > a.seq_k) {  // last tile: keys past seq_k do not exist
@@ -486,20 +524,19 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
   // barriers), so each loop's registers are allocated for that group alone.
   if (grp_a) {
     load_v(0);
-    __syncthreads();  // prologue: B has K(0), K(1) in LDS
-    scores(0);
-    __syncthreads();
+    phase_barrier();  // prologue: B has K(0), K(1) in LDS
+    scores_only(0);
+    phase_barrier();
     for (int jt = 0; jt < ntiles; ++jt) {
       const int j0 = jt * BLOCK_N;
       softmax(j0);  // phase 2j
       store_v(jt & 1);
       if (jt + 1 < ntiles) load_v(j0 + BLOCK_N);
-      __syncthreads();
-      __builtin_amdgcn_s_setprio(1);  // phase 2j + 1
-      pv(jt & 1);
-      if (jt + 1 < ntiles) scores((jt + 1) & 1);
+      phase_barrier();
+      __builtin_amdgcn_s_setprio(1);  // phase 2j + 1 (past the last tile the scores read
+      mfma_phase(jt & 1, (jt + 1) & 1);  // the idle K buffer and go unused)
       __builtin_amdgcn_s_setprio(0);
-      __syncthreads();
+      phase_barrier();
     }
   } else {
     load_k(0);
@@ -509,21 +546,24 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
       store_k(1);
     }
     if (ntiles > 2) load_k(2 * BLOCK_N);
-    __syncthreads();
-    __syncthreads();  // A scores tile 0
+    // sv[1] is read as "tile -1" by the first P V (with P = 0): zeros, not stale LDS that
+    // could hold NaN patterns
+    for (int i = gt; i < HD * VT_PITCH / 16; i += 256)
+      *reinterpret_cast<u32x4*>(&sv[1][i * 16]) = u32x4{0u, 0u, 0u, 0u};
+    phase_barrier();
+    phase_barrier();  // A scores tile 0
     for (int jt = 0; jt < ntiles; ++jt) {
       const int j0 = jt * BLOCK_N;
-      __builtin_amdgcn_s_setprio(1);  // phase 2j
-      if (jt > 0) pv((jt - 1) & 1);
-      scores(jt & 1);
+      __builtin_amdgcn_s_setprio(1);  // phase 2j (the first P V is of "tile -1": P = 0)
+      mfma_phase((jt - 1) & 1, jt & 1);
       __builtin_amdgcn_s_setprio(0);
-      __syncthreads();
+      phase_barrier();
       softmax(j0);  // phase 2j + 1
       if (jt + 2 < ntiles) store_k(jt & 1);
       if (jt + 3 < ntiles) load_k(j0 + 3 * BLOCK_N);
-      __syncthreads();
+      phase_barrier();
     }
-    pv((ntiles - 1) & 1);  // phase 2n
+    mfma_phase((ntiles - 1) & 1, ntiles & 1);  // phase 2n: the last P V (scores unused)
   }
 
   const float inv = 1.0f / pair_sum(l_run);
