@@ -125,11 +125,11 @@ template <typename TX, typename TY, typename TM, int NV>
 __global__ __launch_bounds__(256) void layernorm_modulate_kernel(
     const TX* __restrict__ x, int64_t ldx, TY* __restrict__ y, int64_t ldy, int64_t rows,
     int dim, const TM* __restrict__ mul, const TM* __restrict__ add, int64_t mod_stride,
-    int64_t rows_per_batch, int one_plus, float eps) {
+    int64_t rows_per_batch, int64_t split, int one_plus, float eps) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const int64_t b = row / rows_per_batch;
+  const int64_t b = split > 0 ? (row >= split ? 1 : 0) : row / rows_per_batch;
   float v[NV][8];
   ln_modulate_row<TX, TM, NV>(x + row * ldx, dim, mul ? mul + b * mod_stride : nullptr,
                               add ? add + b * mod_stride : nullptr, one_plus, eps, lane, v);
@@ -147,12 +147,12 @@ template <typename TX, typename TM, int NV>
 __global__ __launch_bounds__(256) void layernorm_modulate_fp8_kernel(
     const TX* __restrict__ x, int64_t ldx, uint8_t* __restrict__ q, int64_t ldq,
     float* __restrict__ scale, int64_t rows, int dim, const TM* __restrict__ mul,
-    const TM* __restrict__ add, int64_t mod_stride, int64_t rows_per_batch, int one_plus,
-    float eps) {
+    const TM* __restrict__ add, int64_t mod_stride, int64_t rows_per_batch, int64_t split,
+    int one_plus, float eps) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const int64_t b = row / rows_per_batch;
+  const int64_t b = split > 0 ? (row >= split ? 1 : 0) : row / rows_per_batch;
   float v[NV][8];
   ln_modulate_row<TX, TM, NV>(x + row * ldx, dim, mul ? mul + b * mod_stride : nullptr,
                               add ? add + b * mod_stride : nullptr, one_plus, eps, lane, v);
@@ -253,7 +253,8 @@ __device__ __forceinline__ void rope8(float* v, const float* cs, const float* sn
 template <typename T, typename TW, int LPH>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     T* __restrict__ buf, int64_t ld, int64_t rows, int heads, int64_t q_off, int64_t k_off,
-    int do_norm, const TW* __restrict__ wq, const TW* __restrict__ wk, float eps,
+    int do_norm, const TW* __restrict__ wq, const TW* __restrict__ wk, int64_t split,
+    const TW* __restrict__ wq2, const TW* __restrict__ wk2, float eps,
     const float* __restrict__ cosb, const float* __restrict__ sinb, int64_t rope_rows,
     int law) {
   constexpr int HD = LPH * 8;
@@ -270,7 +271,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   for (int t = 0; t < 2; ++t) {
     const int64_t off = t == 0 ? q_off : k_off;
     if (off < 0) continue;
-    const TW* w = t == 0 ? wq : wk;
+    const bool second = split > 0 && row >= split;  // rows past split: the second weights
+    const TW* w = t == 0 ? (second ? wq2 : wq) : (second ? wk2 : wk);
     T* base = buf + row * ld + off;
     float r_row = 1.f;
     if (do_norm == 2) {
@@ -498,13 +500,13 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 template <typename TX, typename TY, typename TM>
 static int launch_ln(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
                      int64_t dim, const void* mul, const void* add, int64_t mod_stride,
-                     int64_t rpb, int one_plus, float eps, hipStream_t s) {
+                     int64_t rpb, int64_t split, int one_plus, float eps, hipStream_t s) {
   const int nv = (int)((dim + 511) / 512);
   dim3 grid((unsigned)((rows + 3) / 4)), block(256);
 #define DLT_LN(NV)                                                                      \
   hipLaunchKernelGGL((layernorm_modulate_kernel<TX, TY, TM, NV>), grid, block, 0, s,  \
                      (const TX*)x, ldx, (TY*)y, ldy, rows, (int)dim, (const TM*)mul,   \
-                     (const TM*)add, mod_stride, rpb, one_plus, eps)
+                     (const TM*)add, mod_stride, rpb, split, one_plus, eps)
   if (nv <= 2) DLT_LN(2);
   else if (nv <= 4) DLT_LN(4);
   else if (nv <= 6) DLT_LN(6);
@@ -521,9 +523,10 @@ extern "C" int difflet_rocm_layernorm_modulate(const void* x, int64_t ldx, void*
                                                int64_t rows, int64_t dim, const void* mul,
                                                const void* add, int mod_dtype,
                                                int64_t mod_stride, int64_t rows_per_batch,
-                                               int one_plus, float eps,
+                                               int64_t split, int one_plus, float eps,
                                                difflet_stream_t stream) {
   DLT_REQUIRE(x && y, DIFFLET_EINVAL, "layernorm: null pointer");
+  DLT_REQUIRE(split >= 0, DIFFLET_EINVAL, "layernorm: split must be >= 0");
   DLT_REQUIRE(rows >= 0 && dim > 0 && dim % 8 == 0, DIFFLET_EINVAL,
               "layernorm: dim %lld must be a positive multiple of 8", (long long)dim);
   DLT_REQUIRE(ldx % 8 == 0 && ldy % 8 == 0 && (mod_stride % 8 == 0 || (!mul && !add)),
@@ -538,21 +541,21 @@ extern "C" int difflet_rocm_layernorm_modulate(const void* x, int64_t ldx, void*
     DLT_DISPATCH_FLOAT(out_dtype, TY,
       DLT_DISPATCH_FLOAT(mod_dtype, TM,
         return launch_ln<TX, TY, TM>(x, ldx, y, ldy, rows, dim, mul, add, mod_stride,
-                                     rows_per_batch, one_plus, eps, s))));
+                                     rows_per_batch, split, one_plus, eps, s))));
   return DIFFLET_OK;
 }
 
 template <typename TX, typename TM>
 static int launch_ln_fp8(const void* x, int64_t ldx, uint8_t* q, int64_t ldq, float* scale,
                          int64_t rows, int64_t dim, const void* mul, const void* add,
-                         int64_t mod_stride, int64_t rpb, int one_plus, float eps,
-                         hipStream_t s) {
+                         int64_t mod_stride, int64_t rpb, int64_t split, int one_plus,
+                         float eps, hipStream_t s) {
   const int nv = (int)((dim + 511) / 512);
   dim3 grid((unsigned)((rows + 3) / 4)), block(256);
 #define DLT_LNQ(NV)                                                                     \
   hipLaunchKernelGGL((layernorm_modulate_fp8_kernel<TX, TM, NV>), grid, block, 0, s,  \
                      (const TX*)x, ldx, q, ldq, scale, rows, (int)dim, (const TM*)mul,  \
-                     (const TM*)add, mod_stride, rpb, one_plus, eps)
+                     (const TM*)add, mod_stride, rpb, split, one_plus, eps)
   if (nv <= 2) DLT_LNQ(2);
   else if (nv <= 4) DLT_LNQ(4);
   else if (nv <= 6) DLT_LNQ(6);
@@ -569,9 +572,10 @@ extern "C" int difflet_rocm_layernorm_modulate_fp8(const void* x, int64_t ldx, u
                                                    int64_t rows, int64_t dim, const void* mul,
                                                    const void* add, int mod_dtype,
                                                    int64_t mod_stride, int64_t rows_per_batch,
-                                                   int one_plus, float eps,
+                                                   int64_t split, int one_plus, float eps,
                                                    difflet_stream_t stream) {
   DLT_REQUIRE(x && q && scale, DIFFLET_EINVAL, "layernorm_modulate_fp8: null pointer");
+  DLT_REQUIRE(split >= 0, DIFFLET_EINVAL, "layernorm_modulate_fp8: split must be >= 0");
   DLT_REQUIRE(rows >= 0 && dim > 0 && dim % 8 == 0, DIFFLET_EINVAL,
               "layernorm_modulate_fp8: dim %lld must be a positive multiple of 8",
               (long long)dim);
@@ -586,7 +590,7 @@ extern "C" int difflet_rocm_layernorm_modulate_fp8(const void* x, int64_t ldx, u
   DLT_DISPATCH_FLOAT(dtype, TX,
     DLT_DISPATCH_FLOAT(mod_dtype, TM,
       return launch_ln_fp8<TX, TM>(x, ldx, q, ldq, scale, rows, dim, mul, add, mod_stride,
-                                   rows_per_batch, one_plus, eps, s)));
+                                   rows_per_batch, split, one_plus, eps, s)));
   return DIFFLET_OK;
 }
 
@@ -628,13 +632,15 @@ extern "C" int difflet_rocm_rms_norm(const void* x, int64_t ldx, void* y, int64_
 template <typename T, typename TW>
 static int launch_qk(void* buf, int64_t ld, int64_t rows, int64_t heads, int64_t hd,
                      int64_t q_off, int64_t k_off, int do_norm, const void* wq,
-                     const void* wk, float eps, const float* c, const float* sn,
-                     int64_t rope_rows, int law, hipStream_t s) {
+                     const void* wk, int64_t split, const void* wq2, const void* wk2,
+                     float eps, const float* c, const float* sn, int64_t rope_rows, int law,
+                     hipStream_t s) {
   dim3 grid((unsigned)((rows + 3) / 4)), block(256);
 #define DLT_QK(LPH)                                                                        \
   hipLaunchKernelGGL((qk_norm_rope_kernel<T, TW, LPH>), grid, block, 0, s, (T*)buf, ld,    \
                      rows, (int)heads, q_off, k_off, do_norm, (const TW*)wq,                \
-                     (const TW*)wk, eps, c, sn, rope_rows, law)
+                     (const TW*)wk, split, (const TW*)wq2, (const TW*)wk2, eps, c, sn,       \
+                     rope_rows, law)
   switch (hd) {
     case 32: DLT_QK(4); break;
     case 64: DLT_QK(8); break;
@@ -650,7 +656,8 @@ static int launch_qk(void* buf, int64_t ld, int64_t rows, int64_t heads, int64_t
 extern "C" int difflet_rocm_qk_norm_rope(void* buf, int64_t ld, int dtype, int64_t rows,
                                          int64_t heads, int64_t head_dim, int64_t q_off,
                                          int64_t k_off, int do_norm, const void* wq,
-                                         const void* wk, int wdtype, float eps,
+                                         const void* wk, int64_t split, const void* wq2,
+                                         const void* wk2, int wdtype, float eps,
                                          const float* cos, const float* sin,
                                          int64_t rope_rows, int law,
                                          difflet_stream_t stream) {
@@ -662,6 +669,12 @@ extern "C" int difflet_rocm_qk_norm_rope(void* buf, int64_t ld, int dtype, int64
   DLT_REQUIRE(!cos || rope_rows > 0, DIFFLET_EINVAL, "qk_norm_rope: rope_rows must be > 0");
   DLT_REQUIRE(law == 0 || law == 1, DIFFLET_EINVAL, "qk_norm_rope: law must be 0 or 1");
   DLT_REQUIRE(do_norm >= 0 && do_norm <= 2, DIFFLET_EINVAL, "qk_norm_rope: do_norm must be 0, 1 or 2");
+  DLT_REQUIRE(split >= 0, DIFFLET_EINVAL, "qk_norm_rope: split must be >= 0");
+  if (split == 0 || split >= rows) {  // one segment: the second weights are not read
+    split = 0;
+    wq2 = wq;
+    wk2 = wk;
+  }
   DLT_REQUIRE(aligned16(buf) && (!cos || (aligned16(cos) && aligned16(sin))), DIFFLET_EINVAL,
               "qk_norm_rope: pointers must be 16-byte aligned");
   if (rows == 0) return DIFFLET_OK;
@@ -669,7 +682,7 @@ extern "C" int difflet_rocm_qk_norm_rope(void* buf, int64_t ld, int dtype, int64
   DLT_DISPATCH_FLOAT(dtype, T,
     DLT_DISPATCH_FLOAT(wdtype, TW,
       return launch_qk<T, TW>(buf, ld, rows, heads, head_dim, q_off, k_off, do_norm, wq, wk,
-                              eps, cos, sin, rope_rows, law, s)));
+                              split, wq2, wk2, eps, cos, sin, rope_rows, law, s)));
   return DIFFLET_OK;
 }
 

@@ -60,6 +60,30 @@ class JointDiT:
         kernels.layernorm_modulate(h[rows], sc, sh, eps=EPS, out=bufs["n"][rows])
         return None
 
+    def _ln_joint(self, bufs, st: int, txt_sc, txt_sh, img_sc, img_sh, fused: bool = True):
+        """adaLN of all rows of h in one launch, text rows [0, st) with the text vectors and the
+        image rows with the image ones. Returns the text and image `prepared` operands."""
+        h, s = bufs["h"], bufs["h"].shape[0]
+        T, I = slice(0, st), slice(st, s)
+        kw = dict(eps=EPS, split=st, mul2=img_sc, add2=img_sh) if st else dict(eps=EPS)
+        sc, sh = (txt_sc, txt_sh) if st else (img_sc, img_sh)
+        if fused and self.kind == "fp8":
+            nq, ns = bufs["nq"], bufs["ns"]
+            kernels.layernorm_modulate_fp8(h, sc, sh, out=(nq, ns), **kw)
+            return (nq[T], ns[T]), (nq[I], ns[I])
+        kernels.layernorm_modulate(h, sc, sh, out=bufs["n"], **kw)
+        return None, None
+
+    def _prep_joint(self, lin_txt, lin_img, a, st: int):
+        """The A operands of a text / image GEMM pair from one activation buffer a [S, K],
+        quantized (fp8 kinds) in one launch over all rows."""
+        if lin_txt.kind != lin_img.kind:
+            raise ValueError("a joint GEMM pair shares one kind")
+        if lin_img.kind == "bf16":
+            return None, None
+        q, sc = lin_img.prep(a)
+        return (q[:st], sc[:st]), (q[st:], sc[st:])
+
     def _qk(self, buf, rows: slice, q_off: int, k_off: int, wq, wk, cos, sin):
         c = self.cfg
         kernels.qk_norm_rope(buf[rows], heads=c.heads, head_dim=c.head_dim, q_off=q_off,
@@ -91,23 +115,31 @@ class JointDiT:
         T, I = slice(0, st), slice(st, s)
         x_sh, x_sc, x_g, x_sh2, x_sc2, x_g2 = img_mods
         c_sh, c_sc, c_g, c_sh2, c_sc2, c_g2 = txt_mods
+        # every elementwise step runs once over all rows: the text and image rows of each
+        # launch differ only in their modulation vectors or norm weights
         fq = blk.qkv_img.kind == "fp8"
-        pt, pi = self._ln(bufs, T, c_sc, c_sh, fq), self._ln(bufs, I, x_sc, x_sh, fq)
+        pt, pi = self._ln_joint(bufs, st, c_sc, c_sh, x_sc, x_sh, fq)
         self._gemm(f"gemm.{tag}.qkv", [blk.qkv_txt.problem(n[T], qkv[T], prepared=pt),
                                        blk.qkv_img.problem(n[I], qkv[I], prepared=pi)],
                    blk.qkv_img.kind)
-        self._qk(qkv, T, 0, d, blk.naq, blk.nak, cos, sin)
-        self._qk(qkv, I, 0, d, blk.nq, blk.nk, cos, sin)
+        c = self.cfg
+        kernels.qk_norm_rope(qkv, heads=c.heads, head_dim=c.head_dim, q_off=0, k_off=d,
+                             wq=blk.naq, wk=blk.nak, eps=EPS, cos=cos, sin=sin, law=0, split=st,
+                             wq2=blk.nq, wk2=blk.nk)
         self._attn(qkv, 0, d, 2 * d)
         o = qkv[:, :d]
-        self._gemm(f"gemm.{tag}.out", [blk.out_txt.problem(o[T], h[T], gate=c_g, residual=h[T]),
-                                       blk.out_img.problem(o[I], h[I], gate=x_g, residual=h[I])],
+        pt, pi = self._prep_joint(blk.out_txt, blk.out_img, o, st)
+        self._gemm(f"gemm.{tag}.out",
+                   [blk.out_txt.problem(o[T], h[T], gate=c_g, residual=h[T], prepared=pt),
+                    blk.out_img.problem(o[I], h[I], gate=x_g, residual=h[I], prepared=pi)],
                    blk.out_img.kind, _lib.EPI_GATE_RESIDUAL)
         fq = blk.ff1_img.kind == "fp8"
-        pt, pi = self._ln(bufs, T, c_sc2, c_sh2, fq), self._ln(bufs, I, x_sc2, x_sh2, fq)
+        pt, pi = self._ln_joint(bufs, st, c_sc2, c_sh2, x_sc2, x_sh2, fq)
         self._gemm(f"gemm.{tag}.ff1", [blk.ff1_txt.problem(n[T], ff[T], prepared=pt),
                                        blk.ff1_img.problem(n[I], ff[I], prepared=pi)],
                    blk.ff1_img.kind, _lib.EPI_GELU)
-        self._gemm(f"gemm.{tag}.ff2", [blk.ff2_txt.problem(ff[T], h[T], gate=c_g2, residual=h[T]),
-                                       blk.ff2_img.problem(ff[I], h[I], gate=x_g2, residual=h[I])],
+        pt, pi = self._prep_joint(blk.ff2_txt, blk.ff2_img, ff, st)
+        self._gemm(f"gemm.{tag}.ff2",
+                   [blk.ff2_txt.problem(ff[T], h[T], gate=c_g2, residual=h[T], prepared=pt),
+                    blk.ff2_img.problem(ff[I], h[I], gate=x_g2, residual=h[I], prepared=pi)],
                    blk.ff2_img.kind, _lib.EPI_GATE_RESIDUAL)

@@ -276,23 +276,50 @@ def quantize_mxfp8(x: torch.Tensor, *, swizzled: bool = False
 # ---------------------------------------------------------------------------- norms, rope
 def layernorm_modulate(x: torch.Tensor, mul: torch.Tensor | None, add: torch.Tensor | None, *,
                        eps: float, one_plus: bool = True, out_dtype: torch.dtype | None = None,
-                       rows_per_batch: int | None = None,
+                       rows_per_batch: int | None = None, split: int = 0,
+                       mul2: torch.Tensor | None = None, add2: torch.Tensor | None = None,
                        out: torch.Tensor | None = None) -> torch.Tensor:
     """LN(x) * (1 + mul) + add (one_plus) or LN(x) * mul + add, over the last dim.
 
-    mul / add: [dim] or [batches, dim], broadcast over the rows of each batch element."""
+    mul / add: [dim] or [batches, dim], broadcast over the rows of each batch element. With
+    split > 0, rows >= split take mul2 / add2 instead (two segments in one launch)."""
     dev = _on_gpu(x)
     x2 = _rows2d(x, "layernorm")
     rows, dim = x2.shape
     out_dtype = out_dtype or x.dtype
     y = out if out is not None else torch.empty((rows, dim), dtype=out_dtype, device=dev)
-    mul, add, mod_dt, mod_stride = _mod_vectors(mul, add, dim)
+    mul, add, mod_dt, mod_stride, split = _mod_args(mul, add, mul2, add2, dim, split)
     rpb = rows_per_batch or rows
     check(lib().difflet_rocm_layernorm_modulate(
         _ptr(x2), x2.stride(0), _ptr(y), y.stride(0), _dt(x2), _dt(y), rows, dim, _ptr(mul),
-        _ptr(add), mod_dt, mod_stride, rpb, int(one_plus), float(eps), _stream(dev)),
+        _ptr(add), mod_dt, mod_stride, rpb, split, int(one_plus), float(eps), _stream(dev)),
         "layernorm_modulate")
     return y.reshape(*x.shape[:-1], dim) if out is None else y
+
+
+def _mod_args(mul, add, mul2, add2, dim, split):
+    """Kernel arguments for the modulation vectors: one set ([batches, dim]), or with split > 0
+    two [dim] vectors per operand whose distance in elements becomes the batch stride."""
+    if not split:
+        return (*_mod_vectors(mul, add, dim), 0)
+    for a, b2 in ((mul, mul2), (add, add2)):
+        if (a is None) != (b2 is None):
+            raise ValueError("split modulation: give both segments' vectors or neither")
+    pairs = [(a, b2) for a, b2 in ((mul, mul2), (add, add2)) if a is not None]
+    if not pairs:
+        return None, None, _lib.F32, 0, int(split)
+    dtype = pairs[0][0].dtype
+    stride = None
+    for a, b2 in pairs:
+        if a.dtype != dtype or b2.dtype != dtype or a.numel() != dim or b2.numel() != dim or \
+                a.stride(-1) != 1 or b2.stride(-1) != 1:
+            raise ValueError("split modulation: [dim] vectors of one dtype with contiguous rows")
+        d, r = divmod(b2.data_ptr() - a.data_ptr(), a.element_size())
+        if r or (stride is not None and d != stride):
+            raise ValueError("split modulation: both operands' second vectors must sit at one "
+                             "distance from their first")
+        stride = d
+    return mul, add, _dt(pairs[0][0]), stride, int(split)
 
 
 def _mod_vectors(mul, add, dim):
@@ -316,7 +343,8 @@ def _mod_vectors(mul, add, dim):
 
 def layernorm_modulate_fp8(x: torch.Tensor, mul: torch.Tensor | None,
                            add: torch.Tensor | None, *, eps: float, one_plus: bool = True,
-                           rows_per_batch: int | None = None,
+                           rows_per_batch: int | None = None, split: int = 0,
+                           mul2: torch.Tensor | None = None, add2: torch.Tensor | None = None,
                            out: tuple[torch.Tensor, torch.Tensor] | None = None):
     """layernorm_modulate rounded to bf16 and quantized per row to e4m3 in one pass:
     (codes float8_e4m3fn [rows, dim], scales fp32 [rows]), equal to quantize_fp8_rowwise of the
@@ -333,11 +361,11 @@ def layernorm_modulate_fp8(x: torch.Tensor, mul: torch.Tensor | None,
                 q.shape[-1] < dim or sc.numel() < rows or not sc.is_contiguous():
             raise ValueError("layernorm_modulate_fp8: out must be (8-bit [rows, >=dim], "
                              "contiguous fp32 [rows])")
-    mul, add, mod_dt, mod_stride = _mod_vectors(mul, add, dim)
+    mul, add, mod_dt, mod_stride, split = _mod_args(mul, add, mul2, add2, dim, split)
     rpb = rows_per_batch or rows
     check(lib().difflet_rocm_layernorm_modulate_fp8(
         _ptr(x2), x2.stride(0), _ptr(q), q.stride(0), _ptr(sc), _dt(x2), rows, dim, _ptr(mul),
-        _ptr(add), mod_dt, mod_stride, rpb, int(one_plus), float(eps), _stream(dev)),
+        _ptr(add), mod_dt, mod_stride, rpb, split, int(one_plus), float(eps), _stream(dev)),
         "layernorm_modulate_fp8")
     return q, sc
 
@@ -356,10 +384,14 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float) -> torch.
 def qk_norm_rope(buf: torch.Tensor, *, heads: int, head_dim: int, q_off: int, k_off: int,
                  wq: torch.Tensor | None, wk: torch.Tensor | None, eps: float,
                  cos: torch.Tensor | None, sin: torch.Tensor | None, law: int = 0,
-                 do_norm: bool | int = True) -> None:
+                 do_norm: bool | int = True, split: int = 0, wq2: torch.Tensor | None = None,
+                 wk2: torch.Tensor | None = None) -> None:
     """In place on a [rows, ld] projection buffer: RMSNorm of q (columns q_off + h * head_dim ..;
     q_off < 0 skips q) and k, per head (do_norm True / 1) or over all heads of the row (2), then
-    the rotary embedding with fp32 tables [S, head_dim] (cos None skips it)."""
+    the rotary embedding with fp32 tables [S, head_dim] (cos None skips it). With split > 0,
+    rows >= split use the weights wq2 / wk2."""
+    if split and ((wq2 is None) != (wq is None) or (wk2 is None) != (wk is None)):
+        raise ValueError("qk_norm_rope: split needs second weights wherever there are first")
     dev = _on_gpu(buf)
     if buf.dim() != 2 or buf.stride(1) != 1:
         raise ValueError("qk_norm_rope: buf must be 2-D with contiguous rows")
@@ -369,10 +401,13 @@ def qk_norm_rope(buf: torch.Tensor, *, heads: int, head_dim: int, q_off: int, k_
         if cos.dtype != torch.float32 or sin.dtype != torch.float32:
             raise TypeError("rope tables must be fp32")
         cos, sin = cos.contiguous(), sin.contiguous()
+    for w2 in (wq2, wk2):
+        if split and w2 is not None and _dt(w2) != wdt:
+            raise TypeError("qk_norm_rope: both segments' weights share one dtype")
     check(lib().difflet_rocm_qk_norm_rope(
         _ptr(buf), buf.stride(0), _dt(buf), rows, heads, head_dim, q_off, k_off, int(do_norm),
-        _ptr(wq), _ptr(wk), wdt, float(eps), _ptr(cos), _ptr(sin),
-        cos.shape[0] if cos is not None else 0, law, _stream(dev)), "qk_norm_rope")
+        _ptr(wq), _ptr(wk), int(split), _ptr(wq2), _ptr(wk2), wdt, float(eps), _ptr(cos),
+        _ptr(sin), cos.shape[0] if cos is not None else 0, law, _stream(dev)), "qk_norm_rope")
 
 
 def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *, law: int) -> torch.Tensor:

@@ -178,12 +178,14 @@ int difflet_rocm_quantize_mxfp8(const void* x, int dtype, int64_t rows, int64_t 
  *   one_plus = 0: y = LN(x) * mul + add               (nn.LayerNorm, difflet/backends/cpu/
  *                 ops_impl/norm.py:9); mul / add may be NULL (no affine).
  * mul / add: [batches, dim] of mod_dtype with batch stride mod_stride, batch = row /
- * rows_per_batch. */
+ * rows_per_batch; or, with split > 0, two segments: rows < split use mul / add and rows >=
+ * split use mul + mod_stride / add + mod_stride (mod_stride may be negative), e.g. the text and
+ * image rows of a joint block in one launch with their own modulation vectors. */
 int difflet_rocm_layernorm_modulate(const void* x, int64_t ldx, void* y, int64_t ldy,
                                     int dtype, int out_dtype, int64_t rows, int64_t dim,
                                     const void* mul, const void* add, int mod_dtype,
-                                    int64_t mod_stride, int64_t rows_per_batch, int one_plus,
-                                    float eps, difflet_stream_t stream);
+                                    int64_t mod_stride, int64_t rows_per_batch, int64_t split,
+                                    int one_plus, float eps, difflet_stream_t stream);
 
 /* difflet_rocm_layernorm_modulate with bf16 output followed by difflet_rocm_quantize_fp8_rowwise,
  * in one pass and bit-identical with that pair: the modulated row is rounded to bf16, then
@@ -194,7 +196,8 @@ int difflet_rocm_layernorm_modulate_fp8(const void* x, int64_t ldx, uint8_t* q, 
                                         float* scale, int dtype, int64_t rows, int64_t dim,
                                         const void* mul, const void* add, int mod_dtype,
                                         int64_t mod_stride, int64_t rows_per_batch,
-                                        int one_plus, float eps, difflet_stream_t stream);
+                                        int64_t split, int one_plus, float eps,
+                                        difflet_stream_t stream);
 
 /* RMSNorm with fp32 statistics, normalisation and affine and one cast back to dtype: the
  * law of rms_norm_fp32 (difflet/backends/_torch_megatron/norm.py:35-45) and of the CUDA
@@ -216,11 +219,14 @@ int difflet_rocm_rms_norm(const void* x, int64_t ldx, void* y, int64_t ldy, int 
  *          even, sin of the odd table entries).
  * Replaces the norm_q/norm_k + apply_rotary_emb sequence of difflet/models/flux/
  * modeling_flux.py:1249-1252,1289-1294,1407-1411. cos / sin: fp32 [rope_rows, head_dim], row
- * index r % rope_rows; NULL skips the rotation. wq / wk NULL: unit weights. */
+ * index r % rope_rows; NULL skips the rotation. wq / wk NULL: unit weights. With
+ * 0 < split < rows, rows >= split use the weights wq2 / wk2 (the image rows of a joint block
+ * whose text rows come first). */
 int difflet_rocm_qk_norm_rope(void* buf, int64_t ld, int dtype, int64_t rows, int64_t heads,
                               int64_t head_dim, int64_t q_off, int64_t k_off, int do_norm,
-                              const void* wq, const void* wk, int wdtype, float eps,
-                              const float* cos, const float* sin, int64_t rope_rows, int law,
+                              const void* wq, const void* wk, int64_t split, const void* wq2,
+                              const void* wk2, int wdtype, float eps, const float* cos,
+                              const float* sin, int64_t rope_rows, int law,
                               difflet_stream_t stream);
 
 /* Rotary embedding out of place on a strided [batch*heads, seq, head_dim] tensor with tables

@@ -352,6 +352,38 @@ def test_qk_norm_rope_in_place(gpu):
     assert torch.equal(gb[:, 2 * d:].cpu(), buf[:, 2 * d:])
 
 
+def test_split_launches_equal_one_launch_per_segment(gpu):
+    """Joint-block launches over text + image rows (split): the LayerNorm modulations (bf16
+    and fused e4m3) and the q/k norm + rope equal one launch per segment, bit for bit. The
+    image vectors sit before the text ones in memory (a negative batch stride)."""
+    g = torch.Generator().manual_seed(21)
+    st, s, d, h = 96, 352, 1024, 8
+    x = rnd(g, s, d, std=2.0).to(gpu)
+    mod = rnd(g, 1, 4 * d, std=0.3).to(gpu)
+    img_sh, img_sc, txt_sh, txt_sc = (mod[:, i * d:(i + 1) * d] for i in range(4))
+    one = kernels.layernorm_modulate(x, txt_sc, txt_sh, eps=1e-6, split=st, mul2=img_sc,
+                                     add2=img_sh)
+    ref = torch.cat([kernels.layernorm_modulate(x[:st], txt_sc, txt_sh, eps=1e-6),
+                     kernels.layernorm_modulate(x[st:], img_sc, img_sh, eps=1e-6)])
+    assert torch.equal(one.view(torch.int16), ref.view(torch.int16))
+    q1, s1 = kernels.layernorm_modulate_fp8(x, txt_sc, txt_sh, eps=1e-6, split=st,
+                                            mul2=img_sc, add2=img_sh)
+    qa, sa = kernels.layernorm_modulate_fp8(x[:st], txt_sc, txt_sh, eps=1e-6)
+    qb, sb = kernels.layernorm_modulate_fp8(x[st:], img_sc, img_sh, eps=1e-6)
+    assert torch.equal(q1.view(torch.uint8), torch.cat([qa, qb]).view(torch.uint8))
+    assert torch.equal(s1, torch.cat([sa, sb]))
+    buf = rnd(g, s, 3 * h * 128).to(gpu)
+    w = [(1 + 0.1 * torch.randn(128, generator=g)).bfloat16().to(gpu) for _ in range(4)]
+    cos, sin = (torch.randn(s, 128, generator=g).to(gpu) for _ in range(2))
+    b1, b2 = buf.clone(), buf.clone()
+    kw = dict(heads=h, head_dim=128, q_off=0, k_off=h * 128, eps=1e-6, law=0)
+    kernels.qk_norm_rope(b1, wq=w[0], wk=w[1], cos=cos, sin=sin, split=st, wq2=w[2], wk2=w[3],
+                         **kw)
+    kernels.qk_norm_rope(b2[:st], wq=w[0], wk=w[1], cos=cos[:st], sin=sin[:st], **kw)
+    kernels.qk_norm_rope(b2[st:], wq=w[2], wk=w[3], cos=cos[st:], sin=sin[st:], **kw)
+    assert torch.equal(b1.view(torch.int16), b2.view(torch.int16))
+
+
 @pytest.mark.parametrize("law", [0, 1])
 def test_rope_laws(gpu, law):
     g = torch.Generator().manual_seed(11 + law)
