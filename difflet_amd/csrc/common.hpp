@@ -95,15 +95,22 @@ __device__ __forceinline__ float rowwise_inv(float amax) {
 __device__ __forceinline__ float rowwise_scale(float amax) {
   return __fdiv_rn(__builtin_fmaxf(amax, 1.925929944387236e-34f), 448.0f);
 }
+// Four e4m3fn codes (a in the low byte) of values already clamped to [-448, 448], rounded to
+// nearest even by the hardware conversion (v_cvt_pk_fp8_f32 writes two codes into the selected
+// half of its destination). Its codes equal f32_to_e4m3fn's for every fp32 input in
+// [-448, 448], both signs (checked exhaustively on gfx950).
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
 // Eight codes e4m3(clamp(v * inv)), little-endian in two dwords.
 __device__ __forceinline__ u32x2 encode8_rowwise(const float* v, float inv) {
-  u32x2 o = {0u, 0u};
+  float c[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t code = f32_to_e4m3fn(clamp448(__fmul_rn(v[i], inv)));
-    o[i >> 2] |= code << (8 * (i & 3));
-  }
-  return o;
+  for (int i = 0; i < 8; ++i) c[i] = clamp448(__fmul_rn(v[i], inv));
+  return u32x2{e4m3x4(c[0], c[1], c[2], c[3]), e4m3x4(c[4], c[5], c[6], c[7])};
 }
 
 // ------------------------------------------------------------------ wave reductions

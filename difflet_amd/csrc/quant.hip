@@ -187,31 +187,27 @@ __global__ __launch_bounds__(256) void quant_mx_kernel(const T* __restrict__ x, 
   scale[row * lds + blk] = (uint8_t)su;
   // x / 2^(su - 127) == x * 2^(127 - su): both exact powers of two, same rounding
   const float mul = __builtin_bit_cast(float, (uint32_t)(254 - su) << 23);
-  uint8_t codes[4][8];
+  float c[4][8];  // clamped scaled values, encoded by e4m3x4 (round to nearest even)
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      codes[j][i] = (uint8_t)f32_to_e4m3fn(clamp448(__fmul_rn(v[j][i], mul)));
+    for (int i = 0; i < 8; ++i) c[j][i] = clamp448(__fmul_rn(v[j][i], mul));
   uint8_t* qr = q + row * ldq;
   if (swizzled_out) {
     // swizzled position (8 b + r) * 4 + j holds logical run j, element r
     u32x4 o0, o1;
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      o0[r] = codes[0][r] | (codes[1][r] << 8) | (codes[2][r] << 16) | ((uint32_t)codes[3][r] << 24);
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      o1[r] = codes[0][4 + r] | (codes[1][4 + r] << 8) | (codes[2][4 + r] << 16) |
-              ((uint32_t)codes[3][4 + r] << 24);
+    for (int r = 0; r < 4; ++r) {
+      o0[r] = e4m3x4(c[0][r], c[1][r], c[2][r], c[3][r]);
+      o1[r] = e4m3x4(c[0][4 + r], c[1][4 + r], c[2][4 + r], c[3][4 + r]);
+    }
     *reinterpret_cast<u32x4*>(qr + k0 + 32 * b) = o0;
     *reinterpret_cast<u32x4*>(qr + k0 + 32 * b + 16) = o1;
   } else {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      u32x2 o;
-      o[0] = codes[j][0] | (codes[j][1] << 8) | (codes[j][2] << 16) | ((uint32_t)codes[j][3] << 24);
-      o[1] = codes[j][4] | (codes[j][5] << 8) | (codes[j][6] << 16) | ((uint32_t)codes[j][7] << 24);
+      const u32x2 o = {e4m3x4(c[j][0], c[j][1], c[j][2], c[j][3]),
+                       e4m3x4(c[j][4], c[j][5], c[j][6], c[j][7])};
       *reinterpret_cast<u32x2*>(qr + k0 + j * sub + 8 * b) = o;
     }
   }

@@ -119,6 +119,33 @@ def test_quantize_fp8_rowwise_bit_exact(gpu, rows, cols, dtype):
     assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
 
 
+def test_fp8_encode_every_code_and_rounding_midpoint(gpu):
+    """The device encodes with the hardware conversion: every e4m3 value, every midpoint
+    between neighbours (ties to even, including the subnormal ones and the one below the
+    smallest subnormal), and values just off each midpoint, all in fp32 rows whose max is 448
+    (scale 1, so these are the encoder's exact inputs), give the oracle's codes."""
+    codes = np.arange(0, 0x7f, dtype=np.uint8)  # +0 .. 448 (0x7e); 0x7f is NaN
+    vals = omx.e4m3_decode(codes).astype(np.float64)
+    mids = (vals[:-1] + vals[1:]) / 2
+    off = np.concatenate([np.nextafter(mids.astype(np.float32), np.float32(0)),
+                          np.nextafter(mids.astype(np.float32), np.float32(1e9))])
+    pos = np.concatenate([vals, mids, off, [2.0 ** -10, 2.0 ** -11, 1e-30, 1e-45]])
+    row = np.concatenate([pos, -pos]).astype(np.float32)
+    row = np.concatenate([[448.0], row]).astype(np.float32)
+    row = np.pad(row, (0, (-row.size) % 8))
+    x = torch.from_numpy(np.stack([row, row[::-1].copy()]))
+    q, s = kernels.quantize_fp8_rowwise(x.to(gpu))
+    q_ref, s_ref = ofp8.quantize_rowwise(x.numpy())
+    assert np.array_equal(s.cpu().numpy(), np.ones(2, np.float32))
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), q_ref)
+    # the MX quantizer's encoder on the same values (one block scale per 32, E8M0 of 448 is 1)
+    xm = x[:, :x.shape[1] // 128 * 128].contiguous()
+    qm, sm = kernels.quantize_mxfp8(xm.to(gpu))
+    qm_ref, sm_ref = omx.quantize_mx(xm.numpy())
+    assert np.array_equal(sm.cpu().numpy(), sm_ref)
+    assert np.array_equal(qm.view(torch.uint8).cpu().numpy(), qm_ref)
+
+
 @pytest.mark.parametrize("rows,dim", [(5, 64), (512, 3072), (77, 5120)])
 def test_layernorm_modulate_fp8_equals_layernorm_then_quantize(gpu, rows, dim):
     g = torch.Generator().manual_seed(rows * 3 + dim)
