@@ -321,6 +321,59 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   }
 }
 
+// The per-head forms (do_norm 0 / 1) with one wavefront per (row, q or k, group of 64 / LPH
+// heads): a head's norm needs only its own LPH lanes, so the row's head groups run in parallel
+// instead of one after another behind each load's latency.
+template <typename T, typename TW, int LPH>
+__global__ __launch_bounds__(256) void qk_norm_rope_heads_kernel(
+    T* __restrict__ buf, int64_t ld, int64_t rows, int heads, int64_t q_off, int64_t k_off,
+    int do_norm, const TW* __restrict__ wq, const TW* __restrict__ wk, int64_t split,
+    const TW* __restrict__ wq2, const TW* __restrict__ wk2, float eps,
+    const float* __restrict__ cosb, const float* __restrict__ sinb, int64_t rope_rows,
+    int law) {
+  constexpr int HD = LPH * 8;
+  constexpr int HPS = 64 / LPH;  // heads per wavefront
+  const int lane = threadIdx.x & 63;
+  const int steps = (heads + HPS - 1) / HPS;
+  const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t rt = task / steps;
+  const int step = (int)(task - rt * steps);
+  const int64_t row = rt >> 1;
+  const int t = (int)(rt & 1);
+  if (row >= rows) return;
+  const int64_t off = t == 0 ? q_off : k_off;
+  const int h = step * HPS + lane / LPH;
+  if (off < 0 || h >= heads) return;
+  const int d0 = (lane % LPH) * 8;
+  const bool second = split > 0 && row >= split;  // rows past split: the second weights
+  const TW* w = t == 0 ? (second ? wq2 : wq) : (second ? wk2 : wk);
+  T* p = buf + row * ld + off + (int64_t)h * HD + d0;
+  float v[8];
+  V8<T>::load(p, v);
+  if (do_norm) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s += v[i] * v[i];
+#pragma unroll
+    for (int o = LPH / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    const float r = 1.0f / __builtin_sqrtf(s / (float)HD + eps);
+    float w8[8];
+    if (w) {
+      V8<TW>::load(w + d0, w8);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) w8[i] = 1.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = v[i] * r * w8[i];
+  }
+  if (cosb) {
+    const int64_t rr = row % rope_rows;
+    rope8(v, cosb + rr * HD + d0, sinb + rr * HD + d0, law);
+  }
+  V8<T>::store(p, v);
+}
+
 // ------------------------------------------------------------------ RoPE, out of place
 template <typename T, int LPH>
 __global__ __launch_bounds__(256) void rope_kernel(const T* __restrict__ x, T* __restrict__ y,
@@ -387,14 +440,14 @@ __global__ __launch_bounds__(256) void gate_residual_kernel(
 // per lane per step, so the kernel runs at HBM speed. M is a compile-time bound on the rows;
 // rows m..M-1 of the LDS stage are zero and never stored.
 template <typename T, int M>
-__global__ __launch_bounds__(256) void gemv_kernel(const T* __restrict__ x, int m, int64_t k,
+__global__ __launch_bounds__(256) void gemv_kernel(const T* __restrict__ x, int m, int k,
                                                    int64_t ldx, const bf16* __restrict__ w,
                                                    int64_t ldw, int64_t n,
                                                    const T* __restrict__ bias,
                                                    T* __restrict__ y, int64_t ldy, int act) {
   extern __shared__ float xs[];  // [M][k]
-  for (int64_t i = threadIdx.x; i < (int64_t)M * k; i += 256) {
-    const int64_t r = i / k, kk = i % k;
+  for (int i = threadIdx.x; i < M * k; i += 256) {
+    const int r = i / k, kk = i - r * k;
     float v = 0.f;
     if (r < m) {
       v = Elt<T>::load(x + r * ldx + kk);
@@ -408,50 +461,56 @@ __global__ __launch_bounds__(256) void gemv_kernel(const T* __restrict__ x, int 
   }
   __syncthreads();
   const int lane = threadIdx.x & 63;
-  const int64_t waves = (int64_t)gridDim.x * 4;
-  for (int64_t col = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); col < n; col += waves) {
-    const bf16* wr = w + col * ldw;
-    float acc[M];
+  // Two columns per wave and 3072-wide groups of six 1 KB loads per column, unguarded: twelve
+  // loads in flight per wave before the first multiply; the k % 3072 tail is guarded.
+  constexpr int U = 6, CP = 2;
+  const int kfull = k - k % (U * 512);
+  const int64_t step = (int64_t)gridDim.x * 4 * CP;
+  for (int64_t c0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * CP; c0 < n; c0 += step) {
+    const bf16* wr[CP];
 #pragma unroll
-    for (int r = 0; r < M; ++r) acc[r] = 0.f;
-    constexpr int U = 4;
-    int64_t c0 = 0;
-    for (; c0 + (int64_t)U * 512 <= k; c0 += U * 512) {
-      u32x4 wv[U];
+    for (int p = 0; p < CP; ++p) wr[p] = w + (c0 + p < n ? c0 + p : n - 1) * ldw + lane * 8;
+    float acc[CP][M];
 #pragma unroll
-      for (int u = 0; u < U; ++u)
-        wv[u] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(wr + c0 + u * 512 + lane * 8));
+    for (int p = 0; p < CP; ++p)
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int64_t c = c0 + u * 512 + lane * 8;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float w0 = bf16bits_to_f32(wv[u][i] & 0xffffu);
-          const float w1 = bf16bits_to_f32(wv[u][i] >> 16);
-#pragma unroll
-          for (int r = 0; r < M; ++r)
-            acc[r] += w0 * xs[r * k + c + 2 * i] + w1 * xs[r * k + c + 2 * i + 1];
-        }
-      }
-    }
-    for (int64_t c = c0 + lane * 8; c < k; c += 512) {
-      const u32x4 wv = *reinterpret_cast<const u32x4*>(wr + c);
+      for (int r = 0; r < M; ++r) acc[p][r] = 0.f;
+    auto fma8 = [&](const u32x4& wv, int c, float* a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float w0 = bf16bits_to_f32(wv[i] & 0xffffu);
         const float w1 = bf16bits_to_f32(wv[i] >> 16);
 #pragma unroll
         for (int r = 0; r < M; ++r)
-          acc[r] += w0 * xs[r * k + c + 2 * i] + w1 * xs[r * k + c + 2 * i + 1];
+          a[r] += w0 * xs[r * k + c + 2 * i] + w1 * xs[r * k + c + 2 * i + 1];
       }
+    };
+    for (int g = 0; g < kfull; g += U * 512) {
+      u32x4 wv[CP][U];
+#pragma unroll
+      for (int p = 0; p < CP; ++p)
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          wv[p][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr[p] + g + u * 512));
+#pragma unroll
+      for (int p = 0; p < CP; ++p)
+#pragma unroll
+        for (int u = 0; u < U; ++u) fma8(wv[p][u], g + u * 512 + lane * 8, acc[p]);
+    }
+    for (int c = kfull; c + lane * 8 < k; c += 512) {
+#pragma unroll
+      for (int p = 0; p < CP; ++p)
+        fma8(*reinterpret_cast<const u32x4*>(wr[p] + c), c + lane * 8, acc[p]);
     }
 #pragma unroll
-    for (int r = 0; r < M; ++r) {
-      const float t = wave_sum(acc[r]);
-      if (lane == 0 && r < m) {
-        const float bv = bias ? Elt<T>::load(bias + col) : 0.f;
-        Elt<T>::store(y + r * ldy + col, t + bv);
+    for (int p = 0; p < CP; ++p) {
+#pragma unroll
+      for (int r = 0; r < M; ++r) {
+        const float t = wave_sum(acc[p][r]);
+        if (lane == 0 && r < m && c0 + p < n) {
+          const float bv = bias ? Elt<T>::load(bias + c0 + p) : 0.f;
+          Elt<T>::store(y + r * ldy + c0 + p, t + bv);
+        }
       }
     }
   }
@@ -637,6 +696,13 @@ static int launch_qk(void* buf, int64_t ld, int64_t rows, int64_t heads, int64_t
                      hipStream_t s) {
   dim3 grid((unsigned)((rows + 3) / 4)), block(256);
 #define DLT_QK(LPH)                                                                        \
+  if (do_norm != 2) {                                                                      \
+    const int64_t tasks = rows * 2 * ((heads + 64 / (LPH) - 1) / (64 / (LPH)));            \
+    hipLaunchKernelGGL((qk_norm_rope_heads_kernel<T, TW, LPH>), dim3((unsigned)((tasks + 3) / 4)), \
+                       block, 0, s, (T*)buf, ld, rows, (int)heads, q_off, k_off, do_norm,  \
+                       (const TW*)wq, (const TW*)wk, split, (const TW*)wq2, (const TW*)wk2, \
+                       eps, c, sn, rope_rows, law);                                        \
+  } else                                                                                   \
   hipLaunchKernelGGL((qk_norm_rope_kernel<T, TW, LPH>), grid, block, 0, s, (T*)buf, ld,    \
                      rows, (int)heads, q_off, k_off, do_norm, (const TW*)wq,                \
                      (const TW*)wk, split, (const TW*)wq2, (const TW*)wk2, eps, c, sn,       \
@@ -773,12 +839,12 @@ template <typename T>
 static int launch_gemv(const void* x, int64_t m, int mb, int64_t k, int64_t ldx, const void* w,
                        int64_t ldw, int64_t n, const void* bias, void* y, int64_t ldy, int act,
                        hipStream_t s) {
-  int64_t blocks = (n + 3) / 4;
+  int64_t blocks = (n + 7) / 8;
   if (blocks > 8192) blocks = 8192;
   const size_t lds = (size_t)(mb * k * 4);
 #define DLT_GEMV(M)                                                                          \
   hipLaunchKernelGGL((gemv_kernel<T, M>), dim3((unsigned)blocks), dim3(256), lds, s,         \
-                     (const T*)x, (int)m, k, ldx, (const bf16*)w, ldw, n, (const T*)bias,     \
+                     (const T*)x, (int)m, (int)k, ldx, (const bf16*)w, ldw, n, (const T*)bias,     \
                      (T*)y, ldy, act)
   switch (mb) {
     case 1: DLT_GEMV(1); break;
@@ -796,8 +862,8 @@ extern "C" int difflet_rocm_gemv(const void* x, int dtype, int64_t m, int64_t k,
   DLT_REQUIRE(x && w && y, DIFFLET_EINVAL, "gemv: null pointer");
   DLT_REQUIRE(m >= 1 && m <= 8, DIFFLET_EUNSUPPORTED, "gemv: m = %lld not in [1, 8]",
               (long long)m);
-  DLT_REQUIRE(k > 0 && k % 8 == 0 && ldw % 8 == 0 && aligned16(w), DIFFLET_EINVAL,
-              "gemv: k and ldw must be multiples of 8 and w 16-byte aligned");
+  DLT_REQUIRE(k > 0 && k % 8 == 0 && ldw % 8 == 0 && ldw >= k && aligned16(w), DIFFLET_EINVAL,
+              "gemv: k and ldw must be multiples of 8, ldw >= k and w 16-byte aligned");
   const int mb = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
   DLT_REQUIRE(mb * k * 4 <= 64 * 1024, DIFFLET_EUNSUPPORTED,
               "gemv: m * k = %lld exceeds the 16384-element LDS stage", (long long)(mb * k));

@@ -423,6 +423,30 @@ def test_rope_laws(gpu, law):
     assert rel_l2(out, ref) < 1e-6
 
 
+@pytest.mark.parametrize("m,k,n,xdt", [(1, 256, 3072, torch.bfloat16), (1, 3072, 1001, torch.bfloat16),
+                                        (2, 5120, 777, torch.bfloat16), (2, 6656, 301, torch.float32),
+                                        (8, 1536, 64, torch.bfloat16), (1, 3072, 7, torch.float32)])
+def test_gemv_shapes_tail_and_strided_weights(gpu, m, k, n, xdt):
+    """Whole 3072-wide groups, the guarded tail after them (k = 256, 5120, 6656, 1536), column
+    counts that leave the last wave's second column out of range, and a weight view whose row
+    stride exceeds k."""
+    print(f"gemv m={m} k={k} n={n} {xdt}", flush=True)
+    g = torch.Generator().manual_seed(k + n)
+    xv = rnd(g, m, k).to(xdt)
+    wfull = rnd(g, n, k + 64, std=0.02)
+    w = wfull[:, 32:32 + k]
+    b = rnd(g, n, std=0.1)
+    for act in (0, 1):
+        xin = torch.nn.functional.silu(xv.float()).to(xdt).float() if act else xv.float()
+        ref = ops.linear(xin, w.float(), b.float())
+        out = kernels.gemv(xv.to(gpu), wfull.to(gpu)[:, 32:32 + k], b.to(gpu), act=act)
+        assert out.dtype == xdt
+        assert rel_l2(out, ref) < (4e-3 if xdt == torch.bfloat16 else 1e-5)
+    if m == 8:  # m rounds up to an 8-row LDS stage: 8 * k must stay within 16384
+        with pytest.raises(NotImplementedError):
+            kernels.gemv(torch.zeros(8, 2056, device=gpu), w.to(gpu)[:, :8].repeat(1, 257))
+
+
 def test_gelu_gate_residual_gemv_timestep(gpu):
     g = torch.Generator().manual_seed(12)
     x = rnd(g, 1001, dtype=torch.float32) * 4
