@@ -30,11 +30,17 @@ constexpr int kWave = 64;
 // ------------------------------------------------------------------ bf16 conversions
 // Round-to-nearest-even fp32 -> bf16 on the bit pattern (NaN kept quiet), the same rounding
 // torch uses for `.to(torch.bfloat16)`.
+// fp32 -> bf16 rounding to nearest even, NaN quieted to (bits >> 16) | 0x40: gfx950's
+// v_cvt_pk_bf16_f32, which equals u += 0x7fff + ((u >> 16) & 1), u >> 16 (NaN: the quieted top
+// half) on all 2^32 fp32 bit patterns in both halves of the pair (checked exhaustively on the
+// GPU), in one instruction per two values instead of five per value. a goes in the low half.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  return (uint16_t)(pack_bf16x2(f, 0.0f) & 0xffffu);
 }
 __device__ __forceinline__ bf16 f32_to_bf16(float f) {
   return __builtin_bit_cast(bf16, f32_to_bf16_bits(f));
@@ -44,10 +50,6 @@ __device__ __forceinline__ float bf16_to_f32(bf16 h) {
 }
 __device__ __forceinline__ float bf16bits_to_f32(uint32_t bits16) {
   return __builtin_bit_cast(float, bits16 << 16);
-}
-// Two bf16 packed in one dword (low half = first element).
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
 }
 
 // Element loaders/storers for the activation dtypes the kernels accept.

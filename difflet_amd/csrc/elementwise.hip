@@ -5,6 +5,8 @@
 // Layout: activations are token-major rows ([rows, dim], innermost contiguous). One wavefront
 // owns one row, so every statistic is a wavefront reduction with no LDS and no barrier, and
 // each lane moves 16-byte vectors (8 bf16) so HBM traffic is fully coalesced.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace dlt {
@@ -64,64 +66,116 @@ template <> struct V8<float> {
   }
 };
 
+// Raw 16-byte (fp32: 32-byte) loads converted in a separate step, so a load inside a branch has
+// no use there and the compiler need not wait for it before the branch ends.
+template <typename T> struct Raw8 {
+  u32x4 r;
+  static __device__ __forceinline__ Raw8 load(const T* p) {
+    return Raw8{*reinterpret_cast<const u32x4*>(p)};
+  }
+  static __device__ __forceinline__ Raw8 zero() { return Raw8{u32x4{0u, 0u, 0u, 0u}}; }
+  __device__ __forceinline__ void cvt(float* v) const {
+    if constexpr (std::is_same<T, bf16>::value) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = bf16bits_to_f32(r[i] & 0xffffu);
+        v[2 * i + 1] = bf16bits_to_f32(r[i] >> 16);
+      }
+    } else {
+      typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+      const h8 h = __builtin_bit_cast(h8, r);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = (float)h[i];
+    }
+  }
+};
+template <> struct Raw8<float> {
+  f32x4 a, b;
+  static __device__ __forceinline__ Raw8 load(const float* p) {
+    return Raw8{*reinterpret_cast<const f32x4*>(p), *reinterpret_cast<const f32x4*>(p + 4)};
+  }
+  static __device__ __forceinline__ Raw8 zero() { return Raw8{f32x4{}, f32x4{}}; }
+  __device__ __forceinline__ void cvt(float* v) const {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = a[i];
+      v[4 + i] = b[i];
+    }
+  }
+};
+
 // ------------------------------------------------------------------ LayerNorm + modulation
 // NV = 16-byte vectors per lane; dim <= 64 * 8 * NV and dim % 8 == 0. One wavefront per row:
-// v[j] holds elements (lane + 64 j) * 8 .. + 8 of the row, replaced by the modulated output.
-template <typename TX, typename TM, int NV>
-__device__ __forceinline__ void ln_modulate_row(const TX* __restrict__ xr, int dim,
-                                                const TM* mb, const TM* ab, int one_plus,
-                                                float eps, int lane, float (&v)[NV][8]) {
-  float s = 0.f;
-#pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int c = (lane + 64 * j) * 8;
-    if (c < dim) {
-      V8<TX>::load(xr + c, v[j]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) s += v[j][i];
-    }
-  }
-  const float mean = wave_sum(s) / (float)dim;
-  float q = 0.f;
-#pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int c = (lane + 64 * j) * 8;
-    if (c < dim) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float d = v[j][i] - mean;
-        q += d * d;
-      }
-    }
-  }
-  const float rstd = 1.0f / __builtin_sqrtf(wave_sum(q) / (float)dim + eps);
-#pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int c = (lane + 64 * j) * 8;
-    if (c < dim) {
-      float m8[8], a8[8];
-      if (mb) {
-        V8<TM>::load(mb + c, m8);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) m8[i] = one_plus ? 0.f : 1.f;
-      }
-      if (ab) {
-        V8<TM>::load(ab + c, a8);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) a8[i] = 0.f;
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float mm = one_plus ? 1.0f + m8[i] : m8[i];
-        v[j][i] = (v[j][i] - mean) * rstd * mm + a8[i];
-      }
-    }
-  }
-}
+// chunk j of a lane is elements (lane + 64 j) * 8 .. + 8 of the row.
+template <typename TX, typename TM, int NV, bool FULL>
+struct LnRow {
+  Raw8<TX> x[NV];
+  Raw8<TM> m[NV], a[NV];
+  float mean, rstd, madd;
 
-template <typename TX, typename TY, typename TM, int NV>
+  // Every load of the row and of both modulation vectors is issued before the first use, from
+  // an in-bounds address (chunks past dim re-read chunk 0 and are excluded after): a load
+  // guarded by c < dim next to its use makes the compiler wait for each chunk in turn. The
+  // row stays in registers as loaded (16-bit words), so a wave needs few registers and many
+  // rows are in flight per compute unit. A missing modulation vector reads as zeros, and the
+  // output is LN(x) * (m + madd) + a with madd = 1 for one_plus or no mul vector.
+  __device__ __forceinline__ void load(const TX* __restrict__ xr, int dim, const TM* mb,
+                                       const TM* ab, int one_plus, float eps, int lane) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = (lane + 64 * j) * 8;
+      x[j] = Raw8<TX>::load(xr + (FULL || c < dim ? c : 0));
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = (lane + 64 * j) * 8;
+      m[j] = mb ? Raw8<TM>::load(mb + (FULL || c < dim ? c : 0)) : Raw8<TM>::zero();
+      a[j] = ab ? Raw8<TM>::load(ab + (FULL || c < dim ? c : 0)) : Raw8<TM>::zero();
+    }
+    madd = (one_plus || !mb) ? 1.0f : 0.0f;
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      if (FULL || (lane + 64 * j) * 8 < dim) {
+        float v[8];
+        x[j].cvt(v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s += v[i];
+      }
+    }
+    mean = wave_sum(s) / (float)dim;
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      if (FULL || (lane + 64 * j) * 8 < dim) {
+        float v[8];
+        x[j].cvt(v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float d = v[i] - mean;
+          q += d * d;
+        }
+      }
+    }
+    rstd = 1.0f / __builtin_sqrtf(wave_sum(q) / (float)dim + eps);
+  }
+
+  // modulated output of chunk j (elements (lane + 64 j) * 8 .. + 8)
+  __device__ __forceinline__ void out(int j, float (&o)[8]) const {
+    float v[8], m8[8], a8[8];
+    x[j].cvt(v);
+    m[j].cvt(m8);
+    a[j].cvt(a8);
+    const float nm = -mean * rstd;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      o[i] = __builtin_fmaf(__builtin_fmaf(v[i], rstd, nm), m8[i] + madd, a8[i]);
+  }
+};
+
+// One wavefront per row; rows of batch b use mul / add + b * mod_stride (split > 0: rows below
+// split are batch 0, the rest batch 1).
+template <typename TX, typename TY, typename TM, int NV, bool FULL>
 __global__ __launch_bounds__(256) void layernorm_modulate_kernel(
     const TX* __restrict__ x, int64_t ldx, TY* __restrict__ y, int64_t ldy, int64_t rows,
     int dim, const TM* __restrict__ mul, const TM* __restrict__ add, int64_t mod_stride,
@@ -130,20 +184,25 @@ __global__ __launch_bounds__(256) void layernorm_modulate_kernel(
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int64_t b = split > 0 ? (row >= split ? 1 : 0) : row / rows_per_batch;
-  float v[NV][8];
-  ln_modulate_row<TX, TM, NV>(x + row * ldx, dim, mul ? mul + b * mod_stride : nullptr,
-                              add ? add + b * mod_stride : nullptr, one_plus, eps, lane, v);
+  LnRow<TX, TM, NV, FULL> r;
+  r.load(x + row * ldx, dim, mul ? mul + b * mod_stride : nullptr,
+         add ? add + b * mod_stride : nullptr, one_plus, eps, lane);
   TY* yr = y + row * ldy;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = (lane + 64 * j) * 8;
-    if (c < dim) V8<TY>::store(yr + c, v[j]);
+    if (FULL || c < dim) {
+      float o[8];
+      r.out(j, o);
+      V8<TY>::store(yr + c, o);
+    }
   }
 }
 
-// The same row, rounded to bf16, then quantized by the per-row fp8 law: the codes and scale
-// equal layernorm_modulate (bf16 out) followed by quantize_fp8_rowwise, without the round trip.
-template <typename TX, typename TM, int NV>
+// layernorm_modulate rounded to bf16, then quantized per row to e4m3 (absmax / 448 scale): the
+// output equals quantize_fp8_rowwise of layernorm_modulate's bf16 result. The rounded row is kept
+// packed in registers between the absmax and the encoding.
+template <typename TX, typename TM, int NV, bool FULL>
 __global__ __launch_bounds__(256) void layernorm_modulate_fp8_kernel(
     const TX* __restrict__ x, int64_t ldx, uint8_t* __restrict__ q, int64_t ldq,
     float* __restrict__ scale, int64_t rows, int dim, const TM* __restrict__ mul,
@@ -153,19 +212,22 @@ __global__ __launch_bounds__(256) void layernorm_modulate_fp8_kernel(
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int64_t b = split > 0 ? (row >= split ? 1 : 0) : row / rows_per_batch;
-  float v[NV][8];
-  ln_modulate_row<TX, TM, NV>(x + row * ldx, dim, mul ? mul + b * mod_stride : nullptr,
-                              add ? add + b * mod_stride : nullptr, one_plus, eps, lane, v);
+  LnRow<TX, TM, NV, FULL> r;
+  r.load(x + row * ldx, dim, mul ? mul + b * mod_stride : nullptr,
+         add ? add + b * mod_stride : nullptr, one_plus, eps, lane);
+  u32x4 ob[NV];  // the bf16-rounded output, packed
   float amax = 0.f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    const int c = (lane + 64 * j) * 8;
-    if (c < dim) {
+    float o[8];
+    r.out(j, o);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        v[j][i] = bf16bits_to_f32(f32_to_bf16_bits(v[j][i]));
-        amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j][i]));
-      }
+    for (int i = 0; i < 4; ++i) ob[j][i] = pack_bf16x2(o[2 * i], o[2 * i + 1]);
+    if (FULL || (lane + 64 * j) * 8 < dim) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        amax = __builtin_fmaxf(amax, __builtin_fmaxf(__builtin_fabsf(bf16bits_to_f32(ob[j][i] & 0xffffu)),
+                                                     __builtin_fabsf(bf16bits_to_f32(ob[j][i] >> 16))));
     }
   }
   amax = wave_max(amax);
@@ -175,7 +237,15 @@ __global__ __launch_bounds__(256) void layernorm_modulate_fp8_kernel(
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = (lane + 64 * j) * 8;
-    if (c < dim) *reinterpret_cast<u32x2*>(qr + c) = encode8_rowwise(v[j], inv);
+    if (FULL || c < dim) {
+      float o[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o[2 * i] = bf16bits_to_f32(ob[j][i] & 0xffffu);
+        o[2 * i + 1] = bf16bits_to_f32(ob[j][i] >> 16);
+      }
+      *reinterpret_cast<u32x2*>(qr + c) = encode8_rowwise(o, inv);
+    }
   }
 }
 
@@ -562,10 +632,15 @@ static int launch_ln(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t r
                      int64_t rpb, int64_t split, int one_plus, float eps, hipStream_t s) {
   const int nv = (int)((dim + 511) / 512);
   dim3 grid((unsigned)((rows + 3) / 4)), block(256);
-#define DLT_LN(NV)                                                                      \
-  hipLaunchKernelGGL((layernorm_modulate_kernel<TX, TY, TM, NV>), grid, block, 0, s,  \
-                     (const TX*)x, ldx, (TY*)y, ldy, rows, (int)dim, (const TM*)mul,   \
+#define DLT_LN1(NV, FULL)                                                                     \
+  hipLaunchKernelGGL((layernorm_modulate_kernel<TX, TY, TM, NV, FULL>), grid, block, 0, s,  \
+                     (const TX*)x, ldx, (TY*)y, ldy, rows, (int)dim, (const TM*)mul,         \
                      (const TM*)add, mod_stride, rpb, split, one_plus, eps)
+#define DLT_LN(NV)                          \
+  do {                                      \
+    if (dim == 512 * (NV)) DLT_LN1(NV, true); \
+    else DLT_LN1(NV, false);                \
+  } while (0)
   if (nv <= 2) DLT_LN(2);
   else if (nv <= 4) DLT_LN(4);
   else if (nv <= 6) DLT_LN(6);
@@ -574,6 +649,7 @@ static int launch_ln(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t r
   else if (nv <= 16) DLT_LN(16);
   else { dlt_set_error("layernorm: dim %lld exceeds 8192", (long long)dim); return DIFFLET_EUNSUPPORTED; }
 #undef DLT_LN
+#undef DLT_LN1
   return dlt_check_launch("layernorm_modulate");
 }
 
@@ -611,10 +687,15 @@ static int launch_ln_fp8(const void* x, int64_t ldx, uint8_t* q, int64_t ldq, fl
                          float eps, hipStream_t s) {
   const int nv = (int)((dim + 511) / 512);
   dim3 grid((unsigned)((rows + 3) / 4)), block(256);
-#define DLT_LNQ(NV)                                                                     \
-  hipLaunchKernelGGL((layernorm_modulate_fp8_kernel<TX, TM, NV>), grid, block, 0, s,  \
-                     (const TX*)x, ldx, q, ldq, scale, rows, (int)dim, (const TM*)mul,  \
+#define DLT_LNQ1(NV, FULL)                                                                    \
+  hipLaunchKernelGGL((layernorm_modulate_fp8_kernel<TX, TM, NV, FULL>), grid, block, 0, s,  \
+                     (const TX*)x, ldx, q, ldq, scale, rows, (int)dim, (const TM*)mul,        \
                      (const TM*)add, mod_stride, rpb, split, one_plus, eps)
+#define DLT_LNQ(NV)                          \
+  do {                                       \
+    if (dim == 512 * (NV)) DLT_LNQ1(NV, true); \
+    else DLT_LNQ1(NV, false);                \
+  } while (0)
   if (nv <= 2) DLT_LNQ(2);
   else if (nv <= 4) DLT_LNQ(4);
   else if (nv <= 6) DLT_LNQ(6);
@@ -623,6 +704,7 @@ static int launch_ln_fp8(const void* x, int64_t ldx, uint8_t* q, int64_t ldq, fl
   else if (nv <= 16) DLT_LNQ(16);
   else { dlt_set_error("layernorm_modulate_fp8: dim %lld exceeds 8192", (long long)dim); return DIFFLET_EUNSUPPORTED; }
 #undef DLT_LNQ
+#undef DLT_LNQ1
   return dlt_check_launch("layernorm_modulate_fp8");
 }
 

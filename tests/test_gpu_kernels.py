@@ -447,6 +447,33 @@ def test_gemv_shapes_tail_and_strided_weights(gpu, m, k, n, xdt):
             kernels.gemv(torch.zeros(8, 2056, device=gpu), w.to(gpu)[:, :8].repeat(1, 257))
 
 
+def test_bf16_rounding_every_upper_half_and_midpoint(gpu):
+    """Kernels round fp32 results to bf16 to nearest even: LN(x) * 0 + add with fp32 add vectors
+    returns bf16(add) exactly. Every upper half-word with the low halves that decide the rounding
+    (0, below the tie, the tie, above it, all ones, one random) against torch's rounding, bit for
+    bit; NaN stays NaN (torch writes one canonical NaN, the kernels keep the payload)."""
+    g = torch.Generator().manual_seed(5)
+    hi = torch.arange(65536, dtype=torch.int64) << 16
+    lows = [torch.full((65536,), lo, dtype=torch.int64) for lo in (0, 0x7fff, 0x8000, 0x8001, 0xffff)]
+    lows.append(torch.randint(0, 65536, (65536,), generator=g, dtype=torch.int64))
+    bits = torch.cat([hi | lo for lo in lows])
+    vals = torch.where(bits >= 2**31, bits - 2**32, bits).to(torch.int32).view(torch.float32)
+    dim = 8192
+    add = vals.reshape(-1, dim)
+    rows = add.shape[0]
+    x = torch.randn(rows, dim, generator=g)
+    out = kernels.layernorm_modulate(x.to(gpu), torch.zeros(rows, dim, device=gpu), add.to(gpu),
+                                     eps=1e-6, one_plus=False, out_dtype=torch.bfloat16,
+                                     rows_per_batch=1).cpu().reshape(-1)
+    ref = vals.bfloat16()
+    nan = torch.isnan(vals)
+    assert torch.isnan(out[nan]).all()
+    got, want = out[~nan].view(torch.int16), ref[~nan].view(torch.int16)
+    zero = vals[~nan] == 0  # LN(x) * 0 + (-0) may be +0
+    assert torch.equal(got[~zero], want[~zero])
+    assert (out[~nan][zero] == 0).all()
+
+
 def test_gelu_gate_residual_gemv_timestep(gpu):
     g = torch.Generator().manual_seed(12)
     x = rnd(g, 1001, dtype=torch.float32) * 4
