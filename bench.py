@@ -50,10 +50,10 @@ COPY_BYTES = 256 << 20
 # --calibrate-copy 256 MiB copy). MALL hits are counted too, so this bounds HBM bytes from above.
 # Keyed by (workload, kind); absent -> null.
 TRAFFIC: dict = {
-    # 4608 x 21504 x 3072 GELU GEMM: 1139.1 MB read (A + W = 160 MB once) + 198.3 MB written
-    ("flux", "bf16"): 1_337_400_000,
-    # same GEMM, e4m3 operands: 581.5 MB read (80 MB once) + 203.0 MB written
-    ("flux", "fp8"): 784_500_000,
+    # 4608 x 21504 x 3072 GELU GEMM: 1293.9 MB read (A + W = 160 MB once) + 203.5 MB written
+    ("flux", "bf16"): 1_497_400_000,
+    # same GEMM, e4m3 operands: 577.6 MB read (80 MB once) + 200.4 MB written
+    ("flux", "fp8"): 778_000_000,
 }
 
 
