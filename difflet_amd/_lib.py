@@ -57,7 +57,9 @@ SIGNATURES: dict[str, tuple] = {
     "difflet_rocm_device_count": (_i32, []),
     "difflet_rocm_attention": (_i32, [
         _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64,
-        _i64p, _i64p, _i64p, _i64p, _f32, _i32, _vp, _i32, _i64p, _vp, _vp, _i64p, _vp]),
+        _i64p, _i64p, _i64p, _i64p, _f32, _i32, _vp, _i32, _i64p, _vp, _vp, _i64p, _vp, _i64,
+        _vp]),
+    "difflet_rocm_attention_workspace_bytes": (_i64, []),
     "difflet_rocm_gemm_workspace_bytes": (_i64, []),
     "difflet_rocm_gemm_bf16": (_i32, [_i32, ctypes.POINTER(GemmProblem), _i64, _i64, _i32,
                                       _i64, _vp, _i64, _vp]),

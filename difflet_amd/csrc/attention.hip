@@ -61,7 +61,30 @@ struct AttnArgs {
   const int32_t* bmin;
   const int32_t* bmax;
   int64_t bs[3];
+  // split schedule of the ping-pong kernel (split_groups == 0: one query tile per workgroup)
+  int split_groups;
+  int64_t split_units;
+  uint8_t* ws;
 };
+
+// Split schedule of the ping-pong kernel, for launches whose last wave of workgroups would leave
+// many compute units idle: one workgroup per compute unit, each taking an equal contiguous range
+// of the (query tile, key tile) units, query-tile-major. A query tile cut between workgroups
+// c0 .. c1 is finished by the last of them to arrive: every contributor stores its unnormalized
+// output, running max and running sum to a workspace slot and counts itself in the tile's
+// counter; the last one merges the slots in contributor order (a fixed order: the result does
+// not depend on which one arrives last), normalizes and writes the output. A workgroup's range
+// holds at most two cut query tiles (its first and its last), hence two slots per workgroup.
+constexpr int64_t ATT_CTR_BYTES = 16384;                  // one int counter per query tile
+constexpr int ATT_MAX_TILES = (int)(ATT_CTR_BYTES / 4);
+constexpr int64_t ATT_SLOT_OUT = 8 * 16 * 1024;           // fp32 output: 8 waves x 16 KB
+constexpr int64_t ATT_SLOT_BYTES = ATT_SLOT_OUT + 8 * 64 * 8;  // + (max, sum) per lane
+__host__ __device__ inline int64_t att_lo(int64_t units, int groups, int s) {
+  return (int64_t)s * units / groups;
+}
+__host__ __device__ inline int att_owner(int64_t units, int groups, int64_t x) {
+  return (int)(((x + 1) * groups - 1) / units);
+}
 
 template <typename T> struct MfmaT;
 template <> struct MfmaT<bf16> {
@@ -357,10 +380,24 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
   const int gt = tid & 255;  // thread index within the group
   const int col = lane & 31, g = lane >> 5;
 
+  __shared__ int last_flag;
+  const int ntiles = (a.seq_k + BLOCK_N - 1) / BLOCK_N;
   int bid = blockIdx.x;  // XCD-contiguous runs of query tiles (whole heads share an L2)
-  if ((a.total & 7) == 0) bid = (bid & 7) * (a.total >> 3) + (bid >> 3);
-  const int bh = bid / a.q_tiles;
-  const int qt = bid % a.q_tiles;
+  if ((gridDim.x & 7) == 0) bid = (bid & 7) * (gridDim.x >> 3) + (bid >> 3);
+  // work: one query tile, or (split schedule) a range of (query tile, key tile) units
+  int64_t u_lo = (int64_t)bid * ntiles, u_hi = u_lo + ntiles;
+  if (a.split_groups) {
+    u_lo = att_lo(a.split_units, a.split_groups, bid);
+    u_hi = att_lo(a.split_units, a.split_groups, bid + 1);
+  }
+  for (int64_t u = u_lo; u < u_hi;) {
+  const int item = (int)(u / ntiles);
+  const int t0 = (int)(u - (int64_t)item * ntiles);  // key tiles [t0, t0 + nt) run here
+  const int nt = (int)min((int64_t)(ntiles - t0), u_hi - u);
+  if (u != u_lo) __syncthreads();  // the previous query tile's LDS reads are done
+  u += nt;
+  const int bh = item / a.q_tiles;
+  const int qt = item % a.q_tiles;
   const int b = bh / a.heads, h = bh % a.heads;
   const int my_q = qt * (2 * BLOCK_M) + wave * 32 + col;
 
@@ -420,7 +457,6 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
   uint32_t pp[2][8] = {};  // P of the tile being multiplied next, packed 16-bit pairs
   float m_run = -INFINITY, l_run = 0.f;
   const float cmul = a.scale_log2;
-  const int ntiles = (a.seq_k + BLOCK_N - 1) / BLOCK_N;
 
   // One MFMA phase: O^T += V^T P^T of the tile in sv[vst] (4 groups of 4 MFMAs, one per
   // 16 keys), then S^T = K Q^T of the tile in sk[kst] (4 groups: two d-chunks for both 32-key
@@ -428,7 +464,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
   // while group i's MFMAs run; sched_barrier keeps the compiler from pulling each read down
   // next to its MFMA, where every MFMA would wait out a full LDS latency.
   auto mfma_phase = [&](int vst, int kst) {
-    frag fb[2][4];
+    frag fb[4][4];
     auto load_group = [&](int gi, frag (&f)[4]) {
       if (gi < 4) {
         const int base = (gi >> 1) * 32 + (gi & 1) * 16;
@@ -462,11 +498,13 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
       }
     };
     load_group(0, fb[0]);
+    load_group(1, fb[1]);
+    load_group(2, fb[2]);
 #pragma unroll
     for (int gi = 0; gi < 8; ++gi) {
-      if (gi < 7) load_group(gi + 1, fb[(gi + 1) & 1]);
+      if (gi < 5) load_group(gi + 3, fb[(gi + 3) & 3]);
       __builtin_amdgcn_sched_barrier(0);
-      run_group(gi, fb[gi & 1]);
+      run_group(gi, fb[gi & 3]);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -520,18 +558,19 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
     }
   };
 
-  // The two groups run separate loops with the same barrier sequence (2 + 2 ntiles
-  // barriers), so each loop's registers are allocated for that group alone.
+  // The two groups run separate loops with the same barrier sequence (2 + 2 nt barriers), so
+  // each loop's registers are allocated for that group alone. Key tiles t0 .. t0 + nt - 1.
+  const int k0 = t0 * BLOCK_N;
   if (grp_a) {
-    load_v(0);
-    phase_barrier();  // prologue: B has K(0), K(1) in LDS
+    load_v(k0);
+    phase_barrier();  // prologue: B has K(t0), K(t0 + 1) in LDS
     scores_only(0);
     phase_barrier();
-    for (int jt = 0; jt < ntiles; ++jt) {
-      const int j0 = jt * BLOCK_N;
+    for (int jt = 0; jt < nt; ++jt) {
+      const int j0 = k0 + jt * BLOCK_N;
       softmax(j0);  // phase 2j
       store_v(jt & 1);
-      if (jt + 1 < ntiles) load_v(j0 + BLOCK_N);
+      if (jt + 1 < nt) load_v(j0 + BLOCK_N);
       phase_barrier();
       __builtin_amdgcn_s_setprio(1);  // phase 2j + 1 (past the last tile the scores read
       mfma_phase(jt & 1, (jt + 1) & 1);  // the idle K buffer and go unused)
@@ -539,31 +578,103 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
       phase_barrier();
     }
   } else {
-    load_k(0);
+    load_k(k0);
     store_k(0);
-    if (ntiles > 1) {
-      load_k(BLOCK_N);
+    if (nt > 1) {
+      load_k(k0 + BLOCK_N);
       store_k(1);
     }
-    if (ntiles > 2) load_k(2 * BLOCK_N);
+    if (nt > 2) load_k(k0 + 2 * BLOCK_N);
     // sv[1] is read as "tile -1" by the first P V (with P = 0): zeros, not stale LDS that
     // could hold NaN patterns
     for (int i = gt; i < HD * VT_PITCH / 16; i += 256)
       *reinterpret_cast<u32x4*>(&sv[1][i * 16]) = u32x4{0u, 0u, 0u, 0u};
     phase_barrier();
     phase_barrier();  // A scores tile 0
-    for (int jt = 0; jt < ntiles; ++jt) {
-      const int j0 = jt * BLOCK_N;
+    for (int jt = 0; jt < nt; ++jt) {
+      const int j0 = k0 + jt * BLOCK_N;
       __builtin_amdgcn_s_setprio(1);  // phase 2j (the first P V is of "tile -1": P = 0)
       mfma_phase((jt - 1) & 1, jt & 1);
       __builtin_amdgcn_s_setprio(0);
       phase_barrier();
       softmax(j0);  // phase 2j + 1
-      if (jt + 2 < ntiles) store_k(jt & 1);
-      if (jt + 3 < ntiles) load_k(j0 + 3 * BLOCK_N);
+      if (jt + 2 < nt) store_k(jt & 1);
+      if (jt + 3 < nt) load_k(j0 + 3 * BLOCK_N);
       phase_barrier();
     }
-    mfma_phase((ntiles - 1) & 1, ntiles & 1);  // phase 2n: the last P V (scores unused)
+    mfma_phase((nt - 1) & 1, nt & 1);  // phase 2n: the last P V (scores unused)
+  }
+
+  if (nt != ntiles) {
+    // a query tile cut between split workgroups: store this part (device-scope sc1 stores,
+    // complete before the count, so the last contributor's device-scope loads see them)
+    const int64_t x0 = (int64_t)item * ntiles;
+    const int c0 = att_owner(a.split_units, a.split_groups, x0);
+    const int c1 = att_owner(a.split_units, a.split_groups, x0 + ntiles - 1);
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(a.ws + ATT_CTR_BYTES, (uint32_t)(2 * a.split_groups * ATT_SLOT_BYTES));
+    constexpr int SC1 = 16;
+    auto slot = [&](int c) {
+      return (uint32_t)((2 * c + (att_lo(a.split_units, a.split_groups, c) >= x0 ? 0 : 1)) *
+                        ATT_SLOT_BYTES);
+    };
+    const uint32_t vo = (uint32_t)lane * 16, mo = (uint32_t)(ATT_SLOT_OUT + (wave * 64 + lane) * 8);
+    {
+      const uint32_t so = slot(bid);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const f32x4 v = {acc[dt][q4 * 4], acc[dt][q4 * 4 + 1], acc[dt][q4 * 4 + 2],
+                           acc[dt][q4 * 4 + 3]};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, vo,
+                                                 so + (uint32_t)((wave * 16 + dt * 4 + q4) * 1024),
+                                                 SC1);
+        }
+      const u32x2 ml = {__builtin_bit_cast(uint32_t, m_run), __builtin_bit_cast(uint32_t, l_run)};
+      __builtin_amdgcn_raw_buffer_store_b64(ml, rs, mo, so, SC1);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the stores are complete
+    __syncthreads();
+    int* ctr = reinterpret_cast<int*>(a.ws) + item;
+    if (tid == 0)
+      last_flag = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == c1 - c0;
+    __syncthreads();
+    if (!last_flag) continue;  // another contributor finishes this query tile
+    // merge the parts in contributor order: running max, then the rescaled sums
+    // (loaded vectors are cast whole: hipcc lowers a bit_cast of one vector element to a read
+    // of element 0)
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    float m_all = -INFINITY;
+    for (int c = c0; c <= c1; ++c) {
+      const f32x2_t ml =
+          __builtin_bit_cast(f32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rs, mo, slot(c), SC1));
+      m_all = fmaxf(m_all, ml[0]);
+    }
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x16{};
+    l_run = 0.f;
+    for (int c = c0; c <= c1; ++c) {
+      const uint32_t so = slot(c);
+      const f32x2_t ml =
+          __builtin_bit_cast(f32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rs, mo, so, SC1));
+      const float f = ml[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml[0] - m_all);
+      l_run += f * ml[1];
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        f32x4 v[4];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4)
+          v[q4] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         rs, vo, so + (uint32_t)((wave * 16 + dt * 4 + q4) * 1024), SC1));
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[dt][q4 * 4 + e] += f * v[q4][e];
+      }
+    }
+    if (tid == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
   const float inv = 1.0f / pair_sum(l_run);
@@ -579,11 +690,35 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
         *reinterpret_cast<u32x2*>(op + dt * 32 + q4 * 8 + g * 4) = w;
       }
   }
+  }  // query tiles of this workgroup
 }
 
 }  // namespace dlt
 
 using namespace dlt;
+
+// Compute units of the current device (one ping-pong workgroup fills a CU's LDS share).
+static int att_device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    cached[dev] = v;
+  }
+  return cached[dev];
+}
+
+static int64_t att_workspace_bytes(int groups) {
+  return ATT_CTR_BYTES + 2 * (int64_t)groups * ATT_SLOT_BYTES;
+}
+
+extern "C" int64_t difflet_rocm_attention_workspace_bytes(void) {
+  const int cus = att_device_cus();
+  return cus > 0 ? att_workspace_bytes(cus) : 0;
+}
 
 extern "C" int difflet_rocm_attention(const void* q, const void* k, const void* v, void* o,
                                       int dtype, int64_t batch, int64_t heads, int64_t seq_q,
@@ -593,6 +728,7 @@ extern "C" int difflet_rocm_attention(const void* q, const void* k, const void* 
                                       const void* mask, int mask_dtype,
                                       const int64_t* mask_strides, const int32_t* bound_min,
                                       const int32_t* bound_max, const int64_t* bound_strides,
+                                      void* workspace, int64_t workspace_bytes,
                                       difflet_stream_t stream) {
   DLT_REQUIRE(q && k && v && o && q_strides && k_strides && v_strides && o_strides,
               DIFFLET_EINVAL, "attention: null pointer");
@@ -665,6 +801,18 @@ extern "C" int difflet_rocm_attention(const void* q, const void* k, const void* 
     for (int i = 0; i < 3; ++i) args.bs[i] = bound_strides[i];
   hipStream_t s = (hipStream_t)stream;
   dim3 grid((unsigned)total);
+  if (pingpong && workspace) {
+    // split schedule when the last wave of workgroups would leave > 10 % of the CUs idle
+    const int cus = att_device_cus();
+    const int64_t tail = cus > 0 ? total % cus : 0;
+    if (cus > 0 && total > cus && tail != 0 && tail * 10 < cus * 9 && total <= ATT_MAX_TILES &&
+        workspace_bytes >= att_workspace_bytes(cus)) {
+      args.split_groups = cus;
+      args.split_units = total * ((seq_k + BLOCK_N - 1) / BLOCK_N);
+      args.ws = (uint8_t*)workspace;
+      grid = dim3((unsigned)cus);
+    }
+  }
   if (dtype == DIFFLET_BF16) {
     if (pingpong) hipLaunchKernelGGL((attn_pp_kernel<bf16>), grid, dim3(512), 0, s, args);
     else if (masked) hipLaunchKernelGGL((attn_fwd_kernel<bf16, true>), grid, dim3(256), 0, s, args);

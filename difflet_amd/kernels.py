@@ -80,8 +80,13 @@ def _rows2d(t: torch.Tensor, name: str) -> torch.Tensor:
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float,
               causal: bool = False, attention_mask: torch.Tensor | None = None,
               bound_min: torch.Tensor | None = None, bound_max: torch.Tensor | None = None,
-              out: torch.Tensor | None = None) -> torch.Tensor:
-    """softmax(q k^T scale [+ mask]) v on [B, H, S, D] (or [B*H, S, D]) tensors."""
+              out: torch.Tensor | None = None,
+              workspace: torch.Tensor | None | str = "shared") -> torch.Tensor:
+    """softmax(q k^T scale [+ mask]) v on [B, H, S, D] (or [B*H, S, D]) tensors.
+
+    workspace: "shared" (the device's attention workspace, for work issued in order on one
+    stream), a zero-filled uint8 tensor of attention_workspace_bytes(), or None (every query
+    tile runs whole on one workgroup)."""
     dev = _on_gpu(q, k, v)
     folded = q.dim() == 3
     scores_shape = tuple(q.shape[:-1]) + (k.shape[-2],)
@@ -132,11 +137,16 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float
         keep += [bmn, bmx]
         bmin_ptr, bmax_ptr = _ptr(bmn), _ptr(bmx)
         bstr = _arr(bmn.stride())
+    if isinstance(workspace, str):
+        if workspace != "shared":
+            raise ValueError(f"workspace must be 'shared', a tensor or None, not {workspace!r}")
+        workspace = attention_workspace(dev)
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (_ptr(workspace), workspace.numel())
     st = lib().difflet_rocm_attention(
         _ptr(q), _ptr(k), _ptr(v), _ptr(o), _dt(q), b, h, sq, sk, d,
         _arr(q.stride()[:3]), _arr(k.stride()[:3]), _arr(v.stride()[:3]), _arr(o.stride()[:3]),
         float(scale), int(bool(causal)), mask_ptr, mask_dt, mask_strides, bmin_ptr, bmax_ptr,
-        bstr, _stream(dev))
+        bstr, ws_ptr, ws_bytes, _stream(dev))
     check(st, "attention")
     return out
 
@@ -161,6 +171,20 @@ _GEMM_FN = {"bf16": "difflet_rocm_gemm_bf16", "fp8": "difflet_rocm_gemm_fp8_roww
 
 
 _WORKSPACE: dict[int, torch.Tensor] = {}
+_ATT_WORKSPACE: dict[int, torch.Tensor] = {}
+
+
+def attention_workspace(dev: torch.device) -> torch.Tensor:
+    """The device's shared attention workspace (split schedule), zero-filled once on first use.
+    It serves attention launches issued in order on one stream at a time."""
+    i = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _ATT_WORKSPACE.get(i)
+    if ws is None:
+        with torch.cuda.device(i):
+            nbytes = int(lib().difflet_rocm_attention_workspace_bytes())
+        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=torch.device("cuda", i))
+        _ATT_WORKSPACE[i] = ws
+    return ws
 
 
 def gemm_workspace(dev: torch.device) -> torch.Tensor:

@@ -60,6 +60,14 @@ int difflet_rocm_device_count(void);
  * bound_max: optional int32 [batch, heads, seq_q] through strides; keys in [min, max) attend
  * (difflet/backends/cpu/ops_impl/attention.py:24-35). Masked scores take the dtype's lowest
  * finite value, so a fully masked row averages v exactly as the reference does.
+ * workspace / workspace_bytes: optional device memory for the split schedule of unmasked
+ * attention over more than 1024 keys. When the launch's 256-query tiles would leave the last
+ * wave of workgroups under 90 % full, one workgroup per compute unit takes an equal range of
+ * (query tile, key tile) units and query tiles cut between workgroups are merged, in a fixed
+ * order, by the last contributor (a deterministic result; the summation order differs from the
+ * unsplit one by fp32 rounding). With workspace NULL or too small every query tile runs whole.
+ * The workspace must be zero-filled once when allocated (the kernels leave it zeroed), and
+ * launches that may overlap in time must not share one.
  * ---------------------------------------------------------------------------------------- */
 int difflet_rocm_attention(const void* q, const void* k, const void* v, void* o, int dtype,
                            int64_t batch, int64_t heads, int64_t seq_q, int64_t seq_k,
@@ -68,7 +76,12 @@ int difflet_rocm_attention(const void* q, const void* k, const void* v, void* o,
                            int causal, const void* mask, int mask_dtype,
                            const int64_t* mask_strides, const int32_t* bound_min,
                            const int32_t* bound_max, const int64_t* bound_strides,
-                           difflet_stream_t stream);
+                           void* workspace, int64_t workspace_bytes, difflet_stream_t stream);
+
+/* Bytes of attention workspace the split schedule needs on the current device: 16 KiB of
+ * counters + 2 x 132 KiB per compute unit (0 without a device). No counterpart in the
+ * reference, whose attention calls torch's SDPA (difflet/backends/cuda/ops_impl/attention.py:41-86). */
+int64_t difflet_rocm_attention_workspace_bytes(void);
 
 /* ------------------------------------------------------------------------------------------
  * GEMM with fused epilogues: for each problem p, C_p = epilogue(A_p W_p^T + bias_p).

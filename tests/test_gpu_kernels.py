@@ -265,6 +265,29 @@ def test_attention_matches_fp32(gpu, b, h, sq, sk, dtype):
     assert rel_l2(out, ref) < 1e-2  # probabilities rounded to 16 bits before P V
 
 
+# more 256-query tiles than compute units with a last wave under 90 % full: the split schedule
+# (query tiles cut between workgroups, merged by the last contributor) runs with the workspace
+@pytest.mark.parametrize("b,h,sq,sk", [(1, 24, 4600, 1100), (2, 20, 2048, 2048)])
+def test_attention_split_schedule_equals_whole_tiles(gpu, b, h, sq, sk):
+    print(f"attention split b={b} h={h} sq={sq} sk={sk}", flush=True)
+    g = torch.Generator().manual_seed(sq + sk + h)
+    q, k, v = (t.to(gpu) for t in _attn_case(g, b, h, sq, sk))
+    scale = 1 / math.sqrt(128)
+    ws = kernels.attention_workspace(torch.device(gpu))
+    split1 = kernels.attention(q, k, v, scale=scale, workspace=ws)
+    split2 = kernels.attention(q, k, v, scale=scale, workspace=ws)
+    whole = kernels.attention(q, k, v, scale=scale, workspace=None)
+    torch.cuda.synchronize()
+    assert torch.equal(split1.view(torch.int16), split2.view(torch.int16))  # deterministic
+    assert not torch.isnan(split1).any()
+    # merged parts sum in another order than one pass: a bf16 rounding step apart at most
+    assert rel_l2(split1, whole) < 2e-3
+    assert int(torch.count_nonzero(ws[:16384].view(torch.int32))) == 0  # counters back at zero
+    ref = ops.attention(q[:1, :2].float().cpu(), k[:1, :2].float().cpu(), v[:1, :2].float().cpu(),
+                        scale=scale)
+    assert rel_l2(split1[:1, :2], ref) < 1e-2
+
+
 def test_attention_folded_heads_and_scale_one(gpu):
     g = torch.Generator().manual_seed(5)
     q, k, v = (rnd(g, 6, 96, 128, std=0.2) for _ in range(3))
