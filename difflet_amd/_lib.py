@@ -46,6 +46,17 @@ class GemmProblem(ctypes.Structure):
         ("residual", _vp), ("ldr", _i64),
         ("a_scale", _vp), ("w_scale", _vp),
         ("m", _i64), ("rows_per_batch", _i64),
+        ("norm_q", _vp), ("norm_k", _vp), ("rope_row0", _i64),
+    ]
+
+
+class GemmQk(ctypes.Structure):
+    """``difflet_gemm_qk`` of include/difflet_rocm.h."""
+
+    _fields_ = [
+        ("q_col", _i64), ("k_col", _i64), ("cols", _i64),
+        ("cos", _vp), ("sin", _vp),
+        ("law", _i32), ("eps", _f32),
     ]
 
 
@@ -62,11 +73,11 @@ SIGNATURES: dict[str, tuple] = {
     "difflet_rocm_attention_workspace_bytes": (_i64, []),
     "difflet_rocm_gemm_workspace_bytes": (_i64, []),
     "difflet_rocm_gemm_bf16": (_i32, [_i32, ctypes.POINTER(GemmProblem), _i64, _i64, _i32,
-                                      _i64, _vp, _i64, _vp]),
+                                      _i64, _vp, _i64, ctypes.POINTER(GemmQk), _vp]),
     "difflet_rocm_gemm_fp8_rowwise": (_i32, [_i32, ctypes.POINTER(GemmProblem), _i64, _i64,
-                                             _i32, _i64, _vp, _i64, _vp]),
+                                             _i32, _i64, _vp, _i64, ctypes.POINTER(GemmQk), _vp]),
     "difflet_rocm_gemm_mxfp8": (_i32, [_i32, ctypes.POINTER(GemmProblem), _i64, _i64, _i32,
-                                       _i64, _vp, _i64, _vp]),
+                                       _i64, _vp, _i64, ctypes.POINTER(GemmQk), _vp]),
     "difflet_rocm_gemm_schedule_check": (_i32, [_i32, _i32, _i32, _i32, _i64,
                                                 ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
     "difflet_rocm_quantize_fp8_rowwise": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _vp,

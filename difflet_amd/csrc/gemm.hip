@@ -56,6 +56,9 @@ struct GemmProblemDev {
   int64_t lda, ldw, ldc, ldr, gate_stride;  // element strides (A / W in elements of Elem)
   int64_t m, rows_per_batch;
   int tiles_m, tile_start;
+  const bf16* nq;     // fused q/k norm: RMSNorm weights of q and k heads (NULL: 1)
+  const bf16* nk;
+  int64_t rope_row0;  // RoPE table row of row 0
 };
 
 // Split schedule (stream-K). Tiles [0, dp) run one per workgroup. The other S tiles are cut
@@ -96,6 +99,12 @@ struct GemmArgs {
   int act_col_start;
   SkPlan sk;
   uint8_t* ws;  // split workspace: counters, then 2 slots per split workgroup
+  // fused q/k RMSNorm + RoPE on output columns [q_col, q_col + qk_cols) and [k_col, ..)
+  // (qk_cols 0: off; all multiples of 256, so a tile lies wholly inside or outside)
+  int qk_cols, q_col, k_col, rope_law;
+  float qk_eps;
+  const float* rope_cos;
+  const float* rope_sin;
 };
 
 // KT: K elements per stage. WN: wavefronts along N (two along M). Every type runs 8 wavefronts
@@ -146,7 +155,7 @@ __device__ __forceinline__ int lds_off(int row, int chunk) {
 }
 
 // WN = ElemTraits<E>::WN wavefronts along N, 2 along M: 128 WN threads.
-template <Elem E, int EPI, int WN>
+template <Elem E, int EPI, int WN, bool QK>
 __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) {
   constexpr int KT = ElemTraits<E>::KT;
   constexpr int EB = ElemTraits<E>::BYTES;
@@ -530,6 +539,99 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
   // alias C, so loads left between stores would each wait out a full memory latency.
   const int act_start = args.act_col_start;
   const float* ws = reinterpret_cast<const float*>(P.w_scale);
+  // fused q/k RMSNorm + RoPE: this tile's 256 columns are two heads of q or of k; a head's 128
+  // columns are the 64 of waves wn = 2 h and 2 h + 1, whose per-row sums of squares meet in LDS
+  bool qk_tile = false;
+  if constexpr (QK)
+    qk_tile = (n0 >= args.q_col && n0 < (int64_t)args.q_col + args.qk_cols) ||
+              (n0 >= args.k_col && n0 < (int64_t)args.k_col + args.qk_cols);
+  if constexpr (QK) if (qk_tile) {
+    // The tile's bf16 output (the plain GEMM's values) goes through the idle LDS ring as
+    // [256 rows][32 chunks of 16 bytes], chunk c of row r at c ^ (r & 31); then each half-wave
+    // takes one row: 16 lanes per 128-column head reduce its sum of squares with xor shuffles,
+    // scale by rsqrt(mean + eps) and the norm weights, rotate and store 16 bytes per lane.
+    const bf16* nw = (n0 >= args.q_col && n0 < (int64_t)args.q_col + args.qk_cols) ? P.nq : P.nk;
+    uint8_t* tile = lds;
+    __syncthreads();  // every wave's last fragment reads of the ring are done
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = wm * 128 + i * 32 + frow;  // tile row
+      const int64_t mc = min(m0 + r, (int64_t)M - 1);
+      float sa = 1.f;
+      if constexpr (E == Elem::FP8) sa = reinterpret_cast<const float*>(P.a_scale)[mc];
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int cl = wn * WTN + j * 32 + q * 8 + fhalf * 4;  // tile column of the 4 values
+          const int64_t n = n0 + cl;  // < N: the q/k columns lie inside N
+          const u32x2 bv = P.bias ? *reinterpret_cast<const u32x2*>(P.bias + n) : u32x2{0u, 0u};
+          f32x4 wsv = {1.f, 1.f, 1.f, 1.f};
+          if constexpr (E == Elem::FP8) wsv = *reinterpret_cast<const f32x4*>(ws + n);
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[e] = acc[i][j][q * 4 + e];
+            if constexpr (E == Elem::FP8) v[e] = v[e] * (sa * wsv[e]);
+            v[e] += bf16bits_to_f32(e & 1 ? bv[e >> 1] >> 16 : bv[e >> 1] & 0xffffu);
+          }
+          const u32x2 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+          *reinterpret_cast<u32x2*>(tile + r * 512 + (((cl >> 3) ^ (r & 31)) << 4) + (cl & 7) * 2) = o;
+        }
+    }
+    __syncthreads();
+    const int ch = lane & 31, half = lane >> 5;  // 16-byte chunk of the row, which row of two
+    const int d = (ch & 15) * 8;                 // column within the head
+    const u32x4 wraw = nw ? *reinterpret_cast<const u32x4*>(nw + d)
+                          : u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+    for (int r = wave * 2 + half; r < BM; r += 2 * NWAVES) {
+      const int64_t m = m0 + r;
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(tile + r * 512 + ((ch ^ (r & 31)) << 4));
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[2 * e] = bf16bits_to_f32(raw[e] & 0xffffu);
+        v[2 * e + 1] = bf16bits_to_f32(raw[e] >> 16);
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o, 64);
+      const float rs = 1.0f / __builtin_sqrtf(ss / 128.0f + args.qk_eps);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[2 * e] = v[2 * e] * rs * bf16bits_to_f32(wraw[e] & 0xffffu);
+        v[2 * e + 1] = v[2 * e + 1] * rs * bf16bits_to_f32(wraw[e] >> 16);
+      }
+      if (m < M) {
+        const int64_t rr = P.rope_row0 + m;
+        const float* cp = args.rope_cos + rr * 128 + d;
+        const float* sp = args.rope_sin + rr * 128 + d;
+        float c[8], sn[8];
+        *reinterpret_cast<f32x4*>(c) = *reinterpret_cast<const f32x4*>(cp);
+        *reinterpret_cast<f32x4*>(c + 4) = *reinterpret_cast<const f32x4*>(cp + 4);
+        *reinterpret_cast<f32x4*>(sn) = *reinterpret_cast<const f32x4*>(sp);
+        *reinterpret_cast<f32x4*>(sn + 4) = *reinterpret_cast<const f32x4*>(sp + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float a0 = v[2 * e], b0 = v[2 * e + 1];
+          if (args.rope_law == 0) {
+            v[2 * e] = a0 * c[2 * e] - b0 * sn[2 * e];
+            v[2 * e + 1] = b0 * c[2 * e + 1] + a0 * sn[2 * e + 1];
+          } else {
+            v[2 * e] = a0 * c[2 * e] - b0 * sn[2 * e + 1];
+            v[2 * e + 1] = a0 * sn[2 * e + 1] + b0 * c[2 * e];
+          }
+        }
+        u32x4 st;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) st[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+        *reinterpret_cast<u32x4*>(reinterpret_cast<bf16*>(P.c) + m * P.ldc + n0 + ch * 8) = st;
+      }
+    }
+    continue;  // this tile is stored
+  }
   const bf16* bias = P.bias;
   u32x2 bias_v[4][4], gate_v[4][4];  // [j < TJ][q]
   f32x4 ws_v[4][4];
@@ -650,7 +752,8 @@ static SkPlan sk_plan(int T, int nk, int gran, int cus, int64_t ws_bytes) {
 template <Elem E>
 static int gemm_launch(const char* name, int nproblems, const difflet_gemm_problem* problems,
                        int64_t n, int64_t k, int epilogue, int64_t act_col_start,
-                       void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+                       void* workspace, int64_t workspace_bytes, const difflet_gemm_qk* qk,
+                       hipStream_t stream) {
   constexpr int KT = ElemTraits<E>::KT;
   constexpr int EB = ElemTraits<E>::BYTES;
   DLT_REQUIRE(problems && nproblems >= 1 && nproblems <= MAX_PROBLEMS, DIFFLET_EINVAL,
@@ -719,6 +822,13 @@ static int gemm_launch(const char* name, int nproblems, const difflet_gemm_probl
                 DIFFLET_EUNSUPPORTED,
                 "%s: with several batches per problem, rows_per_batch must be a multiple of 128",
                 name);
+    d.nq = (const bf16*)q.norm_q;
+    d.nk = (const bf16*)q.norm_k;
+    d.rope_row0 = q.rope_row0;
+    DLT_REQUIRE(!qk || (q.rope_row0 >= 0 && ((uintptr_t)q.norm_q & 7) == 0 &&
+                        ((uintptr_t)q.norm_k & 7) == 0),
+                DIFFLET_EINVAL, "%s: q/k norm weights must be 8-byte aligned, rope_row0 >= 0",
+                name);
     d.tiles_m = (int)((q.m + BM - 1) / BM);
     d.tile_start = (int)tiles;
     tiles += (int64_t)d.tiles_m * args.tiles_n;
@@ -729,20 +839,58 @@ static int gemm_launch(const char* name, int nproblems, const difflet_gemm_probl
   args.total_tiles = (int)tiles;
   DLT_REQUIRE(workspace_bytes >= 0 && (workspace == nullptr || ((uintptr_t)workspace & 255) == 0),
               DIFFLET_EINVAL, "%s: workspace must be 256-byte aligned", name);
+  if (qk) {
+    const bool q_on = qk->q_col >= 0, k_on = qk->k_col >= 0;
+    DLT_REQUIRE(epilogue != DIFFLET_EPI_GATE_RESIDUAL, DIFFLET_EUNSUPPORTED,
+                "%s: the q/k norm epilogue combines with EPI_NONE or EPI_GELU only", name);
+    DLT_REQUIRE(qk->cols > 0 && qk->cols % 256 == 0 && (q_on || k_on) &&
+                    (!q_on || (qk->q_col % 256 == 0 && qk->q_col + qk->cols <= n)) &&
+                    (!k_on || (qk->k_col % 256 == 0 && qk->k_col + qk->cols <= n)) &&
+                    (!q_on || !k_on || qk->q_col + qk->cols <= qk->k_col ||
+                     qk->k_col + qk->cols <= qk->q_col),
+                DIFFLET_EINVAL,
+                "%s: q/k columns must be disjoint ranges of n starting and ending at multiples "
+                "of 256", name);
+    DLT_REQUIRE(epilogue != DIFFLET_EPI_GELU ||
+                    ((!q_on || qk->q_col + qk->cols <= act_col_start) &&
+                     (!k_on || qk->k_col + qk->cols <= act_col_start)),
+                DIFFLET_EINVAL, "%s: q/k columns must lie below act_col_start", name);
+    DLT_REQUIRE(qk->cos && qk->sin && ((uintptr_t)qk->cos & 15) == 0 &&
+                    ((uintptr_t)qk->sin & 15) == 0 && (qk->law == 0 || qk->law == 1),
+                DIFFLET_EINVAL, "%s: RoPE tables (16-byte aligned) and law 0 or 1 required",
+                name);
+    args.qk_cols = (int)qk->cols;
+    args.q_col = q_on ? (int)qk->q_col : -(1 << 30);
+    args.k_col = k_on ? (int)qk->k_col : -(1 << 30);
+    args.rope_law = qk->law;
+    args.qk_eps = qk->eps;
+    args.rope_cos = qk->cos;
+    args.rope_sin = qk->sin;
+  }
   args.sk = sk_plan((int)tiles, (int)(k / KT), E == Elem::MX ? 8 : 1,
                     workspace ? device_cus() : 0, workspace ? workspace_bytes : 0);
   args.ws = (uint8_t*)workspace;
   constexpr int NT = ElemTraits<E>::WN;
   dim3 grid((unsigned)(args.sk.dp + args.sk.groups)), block(128 * NT);
-  switch (epilogue) {
-    case DIFFLET_EPI_NONE:
-      hipLaunchKernelGGL((gemm_kernel<E, DIFFLET_EPI_NONE, NT>), grid, block, 0, stream, args);
+  switch (epilogue * 2 + (qk ? 1 : 0)) {
+    case 2 * DIFFLET_EPI_NONE:
+      hipLaunchKernelGGL((gemm_kernel<E, DIFFLET_EPI_NONE, NT, false>), grid, block, 0, stream,
+                         args);
       break;
-    case DIFFLET_EPI_GELU:
-      hipLaunchKernelGGL((gemm_kernel<E, DIFFLET_EPI_GELU, NT>), grid, block, 0, stream, args);
+    case 2 * DIFFLET_EPI_NONE + 1:
+      hipLaunchKernelGGL((gemm_kernel<E, DIFFLET_EPI_NONE, NT, true>), grid, block, 0, stream,
+                         args);
+      break;
+    case 2 * DIFFLET_EPI_GELU:
+      hipLaunchKernelGGL((gemm_kernel<E, DIFFLET_EPI_GELU, NT, false>), grid, block, 0, stream,
+                         args);
+      break;
+    case 2 * DIFFLET_EPI_GELU + 1:
+      hipLaunchKernelGGL((gemm_kernel<E, DIFFLET_EPI_GELU, NT, true>), grid, block, 0, stream,
+                         args);
       break;
     default:
-      hipLaunchKernelGGL((gemm_kernel<E, DIFFLET_EPI_GATE_RESIDUAL, NT>), grid, block, 0,
+      hipLaunchKernelGGL((gemm_kernel<E, DIFFLET_EPI_GATE_RESIDUAL, NT, false>), grid, block, 0,
                          stream, args);
       break;
   }
@@ -761,25 +909,30 @@ extern "C" int64_t difflet_rocm_gemm_workspace_bytes(void) {
 extern "C" int difflet_rocm_gemm_bf16(int nproblems, const difflet_gemm_problem* problems,
                                       int64_t n, int64_t k, int epilogue,
                                       int64_t act_col_start, void* workspace,
-                                      int64_t workspace_bytes, difflet_stream_t stream) {
+                                      int64_t workspace_bytes, const difflet_gemm_qk* qk,
+                                      difflet_stream_t stream) {
   return gemm_launch<Elem::BF16>("gemm_bf16", nproblems, problems, n, k, epilogue,
-                                 act_col_start, workspace, workspace_bytes, (hipStream_t)stream);
+                                 act_col_start, workspace, workspace_bytes, qk,
+                                 (hipStream_t)stream);
 }
 
 extern "C" int difflet_rocm_gemm_fp8_rowwise(int nproblems, const difflet_gemm_problem* problems,
                                              int64_t n, int64_t k, int epilogue,
                                              int64_t act_col_start, void* workspace,
-                                             int64_t workspace_bytes, difflet_stream_t stream) {
+                                             int64_t workspace_bytes, const difflet_gemm_qk* qk,
+                                      difflet_stream_t stream) {
   return gemm_launch<Elem::FP8>("gemm_fp8_rowwise", nproblems, problems, n, k, epilogue,
-                                act_col_start, workspace, workspace_bytes, (hipStream_t)stream);
+                                act_col_start, workspace, workspace_bytes, qk,
+                                 (hipStream_t)stream);
 }
 
 extern "C" int difflet_rocm_gemm_mxfp8(int nproblems, const difflet_gemm_problem* problems,
                                        int64_t n, int64_t k, int epilogue, int64_t act_col_start,
                                        void* workspace, int64_t workspace_bytes,
-                                       difflet_stream_t stream) {
+                                       const difflet_gemm_qk* qk, difflet_stream_t stream) {
   return gemm_launch<Elem::MX>("gemm_mxfp8", nproblems, problems, n, k, epilogue,
-                               act_col_start, workspace, workspace_bytes, (hipStream_t)stream);
+                               act_col_start, workspace, workspace_bytes, qk,
+                                 (hipStream_t)stream);
 }
 
 // Host walk of the split schedule the kernels follow (same functions): every (tile, K stage)

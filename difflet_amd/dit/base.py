@@ -84,12 +84,6 @@ class JointDiT:
         q, sc = lin_img.prep(a)
         return (q[:st], sc[:st]), (q[st:], sc[st:])
 
-    def _qk(self, buf, rows: slice, q_off: int, k_off: int, wq, wk, cos, sin):
-        c = self.cfg
-        kernels.qk_norm_rope(buf[rows], heads=c.heads, head_dim=c.head_dim, q_off=q_off,
-                             k_off=k_off, wq=wq, wk=wk, eps=EPS, cos=cos[rows], sin=sin[rows],
-                             law=0)
-
     def _attn(self, buf, q_off: int, k_off: int, v_off: int):
         """Joint attention over all rows of `buf` [S, ld]; output written over q."""
         c = self.cfg
@@ -100,10 +94,16 @@ class JointDiT:
         with self._timed("attn"):
             kernels.attention(q, k, v, scale=1.0 / math.sqrt(c.head_dim), out=q)
 
-    def _gemm(self, name: str, problems, kind: str, epilogue: int = 0, act_col_start: int = 0):
+    def _gemm(self, name: str, problems, kind: str, epilogue: int = 0, act_col_start: int = 0,
+              qk=None):
         """One grouped GEMM launch (activation quantization already done by problem())."""
         with self._timed(name):
-            run(problems, kind, epilogue, act_col_start)
+            run(problems, kind, epilogue, act_col_start, qk)
+
+    def _qk_epilogue(self, q_col, k_col, cos, sin):
+        """The fused q/k RMSNorm + RoPE of an attention projection (law 0, per head)."""
+        c = self.cfg
+        return kernels.QkNormRope(q_col, k_col, c.heads * c.head_dim, cos, sin, law=0, eps=EPS)
 
     def joint_block(self, blk, bufs, st: int, img_mods, txt_mods, cos, sin, tag: str):
         """One joint block over h (text rows [0, st), image rows [st, S)). blk holds the device
@@ -119,13 +119,13 @@ class JointDiT:
         # launch differ only in their modulation vectors or norm weights
         fq = blk.qkv_img.kind == "fp8"
         pt, pi = self._ln_joint(bufs, st, c_sc, c_sh, x_sc, x_sh, fq)
-        self._gemm(f"gemm.{tag}.qkv", [blk.qkv_txt.problem(n[T], qkv[T], prepared=pt),
-                                       blk.qkv_img.problem(n[I], qkv[I], prepared=pi)],
-                   blk.qkv_img.kind)
-        c = self.cfg
-        kernels.qk_norm_rope(qkv, heads=c.heads, head_dim=c.head_dim, q_off=0, k_off=d,
-                             wq=blk.naq, wk=blk.nak, eps=EPS, cos=cos, sin=sin, law=0, split=st,
-                             wq2=blk.nq, wk2=blk.nk)
+        # q/k RMSNorm (text rows with the added-stream weights) and RoPE in the GEMM epilogue
+        self._gemm(f"gemm.{tag}.qkv",
+                   [blk.qkv_txt.problem(n[T], qkv[T], prepared=pt, norm_q=blk.naq,
+                                        norm_k=blk.nak, rope_row0=0),
+                    blk.qkv_img.problem(n[I], qkv[I], prepared=pi, norm_q=blk.nq,
+                                        norm_k=blk.nk, rope_row0=st)],
+                   blk.qkv_img.kind, qk=self._qk_epilogue(0, d, cos, sin))
         self._attn(qkv, 0, d, 2 * d)
         o = qkv[:, :d]
         pt, pi = self._prep_joint(blk.out_txt, blk.out_img, o, st)

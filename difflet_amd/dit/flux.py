@@ -165,9 +165,10 @@ class FluxDiT(JointDiT):
         h, n, big = bufs["h"], bufs["n"], bufs["big"]
         sh, sc, g = self._mods(mod, self.mod_off[("s", i)], 3)
         p = self._ln(bufs, slice(0, h.shape[0]), sc, sh)
-        self._gemm("gemm.single.w1", [blk.w1.problem(n, big, prepared=p)], self.kind,
-                   _lib.EPI_GELU, 3 * d)
-        self._qk(big, slice(0, h.shape[0]), 2 * d, 0, blk.nq, blk.nk, cos, sin)
+        # [k | v | q | mlp]: GELU on the MLP columns, q/k RMSNorm + RoPE in the same epilogue
+        self._gemm("gemm.single.w1",
+                   [blk.w1.problem(n, big, prepared=p, norm_q=blk.nq, norm_k=blk.nk)],
+                   self.kind, _lib.EPI_GELU, 3 * d, qk=self._qk_epilogue(2 * d, 0, cos, sin))
         self._attn(big, 2 * d, 0, d)
         self._gemm("gemm.single.w2", [blk.w2.problem(big[:, 2 * d:], h, gate=g, residual=h)],
                    self.kind, _lib.EPI_GATE_RESIDUAL)

@@ -44,9 +44,10 @@ class DeviceLinear:
         return kernels.quantize_mxfp8(a, swizzled=True)
 
     def problem(self, a: torch.Tensor, c: torch.Tensor, *, gate=None, residual=None,
-                prepared=None) -> Problem:
+                prepared=None, norm_q=None, norm_k=None, rope_row0: int = 0) -> Problem:
         aq, asc = prepared if prepared is not None else self.prep(a)
-        return Problem(aq, self.w, c, self.bias, gate, residual, asc, self.ws)
+        return Problem(aq, self.w, c, self.bias, gate, residual, asc, self.ws,
+                       norm_q=norm_q, norm_k=norm_k, rope_row0=rope_row0)
 
     def __call__(self, a: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         c = out if out is not None else torch.empty((a.shape[0], self.n), dtype=torch.bfloat16,
@@ -61,5 +62,6 @@ class DeviceLinear:
         return b
 
 
-def run(problems, kind: str, epilogue: int = 0, act_col_start: int = 0) -> None:
-    kernels.gemm_grouped(problems, kind=kind, epilogue=epilogue, act_col_start=act_col_start)
+def run(problems, kind: str, epilogue: int = 0, act_col_start: int = 0, qk=None) -> None:
+    kernels.gemm_grouped(problems, kind=kind, epilogue=epilogue, act_col_start=act_col_start,
+                         qk=qk)

@@ -156,14 +156,30 @@ class Problem:
     """One problem of a grouped GEMM: C = epilogue(A W^T + bias)."""
 
     __slots__ = ("a", "w", "c", "bias", "gate", "residual", "a_scale", "w_scale",
-                 "rows_per_batch")
+                 "rows_per_batch", "norm_q", "norm_k", "rope_row0")
 
     def __init__(self, a, w, c, bias=None, gate=None, residual=None, a_scale=None,
-                 w_scale=None, rows_per_batch=None):
+                 w_scale=None, rows_per_batch=None, norm_q=None, norm_k=None, rope_row0=0):
         self.a, self.w, self.c = a, w, c
         self.bias, self.gate, self.residual = bias, gate, residual
         self.a_scale, self.w_scale = a_scale, w_scale
         self.rows_per_batch = rows_per_batch
+        # fused q/k norm (gemm_grouped(..., qk=QkNormRope)): this problem's [128] bf16 RMSNorm
+        # weights and the RoPE table row of its row 0
+        self.norm_q, self.norm_k, self.rope_row0 = norm_q, norm_k, rope_row0
+
+
+class QkNormRope:
+    """Fused q/k RMSNorm + RoPE epilogue of a GEMM whose output holds 128-column q and k heads
+    in columns [q_col, q_col + cols) and [k_col, k_col + cols) (multiples of 256; None skips
+    one): the GEMM followed by qk_norm_rope(do_norm=True), up to fp32 summation order. cos / sin
+    are fp32 [rows, 128] tables indexed by each problem's rope_row0 + row."""
+
+    __slots__ = ("q_col", "k_col", "cols", "cos", "sin", "law", "eps")
+
+    def __init__(self, q_col, k_col, cols, cos, sin, *, law=0, eps=1e-6):
+        self.q_col, self.k_col, self.cols = q_col, k_col, cols
+        self.cos, self.sin, self.law, self.eps = cos, sin, law, eps
 
 
 _GEMM_FN = {"bf16": "difflet_rocm_gemm_bf16", "fp8": "difflet_rocm_gemm_fp8_rowwise",
@@ -202,7 +218,8 @@ def gemm_workspace(dev: torch.device) -> torch.Tensor:
 
 def gemm_grouped(problems: Sequence[Problem], *, kind: str = "bf16",
                  epilogue: int = _lib.EPI_NONE, act_col_start: int = 0,
-                 workspace: torch.Tensor | None | str = None) -> None:
+                 workspace: torch.Tensor | None | str = None,
+                 qk: QkNormRope | None = None) -> None:
     """Runs up to 4 GEMMs sharing N, K and the epilogue in one launch (writes each p.c).
     workspace: None (every tile whole on one workgroup, the default), "shared" (the device's,
     see gemm_workspace) or a zero-filled uint8 tensor of difflet_rocm_gemm_workspace_bytes()
@@ -241,15 +258,31 @@ def gemm_grouped(problems: Sequence[Problem], *, kind: str = "bf16",
         q.w_scale = p.w_scale.data_ptr() if p.w_scale is not None else None
         q.m = p.a.shape[0]
         q.rows_per_batch = p.rows_per_batch or p.a.shape[0]
+        if qk is not None:
+            for t in (p.norm_q, p.norm_k):
+                if t is not None and (t.dtype != torch.bfloat16 or t.numel() != 128):
+                    raise ValueError("q/k norm weights are [128] bf16")
+            q.norm_q = p.norm_q.data_ptr() if p.norm_q is not None else None
+            q.norm_k = p.norm_k.data_ptr() if p.norm_k is not None else None
+            q.rope_row0 = int(p.rope_row0)
     if isinstance(workspace, str):
         if workspace != "shared":
             raise ValueError(f"workspace must be 'shared', a tensor or None, got {workspace!r}")
         workspace = gemm_workspace(dev)
     ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
                                                            workspace.numel())
+    qk_arg = None
+    if qk is not None:
+        for t in (qk.cos, qk.sin):
+            if t.dtype != torch.float32 or t.dim() != 2 or t.shape[1] != 128 or not t.is_contiguous():
+                raise ValueError("RoPE tables are contiguous fp32 [rows, 128]")
+        qk_arg = ctypes.byref(_lib.GemmQk(-1 if qk.q_col is None else qk.q_col,
+                                          -1 if qk.k_col is None else qk.k_col, qk.cols,
+                                          qk.cos.data_ptr(), qk.sin.data_ptr(), int(qk.law),
+                                          float(qk.eps)))
     fn = getattr(lib(), _GEMM_FN[kind])
     check(fn(len(problems), arr, n, k, int(epilogue), int(act_col_start), ws_ptr, ws_bytes,
-             _stream(dev)), f"gemm_{kind}")
+             qk_arg, _stream(dev)), f"gemm_{kind}")
 
 
 def linear(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, *,

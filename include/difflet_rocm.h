@@ -113,7 +113,28 @@ typedef struct difflet_gemm_problem {
   const void* w_scale;  /* fp8 GEMMs: per-column (per-row of W) scales */
   int64_t m;
   int64_t rows_per_batch; /* rows of A per batch element, for gate indexing (>= m for one) */
+  const void* norm_q;   /* fused q/k norm (difflet_gemm_qk): [128] bf16 RMSNorm weights of q */
+  const void* norm_k;   /*   and of k for this problem's rows (NULL: weight 1) */
+  int64_t rope_row0;    /*   RoPE table row of this problem's row 0 */
 } difflet_gemm_problem;
+
+/* Optional fused q/k RMSNorm + RoPE epilogue (EPI_NONE or EPI_GELU), for attention
+ * projections whose output holds q and k heads of 128 columns: in columns [q_col, q_col + cols)
+ * and [k_col, k_col + cols) each head's 128 values of a row are rounded to bf16 (the plain
+ * GEMM's output), scaled by rsqrt(mean of squares + eps) and the problem's norm weights, rotated
+ * by the fp32 tables cos / sin [rows, 128] at row rope_row0 + m (law 0: interleaved pairs with
+ * per-element angles, 1: the reference's stride-2 form) and stored as bf16: the result of the
+ * GEMM followed by difflet_rocm_qk_norm_rope (do_norm 1), up to fp32 summation order. q_col,
+ * k_col and cols are multiples of 256 (q_col or k_col -1 skips that part); with EPI_GELU the
+ * columns lie below act_col_start. Replaces the pair linear + norm_q/norm_k + apply_rotary_emb
+ * of the reference's attention processors (difflet/models/flux/modeling_flux.py:616-949). */
+typedef struct difflet_gemm_qk {
+  int64_t q_col, k_col, cols;
+  const float* cos;
+  const float* sin;
+  int law;
+  float eps;
+} difflet_gemm_qk;
 
 /* Workspace of the GEMMs below (all three take the same one). With a workspace, a launch whose
  * output tiles would leave the last wave of workgroups less than 92 % full cuts part of its tiles
@@ -132,7 +153,8 @@ int64_t difflet_rocm_gemm_workspace_bytes(void);
 /* bf16 x bf16 -> fp32 accumulate -> bf16. k % 64 == 0. */
 int difflet_rocm_gemm_bf16(int nproblems, const difflet_gemm_problem* problems, int64_t n,
                            int64_t k, int epilogue, int64_t act_col_start, void* workspace,
-                           int64_t workspace_bytes, difflet_stream_t stream);
+                           int64_t workspace_bytes, const difflet_gemm_qk* qk,
+                           difflet_stream_t stream);
 
 /* fp8 e4m3 x e4m3 with per-row scales: acc * a_scale[m] * w_scale[n] (both fp32), then the
  * epilogue. a_scale / w_scale come from difflet_rocm_quantize_fp8_rowwise. k % 128 == 0.
@@ -141,7 +163,7 @@ int difflet_rocm_gemm_bf16(int nproblems, const difflet_gemm_problem* problems, 
 int difflet_rocm_gemm_fp8_rowwise(int nproblems, const difflet_gemm_problem* problems,
                                   int64_t n, int64_t k, int epilogue, int64_t act_col_start,
                                   void* workspace, int64_t workspace_bytes,
-                                  difflet_stream_t stream);
+                                  const difflet_gemm_qk* qk, difflet_stream_t stream);
 
 /* MXFP8: e4m3 codes in swizzled K order with one E8M0 scale (uint8) per 32 values along K,
  * a_scale [m, k/32] and w_scale [n, k/32] (row strides k/32). Replaces the nkilib
@@ -150,7 +172,8 @@ int difflet_rocm_gemm_fp8_rowwise(int nproblems, const difflet_gemm_problem* pro
  * k % 128 == 0. */
 int difflet_rocm_gemm_mxfp8(int nproblems, const difflet_gemm_problem* problems, int64_t n,
                             int64_t k, int epilogue, int64_t act_col_start, void* workspace,
-                            int64_t workspace_bytes, difflet_stream_t stream);
+                            int64_t workspace_bytes, const difflet_gemm_qk* qk,
+                            difflet_stream_t stream);
 
 /* Host-side check of the split schedule the GEMMs use for `tiles` output tiles of `k_stages`
  * K stages, cut in units of `gran` stages (1; 8 for MXFP8), on `cus` compute units with

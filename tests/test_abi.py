@@ -30,7 +30,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     lib = _lib.load()
     for name in declared_symbols():
         assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
-    assert lib.difflet_rocm_abi_version() == 3
+    assert lib.difflet_rocm_abi_version() == 4
     assert b"gfx950" in lib.difflet_rocm_version()
 
 
@@ -39,7 +39,7 @@ def test_error_paths_report_without_a_gpu():
     from difflet_amd import _lib
 
     lib = _lib.load()
-    st = lib.difflet_rocm_gemm_bf16(0, None, 64, 64, 0, 0, None, 0, None)
+    st = lib.difflet_rocm_gemm_bf16(0, None, 64, 64, 0, 0, None, 0, None, None)
     assert st == _lib.EINVAL
     assert b"nproblems" in lib.difflet_rocm_last_error()
     st = lib.difflet_rocm_attention(None, None, None, None, _lib.BF16, 1, 1, 1, 1, 128, None,

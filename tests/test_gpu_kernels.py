@@ -73,6 +73,95 @@ def test_gemm_epilogues_gelu_and_gate_residual(gpu):
     assert rel_l2(r, ref2) < 4e-3
 
 
+def _gemm_operands(kind, a, w, gpu):
+    if kind == "bf16":
+        return a.to(gpu), w.to(gpu), None, None
+    if kind == "fp8":
+        aq, sa = kernels.quantize_fp8_rowwise(a.to(gpu))
+        wq, sw = kernels.quantize_fp8_rowwise(w.to(gpu))
+        return aq, wq, sa, sw
+    aq, sa = kernels.quantize_mxfp8(a.to(gpu), swizzled=True)
+    wq, sw = kernels.quantize_mxfp8(w.to(gpu), swizzled=True)
+    return aq, wq, sa, sw
+
+
+def _rope_tables(g, rows):
+    ang = torch.rand(rows, 64, generator=g) * 6.0
+    cos = ang.cos().repeat_interleave(2, dim=1).contiguous()
+    sin = ang.sin().repeat_interleave(2, dim=1).contiguous()
+    sin[:, 0::2] *= 0.9  # distinct angles for the two elements of a pair (law 1 reads both)
+    return cos, sin
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp8", "mx"])
+@pytest.mark.parametrize("law", [0, 1])
+def test_gemm_fused_qk_norm_rope_equals_gemm_then_qk_norm_rope(gpu, kind, law):
+    """Joint-block layout: text and image problems (ragged rows) write [q | k | v] of 4 heads;
+    each problem has its own q/k norm weights and RoPE row offset. The fused epilogue equals
+    the plain GEMM followed by qk_norm_rope within fp32 summation order."""
+    print(f"fused qk gemm {kind} law={law}", flush=True)
+    g = torch.Generator().manual_seed(40 + law)
+    heads, d, k = 4, 512, 256
+    mt, mi = 96, 300
+    ws = [rnd(g, 3 * d, k, std=0.05) for _ in range(2)]
+    bs = [rnd(g, 3 * d, std=0.1) for _ in range(2)]
+    nw = [(1 + 0.3 * rnd(g, 128)).to(torch.bfloat16) for _ in range(4)]  # naq, nak, nq, nk
+    a = rnd(g, mt + mi, k)
+    cos, sin = (t.to(gpu) for t in _rope_tables(g, mt + mi))
+    out = {}
+    for fused in (True, False):
+        buf = torch.full((mt + mi, 3 * d), float("nan"), dtype=torch.bfloat16, device=gpu)
+        probs = []
+        for p, rows in enumerate((slice(0, mt), slice(mt, mt + mi))):
+            aq, wq, sa, sw = _gemm_operands(kind, a[rows], ws[p], gpu)
+            probs.append(kernels.Problem(aq, wq, buf[rows], bs[p].to(gpu), a_scale=sa, w_scale=sw,
+                                         norm_q=nw[2 * p].to(gpu), norm_k=nw[2 * p + 1].to(gpu),
+                                         rope_row0=rows.start))
+        qk = kernels.QkNormRope(0, d, d, cos, sin, law=law, eps=1e-6) if fused else None
+        kernels.gemm_grouped(probs, kind=kind, qk=qk)
+        if not fused:
+            kernels.qk_norm_rope(buf, heads=heads, head_dim=128, q_off=0, k_off=d,
+                                 wq=nw[0].to(gpu), wk=nw[1].to(gpu), eps=1e-6, cos=cos, sin=sin,
+                                 law=law, split=mt, wq2=nw[2].to(gpu), wk2=nw[3].to(gpu))
+        out[fused] = buf
+    torch.cuda.synchronize()
+    f, u = out[True], out[False]
+    assert not torch.isnan(f).any()
+    assert torch.equal(f[:, 2 * d:], u[:, 2 * d:])  # v untouched by the norm
+    assert rel_l2(f, u) < 1e-3
+    assert (f == u).float().mean().item() > 0.97  # most values bit-identical
+
+
+def test_gemm_fused_qk_norm_rope_single_block_layout_and_errors(gpu):
+    """[k | v | q | mlp] with GELU from the MLP columns: the norm on k and q, GELU on the MLP
+    part, v plain; bad column ranges are refused before any launch."""
+    g = torch.Generator().manual_seed(44)
+    d, k, m = 256, 256, 333
+    n = 3 * d + 4 * d
+    a, w, b = rnd(g, m, k), rnd(g, n, k, std=0.05), rnd(g, n, std=0.1)
+    nq, nk = (1 + 0.3 * rnd(g, 128)).to(torch.bfloat16), (1 + 0.3 * rnd(g, 128)).to(torch.bfloat16)
+    cos, sin = (t.to(gpu) for t in _rope_tables(g, m))
+    f = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+    kernels.gemm_grouped([kernels.Problem(a.to(gpu), w.to(gpu), f, b.to(gpu), norm_q=nq.to(gpu),
+                                          norm_k=nk.to(gpu))],
+                         epilogue=_lib.EPI_GELU, act_col_start=3 * d,
+                         qk=kernels.QkNormRope(2 * d, 0, d, cos, sin))
+    u = kernels.linear(a.to(gpu), w.to(gpu), b.to(gpu), epilogue=_lib.EPI_GELU,
+                       act_col_start=3 * d)
+    kernels.qk_norm_rope(u, heads=2, head_dim=128, q_off=2 * d, k_off=0, wq=nq.to(gpu),
+                         wk=nk.to(gpu), eps=1e-6, cos=cos, sin=sin, law=0)
+    torch.cuda.synchronize()
+    assert torch.equal(f[:, d:2 * d], u[:, d:2 * d]) and torch.equal(f[:, 3 * d:], u[:, 3 * d:])
+    assert rel_l2(f, u) < 1e-3
+    p = [kernels.Problem(a.to(gpu), w.to(gpu), f, b.to(gpu))]
+    for bad, epi in ((kernels.QkNormRope(128, None, d, cos, sin), 0),      # not a multiple of 256
+                     (kernels.QkNormRope(0, 256, 512, cos, sin), 0),        # overlapping ranges
+                     (kernels.QkNormRope(2 * d, 0, d, cos, sin), _lib.EPI_GELU),  # GELU overlap
+                     (kernels.QkNormRope(0, None, d, cos, sin), _lib.EPI_GATE_RESIDUAL)):
+        with pytest.raises((ValueError, NotImplementedError)):
+            kernels.gemm_grouped(p, epilogue=epi, act_col_start=d, qk=bad)
+
+
 def test_gemm_grouped_problems_share_n_k(gpu):
     g = torch.Generator().manual_seed(3)
     n, k = 384, 192
