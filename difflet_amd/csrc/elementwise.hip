@@ -109,8 +109,14 @@ template <> struct Raw8<float> {
 // chunk j of a lane is elements (lane + 64 j) * 8 .. + 8 of the row.
 template <typename TX, typename TM, int NV, bool FULL>
 struct LnRow {
+  // 16-bit modulation vectors are held like the row; fp32 ones (8 registers per chunk each)
+  // are read where they are used, from L1 / L2 (every row of a batch shares them)
+  static constexpr bool HOLD = sizeof(TM) == 2;
   Raw8<TX> x[NV];
-  Raw8<TM> m[NV], a[NV];
+  Raw8<TM> m[HOLD ? NV : 1], a[HOLD ? NV : 1];
+  const TM* mp;
+  const TM* ap;
+  int lane_, dim_;
   float mean, rstd, madd;
 
   // Every load of the row and of both modulation vectors is issued before the first use, from
@@ -126,11 +132,17 @@ struct LnRow {
       const int c = (lane + 64 * j) * 8;
       x[j] = Raw8<TX>::load(xr + (FULL || c < dim ? c : 0));
     }
+    mp = mb;
+    ap = ab;
+    lane_ = lane;
+    dim_ = dim;
+    if constexpr (HOLD) {
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const int c = (lane + 64 * j) * 8;
-      m[j] = mb ? Raw8<TM>::load(mb + (FULL || c < dim ? c : 0)) : Raw8<TM>::zero();
-      a[j] = ab ? Raw8<TM>::load(ab + (FULL || c < dim ? c : 0)) : Raw8<TM>::zero();
+      for (int j = 0; j < NV; ++j) {
+        const int c = (lane + 64 * j) * 8;
+        m[j] = mb ? Raw8<TM>::load(mb + (FULL || c < dim ? c : 0)) : Raw8<TM>::zero();
+        a[j] = ab ? Raw8<TM>::load(ab + (FULL || c < dim ? c : 0)) : Raw8<TM>::zero();
+      }
     }
     madd = (one_plus || !mb) ? 1.0f : 0.0f;
     float s = 0.f;
@@ -164,8 +176,14 @@ struct LnRow {
   __device__ __forceinline__ void out(int j, float (&o)[8]) const {
     float v[8], m8[8], a8[8];
     x[j].cvt(v);
-    m[j].cvt(m8);
-    a[j].cvt(a8);
+    if constexpr (HOLD) {
+      m[j].cvt(m8);
+      a[j].cvt(a8);
+    } else {  // (chunks past dim re-read chunk 0; their outputs are not stored)
+      const int c0 = (lane_ + 64 * j) * 8, c = FULL || c0 < dim_ ? c0 : 0;
+      (mp ? Raw8<TM>::load(mp + c) : Raw8<TM>::zero()).cvt(m8);
+      (ap ? Raw8<TM>::load(ap + c) : Raw8<TM>::zero()).cvt(a8);
+    }
     const float nm = -mean * rstd;
 #pragma unroll
     for (int i = 0; i < 8; ++i)
