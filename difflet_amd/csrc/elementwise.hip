@@ -333,6 +333,68 @@ __device__ __forceinline__ void rope8(float* v, const float* cs, const float* sn
   }
 }
 
+// ------------------------------------------------------------------ q/k RMSNorm across heads
+// do_norm 2 with head_dim 128 and rows of NV * 512 values (Wan: 40 heads = 5120): one wavefront
+// per row holds q and k as loaded (every load issued before the first use), one reduction
+// each, then scales each 8-value chunk by rsqrt(mean + eps) and the norm weights, rotates it
+// and stores it in place. (Chunk c of a lane: values (lane + 64 c) * 8 .. + 8.)
+template <typename T, typename TW, int NV>
+__global__ __launch_bounds__(256) void qk_rms_rows_kernel(
+    T* __restrict__ buf, int64_t ld, int64_t rows, int64_t q_off, int64_t k_off,
+    const TW* __restrict__ wq, const TW* __restrict__ wk, int64_t split,
+    const TW* __restrict__ wq2, const TW* __restrict__ wk2, float eps,
+    const float* __restrict__ cosb, const float* __restrict__ sinb, int64_t rope_rows,
+    int law) {
+  constexpr int HD = 128;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const bool has[2] = {q_off >= 0, k_off >= 0};
+  T* const base[2] = {buf + row * ld + (has[0] ? q_off : 0), buf + row * ld + (has[1] ? k_off : 0)};
+  Raw8<T> x[2][NV];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int j = 0; j < NV; ++j) x[t][j] = Raw8<T>::load(base[t] + (lane + 64 * j) * 8);
+  float ss[2] = {0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      float v[8];
+      x[t][j].cvt(v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss[t] += v[i] * v[i];
+    }
+  ss[0] = wave_sum(ss[0]);
+  ss[1] = wave_sum(ss[1]);
+  const bool second = split > 0 && row >= split;  // rows past split: the second weights
+  const float* cr = cosb ? cosb + (row % rope_rows) * HD : nullptr;
+  const float* sr = sinb ? sinb + (row % rope_rows) * HD : nullptr;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    if (!has[t]) continue;
+    const float r = 1.0f / __builtin_sqrtf(ss[t] / (float)(NV * 512) + eps);
+    const TW* w = t == 0 ? (second ? wq2 : wq) : (second ? wk2 : wk);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = (lane + 64 * j) * 8;
+      float v[8], w8[8];
+      x[t][j].cvt(v);
+      if (w) {
+        Raw8<TW>::load(w + c).cvt(w8);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w8[i] = 1.f;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = v[i] * r * w8[i];
+      if (cr) rope8(v, cr + (c % HD), sr + (c % HD), law);
+      V8<T>::store(base[t] + c, v);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ q/k RMSNorm + RoPE
 // One wavefront per row; LPH = lanes per head (head_dim / 8); a wave covers 64 / LPH heads
 // per step. do_norm 1: per-head RMS, reduced over the LPH lanes of one head with xor shuffles,
@@ -795,6 +857,21 @@ static int launch_qk(void* buf, int64_t ld, int64_t rows, int64_t heads, int64_t
                      float eps, const float* c, const float* sn, int64_t rope_rows, int law,
                      hipStream_t s) {
   dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+#define DLT_QKR(NV)                                                                          \
+  hipLaunchKernelGGL((qk_rms_rows_kernel<T, TW, NV>), grid, block, 0, s, (T*)buf, ld, rows,   \
+                     q_off, k_off, (const TW*)wq, (const TW*)wk, split, (const TW*)wq2,       \
+                     (const TW*)wk2, eps, c, sn, rope_rows, law)
+  if (do_norm == 2 && hd == 128) {  // across heads: whole rows in registers when they fit
+    switch (heads * 128) {
+      case 2048: DLT_QKR(4); return dlt_check_launch("qk_norm_rope");
+      case 3072: DLT_QKR(6); return dlt_check_launch("qk_norm_rope");
+      case 4096: DLT_QKR(8); return dlt_check_launch("qk_norm_rope");
+      case 5120: DLT_QKR(10); return dlt_check_launch("qk_norm_rope");
+      case 6144: DLT_QKR(12); return dlt_check_launch("qk_norm_rope");
+      default: break;
+    }
+  }
+#undef DLT_QKR
 #define DLT_QK(LPH)                                                                        \
   if (do_norm != 2) {                                                                      \
     const int64_t tasks = rows * 2 * ((heads + 64 / (LPH) - 1) / (64 / (LPH)));            \

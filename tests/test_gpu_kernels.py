@@ -491,6 +491,39 @@ def test_qk_norm_rope_in_place(gpu):
     assert torch.equal(gb[:, 2 * d:].cpu(), buf[:, 2 * d:])
 
 
+@pytest.mark.parametrize("h,wdt,law", [(40, torch.float32, 1), (40, torch.bfloat16, 0),
+                                       (16, torch.float32, 1), (5, torch.float32, 1)])
+def test_qk_norm_across_heads_in_place(gpu, h, wdt, law):
+    """do_norm 2 (Wan): one RMS over all heads of q (and of k) with [heads * 128] weights, then
+    RoPE per head; 16 / 40 heads hold whole rows in registers, 5 heads take the general kernel.
+    A q-only call leaves k untouched."""
+    print(f"qk across heads h={h} {wdt} law={law}", flush=True)
+    g = torch.Generator().manual_seed(h + law)
+    s, d = 300, h * 128
+    buf = rnd(g, s, 3 * d)
+    wq = (1 + 0.1 * torch.randn(d, generator=g)).to(wdt)
+    wk = (1 + 0.1 * torch.randn(d, generator=g)).to(wdt)
+    ang = torch.rand(s, 64, generator=g) * 6.0
+    cos = ang.cos().repeat_interleave(2, dim=1).contiguous()
+    sin = ang.sin().repeat_interleave(2, dim=1).contiguous()
+    rot = ops.apply_rotary_emb_fp32 if law == 0 else ops.apply_rotary_emb
+    def ref_of(off, w):
+        x = ops.rms_norm_fp32(buf[:, off:off + d].float(), w.float(), 1e-6).reshape(s, h, 128)
+        return rot(x, cos[:, None], sin[:, None]).reshape(s, d)
+    gb = buf.to(gpu)
+    kernels.qk_norm_rope(gb, heads=h, head_dim=128, q_off=0, k_off=d, wq=wq.to(gpu),
+                         wk=wk.to(gpu), eps=1e-6, cos=cos.to(gpu), sin=sin.to(gpu), law=law,
+                         do_norm=2)
+    assert rel_l2(gb[:, :d], ref_of(0, wq)) < 4e-3
+    assert rel_l2(gb[:, d:2 * d], ref_of(d, wk)) < 4e-3
+    assert torch.equal(gb[:, 2 * d:].cpu(), buf[:, 2 * d:])
+    gq = buf.to(gpu)
+    kernels.qk_norm_rope(gq, heads=h, head_dim=128, q_off=0, k_off=-1, wq=wq.to(gpu), wk=None,
+                         eps=1e-6, cos=cos.to(gpu), sin=sin.to(gpu), law=law, do_norm=2)
+    assert rel_l2(gq[:, :d], ref_of(0, wq)) < 4e-3
+    assert torch.equal(gq[:, d:].cpu(), buf[:, d:])
+
+
 def test_split_launches_equal_one_launch_per_segment(gpu):
     """Joint-block launches over text + image rows (split): the LayerNorm modulations (bf16
     and fused e4m3) and the q/k norm + rope equal one launch per segment, bit for bit. The
