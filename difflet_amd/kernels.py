@@ -84,9 +84,9 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float
               workspace: torch.Tensor | None | str = "shared") -> torch.Tensor:
     """softmax(q k^T scale [+ mask]) v on [B, H, S, D] (or [B*H, S, D]) tensors.
 
-    workspace: "shared" (the device's attention workspace, for work issued in order on one
-    stream), a zero-filled uint8 tensor of attention_workspace_bytes(), or None (every query
-    tile runs whole on one workgroup)."""
+    workspace: "shared" (the workspace of the current stream, see attention_workspace), a
+    zero-filled uint8 tensor of attention_workspace_bytes(), or None (every query tile runs
+    whole on one workgroup)."""
     dev = _on_gpu(q, k, v)
     folded = q.dim() == 3
     scores_shape = tuple(q.shape[:-1]) + (k.shape[-2],)
@@ -187,19 +187,21 @@ _GEMM_FN = {"bf16": "difflet_rocm_gemm_bf16", "fp8": "difflet_rocm_gemm_fp8_roww
 
 
 _WORKSPACE: dict[int, torch.Tensor] = {}
-_ATT_WORKSPACE: dict[int, torch.Tensor] = {}
+_ATT_WORKSPACE: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def attention_workspace(dev: torch.device) -> torch.Tensor:
-    """The device's shared attention workspace (split schedule), zero-filled once on first use.
-    It serves attention launches issued in order on one stream at a time."""
+    """The attention workspace (split schedule) of the device's current stream, zero-filled
+    once on first use. Launches on one stream run in order, so they can share it; each stream
+    gets its own, since launches on different streams may overlap."""
     i = dev.index if dev.index is not None else torch.cuda.current_device()
-    ws = _ATT_WORKSPACE.get(i)
+    key = (i, torch.cuda.current_stream(torch.device("cuda", i)).cuda_stream)
+    ws = _ATT_WORKSPACE.get(key)
     if ws is None:
         with torch.cuda.device(i):
             nbytes = int(lib().difflet_rocm_attention_workspace_bytes())
         ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=torch.device("cuda", i))
-        _ATT_WORKSPACE[i] = ws
+        _ATT_WORKSPACE[key] = ws
     return ws
 
 

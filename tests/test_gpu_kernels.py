@@ -377,6 +377,30 @@ def test_attention_split_schedule_equals_whole_tiles(gpu, b, h, sq, sk):
     assert rel_l2(split1[:1, :2], ref) < 1e-2
 
 
+def test_attention_split_schedule_on_two_streams(gpu):
+    """The shared split-schedule workspace is per stream: attention launched on two streams at
+    once uses two workspaces, and both results equal the unsplit ones."""
+    g = torch.Generator().manual_seed(77)
+    dev = torch.device(gpu)
+    cases = [tuple(t.to(gpu) for t in _attn_case(g, 1, 24, 4600, 1100)) for _ in range(2)]
+    scale = 1 / math.sqrt(128)
+    wholes = [kernels.attention(*c, scale=scale, workspace=None) for c in cases]
+    streams = [torch.cuda.Stream(device=dev) for _ in range(2)]
+    torch.cuda.synchronize()
+    outs = []
+    for c, st in zip(cases, streams):
+        with torch.cuda.stream(st):
+            outs.append(kernels.attention(*c, scale=scale))
+    torch.cuda.synchronize()
+    wss = []
+    for st in streams:
+        with torch.cuda.stream(st):
+            wss.append(kernels.attention_workspace(dev))
+    assert wss[0].data_ptr() != wss[1].data_ptr()
+    for o, w in zip(outs, wholes):
+        assert rel_l2(o, w) < 2e-3
+
+
 def test_attention_folded_heads_and_scale_one(gpu):
     g = torch.Generator().manual_seed(5)
     q, k, v = (rnd(g, 6, 96, 128, std=0.2) for _ in range(3))
