@@ -46,50 +46,88 @@ class FluxConfig:
             raise ValueError("heads * head_dim must equal hidden")
 
 
+def _group(get: Callable[[str], torch.Tensor], q, prefixes: list[str], kind: str, *,
+           along_k: bool = False, bias_prefix: str | None = None) -> DeviceLinear:
+    """One device linear over the linears at ``prefixes``, their weights concatenated along N
+    (rows) or, ``along_k``, along K (the single block's proj_out halves, bias ``bias_prefix``).
+
+    Without a quantized checkpoint ``q`` the dense weights are quantized here by ``kind``. With
+    one, the group's stored fp8 codes and scales are loaded as they are (every member of a group
+    stored quantized, or none: then the dense weights run in bf16)."""
+    cat_dim = 1 if along_k else 0
+    bias_names = [bias_prefix] if along_k else prefixes
+    bias = torch.cat([get(f"{p}.bias") for p in bias_names], dim=0)
+    if q is not None:
+        parts = [q.fp8(p) for p in prefixes]
+        stored = [p is not None for p in parts]
+        if all(stored):
+            lk = "fp8" if q.format == "fp8_rowwise" else "mx"
+            if along_k and (lk == "fp8" or parts[0][0].shape[1] % 512):
+                raise ValueError(f"{prefixes}: stored halves fuse along K only as MXFP8 with the "
+                                 "first half's K a multiple of 512 (the swizzle tile)")
+            dev = bias.device
+            codes = torch.cat([c.to(dev) for c, _ in parts], dim=cat_dim)
+            scales = torch.cat([sc.to(dev) for _, sc in parts], dim=cat_dim)
+            return DeviceLinear.from_fp8(codes, scales, bias, lk)
+        if any(stored):
+            raise ValueError(f"{prefixes}: one GEMM runs these linears, so they are stored "
+                             "quantized all together or not at all")
+        kind = "bf16"
+    w = torch.cat([get(f"{p}.weight") for p in prefixes], dim=cat_dim)
+    return DeviceLinear(w, bias, kind)
+
+
 class _Double:
-    def __init__(self, get: Callable[[str], torch.Tensor], pre: str, cfg: FluxConfig, kind: str):
+    def __init__(self, get: Callable[[str], torch.Tensor], pre: str, cfg: FluxConfig, kind: str,
+                 q=None):
         W = lambda n: get(f"{pre}.{n}")  # noqa: E731
-        cat = lambda *ns: torch.cat([W(n) for n in ns], dim=0)  # noqa: E731
+        L = lambda *ns: _group(get, q, [f"{pre}.{n}" for n in ns], kind)  # noqa: E731
         a = "attn."
-        self.qkv_img = DeviceLinear(cat(a + "to_q.weight", a + "to_k.weight", a + "to_v.weight"),
-                                    cat(a + "to_q.bias", a + "to_k.bias", a + "to_v.bias"), kind)
-        self.qkv_txt = DeviceLinear(
-            cat(a + "add_q_proj.weight", a + "add_k_proj.weight", a + "add_v_proj.weight"),
-            cat(a + "add_q_proj.bias", a + "add_k_proj.bias", a + "add_v_proj.bias"), kind)
-        self.out_img = DeviceLinear(W(a + "to_out.0.weight"), W(a + "to_out.0.bias"), kind)
-        self.out_txt = DeviceLinear(W(a + "to_add_out.weight"), W(a + "to_add_out.bias"), kind)
-        self.ff1_img = DeviceLinear(W("ff.net.0.proj.weight"), W("ff.net.0.proj.bias"), kind)
-        self.ff2_img = DeviceLinear(W("ff.net.2.weight"), W("ff.net.2.bias"), kind)
-        self.ff1_txt = DeviceLinear(W("ff_context.net.0.proj.weight"),
-                                    W("ff_context.net.0.proj.bias"), kind)
-        self.ff2_txt = DeviceLinear(W("ff_context.net.2.weight"), W("ff_context.net.2.bias"),
-                                    kind)
+        self.qkv_img = L(a + "to_q", a + "to_k", a + "to_v")
+        self.qkv_txt = L(a + "add_q_proj", a + "add_k_proj", a + "add_v_proj")
+        self.out_img = L(a + "to_out.0")
+        self.out_txt = L(a + "to_add_out")
+        self.ff1_img = L("ff.net.0.proj")
+        self.ff2_img = L("ff.net.2")
+        self.ff1_txt = L("ff_context.net.0.proj")
+        self.ff2_txt = L("ff_context.net.2")
         bf = lambda n: W(n).to(torch.bfloat16).contiguous()  # noqa: E731
         self.nq, self.nk = bf(a + "norm_q.weight"), bf(a + "norm_k.weight")
         self.naq, self.nak = bf(a + "norm_added_q.weight"), bf(a + "norm_added_k.weight")
 
 
 class _Single:
-    def __init__(self, get: Callable[[str], torch.Tensor], pre: str, cfg: FluxConfig, kind: str):
+    def __init__(self, get: Callable[[str], torch.Tensor], pre: str, cfg: FluxConfig, kind: str,
+                 q=None):
         W = lambda n: get(f"{pre}.{n}")  # noqa: E731
         a = "attn."
         # column order [k | v | q | mlp]: attention writes over q, leaving [attn | mlp] adjacent
-        self.w1 = DeviceLinear(
-            torch.cat([W(a + "to_k.weight"), W(a + "to_v.weight"), W(a + "to_q.weight"),
-                       W("proj_mlp.weight")], dim=0),
-            torch.cat([W(a + "to_k.bias"), W(a + "to_v.bias"), W(a + "to_q.bias"),
-                       W("proj_mlp.bias")], dim=0), kind)
-        self.w2 = DeviceLinear(W("proj_out.weight"), W("proj_out.bias"), kind)
+        self.w1 = _group(get, q, [f"{pre}.{a}to_k", f"{pre}.{a}to_v", f"{pre}.{a}to_q",
+                                  f"{pre}.proj_mlp"], kind)
+        if q is not None and f"{pre}.proj_out.weight" not in q:
+            # a checkpoint that splits proj_out stores proj_out_attn [D, D] and proj_out_mlp
+            # [D, 4D]; the step runs them as the one K = 5D GEMM over [attn | mlp]
+            self.w2 = _group(get, q, [f"{pre}.proj_out_attn", f"{pre}.proj_out_mlp"], kind,
+                             along_k=True, bias_prefix=f"{pre}.proj_out")
+        else:
+            self.w2 = _group(get, q, [f"{pre}.proj_out"], kind)
         bf = lambda n: W(n).to(torch.bfloat16).contiguous()  # noqa: E731
         self.nq, self.nk = bf(a + "norm_q.weight"), bf(a + "norm_k.weight")
 
 
 class FluxDiT(JointDiT):
     """The FLUX transformer on the HIP kernels. `get(name)` returns a parameter by its diffusers
-    name (any dtype, on the target device); `kind` picks the block linears' format."""
+    name (any dtype, on the target device); `kind` picks the block linears' format.
+
+    `quantized` (a difflet_amd.quant.checkpoint.QuantizedCheckpoint) loads the block linears
+    that a quantized checkpoint stores as fp8 from their codes and scales, with no quantization
+    at load; `kind` then follows the checkpoint's format and the linears it keeps dense run in
+    bf16. FluxDiT.from_quantized_dir builds the model from such a directory alone."""
 
     def __init__(self, cfg: FluxConfig, get: Callable[[str], torch.Tensor], kind: str = "bf16",
-                 device: str | torch.device = "cuda"):
+                 device: str | torch.device = "cuda", quantized=None):
+        if quantized is not None:
+            kind = "fp8" if quantized.format == "fp8_rowwise" else "mx"
         self.cfg, self.kind = cfg, kind
         self.device = torch.device(device)
         d = cfg.hidden
@@ -128,8 +166,9 @@ class FluxDiT(JointDiT):
         self.mod_w = torch.cat(mod_w, dim=0)
         self.mod_b = torch.cat(mod_b, dim=0)
         del mod_w, mod_b
-        self.double = [_Double(G, f"transformer_blocks.{i}", cfg, kind) for i in range(cfg.n_double)]
-        self.single = [_Single(G, f"single_transformer_blocks.{i}", cfg, kind)
+        self.double = [_Double(G, f"transformer_blocks.{i}", cfg, kind, quantized)
+                       for i in range(cfg.n_double)]
+        self.single = [_Single(G, f"single_transformer_blocks.{i}", cfg, kind, quantized)
                        for i in range(cfg.n_single)]
         self._bufs: dict = {}
         self._rope: dict = {}
@@ -164,14 +203,14 @@ class FluxDiT(JointDiT):
         d = self.cfg.hidden
         h, n, big = bufs["h"], bufs["n"], bufs["big"]
         sh, sc, g = self._mods(mod, self.mod_off[("s", i)], 3)
-        p = self._ln(bufs, slice(0, h.shape[0]), sc, sh)
+        p = self._ln(bufs, slice(0, h.shape[0]), sc, sh, blk.w1.kind == "fp8")
         # [k | v | q | mlp]: GELU on the MLP columns, q/k RMSNorm + RoPE in the same epilogue
         self._gemm("gemm.single.w1",
                    [blk.w1.problem(n, big, prepared=p, norm_q=blk.nq, norm_k=blk.nk)],
-                   self.kind, _lib.EPI_GELU, 3 * d, qk=self._qk_epilogue(2 * d, 0, cos, sin))
+                   blk.w1.kind, _lib.EPI_GELU, 3 * d, qk=self._qk_epilogue(2 * d, 0, cos, sin))
         self._attn(big, 2 * d, 0, d)
         self._gemm("gemm.single.w2", [blk.w2.problem(big[:, 2 * d:], h, gate=g, residual=h)],
-                   self.kind, _lib.EPI_GATE_RESIDUAL)
+                   blk.w2.kind, _lib.EPI_GATE_RESIDUAL)
 
     # -------------------------------------------------------------------------- step
     def embed(self, timestep, guidance, pooled):
@@ -217,6 +256,16 @@ class FluxDiT(JointDiT):
         return self.proj_out(n[st:]).unsqueeze(0)
 
     __call__ = forward
+
+    @classmethod
+    def from_quantized_dir(cls, cfg: FluxConfig, path, device: str | torch.device = "cuda"
+                           ) -> "FluxDiT":
+        """The model from a quantized directory alone (difflet_amd.quant.checkpoint): fp8 block
+        linears from their stored codes, every other tensor as stored."""
+        from difflet_amd.quant.checkpoint import QuantizedCheckpoint
+
+        ckpt = QuantizedCheckpoint(path)
+        return cls(cfg, ckpt.get, device=device, quantized=ckpt)
 
 
 def random_param_source(cfg: FluxConfig, seed: int, device, std: float = 0.02):

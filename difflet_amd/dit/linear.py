@@ -35,6 +35,33 @@ class DeviceLinear:
         else:
             self.w, self.ws = kernels.quantize_mxfp8(w, swizzled=True)
 
+    @classmethod
+    def from_fp8(cls, codes: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None,
+                 kind: str) -> "DeviceLinear":
+        """A linear from stored codes and scales (a quantized checkpoint), with no quantization:
+        kind "fp8": codes [N, K] + fp32 scales [N]; kind "mx": codes [N, K] in logical K order +
+        uint8 E8M0 scales [N, K/32], the codes gathered into the swizzle order the GEMM reads
+        (a permutation of bytes within each row)."""
+        from difflet_amd.quant.linear import _swizzle_index
+
+        if kind not in ("fp8", "mx"):
+            raise ValueError(f"stored codes are kind 'fp8' or 'mx', got {kind!r}")
+        if codes.dtype != torch.float8_e4m3fn or codes.dim() != 2:
+            raise ValueError(f"codes must be float8_e4m3fn [N, K], got {codes.dtype} {list(codes.shape)}")
+        n, k = codes.shape
+        want = ((n,), torch.float32) if kind == "fp8" else ((n, k // 32), torch.uint8)
+        if tuple(scale.shape) != want[0] or scale.dtype != want[1]:
+            raise ValueError(f"kind {kind!r} scales are {want[1]} {list(want[0])}, got "
+                             f"{scale.dtype} {list(scale.shape)}")
+        self = cls.__new__(cls)
+        self.kind, self.n, self.k = kind, n, k
+        if kind == "mx":
+            idx = _swizzle_index(k, codes.device)
+            codes = codes.view(torch.uint8)[:, idx].view(torch.float8_e4m3fn)
+        self.w, self.ws = codes.contiguous(), scale.contiguous()
+        self.bias = None if bias is None else bias.to(device=codes.device, dtype=torch.bfloat16).contiguous()
+        return self
+
     def prep(self, a: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor | None]:
         """The GEMM's A operand for activations a [M, K] (quantized for the fp8 kinds)."""
         if self.kind == "bf16":

@@ -10,8 +10,9 @@ serialisation and cache-key rules, plus
   one fp32 scale per output channel, activations quantized per token at run time;
   include/difflet_rocm.h difflet_rocm_quantize_fp8_rowwise states the law).
 
-For ``mxfp8`` the cache and weight identities are the reference's dicts unchanged (the format
-is not added), so keys of existing specs stay byte-identical; ``fp8_rowwise`` adds its format.
+The cache and weight identities are the reference's dicts, whose ``quant`` field names the
+format: ``"mxfp8"`` as the reference writes it, so keys and directory digests of existing specs
+stay byte-identical, and ``"fp8_rowwise"`` for the new format, so its artifacts never collide.
 """
 
 from __future__ import annotations
@@ -81,6 +82,11 @@ class RocmQuantSpec:
         bare = strip_prefix(name)
         return any(re.fullmatch(p, bare) for p in self.split_linears)
 
+    def unmatched_splits(self, names: Iterable[str]) -> list[str]:
+        """The split patterns that match none of ``names`` (difflet/quant/spec.py:113-119)."""
+        bare = [strip_prefix(n) for n in names]
+        return [p for p in self.split_linears if not any(re.fullmatch(p, n) for n in bare)]
+
     # ------------------------------------------------------------- serialisation
     def to_dict(self) -> dict[str, Any]:
         body = dataclasses.asdict(self)
@@ -105,7 +111,7 @@ class RocmQuantSpec:
         return hashlib.sha256(json.dumps(list(self.targets)).encode()).hexdigest()[:16]
 
     def cache_fields(self) -> dict[str, Any]:
-        """difflet/quant/spec.py:147-157, with the format named only when it is not mxfp8."""
+        """difflet/quant/spec.py:147-157; ``quant`` is the format name."""
         fields = {
             "quant": self.format,
             "quant_schema": self.schema,
@@ -138,6 +144,30 @@ FLUX_ALL_BLOCK_LINEARS: tuple[str, ...] = (
     rf"{_BLOCK}\.(ff|ff_context)\.net\.(0\.proj|2)",
     rf"{_SINGLE}\.attn\.(to_q|to_k|to_v)",
     rf"{_SINGLE}\.(proj_mlp|proj_out)",
+)
+
+#: difflet/quant/targets.py:158 (SINGLE_BLOCK_SPLIT_LINEARS): the single blocks' proj_out, stored
+#: by an mxfp8 checkpoint as proj_out_attn [D, D] and proj_out_mlp [D, 4D].
+SINGLE_BLOCK_SPLIT_LINEARS: tuple[str, ...] = (rf"{_SINGLE}\.proj_out",)
+
+#: difflet/quant/targets.py:162-169 (FLUX_TARGETS), the reference's default FLUX MXFP8 set: both
+#: streams' q/k/v and MLPs, the single blocks' q/k/v, proj_mlp and both proj_out halves; the
+#: double blocks' output projections stay bf16.
+FLUX_MX_TARGETS: tuple[str, ...] = (
+    rf"{_BLOCK}\.attn\.(to_q|to_k|to_v|add_q_proj|add_k_proj|add_v_proj)",
+    rf"{_BLOCK}\.(ff|ff_context)\.net\.0\.proj",
+    rf"{_BLOCK}\.(ff|ff_context)\.net\.2",
+    rf"{_SINGLE}\.attn\.(to_q|to_k|to_v)",
+    rf"{_SINGLE}\.proj_mlp",
+    rf"{_SINGLE}\.proj_out_(attn|mlp)",
+)
+
+#: difflet/quant/targets.py:189-193 (FLUX_ROW_PARALLEL). It changes no byte at tp = 1 but is part
+#: of the spec's weights identity, so a spec that names it keeps the reference's digest.
+FLUX_ROW_PARALLEL: tuple[str, ...] = (
+    rf"{_BLOCK}\.attn\.(to_out\.0|to_add_out)",
+    rf"{_BLOCK}\.(ff|ff_context)\.net\.2",
+    rf"{_SINGLE}\.proj_out_(attn|mlp)",
 )
 
 #: difflet/quant/targets.py:117-121 (QWEN_IMAGE_TARGETS): q/k/v, the added q/k/v and both MLPs;
