@@ -1,6 +1,6 @@
 """Benchmark: one DiT denoise step on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload flux|qwen|wan]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload flux|qwen|wan|weights]
                     [--kinds bf16,fp8] [--no-cpu] [--calibrate-copy]
 
 flux (default): the full FLUX.1-dev-shaped transformer forward of one denoise step, batch 1,
@@ -13,6 +13,9 @@ text tokens (3584-wide encoder states), hidden 3072, 24 x 128 heads, MLP 12288; 
 wan: the Wan-2.2-14B-shaped text-to-video step, 40 blocks, latent 21 x 60 x 104 with patch
 (1, 2, 2) = 32760 video tokens + 512 text tokens (4096-wide), hidden 5120, 40 x 128 heads, FFN
 13824, bf16.
+weights: the quantized-checkpoint writer's device work, every FLUX block linear (19 double x
+12 + 38 single x 5 = 418 weights, 8.61 G values) quantized from bf16 to e4m3 codes and scales,
+per-channel fp8 and MXFP8; `value` is the summed quantizer time in ms, K timed calls per shape.
 Weights are random N(0, 0.02) drawn on the device (norm weights ones); inputs N(0, 1).
 
 Each step starts with its inputs resident in HBM. W untimed warmup steps, then K steps
@@ -64,7 +67,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="flux", choices=("flux", "qwen", "wan"))
+    ap.add_argument("--workload", default="flux", choices=("flux", "qwen", "wan", "weights"))
     ap.add_argument("--kinds", default=None,
                     help="comma list (flux: bf16,fp8 by default; qwen: mx,bf16)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -377,6 +380,89 @@ def cpu_baseline(wl, log):
                        f"{st}+{si} tokens, extrapolated x{shape.n_double} + x{shape.n_single}")}
 
 
+# FLUX block linears by shape [N, K] -> count over 19 double + 38 single blocks
+FLUX_BLOCK_LINEARS = {(3072, 3072): 19 * 8 + 38 * 3, (12288, 3072): 19 * 2 + 38,
+                      (3072, 12288): 19 * 2, (3072, 15360): 38}
+
+
+def weights_bytes(fmt, n, k):
+    """Algorithmic HBM bytes of one quantizer call: bf16 read, e4m3 codes and scales written."""
+    return n * k * 3 + (n * 4 if fmt == "fp8_rowwise" else n * k // 32)
+
+
+def run_weights(args, torch, log):
+    """Times the quantized-checkpoint writer's kernels over FLUX's block linears."""
+    from difflet_amd import kernels
+
+    fmts = {"fp8_rowwise": kernels.quantize_fp8_rowwise,
+            "mxfp8": lambda w: kernels.quantize_mxfp8(w, swizzled=False)}
+    res = {}
+    for fmt, fn in fmts.items():
+        total_ms, total_bytes, shapes = 0.0, 0, {}
+        for (n, k), count in FLUX_BLOCK_LINEARS.items():
+            g = torch.Generator(device="cuda").manual_seed(SEED + n + k)
+            w = (torch.randn((n, k), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+            for _ in range(max(args.warmup, 1)):
+                fn(w)
+            torch.cuda.synchronize()
+            stream = torch.cuda.current_stream()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(args.steps):
+                fn(w)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / args.steps
+            b = weights_bytes(fmt, n, k)
+            shapes[f"{n}x{k}"] = {"count": count, "us": round(ms * 1e3, 2),
+                                  "GB_per_s": round(b / (ms * 1e-3) / 1e9, 1)}
+            total_ms += count * ms
+            total_bytes += count * b
+            log(f"[weights] {fmt} {n}x{k}: {ms * 1e3:.1f} us, {b / (ms * 1e-3) / 1e9:.0f} GB/s")
+            del w
+        res[fmt] = {"ms": round(total_ms, 3), "bytes": total_bytes,
+                    "GB_per_s": round(total_bytes / (total_ms * 1e-3) / 1e9, 1), "shapes": shapes}
+    head = res["fp8_rowwise"]
+    big = head["shapes"]["3072x15360"]
+    line = {
+        "metric": "FLUX block linears quantized to fp8 (checkpoint writer device time, ms)",
+        "value": head["ms"], "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": head["ms"], "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16->e4m3", "data": "synthetic",
+        "config": {"workload": "FLUX.1 block linears, 418 weights, 8.61 G values",
+                   "formats": list(res)},
+        "roofline": {"bound": "hbm", "achieved": big["GB_per_s"], "peak": 8000.0,
+                     "unit": "GB/s", "frac": round(big["GB_per_s"] / 8000.0, 3),
+                     "traffic": None,
+                     "kernel": "quantize_fp8_rowwise on 3072 x 15360 (proj_out)"},
+        "by_format": res,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = weights_cpu_baseline(log)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def weights_cpu_baseline(log):
+    """The oracle's per-channel quantizer (numpy, one thread) on one 3072 x 3072 weight,
+    extrapolated to the 8.61 G values of FLUX's block linears."""
+    import numpy as np
+
+    from oracle import fp8 as ofp8
+
+    w = (np.random.default_rng(SEED).standard_normal((3072, 3072), dtype=np.float32) * 0.02)
+    ofp8.quantize_rowwise(w[:64])
+    t0 = time.perf_counter()
+    ofp8.quantize_rowwise(w)
+    dt = time.perf_counter() - t0
+    values = sum(n * k * c for (n, k), c in FLUX_BLOCK_LINEARS.items())
+    log(f"[cpu] quantize_rowwise 3072x3072: {dt:.2f} s")
+    return {"value": round(dt * values / w.size * 1e3, 1), "unit": "ms (extrapolated)",
+            "cores": 1, "kind": "port",
+            "sample": f"numpy oracle quantize_rowwise on one 3072 x 3072 weight ({dt:.2f} s), "
+                      f"x {values / w.size:.0f}"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -393,6 +479,8 @@ def main():
     from difflet_amd import _lib
 
     _lib.load()
+    if args.workload == "weights":
+        return run_weights(args, torch, log)
     wl = WORKLOADS[args.workload]()
     kinds = [k for k in (args.kinds or ",".join(wl.kinds)).split(",") if k]
     if args.calibrate_copy:
