@@ -23,7 +23,7 @@ from __future__ import annotations
 
 import torch
 
-from difflet_amd import kernels
+from difflet_amd.backends.rocm.ops_impl import library
 
 _SUPPORTED = (torch.bfloat16, torch.float16)
 
@@ -51,8 +51,7 @@ def attention(q, k, v, *, scale: float | None = None, causal: bool = False,
     scale = 1.0 if scale is None else float(scale)
     if attention_mask is not None and attention_mask.dtype not in (torch.bool,) + _SUPPORTED + (torch.float32,):
         attention_mask = attention_mask.to(q.dtype)
-    return kernels.attention(q, k, v, scale=scale, causal=causal, attention_mask=attention_mask,
-                             bound_min=bound_min, bound_max=bound_max)
+    return library.attention(q, k, v, scale, bool(causal), attention_mask, bound_min, bound_max)
 
 
 def cross_attention(q, k, v, *, scale: float | None = None, attention_mask=None, **kwargs):

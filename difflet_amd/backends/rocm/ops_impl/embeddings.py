@@ -16,7 +16,7 @@ from __future__ import annotations
 
 import torch
 
-from difflet_amd import kernels
+from difflet_amd.backends.rocm.ops_impl import library
 
 
 def _table(t, x, pos):
@@ -44,7 +44,7 @@ def _rope(x, cos, sin, law: int):
     if c.shape[0] != x.shape[pos]:
         raise ValueError(f"rotary table length {c.shape[0]} does not match the input's "
                          f"{x.shape[pos]} positions")
-    y = kernels.rope(x.movedim(pos, -2).contiguous(), c, sn, law=law)
+    y = library.rope(x.movedim(pos, -2).contiguous(), c, sn, law)
     return y.movedim(-2, pos).contiguous() if pos != nd - 2 else y
 
 

@@ -19,7 +19,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from difflet_amd import kernels
+from difflet_amd.backends.rocm.ops_impl import library
 
 
 class _RocmLinearBase(nn.Module):
@@ -71,17 +71,10 @@ class _RocmLinearBase(nn.Module):
         m = x2.shape[0]
         if m == 0:
             return x.new_empty(*shape[:-1], self.out_features)
-        if m <= 8 and self.in_features % 8 == 0 and {1: 1, 2: 2}.get(m, 4 if m <= 4 else 8) * self.in_features <= 16384:
-            y = kernels.gemv(x2, w.detach(), b)
-        else:
-            wg, kp, np_ = self._weight_for_gemm()
-            if kp != self.in_features:
-                x2 = F.pad(x2, (0, kp - self.in_features))
-            if np_ != self.out_features and b is not None:
-                b = F.pad(b, (0, np_ - self.out_features))
-            y = kernels.linear(x2.contiguous() if x2.stride(-1) != 1 else x2, wg, b)
-            if np_ != self.out_features:
-                y = y[:, :self.out_features]
+        # a few rows run on the GEMV kernel with the weight as is; the GEMM reads the weight
+        # zero-padded to its tile multiples (built once, only for odd shapes)
+        wg = w.detach() if library._gemv_fits(m, self.in_features) else self._weight_for_gemm()[0]
+        y = library.linear(x2, wg, b, self.out_features)
         return y.reshape(*shape[:-1], self.out_features).to(x.dtype)
 
 

@@ -17,13 +17,13 @@ import numbers
 import torch
 import torch.nn as nn
 
-from difflet_amd import kernels
+from difflet_amd.backends.rocm.ops_impl import library
 
 
 def rms_norm_fp32(x: torch.Tensor, weight: torch.Tensor | None, eps: float) -> torch.Tensor:
     if x.shape[-1] % 8:
         raise NotImplementedError(f"rocm rms_norm needs the last dim a multiple of 8, got {x.shape[-1]}")
-    return kernels.rms_norm(x, weight, float(eps))
+    return library.rms_norm(x, weight, float(eps))
 
 
 class RMSNorm(nn.Module):
@@ -64,7 +64,7 @@ class LayerNorm(nn.Module):
             raise ValueError(f"LayerNorm over {self.normalized_shape}, got input {tuple(x.shape)}")
         if x.shape[-1] % 8:
             raise NotImplementedError("rocm LayerNorm needs the last dim a multiple of 8")
-        return kernels.layernorm_modulate(x, self.weight, self.bias, eps=self.eps, one_plus=False)
+        return library.layer_norm(x, self.weight, self.bias, float(self.eps))
 
     def extra_repr(self) -> str:
         return f"{self.normalized_shape}, eps={self.eps}, elementwise_affine={self.elementwise_affine}"

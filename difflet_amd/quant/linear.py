@@ -24,6 +24,7 @@ import torch
 import torch.nn as nn
 
 from difflet_amd import kernels
+from difflet_amd.backends.rocm.ops_impl import library
 from difflet_amd.quant.spec import BLOCK, LAYOUT_K, RocmQuantSpec
 
 FP8_DTYPE = torch.float8_e4m3fn
@@ -126,20 +127,13 @@ class _FP8LinearBase(nn.Module):
         if self.compute == "dequant":
             if self.weight_bf16 is None:
                 raise RuntimeError("call prepare_fp8_kernels_(module) after the load")
-            y = kernels.linear(x2, self.weight_bf16, b)
+            y = library.linear(x2, self.weight_bf16, b, self.out_features)
         else:
             if self.weight_kernel is None:
                 raise RuntimeError("the fp8 kernel path needs the prepared weight: call "
                                    "prepare_fp8_kernels_(module) after the load")
-            y = torch.empty(x2.shape[0], self.out_features, dtype=torch.bfloat16, device=x.device)
-            if self.format == "mxfp8":
-                aq, asc = kernels.quantize_mxfp8(x2, swizzled=True)
-                kind = "mx"
-            else:
-                aq, asc = kernels.quantize_fp8_rowwise(x2)
-                kind = "fp8"
-            kernels.gemm_grouped([kernels.Problem(aq, self.weight_kernel, y, b, a_scale=asc,
-                                                  w_scale=self.weight_scale)], kind=kind)
+            y = library.fp8_linear(x2, self.weight_kernel, self.weight_scale, b,
+                                   self.format == "mxfp8")
         return y.reshape(*shape[:-1], self.out_features).to(x.dtype)
 
     def _repr_tail(self) -> str:
