@@ -1,6 +1,7 @@
 """Benchmark: one DiT denoise step on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload flux|qwen|wan|weights]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--workload flux|qwen|wan|weights|compile]
                     [--kinds bf16,fp8] [--no-cpu] [--calibrate-copy]
 
 flux (default): the full FLUX.1-dev-shaped transformer forward of one denoise step, batch 1,
@@ -16,6 +17,9 @@ wan: the Wan-2.2-14B-shaped text-to-video step, 40 blocks, latent 21 x 60 x 104 
 weights: the quantized-checkpoint writer's device work, every FLUX block linear (19 double x
 12 + 38 single x 5 = 418 weights, 8.61 G values) quantized from bf16 to e4m3 codes and scales,
 per-channel fp8 and MXFP8; `value` is the summed quantizer time in ms, K timed calls per shape.
+compile: one FLUX single block (4608 tokens, hidden 3072, 24 x 128 heads, MLP 12288) written
+with the op modules, one HIP kernel per op, run eagerly and under torch.compile(fullgraph=True);
+`value` is the compiled block's ms.
 Weights are random N(0, 0.02) drawn on the device (norm weights ones); inputs N(0, 1).
 
 Each step starts with its inputs resident in HBM. W untimed warmup steps, then K steps
@@ -67,7 +71,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="flux", choices=("flux", "qwen", "wan", "weights"))
+    ap.add_argument("--workload", default="flux",
+                    choices=("flux", "qwen", "wan", "weights", "compile"))
     ap.add_argument("--kinds", default=None,
                     help="comma list (flux: bf16,fp8 by default; qwen: mx,bf16)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -463,6 +468,95 @@ def weights_cpu_baseline(log):
                       f"x {values / w.size:.0f}"}
 
 
+def run_compile(args, torch, log):
+    """A FLUX single block on the op modules, eager against torch.compile(fullgraph=True)."""
+    import math
+
+    import torch.nn as nn
+    import torch.nn.functional as F
+
+    from difflet_amd.backends.rocm.ops_impl.attention import attention
+    from difflet_amd.backends.rocm.ops_impl.embeddings import apply_rotary_emb
+    from difflet_amd.backends.rocm.ops_impl.linear import ColumnParallelLinear, RowParallelLinear
+    from difflet_amd.backends.rocm.ops_impl.norm import LayerNorm, RMSNorm
+
+    d, heads, s, dev = 3072, 24, 4608, torch.device("cuda")
+
+    class Single(nn.Module):
+        """difflet/models/flux/modeling_flux.py single block: adaLN, [q|k|v] and MLP-up from one
+        normed input, q/k RMSNorm + RoPE, attention, proj_out over [attn | gelu(mlp)], gated
+        residual."""
+
+        def __init__(self):
+            super().__init__()
+            bf = dict(dtype=torch.bfloat16, device=dev)
+            self.norm = LayerNorm(d, eps=1e-6, elementwise_affine=False)
+            self.qkv = ColumnParallelLinear(d, 3 * d, **bf)
+            self.mlp = ColumnParallelLinear(d, 4 * d, **bf)
+            self.out = RowParallelLinear(5 * d, d, **bf)
+            self.norm_q, self.norm_k = RMSNorm(128).to(dev), RMSNorm(128).to(dev)
+            for m in (self.qkv, self.mlp, self.out):
+                nn.init.normal_(m.weight, std=0.02)
+                nn.init.zeros_(m.bias)
+
+        def forward(self, x, shift, scale, gate, cos, sin):
+            h = self.norm(x) * (1 + scale) + shift
+            q, k, v = self.qkv(h).view(1, s, 3, heads, 128).permute(2, 0, 3, 1, 4).unbind(0)
+            q = apply_rotary_emb(self.norm_q(q), cos, sin)
+            k = apply_rotary_emb(self.norm_k(k), cos, sin)
+            o = attention(q, k, v, scale=1.0 / math.sqrt(128)).transpose(1, 2).reshape(1, s, d)
+            m = F.gelu(self.mlp(h), approximate="tanh")
+            return x + gate * self.out(torch.cat([o, m], dim=-1))
+
+    torch.manual_seed(SEED)
+    blk = Single().eval()
+    x = torch.randn(1, s, d, device=dev).to(torch.bfloat16)
+    shift, scale, gate = (0.1 * torch.randn(1, 1, d, device=dev).to(torch.bfloat16) for _ in range(3))
+    ang = torch.arange(s, device=dev)[:, None] * torch.exp(-torch.arange(64, device=dev) / 8.0)
+    cos = torch.cos(ang).repeat_interleave(2, -1)
+    sin = torch.sin(ang).repeat_interleave(2, -1)
+    inputs = (x, shift, scale, gate, cos, sin)
+
+    def timed(fn):
+        with torch.no_grad():
+            for _ in range(max(args.warmup, 1)):
+                fn(*inputs)
+            torch.cuda.synchronize()
+            stream = torch.cuda.current_stream()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(args.steps):
+                y = fn(*inputs)
+            e1.record(stream)
+            torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps, y
+
+    eager_ms, y0 = timed(blk)
+    t0 = time.perf_counter()
+    compiled = torch.compile(blk, fullgraph=True, mode="default")
+    with torch.no_grad():
+        compiled(*inputs)
+    compile_s = time.perf_counter() - t0
+    comp_ms, y1 = timed(compiled)
+    rel = ((y1.float() - y0.float()).norm() / y0.float().norm()).item()
+    flops = 2 * s * d * (3 * d + 4 * d + 5 * d) + 4 * heads * s * s * 128
+    log(f"[compile] eager {eager_ms:.3f} ms, compiled {comp_ms:.3f} ms, first call "
+        f"{compile_s:.1f} s, rel L2 {rel:.2e}")
+    line = {
+        "metric": "FLUX single block on the op modules, torch.compile(fullgraph=True) ms",
+        "value": round(comp_ms, 3), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(comp_ms, 3), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "FLUX.1 single block, 4608 tokens, hidden 3072, 24 x 128 heads",
+                   "compile_mode": "default"},
+        "eager_ms": round(eager_ms, 3), "compiled_vs_eager_rel_l2": rel,
+        "first_call_s": round(compile_s, 1),
+        "block_tflops": round(flops / (comp_ms * 1e-3) / 1e12, 1),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -481,6 +575,8 @@ def main():
     _lib.load()
     if args.workload == "weights":
         return run_weights(args, torch, log)
+    if args.workload == "compile":
+        return run_compile(args, torch, log)
     wl = WORKLOADS[args.workload]()
     kinds = [k for k in (args.kinds or ",".join(wl.kinds)).split(",") if k]
     if args.calibrate_copy:
