@@ -28,7 +28,7 @@ import torch
 
 from difflet_amd import _lib, kernels
 from difflet_amd.dit.base import EPS, JointDiT
-from difflet_amd.dit.linear import DeviceLinear
+from difflet_amd.dit.linear import DeviceLinear, linear_group
 from difflet_amd.dit.rope import flux_rope_tables
 
 
@@ -46,42 +46,11 @@ class FluxConfig:
             raise ValueError("heads * head_dim must equal hidden")
 
 
-def _group(get: Callable[[str], torch.Tensor], q, prefixes: list[str], kind: str, *,
-           along_k: bool = False, bias_prefix: str | None = None) -> DeviceLinear:
-    """One device linear over the linears at ``prefixes``, their weights concatenated along N
-    (rows) or, ``along_k``, along K (the single block's proj_out halves, bias ``bias_prefix``).
-
-    Without a quantized checkpoint ``q`` the dense weights are quantized here by ``kind``. With
-    one, the group's stored fp8 codes and scales are loaded as they are (every member of a group
-    stored quantized, or none: then the dense weights run in bf16)."""
-    cat_dim = 1 if along_k else 0
-    bias_names = [bias_prefix] if along_k else prefixes
-    bias = torch.cat([get(f"{p}.bias") for p in bias_names], dim=0)
-    if q is not None:
-        parts = [q.fp8(p) for p in prefixes]
-        stored = [p is not None for p in parts]
-        if all(stored):
-            lk = "fp8" if q.format == "fp8_rowwise" else "mx"
-            if along_k and (lk == "fp8" or parts[0][0].shape[1] % 512):
-                raise ValueError(f"{prefixes}: stored halves fuse along K only as MXFP8 with the "
-                                 "first half's K a multiple of 512 (the swizzle tile)")
-            dev = bias.device
-            codes = torch.cat([c.to(dev) for c, _ in parts], dim=cat_dim)
-            scales = torch.cat([sc.to(dev) for _, sc in parts], dim=cat_dim)
-            return DeviceLinear.from_fp8(codes, scales, bias, lk)
-        if any(stored):
-            raise ValueError(f"{prefixes}: one GEMM runs these linears, so they are stored "
-                             "quantized all together or not at all")
-        kind = "bf16"
-    w = torch.cat([get(f"{p}.weight") for p in prefixes], dim=cat_dim)
-    return DeviceLinear(w, bias, kind)
-
-
 class _Double:
     def __init__(self, get: Callable[[str], torch.Tensor], pre: str, cfg: FluxConfig, kind: str,
                  q=None):
         W = lambda n: get(f"{pre}.{n}")  # noqa: E731
-        L = lambda *ns: _group(get, q, [f"{pre}.{n}" for n in ns], kind)  # noqa: E731
+        L = lambda *ns: linear_group(get, q, [f"{pre}.{n}" for n in ns], kind)  # noqa: E731
         a = "attn."
         self.qkv_img = L(a + "to_q", a + "to_k", a + "to_v")
         self.qkv_txt = L(a + "add_q_proj", a + "add_k_proj", a + "add_v_proj")
@@ -102,15 +71,15 @@ class _Single:
         W = lambda n: get(f"{pre}.{n}")  # noqa: E731
         a = "attn."
         # column order [k | v | q | mlp]: attention writes over q, leaving [attn | mlp] adjacent
-        self.w1 = _group(get, q, [f"{pre}.{a}to_k", f"{pre}.{a}to_v", f"{pre}.{a}to_q",
+        self.w1 = linear_group(get, q, [f"{pre}.{a}to_k", f"{pre}.{a}to_v", f"{pre}.{a}to_q",
                                   f"{pre}.proj_mlp"], kind)
         if q is not None and f"{pre}.proj_out.weight" not in q:
             # a checkpoint that splits proj_out stores proj_out_attn [D, D] and proj_out_mlp
             # [D, 4D]; the step runs them as the one K = 5D GEMM over [attn | mlp]
-            self.w2 = _group(get, q, [f"{pre}.proj_out_attn", f"{pre}.proj_out_mlp"], kind,
+            self.w2 = linear_group(get, q, [f"{pre}.proj_out_attn", f"{pre}.proj_out_mlp"], kind,
                              along_k=True, bias_prefix=f"{pre}.proj_out")
         else:
-            self.w2 = _group(get, q, [f"{pre}.proj_out"], kind)
+            self.w2 = linear_group(get, q, [f"{pre}.proj_out"], kind)
         bf = lambda n: W(n).to(torch.bfloat16).contiguous()  # noqa: E731
         self.nq, self.nk = bf(a + "norm_q.weight"), bf(a + "norm_k.weight")
 

@@ -89,6 +89,37 @@ class DeviceLinear:
         return b
 
 
+def linear_group(get, q, prefixes: list[str], kind: str, *,
+           along_k: bool = False, bias_prefix: str | None = None) -> DeviceLinear:
+    """One device linear over the linears at ``prefixes``, their weights concatenated along N
+    (rows) or, ``along_k``, along K (the single block's proj_out halves, bias ``bias_prefix``).
+
+    Without a quantized checkpoint ``q`` the dense weights are quantized here by ``kind``. With
+    one, the group's stored fp8 codes and scales are loaded as they are (every member of a group
+    stored quantized, or none: then the dense weights run in bf16)."""
+    cat_dim = 1 if along_k else 0
+    bias_names = [bias_prefix] if along_k else prefixes
+    bias = torch.cat([get(f"{p}.bias") for p in bias_names], dim=0)
+    if q is not None:
+        parts = [q.fp8(p) for p in prefixes]
+        stored = [p is not None for p in parts]
+        if all(stored):
+            lk = "fp8" if q.format == "fp8_rowwise" else "mx"
+            if along_k and (lk == "fp8" or parts[0][0].shape[1] % 512):
+                raise ValueError(f"{prefixes}: stored halves fuse along K only as MXFP8 with the "
+                                 "first half's K a multiple of 512 (the swizzle tile)")
+            dev = bias.device
+            codes = torch.cat([c.to(dev) for c, _ in parts], dim=cat_dim)
+            scales = torch.cat([sc.to(dev) for _, sc in parts], dim=cat_dim)
+            return DeviceLinear.from_fp8(codes, scales, bias, lk)
+        if any(stored):
+            raise ValueError(f"{prefixes}: one GEMM runs these linears, so they are stored "
+                             "quantized all together or not at all")
+        kind = "bf16"
+    w = torch.cat([get(f"{p}.weight") for p in prefixes], dim=cat_dim)
+    return DeviceLinear(w, bias, kind)
+
+
 def run(problems, kind: str, epilogue: int = 0, act_col_start: int = 0, qk=None) -> None:
     kernels.gemm_grouped(problems, kind=kind, epilogue=epilogue, act_col_start=act_col_start,
                          qk=qk)

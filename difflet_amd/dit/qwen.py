@@ -21,7 +21,7 @@ import torch
 
 from difflet_amd import kernels
 from difflet_amd.dit.base import EPS, JointDiT
-from difflet_amd.dit.linear import DeviceLinear
+from difflet_amd.dit.linear import DeviceLinear, linear_group
 from difflet_amd.dit.rope import qwen_rope_tables
 
 
@@ -36,22 +36,19 @@ class QwenConfig:
 
 
 class _Block:
-    def __init__(self, get: Callable[[str], torch.Tensor], pre: str, kind: str):
+    def __init__(self, get: Callable[[str], torch.Tensor], pre: str, kind: str, q=None):
         W = lambda n: get(f"{pre}.{n}")  # noqa: E731
-        cat = lambda *ns: torch.cat([W(n) for n in ns], dim=0)  # noqa: E731
+        L = lambda *ns, k=kind: linear_group(get, q, [f"{pre}.{n}" for n in ns], k)  # noqa: E731
         a = "attn."
-        self.qkv_img = DeviceLinear(cat(a + "to_q.weight", a + "to_k.weight", a + "to_v.weight"),
-                                    cat(a + "to_q.bias", a + "to_k.bias", a + "to_v.bias"), kind)
-        self.qkv_txt = DeviceLinear(
-            cat(a + "add_q_proj.weight", a + "add_k_proj.weight", a + "add_v_proj.weight"),
-            cat(a + "add_q_proj.bias", a + "add_k_proj.bias", a + "add_v_proj.bias"), kind)
+        self.qkv_img = L(a + "to_q", a + "to_k", a + "to_v")
+        self.qkv_txt = L(a + "add_q_proj", a + "add_k_proj", a + "add_v_proj")
         # the output projections are not MXFP8 targets
-        self.out_img = DeviceLinear(W(a + "to_out.0.weight"), W(a + "to_out.0.bias"), "bf16")
-        self.out_txt = DeviceLinear(W(a + "to_add_out.weight"), W(a + "to_add_out.bias"), "bf16")
-        self.ff1_img = DeviceLinear(W("img_mlp.net.0.proj.weight"), W("img_mlp.net.0.proj.bias"), kind)
-        self.ff2_img = DeviceLinear(W("img_mlp.net.2.weight"), W("img_mlp.net.2.bias"), kind)
-        self.ff1_txt = DeviceLinear(W("txt_mlp.net.0.proj.weight"), W("txt_mlp.net.0.proj.bias"), kind)
-        self.ff2_txt = DeviceLinear(W("txt_mlp.net.2.weight"), W("txt_mlp.net.2.bias"), kind)
+        self.out_img = L(a + "to_out.0", k="bf16")
+        self.out_txt = L(a + "to_add_out", k="bf16")
+        self.ff1_img = L("img_mlp.net.0.proj")
+        self.ff2_img = L("img_mlp.net.2")
+        self.ff1_txt = L("txt_mlp.net.0.proj")
+        self.ff2_txt = L("txt_mlp.net.2")
         bf = lambda n: W(n).to(torch.bfloat16).contiguous()  # noqa: E731
         self.nq, self.nk = bf(a + "norm_q.weight"), bf(a + "norm_k.weight")
         self.naq, self.nak = bf(a + "norm_added_q.weight"), bf(a + "norm_added_k.weight")
@@ -59,11 +56,18 @@ class _Block:
 
 class QwenImageDiT(JointDiT):
     """The Qwen-Image transformer on the HIP kernels. `get(name)` returns a parameter by its
-    diffusers name; `kind` is "bf16" or "mx" (MXFP8 on the targeted block linears)."""
+    diffusers name; `kind` is "bf16" or "mx" (MXFP8 on the targeted block linears).
+
+    `quantized` (a difflet_amd.quant.checkpoint.QuantizedCheckpoint) loads the block linears a
+    quantized checkpoint stores as fp8 from their codes and scales, with no quantization at
+    load (`kind` then follows its format); QwenImageDiT.from_quantized_dir builds the model
+    from such a directory alone."""
 
     def __init__(self, cfg: QwenConfig, get: Callable[[str], torch.Tensor], kind: str = "mx",
-                 device: str | torch.device = "cuda"):
-        if kind not in ("bf16", "mx"):
+                 device: str | torch.device = "cuda", quantized=None):
+        if quantized is not None:
+            kind = "fp8" if quantized.format == "fp8_rowwise" else "mx"
+        elif kind not in ("bf16", "mx"):
             raise ValueError(f"Qwen-Image runs kind 'bf16' or 'mx', got {kind!r}")
         self.cfg, self.kind = cfg, kind
         self.device = torch.device(device)
@@ -91,7 +95,8 @@ class QwenImageDiT(JointDiT):
         self.mod_w = torch.cat(mod_w, dim=0)
         self.mod_b = torch.cat(mod_b, dim=0)
         del mod_w, mod_b
-        self.blocks = [_Block(G, f"transformer_blocks.{i}", kind) for i in range(cfg.n_blocks)]
+        self.blocks = [_Block(G, f"transformer_blocks.{i}", kind, quantized)
+                       for i in range(cfg.n_blocks)]
         self._bufs: dict = {}
         self._rope: dict = {}
         self.probe = None
@@ -141,6 +146,15 @@ class QwenImageDiT(JointDiT):
         return self.proj_out(n[st:]).unsqueeze(0)
 
     __call__ = forward
+
+    @classmethod
+    def from_quantized_dir(cls, cfg: QwenConfig, path, device: str | torch.device = "cuda"
+                           ) -> "QwenImageDiT":
+        """The model from a quantized directory alone (difflet_amd.quant.checkpoint)."""
+        from difflet_amd.quant.checkpoint import QuantizedCheckpoint
+
+        ckpt = QuantizedCheckpoint(path)
+        return cls(cfg, ckpt.get, device=device, quantized=ckpt)
 
 
 def qwen_param_shapes(cfg: QwenConfig) -> dict[str, tuple]:

@@ -230,3 +230,42 @@ def test_fp8_twins_load_from_the_directory(gpu, toy, tmp_path):
     quantize_module_(c, mx_spec)
     with pytest.raises(ValueError, match="holds fp8_rowwise"):
         qc.load_fp8_linears_(c, out)
+
+
+def test_qwen_step_from_mxfp8_directory_equals_quantize_at_load(gpu, tmp_path):
+    """Qwen-Image with the reference's default MXFP8 targets, from a single-file source (no
+    index): the step loaded from the directory equals the step quantizing at load."""
+    from safetensors.torch import save_file
+
+    from difflet_amd.dit.qwen import QwenConfig, QwenImageDiT, qwen_param_shapes
+    from difflet_amd.quant.spec import QWEN_IMAGE_TARGETS
+
+    cfg = QwenConfig(hidden=512, heads=4, mlp=2048, n_blocks=2, txt_dim=896)
+    g = torch.Generator().manual_seed(5)
+    src = {}
+    for name, shape in sorted(qwen_param_shapes(cfg).items()):
+        t = torch.randn(shape, generator=g) * (0.1 if len(shape) == 1 else 0.02)
+        src[name] = (t + 1.0 if "norm" in name and len(shape) == 1 else t).to(torch.bfloat16)
+    d = tmp_path / "qwen" / "transformer"
+    d.mkdir(parents=True)
+    save_file(src, str(d / "diffusion_pytorch_model.safetensors"), metadata={"format": "pt"})
+    spec = RocmQuantSpec(targets=QWEN_IMAGE_TARGETS)
+    out = tmp_path / "mx"
+    manifest = qc.write_quantized_dir(d, out, spec, device=gpu)
+    assert manifest["tensors"]["quantized"] == 2 * 10 and len(manifest["files"]) == 1
+    print("Qwen toy step: mxfp8 directory vs quantize at load", flush=True)
+    dense = QwenImageDiT(cfg, lambda n: src[n], kind="mx", device=gpu)
+    loaded = QwenImageDiT.from_quantized_dir(cfg, out, device=gpu)
+    assert loaded.kind == "mx"
+    for blk_a, blk_b in zip(dense.blocks, loaded.blocks):
+        for n in ("qkv_img", "qkv_txt", "out_img", "out_txt", "ff1_img", "ff2_img", "ff1_txt", "ff2_txt"):
+            _same_linear(getattr(blk_a, n), getattr(blk_b, n), n)
+    g = torch.Generator().manual_seed(6)
+    lat = torch.randn(1, 16 * 16, 64, generator=g).to(gpu)
+    txt = torch.randn(1, 40, 896, generator=g).to(gpu)
+    t = torch.tensor([0.4], device=gpu)
+    y0 = dense(lat, txt, t, (16, 16))
+    y1 = loaded(lat, txt, t, (16, 16))
+    torch.cuda.synchronize()
+    assert torch.isfinite(y0.float()).all()
+    assert torch.equal(y0, y1)
