@@ -119,3 +119,64 @@ def test_forward_shapes_and_weight_draws_are_seeded():
     b = oflux.double_block_weights(shape, 5, 1)
     assert all(torch.equal(a[k], b[k]) for k in a)
     assert not torch.equal(a["ff.net.2.weight"], oflux.double_block_weights(shape, 5, 0)["ff.net.2.weight"])
+
+
+# ------------------------------------------------------------------- against the reference model
+def _reference_vectors():
+    import json
+    from pathlib import Path
+
+    return json.loads((Path(__file__).parent / "golden" / "flux_reference_forward.json").read_text())
+
+
+def test_forward_and_blocks_equal_the_reference_model():
+    """The reference's own NeuronFluxTransformer2DModel (fp32, its CPU backend) ran on the same
+    seeded weights and inputs (tests/golden/make_flux_golden.py): the oracle's forward, first
+    double block (both streams) and first single block give the same values. They agreed to the
+    last bit when the fixture was made; 1e-6 leaves room for another BLAS on another host."""
+    from tests.golden.make_flux_golden import IMG_HW, SEED, SHAPE, TXT, decode, inputs
+
+    g = _reference_vectors()
+    assert g["shape"]["hidden"] == SHAPE.hidden and g["seed"] == SEED
+    ref = {k: decode(v) for k, v in g["tensors"].items()}
+    inp = inputs()
+    f32 = torch.float32
+    out = oflux.forward(SHAPE, SEED, inp["latents"], inp["text"], inp["pooled"], inp["timestep"],
+                        inp["guidance"], IMG_HW, dtype=f32, model_dtype=f32)
+    ew = oflux.embed_weights(SHAPE, SEED, dtype=f32)
+    hidden = ops.linear(inp["latents"], ew["x_embedder.weight"], ew["x_embedder.bias"])
+    context = ops.linear(inp["text"], ew["context_embedder.weight"], ew["context_embedder.bias"])
+    temb = oflux.time_text_embed(ew, inp["timestep"] * 1000, inp["guidance"] * 1000,
+                                 inp["pooled"], SHAPE)
+    cos, sin = ops.flux_pos_embed(ops.flux_ids(TXT, *IMG_HW), SHAPE.axes)
+    c0, h0 = oflux.double_block(oflux.double_block_weights(SHAPE, SEED, 0, dtype=f32),
+                                hidden, context, temb, cos, sin, SHAPE)
+    # the first single block's input: both double blocks, then [txt | img]
+    c1, h1 = oflux.double_block(oflux.double_block_weights(SHAPE, SEED, 1, dtype=f32),
+                                h0, c0, temb, cos, sin, SHAPE)
+    s0 = oflux.single_block(oflux.single_block_weights(SHAPE, SEED, 0, dtype=f32),
+                            torch.cat([c1, h1], dim=1), temb, cos, sin, SHAPE)
+    for name, got in (("output", out), ("double0_context", c0), ("double0_hidden", h0),
+                      ("single0", s0)):
+        want = ref[name]
+        assert got.shape == want.shape, name
+        e = ((got - want).norm() / want.norm()).item()
+        assert e < 1e-6, f"{name}: rel L2 {e:.3e}"
+
+
+def test_a_planted_mistake_is_seen_by_the_reference_vectors():
+    """The check is tight enough to fail a plausible slip: a wrong RoPE table (sin negated)."""
+    from tests.golden.make_flux_golden import IMG_HW, SEED, SHAPE, TXT, decode, inputs
+
+    want = decode(_reference_vectors()["tensors"]["double0_hidden"])
+    inp = inputs()
+    f32 = torch.float32
+    ew = oflux.embed_weights(SHAPE, SEED, dtype=f32)
+    hidden = ops.linear(inp["latents"], ew["x_embedder.weight"], ew["x_embedder.bias"])
+    context = ops.linear(inp["text"], ew["context_embedder.weight"], ew["context_embedder.bias"])
+    temb = oflux.time_text_embed(ew, inp["timestep"] * 1000, inp["guidance"] * 1000,
+                                 inp["pooled"], SHAPE)
+    cos, sin = ops.flux_pos_embed(ops.flux_ids(TXT, *IMG_HW), SHAPE.axes)
+    _, h0 = oflux.double_block(oflux.double_block_weights(SHAPE, SEED, 0, dtype=f32),
+                               hidden, context, temb, cos, -sin, SHAPE)
+    assert ((h0 - want).norm() / want.norm()).item() > 1e-3
