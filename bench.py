@@ -13,7 +13,8 @@ text tokens (3584-wide encoder states), hidden 3072, 24 x 128 heads, MLP 12288; 
 (MXFP8 on the QWEN_IMAGE_TARGETS linears) and "bf16".
 wan: the Wan-2.2-14B-shaped text-to-video step, 40 blocks, latent 21 x 60 x 104 with patch
 (1, 2, 2) = 32760 video tokens + 512 text tokens (4096-wide), hidden 5120, 40 x 128 heads, FFN
-13824, bf16.
+13824; kinds "bf16" and "mx" (MXFP8 on the cross-attention q/k/v and FFN linears, the
+reference's Wan targets).
 weights: the quantized-checkpoint writer's device work, every FLUX block linear (19 double x
 12 + 38 single x 5 = 418 weights, 8.61 G values) quantized from bf16 to e4m3 codes and scales,
 per-channel fp8 and MXFP8; `value` is the summed quantizer time in ms, K timed calls per shape.
@@ -222,7 +223,7 @@ class Qwen:
 
 class Wan:
     name = "wan"
-    kinds = ("bf16",)
+    kinds = ("bf16", "mx")
     latent_fhw, txt = (21, 60, 104), 512
     dominant = "attn.self"
     dominant_desc = "self-attention (40 heads x 32760 queries x 32760 keys x 128, bf16)"
@@ -243,7 +244,7 @@ class Wan:
     def build(self, kind, torch, dev):
         from difflet_amd.dit.wan import WanDiT, random_param_source
 
-        model = WanDiT(self.cfg, random_param_source(self.cfg, SEED, dev), device=dev)
+        model = WanDiT(self.cfg, random_param_source(self.cfg, SEED, dev), device=dev, kind=kind)
         g = torch.Generator(device=dev).manual_seed(SEED + 1)
         c = self.cfg
         lat = torch.randn(1, c.in_channels, *self.latent_fhw, generator=g, device=dev)
@@ -268,7 +269,9 @@ class Wan:
         return c.n_blocks * sum(self.flops().values()) + emb
 
     def peak(self, name, kind):
-        return PEAK["bf16"]
+        # MXFP8 on the reference's Wan targets: cross-attention q / k, v and both FFN linears
+        mx = kind == "mx" and name in ("gemm.q2", "gemm.kv2", "gemm.ffn_in", "gemm.ffn_out")
+        return PEAK["mx" if mx else "bf16"]
 
 
 WORKLOADS = {"flux": Flux, "qwen": Qwen, "wan": Wan}
@@ -592,8 +595,8 @@ def main():
     metric = {"flux": METRIC,
               "qwen": "Qwen-Image 1328² denoise step ms (MXFP8, bf16) at 1 GPU; attn+GEMM % of "
                       "MFMA peak",
-              "wan": "Wan-2.2 480x832x81 denoise step ms (bf16) at 1 GPU; attn+GEMM % of MFMA "
-                     "peak"}[wl.name]
+              "wan": "Wan-2.2 480x832x81 denoise step ms (bf16, MXFP8) at 1 GPU; attn+GEMM % of "
+                     "MFMA peak"}[wl.name]
     line = {
         "metric": metric,
         "value": out[head]["ms_per_step"],

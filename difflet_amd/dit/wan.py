@@ -24,7 +24,7 @@ import torch
 
 from difflet_amd import _lib, kernels
 from difflet_amd.dit.base import EPS
-from difflet_amd.dit.linear import DeviceLinear, run
+from difflet_amd.dit.linear import DeviceLinear, linear_group, run
 from difflet_amd.dit.rope import wan_rope_tables
 
 
@@ -58,19 +58,34 @@ class WanConfig:
             raise ValueError("heads * head_dim must equal hidden")
 
 
+#: difflet/models/wan/dit_config.py:126-139: the module's FFN attributes net_in / net_out are
+#: diffusers' ffn.net.0.proj / ffn.net.2 in a checkpoint.
+_MODULE_TO_CHECKPOINT = ((".ffn.net_in.", ".ffn.net.0.proj."), (".ffn.net_out.", ".ffn.net.2."))
+
+
+def checkpoint_key(name: str) -> str:
+    """The checkpoint key of the module parameter ``name``."""
+    for module_part, ckpt_part in _MODULE_TO_CHECKPOINT:
+        name = name.replace(module_part, ckpt_part)
+    return name
+
+
 class _Block:
-    def __init__(self, get: Callable[[str], torch.Tensor], pre: str):
-        W = lambda n: get(f"{pre}.{n}")  # noqa: E731
-        cat = lambda *ns: torch.cat([W(n) for n in ns], dim=0)  # noqa: E731
-        self.qkv = DeviceLinear(cat("attn1.to_q.weight", "attn1.to_k.weight", "attn1.to_v.weight"),
-                                cat("attn1.to_q.bias", "attn1.to_k.bias", "attn1.to_v.bias"))
-        self.out1 = DeviceLinear(W("attn1.to_out.0.weight"), W("attn1.to_out.0.bias"))
-        self.q2 = DeviceLinear(W("attn2.to_q.weight"), W("attn2.to_q.bias"))
-        self.kv2 = DeviceLinear(cat("attn2.to_k.weight", "attn2.to_v.weight"),
-                                cat("attn2.to_k.bias", "attn2.to_v.bias"))
-        self.out2 = DeviceLinear(W("attn2.to_out.0.weight"), W("attn2.to_out.0.bias"))
-        self.ffn_in = DeviceLinear(W("ffn.net_in.weight"), W("ffn.net_in.bias"))
-        self.ffn_out = DeviceLinear(W("ffn.net_out.weight"), W("ffn.net_out.bias"))
+    """kind "mx": the reference's MXFP8 Wan targets (difflet/quant/targets.py:259-263), the
+    cross-attention's q/k/v and both FFN linears; self-attention and output projections bf16."""
+
+    def __init__(self, get: Callable[[str], torch.Tensor], pre: str, kind: str = "bf16", q=None,
+                 key: Callable[[str], str] = lambda n: n):
+        W = lambda n: get(key(f"{pre}.{n}"))  # noqa: E731
+        L = lambda k, *ns: linear_group(  # noqa: E731
+            get, q, [key(f"{pre}.{n}.weight")[: -len(".weight")] for n in ns], k)
+        self.qkv = L("bf16", "attn1.to_q", "attn1.to_k", "attn1.to_v")
+        self.out1 = L("bf16", "attn1.to_out.0")
+        self.q2 = L(kind, "attn2.to_q")
+        self.kv2 = L(kind, "attn2.to_k", "attn2.to_v")
+        self.out2 = L("bf16", "attn2.to_out.0")
+        self.ffn_in = L(kind, "ffn.net_in")
+        self.ffn_out = L(kind, "ffn.net_out")
         bf = lambda n: W(n).to(torch.bfloat16).contiguous()  # noqa: E731
         self.nq1, self.nk1 = bf("attn1.norm_q.weight"), bf("attn1.norm_k.weight")
         self.nq2, self.nk2 = bf("attn2.norm_q.weight"), bf("attn2.norm_k.weight")
@@ -79,12 +94,21 @@ class _Block:
 
 
 class WanDiT:
-    """The Wan transformer on the HIP kernels (bf16). `get(name)` returns a parameter by the
-    reference module's name (blocks.{i}.attn1.to_q.weight, ...)."""
+    """The Wan transformer on the HIP kernels. `get(name)` returns a parameter by the reference
+    module's name (blocks.{i}.attn1.to_q.weight, ...); `kind` "bf16" or "mx" (MXFP8 on the
+    reference's Wan targets). `quantized` (a difflet_amd.quant.checkpoint.QuantizedCheckpoint)
+    loads the linears it stores as fp8 from their codes and scales, `get` then taking checkpoint
+    keys; WanDiT.from_quantized_dir builds the model from such a directory alone."""
 
     def __init__(self, cfg: WanConfig, get: Callable[[str], torch.Tensor],
-                 device: str | torch.device = "cuda"):
-        self.cfg, self.kind = cfg, "bf16"
+                 device: str | torch.device = "cuda", kind: str = "bf16", quantized=None):
+        key = lambda n: n  # noqa: E731
+        if quantized is not None:
+            kind = "fp8" if quantized.format == "fp8_rowwise" else "mx"
+            key = checkpoint_key
+        elif kind not in ("bf16", "mx"):
+            raise ValueError(f"Wan runs kind 'bf16' or 'mx', got {kind!r}")
+        self.cfg, self.kind = cfg, kind
         self.device = torch.device(device)
         G = lambda n: get(n).to(self.device)  # noqa: E731
         bf = lambda n: G(n).to(torch.bfloat16).contiguous()  # noqa: E731
@@ -101,7 +125,7 @@ class WanDiT:
         self.proj_out = DeviceLinear(G("proj_out.weight"), G("proj_out.bias"))
         self.sst = torch.stack([G(f"blocks.{i}.scale_shift_table").to(torch.float32).reshape(6, d)
                                 for i in range(cfg.n_blocks)])
-        self.blocks = [_Block(G, f"blocks.{i}") for i in range(cfg.n_blocks)]
+        self.blocks = [_Block(G, f"blocks.{i}", kind, quantized, key) for i in range(cfg.n_blocks)]
         self.ones = torch.ones((1, d), dtype=torch.bfloat16, device=self.device)
         self._bufs: dict = {}
         self._rope: dict = {}
@@ -130,9 +154,9 @@ class WanDiT:
                                                self.device)}
         return self._rope[key]
 
-    def _gemm(self, name, problems, epilogue=0, act_col_start=0):
+    def _gemm(self, name, problems, epilogue=0, act_col_start=0, kind="bf16"):
         with self._timed(name):
-            run(problems, "bf16", epilogue, act_col_start)
+            run(problems, kind, epilogue, act_col_start)
 
     def _attention(self, qbuf, q_off, kbuf, k_off, vbuf, v_off):
         c = self.cfg
@@ -151,27 +175,27 @@ class WanDiT:
         h, n, qkv, kvt, ff, txt = (bufs[k] for k in ("h", "n", "qkv", "kv_txt", "ff", "txt"))
         sh, sc, _, c_sh, c_sc, _ = mods
         kernels.layernorm_modulate(h, sc, sh, eps=EPS, out=n)
-        self._gemm("gemm.qkv", [blk.qkv.problem(n, qkv)])
+        self._gemm("gemm.qkv", [blk.qkv.problem(n, qkv)], kind=blk.qkv.kind)
         kernels.qk_norm_rope(qkv, heads=c.heads, head_dim=c.head_dim, q_off=0, k_off=d,
                              wq=blk.nq1, wk=blk.nk1, eps=EPS, cos=cos, sin=sin, law=1, do_norm=2)
         self._attention(qkv, 0, qkv, d, qkv, 2 * d)
         self._gemm("gemm.out1", [blk.out1.problem(qkv[:, :d], h, gate=gates[0:1], residual=h)],
-                   _lib.EPI_GATE_RESIDUAL)
+                   _lib.EPI_GATE_RESIDUAL, kind=blk.out1.kind)
         kernels.layernorm_modulate(h, blk.norm2_w, blk.norm2_b, eps=EPS, one_plus=False, out=n)
         q2 = qkv[:, :d]
-        self._gemm("gemm.q2", [blk.q2.problem(n, q2)])
-        self._gemm("gemm.kv2", [blk.kv2.problem(txt, kvt)])
+        self._gemm("gemm.q2", [blk.q2.problem(n, q2)], kind=blk.q2.kind)
+        self._gemm("gemm.kv2", [blk.kv2.problem(txt, kvt)], kind=blk.kv2.kind)
         kernels.qk_norm_rope(qkv, heads=c.heads, head_dim=c.head_dim, q_off=0, k_off=-1,
                              wq=blk.nq2, wk=None, eps=EPS, cos=None, sin=None, do_norm=2)
         kernels.qk_norm_rope(kvt, heads=c.heads, head_dim=c.head_dim, q_off=0, k_off=-1,
                              wq=blk.nk2, wk=None, eps=EPS, cos=None, sin=None, do_norm=2)
         self._attention(qkv, 0, kvt, 0, kvt, d)
         self._gemm("gemm.out2", [blk.out2.problem(q2, h, gate=self.ones, residual=h)],
-                   _lib.EPI_GATE_RESIDUAL)
+                   _lib.EPI_GATE_RESIDUAL, kind=blk.out2.kind)
         kernels.layernorm_modulate(h, c_sc, c_sh, eps=EPS, out=n)
-        self._gemm("gemm.ffn_in", [blk.ffn_in.problem(n, ff)], _lib.EPI_GELU)
+        self._gemm("gemm.ffn_in", [blk.ffn_in.problem(n, ff)], _lib.EPI_GELU, kind=blk.ffn_in.kind)
         self._gemm("gemm.ffn_out", [blk.ffn_out.problem(ff, h, gate=gates[1:2], residual=h)],
-                   _lib.EPI_GATE_RESIDUAL)
+                   _lib.EPI_GATE_RESIDUAL, kind=blk.ffn_out.kind)
 
     def condition(self, timestep, text, bufs):
         """(temb bf16 [1, D], timestep_proj bf16 [1, 6D]); the text projection into bufs['txt']."""
@@ -209,6 +233,16 @@ class WanDiT:
         return unpatchify(self.proj_out(n), grid, c.patch)
 
     __call__ = forward
+
+    @classmethod
+    def from_quantized_dir(cls, cfg: WanConfig, path, device: str | torch.device = "cuda"
+                           ) -> "WanDiT":
+        """The model from a quantized directory alone (difflet_amd.quant.checkpoint), its keys
+        diffusers' (checkpoint_key maps the module names)."""
+        from difflet_amd.quant.checkpoint import QuantizedCheckpoint
+
+        ckpt = QuantizedCheckpoint(path)
+        return cls(cfg, ckpt.get, device=device, quantized=ckpt)
 
 
 def wan_param_shapes(cfg: WanConfig) -> dict[str, tuple]:

@@ -170,6 +170,14 @@ FLUX_ROW_PARALLEL: tuple[str, ...] = (
     rf"{_SINGLE}\.proj_out_(attn|mlp)",
 )
 
+#: difflet/quant/targets.py:259-263 (WAN_TARGETS), on diffusers' checkpoint names: the
+#: cross-attention's q/k/v and both FFN linears.
+WAN_TARGETS: tuple[str, ...] = (
+    r"blocks\.\d+\.attn2\.(to_q|to_k|to_v)",
+    r"blocks\.\d+\.ffn\.net\.0\.proj",
+    r"blocks\.\d+\.ffn\.net\.2",
+)
+
 #: difflet/quant/targets.py:117-121 (QWEN_IMAGE_TARGETS): q/k/v, the added q/k/v and both MLPs;
 #: the output projections stay bf16.
 QWEN_IMAGE_TARGETS: tuple[str, ...] = (

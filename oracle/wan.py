@@ -145,9 +145,14 @@ def _attend(q, k, v, shape: WanShape):
     return o.reshape(b, h, s, d).transpose(1, 2).reshape(b, s, h * d)
 
 
-def block(w: dict, hidden, text, tproj, cos, sin, shape: WanShape):
-    """hidden [B, S, D], text [B, S_txt, D] (embedded), tproj [B, 6, D] -> hidden."""
+def block(w: dict, hidden, text, tproj, cos, sin, shape: WanShape, quant=None, act_dtype=None):
+    """hidden [B, S, D], text [B, S_txt, D] (embedded), tproj [B, 6, D] -> hidden. `quant`
+    ("mx") applies the MX law to the reference's Wan targets (difflet/quant/targets.py:259-263:
+    the cross-attention's q/k/v and both FFN linears), the rest in fp32."""
+    from oracle.flux import qlinear
+
     L = ops.linear
+    Q = qlinear(quant, act_dtype)
     b, s, d = hidden.shape
     mods = w["scale_shift_table"] + tproj
     sh, sc, g, c_sh, c_sc, c_g = mods.chunk(6, dim=1)
@@ -163,13 +168,13 @@ def block(w: dict, hidden, text, tproj, cos, sin, shape: WanShape):
     hidden = hidden + o * g
     # cross-attention to the text
     nh = torch.nn.functional.layer_norm(hidden, (d,), w["norm2.weight"], w["norm2.bias"], 1e-6)
-    q = ops.rms_norm_fp32(L(nh, w["attn2.to_q.weight"], w["attn2.to_q.bias"]), w["attn2.norm_q.weight"], 1e-6)
-    k = ops.rms_norm_fp32(L(text, w["attn2.to_k.weight"], w["attn2.to_k.bias"]), w["attn2.norm_k.weight"], 1e-6)
-    v = L(text, w["attn2.to_v.weight"], w["attn2.to_v.bias"])
+    q = ops.rms_norm_fp32(Q(nh, w["attn2.to_q.weight"], w["attn2.to_q.bias"]), w["attn2.norm_q.weight"], 1e-6)
+    k = ops.rms_norm_fp32(Q(text, w["attn2.to_k.weight"], w["attn2.to_k.bias"]), w["attn2.norm_k.weight"], 1e-6)
+    v = Q(text, w["attn2.to_v.weight"], w["attn2.to_v.bias"])
     hidden = hidden + L(_attend(q, k, v, shape), w["attn2.to_out.0.weight"], w["attn2.to_out.0.bias"])
     # feed-forward
     nh = ops.layer_norm(hidden) * (1 + c_sc) + c_sh
-    ff = L(ops.gelu_tanh(L(nh, w["ffn.net_in.weight"], w["ffn.net_in.bias"])),
+    ff = Q(ops.gelu_tanh(Q(nh, w["ffn.net_in.weight"], w["ffn.net_in.bias"])),
            w["ffn.net_out.weight"], w["ffn.net_out.bias"])
     return hidden + ff * c_g
 

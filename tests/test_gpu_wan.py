@@ -74,3 +74,76 @@ def test_wan_reduced_depth_step_matches_fp32_oracle(gpu):
     print(f"step rel L2 {e:.3e}", flush=True)
     assert out.shape == (1, 16, 3, 12, 10)
     assert e < 1e-2
+
+
+def test_wan_block_mx_matches_the_oracle_of_the_same_law(gpu):
+    """The reference's MXFP8 Wan targets (cross-attention q/k/v, both FFN linears) on the MX
+    GEMM, against the oracle block with the MX law on the same linears (bf16 activations
+    quantized), at width 1024 (8 heads), FFN 2816, a 2 x 8 x 8 grid and 64 text tokens."""
+    print("wan block, mx", flush=True)
+    kw = dict(hidden=1024, heads=8, ffn=2816, n_blocks=1)
+    shape = owan.WanShape(**kw)
+    w = _source(shape, 1)
+    dit = WanDiT(WanConfig(**kw), lambda n: w[n], device=gpu, kind="mx")
+    assert [getattr(dit.blocks[0], n).kind for n in ("qkv", "out1", "q2", "kv2", "out2", "ffn_in",
+                                                      "ffn_out")] == ["bf16", "bf16", "mx", "mx", "bf16", "mx", "mx"]
+    grid, st = (2, 8, 8), 64
+    s = grid[0] * grid[1] * grid[2]
+    g = torch.Generator().manual_seed(SEED + 1)
+    hidden = torch.randn(1, s, shape.hidden, generator=g).bfloat16().float()
+    text = torch.randn(1, st, shape.hidden, generator=g).bfloat16().float()
+    tproj = (torch.randn(1, 6, shape.hidden, generator=g) * 0.5).bfloat16().float()
+    cos, sin = owan.rope_tables(grid, shape)
+    bw = {k[len("blocks.0."):]: v.float() for k, v in w.items() if k.startswith("blocks.0.")}
+    ref = owan.block(bw, hidden, text, tproj, cos, sin, shape, quant="mx", act_dtype=torch.bfloat16)
+    ref_bf16 = owan.block(bw, hidden, text, tproj, cos, sin, shape)
+    bufs = dit._buffers(s, st)
+    bufs["h"].copy_(hidden[0].to(gpu, torch.bfloat16))
+    bufs["txt"].copy_(text[0].to(gpu, torch.bfloat16))
+    mods = dit.sst[0] + tproj[0].to(gpu)
+    gates = mods[2::3].to(torch.bfloat16).contiguous()
+    gcos, gsin = dit.rope_tables(grid)
+    dit.block(0, bufs, mods, gates, gcos, gsin)
+    torch.cuda.synchronize()
+    e = rel_l2(bufs["h"], ref[0])
+    fmt_dev, fmt_ref = rel_l2(bufs["h"], ref_bf16[0]), rel_l2(ref, ref_bf16)
+    print(f"mx block rel L2 vs the MX oracle {e:.3e}; format error device {fmt_dev:.3e}, "
+          f"oracle {fmt_ref:.3e}", flush=True)
+    assert e < 4e-2
+    assert abs(fmt_dev - fmt_ref) <= 0.1 * fmt_ref + 1e-2
+
+
+def test_wan_step_from_mxfp8_directory_equals_quantize_at_load(gpu, tmp_path):
+    """A Wan checkpoint under diffusers' names (ffn.net.0.proj / ffn.net.2), quantized with the
+    reference's Wan targets: the step built from the directory equals the step that quantizes
+    the same weights at load."""
+    from safetensors.torch import save_file
+
+    from difflet_amd.dit.wan import checkpoint_key, wan_param_shapes
+    from difflet_amd.quant import checkpoint as qc
+    from difflet_amd.quant.spec import WAN_TARGETS, RocmQuantSpec
+
+    cfg = WanConfig(hidden=512, heads=4, ffn=1536, n_blocks=2, text_dim=256)
+    g = torch.Generator().manual_seed(9)
+    src = {n: (torch.randn(shp, generator=g) * 0.02).to(torch.bfloat16)
+           for n, shp in sorted(wan_param_shapes(cfg).items())}
+    d = tmp_path / "wan" / "transformer"
+    d.mkdir(parents=True)
+    save_file({checkpoint_key(n): t for n, t in src.items()},
+              str(d / "diffusion_pytorch_model.safetensors"), metadata={"format": "pt"})
+    out = tmp_path / "mx"
+    manifest = qc.write_quantized_dir(d, out, RocmQuantSpec(targets=WAN_TARGETS), device=gpu)
+    assert manifest["tensors"]["quantized"] == 2 * 5
+    print("Wan toy step: mxfp8 directory vs quantize at load", flush=True)
+    dense = WanDiT(cfg, lambda n: src[n], device=gpu, kind="mx")
+    loaded = WanDiT.from_quantized_dir(cfg, out, device=gpu)
+    assert loaded.kind == "mx"
+    g = torch.Generator().manual_seed(10)
+    lat = torch.randn(1, 16, 2, 8, 8, generator=g).to(gpu)
+    txt = torch.randn(1, 32, 256, generator=g).to(gpu)
+    t = torch.tensor([700.0], device=gpu)
+    y0 = dense(lat, t, txt)
+    y1 = loaded(lat, t, txt)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y0.float()).all()
+    assert torch.equal(y0, y1)
