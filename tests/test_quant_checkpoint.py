@@ -163,6 +163,10 @@ def test_check_quantized_dir(toy, tmp_path):
     shard.write_bytes(shard.read_bytes() + b"\0")
     with pytest.raises(ValueError, match="another checkpoint"):
         qc.check_quantized_dir(good, other, spec)
+    tp2 = tmp_path / "tp2"
+    _fake_quantized(toy, tp2, dict(GOLDEN["specs"]["flux_mx"]["spec"], tp_degree=2))
+    with pytest.raises(ValueError, match="another quantization spec"):
+        qc.check_quantized_dir(tp2, toy, spec)
     with pytest.raises(ValueError, match="write it first"):
         qc.ensure_quantized_dir(tmp_path / "cache", toy, spec, create=False)
 
