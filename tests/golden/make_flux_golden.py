@@ -23,10 +23,8 @@ from pathlib import Path
 import torch
 
 HERE = Path(__file__).resolve().parent
-sys.path.insert(0, str(HERE.parent.parent))
-sys.path.insert(0, "/root/reference")
-os.environ["DIFFLET_BACKEND"] = "cpu"
-os.environ.setdefault("NEURON_PLATFORM_TARGET_OVERRIDE", "trn2")
+if str(HERE.parent.parent) not in sys.path:
+    sys.path.insert(0, str(HERE.parent.parent))
 
 from oracle import flux as oflux  # noqa: E402
 from oracle import ops  # noqa: E402
@@ -68,6 +66,10 @@ def inputs() -> dict:
 
 
 def main() -> None:
+    # only a direct run of this script touches the reference (the tests import the helpers above)
+    sys.path.insert(0, "/root/reference")
+    os.environ["DIFFLET_BACKEND"] = "cpu"
+    os.environ.setdefault("NEURON_PLATFORM_TARGET_OVERRIDE", "trn2")
     import difflet.layers.normalization as norm_mod
     import difflet.models.flux.modeling_flux as mf
     from difflet.models.flux.dit_config import FluxDiTConfig

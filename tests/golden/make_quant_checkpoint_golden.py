@@ -24,8 +24,8 @@ import numpy as np
 import torch
 
 HERE = Path(__file__).resolve().parent
-sys.path.insert(0, str(HERE.parent.parent))
-sys.path.insert(0, "/root/reference")
+if str(HERE.parent.parent) not in sys.path:
+    sys.path.insert(0, str(HERE.parent.parent))
 
 from tests.golden.quant_toy import tensor_digest, write_toy_flux  # noqa: E402
 
@@ -46,6 +46,8 @@ def awkward_rows(k: int) -> np.ndarray:
 
 
 def main() -> None:
+    # only a direct run of this script touches the reference (the tests import the helpers above)
+    sys.path.insert(0, "/root/reference")
     from safetensors import safe_open
 
     from difflet.backends._torch_megatron.checkpoint import build_weight_map
