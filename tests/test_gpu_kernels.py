@@ -663,3 +663,28 @@ def test_gelu_gate_residual_gemv_timestep(gpu):
     out = kernels.timestep_embedding(t.to(gpu), 256, flip_sin_to_cos=True,
                                      downscale_freq_shift=0.0)
     assert (out.cpu() - ref).abs().max().item() < 2e-4
+
+
+def test_attention_matches_the_reference_cpu_op_vectors(gpu):
+    """The HIP kernel on the bf16 inputs the reference CPU attention op was run on
+    (tests/golden/attention_reference.json): every contract form within bf16 rounding of the
+    reference's own bf16 output (it rounds scores and probabilities to bf16; the kernel keeps
+    them in fp32)."""
+    import json
+    from pathlib import Path
+
+    from tests.golden.make_attention_golden import cases, decode
+
+    g = json.loads((Path(__file__).parent / "golden" / "attention_reference.json").read_text())
+    for name, ((q, k, v), kw) in cases(torch.bfloat16).items():
+        print(f"attention vs reference vectors: {name}", flush=True)
+        kw = {key: (val.to(gpu) if torch.is_tensor(val) else val) for key, val in kw.items()}
+        if "scale" not in kw:
+            kw["scale"] = 1.0  # the contract's scale=None
+        out = kernels.attention(q.to(gpu), k.to(gpu), v.to(gpu), **kw)
+        torch.cuda.synchronize()
+        want = decode(g[f"{name}.bfloat16"])
+        assert tuple(out.shape) == tuple(want.shape), name
+        e = rel_l2(out, want)
+        print(f"  rel L2 {e:.3e}", flush=True)
+        assert e < 2e-2, name

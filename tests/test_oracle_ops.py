@@ -124,3 +124,23 @@ def test_flux_rope_tables_closed_form():
             ang = ids[row, axis].item() * 10000.0 ** (-i / d)
             assert abs(cos[row, off + i].item() - math.cos(ang)) < 1e-6
             assert abs(sin[row, off + i + 1].item() - math.sin(ang)) < 1e-6
+
+
+def test_attention_equals_the_reference_cpu_op_on_every_form():
+    """The reference CPU backend's attention op ran on the same seeded inputs
+    (tests/golden/make_attention_golden.py): plain, scale None, causal, bool mask with a fully
+    masked row, additive mask, per-query bounds on the (B*H, S, D) layout, in fp32 and bf16. The
+    oracle matched it to the last bit when the fixture was made."""
+    import json
+    from pathlib import Path
+
+    from tests.golden.make_attention_golden import cases, decode
+
+    g = json.loads((Path(__file__).parent / "golden" / "attention_reference.json").read_text())
+    for dtype, tol in ((torch.float32, 1e-6), (torch.bfloat16, 1e-3)):
+        for name, ((q, k, v), kw) in cases(dtype).items():
+            want = decode(g[f"{name}.{str(dtype).removeprefix('torch.')}"])
+            got = ops.attention(q, k, v, **kw)
+            assert got.dtype == dtype and tuple(got.shape) == tuple(want.shape), name
+            e = ((got.float() - want).norm() / want.norm()).item()
+            assert e < tol, f"{name} {dtype}: rel L2 {e:.3e}"
