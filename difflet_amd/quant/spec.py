@@ -185,3 +185,36 @@ QWEN_IMAGE_TARGETS: tuple[str, ...] = (
     rf"{_BLOCK}\.(img_mlp|txt_mlp)\.net\.0\.proj",
     rf"{_BLOCK}\.(img_mlp|txt_mlp)\.net\.2",
 )
+
+#: difflet/quant/targets.py:138-141 (QWEN_IMAGE_ROW_PARALLEL)
+QWEN_IMAGE_ROW_PARALLEL: tuple[str, ...] = (
+    rf"{_BLOCK}\.attn\.(to_out\.0|to_add_out)",
+    rf"{_BLOCK}\.(img_mlp|txt_mlp)\.net\.2",
+)
+
+#: difflet/quant/targets.py:278-281 (WAN_ROW_PARALLEL)
+WAN_ROW_PARALLEL: tuple[str, ...] = (
+    r"blocks\.\d+\.(attn1|attn2)\.to_out\.0",
+    r"blocks\.\d+\.ffn\.net\.2",
+)
+
+#: difflet/quant/targets.py:376-397: the MXFP8 recipe of each model family this backend runs
+TARGETS_BY_MODEL = {"flux": FLUX_MX_TARGETS, "qwen_image": QWEN_IMAGE_TARGETS, "wan": WAN_TARGETS}
+ROW_PARALLEL_BY_MODEL = {"flux": FLUX_ROW_PARALLEL, "qwen_image": QWEN_IMAGE_ROW_PARALLEL,
+                         "wan": WAN_ROW_PARALLEL}
+SPLITS_BY_MODEL = {"flux": SINGLE_BLOCK_SPLIT_LINEARS}
+
+
+def default_spec(model: str, **overrides) -> RocmQuantSpec:
+    """difflet/quant/targets.py:424-440: the model's MXFP8 recipe (targets, row-parallel and split
+    linears as the reference names them, so the quantized directory's digest is the reference's);
+    ``targets=``, ``compute=`` and ``format=`` override. A per-channel fp8 spec keeps the fused
+    linears (no splits), since one scale per output channel spans the whole K."""
+    if model not in TARGETS_BY_MODEL:
+        raise ValueError(f"no fp8 target layers are defined for {model!r}; models with fp8 "
+                         f"support: {sorted(TARGETS_BY_MODEL)}")
+    overrides.setdefault("row_parallel", ROW_PARALLEL_BY_MODEL.get(model, ()))
+    overrides.setdefault("targets", TARGETS_BY_MODEL[model])
+    if overrides.get("format", "mxfp8") == "mxfp8":
+        overrides.setdefault("split_linears", SPLITS_BY_MODEL.get(model, ()))
+    return RocmQuantSpec(**overrides)

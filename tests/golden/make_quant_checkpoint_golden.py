@@ -86,6 +86,7 @@ def main() -> None:
                 "copied_files": sorted(p.name for p in qdir.iterdir()
                                        if not p.name.endswith((".safetensors", ".json"))),
             }
+    out["default_specs"] = {m: default_spec(m).to_dict() for m in ("flux", "qwen_image", "wan")}
     for k in AWKWARD_K:
         q, s = mx.quantize_mx(torch.from_numpy(awkward_rows(k)))
         out["mx_awkward_k"][str(k)] = {"codes": tensor_digest(q), "scales": tensor_digest(s)}

@@ -207,3 +207,19 @@ def test_golden_tensor_digest_is_stable():
     t = torch.tensor([1.0, -2.0], dtype=torch.bfloat16)
     assert tensor_digest(t) == ["bfloat16", [2], hashlib.sha256(
         np.array([0x3F80, 0xC000], dtype=np.uint16).tobytes()).hexdigest()]
+
+
+@pytest.mark.parametrize("model", ["flux", "qwen_image", "wan"])
+def test_default_specs_are_the_reference_recipes(model):
+    """difflet/quant/targets.py default_spec(model), as the reference wrote it: same targets,
+    row-parallel and split patterns, so a directory written by `difflet compile --quant` for
+    that model has the digest ours computes."""
+    from difflet_amd.quant.spec import default_spec
+
+    want = {k: v for k, v in GOLDEN["default_specs"][model].items() if k != "compute"}
+    spec = default_spec(model)
+    assert {k: v for k, v in spec.to_dict().items() if k != "compute"} == want
+    rw = default_spec(model, format="fp8_rowwise")
+    assert rw.split_linears == () and rw.targets == spec.targets
+    with pytest.raises(ValueError, match="no fp8 target layers"):
+        default_spec("ltx_2")
