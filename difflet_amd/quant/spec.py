@@ -205,16 +205,34 @@ ROW_PARALLEL_BY_MODEL = {"flux": FLUX_ROW_PARALLEL, "qwen_image": QWEN_IMAGE_ROW
 SPLITS_BY_MODEL = {"flux": SINGLE_BLOCK_SPLIT_LINEARS}
 
 
+def _onto_fused(patterns: tuple[str, ...], splits: tuple[str, ...]) -> tuple[str, ...]:
+    """``patterns`` with each name of a split linear's stored halves (``<split>_(attn|mlp)``)
+    turned back into the fused linear's name ``<split>``, duplicates dropped."""
+    halves = {rf"{sp}_(attn|mlp)": sp for sp in splits}
+    out: list[str] = []
+    for pat in patterns:
+        pat = halves.get(pat, pat)
+        if pat not in out:
+            out.append(pat)
+    return tuple(out)
+
+
 def default_spec(model: str, **overrides) -> RocmQuantSpec:
     """difflet/quant/targets.py:424-440: the model's MXFP8 recipe (targets, row-parallel and split
     linears as the reference names them, so the quantized directory's digest is the reference's);
     ``targets=``, ``compute=`` and ``format=`` override. A per-channel fp8 spec keeps the fused
-    linears (no splits), since one scale per output channel spans the whole K."""
+    linears (no splits), since one scale per output channel spans the whole K: patterns that
+    name a split linear's halves name the fused linear instead."""
     if model not in TARGETS_BY_MODEL:
         raise ValueError(f"no fp8 target layers are defined for {model!r}; models with fp8 "
                          f"support: {sorted(TARGETS_BY_MODEL)}")
-    overrides.setdefault("row_parallel", ROW_PARALLEL_BY_MODEL.get(model, ()))
-    overrides.setdefault("targets", TARGETS_BY_MODEL[model])
+    splits = SPLITS_BY_MODEL.get(model, ())
+    row_parallel = ROW_PARALLEL_BY_MODEL.get(model, ())
+    targets = TARGETS_BY_MODEL[model]
     if overrides.get("format", "mxfp8") == "mxfp8":
-        overrides.setdefault("split_linears", SPLITS_BY_MODEL.get(model, ()))
+        overrides.setdefault("split_linears", splits)
+    else:
+        row_parallel, targets = _onto_fused(row_parallel, splits), _onto_fused(targets, splits)
+    overrides.setdefault("row_parallel", row_parallel)
+    overrides.setdefault("targets", targets)
     return RocmQuantSpec(**overrides)

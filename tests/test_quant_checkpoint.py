@@ -220,6 +220,26 @@ def test_default_specs_are_the_reference_recipes(model):
     spec = default_spec(model)
     assert {k: v for k, v in spec.to_dict().items() if k != "compute"} == want
     rw = default_spec(model, format="fp8_rowwise")
-    assert rw.split_linears == () and rw.targets == spec.targets
+    assert rw.split_linears == ()
+    # the per-channel spec names the fused proj_out where the MXFP8 one names its halves
+    fused = lambda pats: tuple(dict.fromkeys(p.replace("proj_out_(attn|mlp)", "proj_out")  # noqa: E731
+                                             for p in pats))
+    assert rw.targets == fused(spec.targets) and rw.row_parallel == fused(spec.row_parallel)
     with pytest.raises(ValueError, match="no fp8 target layers"):
         default_spec("ltx_2")
+
+
+@pytest.mark.parametrize("fmt", ["mxfp8", "fp8_rowwise"])
+def test_default_flux_spec_is_accepted_by_the_writer(toy, fmt):
+    """Both formats' default FLUX spec pass the writer's checks on a FLUX directory: every
+    target and row-parallel pattern names a weight the written directory holds."""
+    from difflet_amd.quant.spec import default_spec
+
+    spec = default_spec("flux", format=fmt)
+    qc._validate(Path(toy), spec)
+    shapes = qc._weight_shapes(Path(toy))
+    names = qc._quantizable_prefixes(shapes, spec)
+    single = [n for n in names if "single_transformer_blocks.0.proj_out" in n]
+    want = ["proj_out_attn", "proj_out_mlp"] if fmt == "mxfp8" else ["proj_out"]
+    assert sorted(n.rsplit(".", 1)[1] for n in single) == want
+    assert all(spec.matches(n) for n in single)
