@@ -56,7 +56,7 @@ class GemmQk(ctypes.Structure):
     _fields_ = [
         ("q_col", _i64), ("k_col", _i64), ("cols", _i64),
         ("cos", _vp), ("sin", _vp),
-        ("law", _i32), ("eps", _f32),
+        ("law", _i32), ("eps", _f32), ("rows", _i64),
     ]
 
 

@@ -855,6 +855,10 @@ static int gemm_launch(const char* name, int nproblems, const difflet_gemm_probl
                     ((!q_on || qk->q_col + qk->cols <= act_col_start) &&
                      (!k_on || qk->k_col + qk->cols <= act_col_start)),
                 DIFFLET_EINVAL, "%s: q/k columns must lie below act_col_start", name);
+    for (int i = 0; i < nproblems; ++i)
+      DLT_REQUIRE(problems[i].rope_row0 + problems[i].m <= qk->rows, DIFFLET_EINVAL,
+                  "%s: problem %d reads RoPE rows up to %lld of a %lld-row table", name, i,
+                  (long long)(problems[i].rope_row0 + problems[i].m), (long long)qk->rows);
     DLT_REQUIRE(qk->cos && qk->sin && ((uintptr_t)qk->cos & 15) == 0 &&
                     ((uintptr_t)qk->sin & 15) == 0 && (qk->law == 0 || qk->law == 1),
                 DIFFLET_EINVAL, "%s: RoPE tables (16-byte aligned) and law 0 or 1 required",

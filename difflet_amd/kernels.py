@@ -218,6 +218,75 @@ def gemm_workspace(dev: torch.device) -> torch.Tensor:
     return ws
 
 
+def _check_epilogue_operands(p: Problem, i: int, kind: str, n: int, k: int,
+                             epilogue: int) -> None:
+    """Every vector the GEMM kernel reads beside A and W, checked against what it reads: the
+    kernel indexes bias[n], gate[row, n], residual[m, n], a_scale[m] and w_scale[n] (fp8), and
+    the E8M0 rows a_scale[m, :k/32] / w_scale[n, :k/32] (MXFP8) without bounds checks of its
+    own, so a short or mistyped tensor is refused here."""
+    m = p.a.shape[0]
+
+    def vec(t, what, dtype, length):
+        if t.dtype != dtype:
+            raise TypeError(f"problem {i}: {what} must be {dtype}, got {t.dtype}")
+        if t.dim() != 1 or t.stride(0) != 1 or t.shape[0] < length:
+            raise ValueError(f"problem {i}: {what} must be a contiguous vector of at least "
+                             f"{length} values, got {tuple(t.shape)}")
+
+    if p.bias is not None:
+        vec(p.bias, "bias", torch.bfloat16, n)
+    if epilogue == _lib.EPI_GATE_RESIDUAL:
+        if p.gate is None or p.residual is None:
+            raise ValueError(f"problem {i}: the gate/residual epilogue needs gate and residual")
+        rpb = p.rows_per_batch or m
+        batches = max(1, -(-m // rpb))
+        g = p.gate if p.gate.dim() == 2 else p.gate.reshape(1, -1)
+        if g.dtype != torch.bfloat16:
+            raise TypeError(f"problem {i}: gate must be bf16, got {g.dtype}")
+        if g.dim() != 2 or g.stride(-1) != 1 or g.shape[1] < n or g.shape[0] < batches:
+            raise ValueError(f"problem {i}: gate must hold {batches} row(s) of at least {n} "
+                             f"contiguous values, got {tuple(p.gate.shape)}")
+        r = p.residual
+        if r.dtype != torch.bfloat16:
+            raise TypeError(f"problem {i}: residual must be bf16, got {r.dtype}")
+        if r.dim() != 2 or r.stride(1) != 1 or r.shape[0] < m or r.shape[1] < n:
+            raise ValueError(f"problem {i}: residual must be [>= {m}, >= {n}] with contiguous "
+                             f"rows, got {tuple(r.shape)}")
+    if kind == "fp8":
+        if p.a_scale is None or p.w_scale is None:
+            raise ValueError(f"problem {i}: fp8 GEMMs need a_scale and w_scale")
+        vec(p.a_scale, "a_scale", torch.float32, m)
+        vec(p.w_scale, "w_scale", torch.float32, n)
+    elif kind == "mx":
+        if p.a_scale is None or p.w_scale is None:
+            raise ValueError(f"problem {i}: MXFP8 GEMMs need a_scale and w_scale")
+        for t, what, rows in ((p.a_scale, "a_scale", m), (p.w_scale, "w_scale", n)):
+            if t.dtype != torch.uint8:
+                raise TypeError(f"problem {i}: {what} must be uint8 E8M0, got {t.dtype}")
+            if t.dim() != 2 or tuple(t.shape) != (rows, k // 32) or not t.is_contiguous():
+                raise ValueError(f"problem {i}: {what} must be contiguous [{rows}, {k // 32}], "
+                                 f"got {tuple(t.shape)}")
+
+
+def _check_qk(qk: QkNormRope, problems: Sequence[Problem]) -> None:
+    """The fused q/k epilogue reads norm_q / norm_k [128] and the RoPE tables at rows
+    rope_row0 .. rope_row0 + m - 1 of every problem."""
+    for t in (qk.cos, qk.sin):
+        if t.dtype != torch.float32 or t.dim() != 2 or t.shape[1] != 128 or not t.is_contiguous():
+            raise ValueError("RoPE tables are contiguous fp32 [rows, 128]")
+    if qk.cos.shape != qk.sin.shape:
+        raise ValueError("RoPE cos and sin tables differ in shape")
+    rows = qk.cos.shape[0]
+    for i, p in enumerate(problems):
+        for t in (p.norm_q, p.norm_k):
+            if t is not None and (t.dtype != torch.bfloat16 or t.numel() != 128
+                                  or not t.is_contiguous()):
+                raise ValueError("q/k norm weights are contiguous [128] bf16")
+        lo, hi = int(p.rope_row0), int(p.rope_row0) + p.a.shape[0]
+        if lo < 0 or hi > rows:
+            raise ValueError(f"problem {i}: RoPE rows [{lo}, {hi}) exceed the {rows}-row tables")
+
+
 def gemm_grouped(problems: Sequence[Problem], *, kind: str = "bf16",
                  epilogue: int = _lib.EPI_NONE, act_col_start: int = 0,
                  workspace: torch.Tensor | None | str = None,
@@ -230,7 +299,6 @@ def gemm_grouped(problems: Sequence[Problem], *, kind: str = "bf16",
     K slices of A and W through their XCD's L2."""
     if not problems:
         return
-    dev = _on_gpu(*[p.a for p in problems], *[p.w for p in problems])
     n, k = problems[0].w.shape[0], problems[0].w.shape[1]
     arr = (GemmProblem * len(problems))()
     for i, p in enumerate(problems):
@@ -246,6 +314,12 @@ def gemm_grouped(problems: Sequence[Problem], *, kind: str = "bf16",
             raise TypeError("fp8 GEMMs take e4m3 codes (uint8 or float8_e4m3fn)")
         if p.c.dtype != torch.bfloat16:
             raise TypeError("GEMM output is bf16")
+        _check_epilogue_operands(p, i, kind, n, k, epilogue)
+    if qk is not None:
+        _check_qk(qk, problems)
+    dev = _on_gpu(*[t for p in problems for t in (p.a, p.w, p.c, p.bias, p.gate, p.residual,
+                                                  p.a_scale, p.w_scale)])
+    for i, p in enumerate(problems):
         q = arr[i]
         q.a, q.lda = p.a.data_ptr(), p.a.stride(0)
         q.w, q.ldw = p.w.data_ptr(), p.w.stride(0)
@@ -261,9 +335,6 @@ def gemm_grouped(problems: Sequence[Problem], *, kind: str = "bf16",
         q.m = p.a.shape[0]
         q.rows_per_batch = p.rows_per_batch or p.a.shape[0]
         if qk is not None:
-            for t in (p.norm_q, p.norm_k):
-                if t is not None and (t.dtype != torch.bfloat16 or t.numel() != 128):
-                    raise ValueError("q/k norm weights are [128] bf16")
             q.norm_q = p.norm_q.data_ptr() if p.norm_q is not None else None
             q.norm_k = p.norm_k.data_ptr() if p.norm_k is not None else None
             q.rope_row0 = int(p.rope_row0)
@@ -275,13 +346,11 @@ def gemm_grouped(problems: Sequence[Problem], *, kind: str = "bf16",
                                                            workspace.numel())
     qk_arg = None
     if qk is not None:
-        for t in (qk.cos, qk.sin):
-            if t.dtype != torch.float32 or t.dim() != 2 or t.shape[1] != 128 or not t.is_contiguous():
-                raise ValueError("RoPE tables are contiguous fp32 [rows, 128]")
+        rows = qk.cos.shape[0]
         qk_arg = ctypes.byref(_lib.GemmQk(-1 if qk.q_col is None else qk.q_col,
                                           -1 if qk.k_col is None else qk.k_col, qk.cols,
                                           qk.cos.data_ptr(), qk.sin.data_ptr(), int(qk.law),
-                                          float(qk.eps)))
+                                          float(qk.eps), rows))
     fn = getattr(lib(), _GEMM_FN[kind])
     check(fn(len(problems), arr, n, k, int(epilogue), int(act_col_start), ws_ptr, ws_bytes,
              qk_arg, _stream(dev)), f"gemm_{kind}")

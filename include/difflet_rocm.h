@@ -134,6 +134,7 @@ typedef struct difflet_gemm_qk {
   const float* sin;
   int law;
   float eps;
+  int64_t rows;  /* rows of cos / sin: every problem needs rope_row0 + m <= rows */
 } difflet_gemm_qk;
 
 /* Workspace of the GEMMs below (all three take the same one). With a workspace, a launch whose
