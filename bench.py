@@ -352,8 +352,12 @@ def summarize(wl, kind, r):
     }
 
 
-def cpu_baseline(wl, log):
-    """The oracle's fp32 CPU path on one double + one single block at the real FLUX shape."""
+def cpu_baseline(wl, log, runs: int = 3):
+    """The oracle's fp32 CPU path on one double and one single block at the real FLUX shape:
+    one full-shape warm-up of each, then the median of `runs` timed runs of each, extrapolated
+    to the 19 + 38 blocks of the step."""
+    import statistics
+
     import torch
 
     from oracle import flux as oflux
@@ -371,21 +375,27 @@ def cpu_baseline(wl, log):
     cos, sin = ops.flux_pos_embed(ops.flux_ids(st, h, w))
     dw = oflux.double_block_weights(shape, SEED, 0)
     sw = oflux.single_block_weights(shape, SEED, 0)
-    # warm the thread pool and allocator on a small slice
-    oflux.double_block(dw, hidden[:, :64], context[:, :64], temb, cos[: 128], sin[: 128], shape)
-    t0 = time.perf_counter()
-    oflux.double_block(dw, hidden, context, temb, cos, sin, shape)
-    t_d = time.perf_counter() - t0
     x = torch.cat([context, hidden], dim=1)
-    t0 = time.perf_counter()
-    oflux.single_block(sw, x, temb, cos, sin, shape)
-    t_s = time.perf_counter() - t0
-    step_ms = (shape.n_double * t_d + shape.n_single * t_s) * 1e3
-    log(f"[cpu] double block {t_d:.2f} s, single block {t_s:.2f} s on {threads} threads")
+    blocks = {"double": lambda: oflux.double_block(dw, hidden, context, temb, cos, sin, shape),
+              "single": lambda: oflux.single_block(sw, x, temb, cos, sin, shape)}
+    med, spread = {}, {}
+    for name, fn in blocks.items():
+        fn()  # warm-up at the full shape: thread pool, allocator, first-touch of the buffers
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        med[name], spread[name] = statistics.median(times), (min(times), max(times))
+        log(f"[cpu] {name} block: median {med[name]:.2f} s of {runs} "
+            f"({min(times):.2f}-{max(times):.2f} s) on {threads} threads")
+    step_ms = (shape.n_double * med["double"] + shape.n_single * med["single"]) * 1e3
     return {"value": round(step_ms, 1), "unit": "ms/step (extrapolated)", "cores": threads,
             "kind": "port",
-            "sample": (f"fp32 oracle, 1 double ({t_d:.2f} s) + 1 single ({t_s:.2f} s) block at "
-                       f"{st}+{si} tokens, extrapolated x{shape.n_double} + x{shape.n_single}")}
+            "sample": (f"fp32 oracle on {threads} threads, one double and one single block at "
+                       f"{st}+{si} tokens: one full-shape warm-up each, then the median of "
+                       f"{runs} runs (double {med['double']:.2f} s, single {med['single']:.2f} s), "
+                       f"extrapolated x{shape.n_double} + x{shape.n_single}")}
 
 
 # FLUX block linears by shape [N, K] -> count over 19 double + 38 single blocks

@@ -124,11 +124,27 @@ class QwenImageDiT(JointDiT):
                                         dtype=torch.bfloat16)
         return kernels.gemv(kernels.gemv(tp, self.t_w1, self.t_b1), self.t_w2, self.t_b2, act=1)
 
-    def forward(self, latents, text, timestep, img_hw):
+    def forward(self, latents, text, timestep, img_hw, text_valid_len=None):
         """latents [1, h*w, in_ch] (packed 2x2 patches), text [1, S_txt, txt_dim], timestep t/1000
-        [1] -> [1, h*w, out_ch] bf16."""
+        [1] -> [1, h*w, out_ch] bf16.
+
+        ``text_valid_len`` (int, or an int tensor of one element) marks a right-padded prompt:
+        only its first rows are keys. The reference masks the padding keys in every block
+        (keys [image | text] bounded at S_img + valid, modeling_qwen_image.py:493-552,
+        738-739); for one request the padded rows are then keys to nobody and their own
+        outputs are dropped, so the step runs the prompt cut to its valid rows, which gives
+        the same image output (the reference's trim_text_padding, :555-576) on a shorter
+        joint sequence."""
         if latents.shape[0] != 1:
             raise NotImplementedError("the fused Qwen-Image step runs batch 1 (one request per call)")
+        if text_valid_len is not None:
+            valid = int(text_valid_len.reshape(-1)[0]) if torch.is_tensor(text_valid_len) \
+                else int(text_valid_len)
+            if torch.is_tensor(text_valid_len) and text_valid_len.numel() != 1:
+                raise NotImplementedError("the fused Qwen-Image step takes one text_valid_len")
+            if not 0 <= valid <= text.shape[1]:
+                raise ValueError(f"text_valid_len {valid} outside [0, {text.shape[1]}]")
+            text = text[:, :valid]
         st, si = text.shape[1], latents.shape[1]
         bufs = self._buffers(st, si)
         cos, sin = self.rope_tables(st, img_hw)

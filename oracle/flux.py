@@ -143,25 +143,19 @@ def qlinear(quant, act_dtype=None):
     quantizes the bf16 tensor."""
     if quant is None:
         return ops.linear
-    import numpy as np
-
+    if quant not in ("fp8", "mx"):
+        raise ValueError(quant)
     from oracle import fp8 as ofp8
     from oracle import mx as omx
 
     def lin(x, w, b=None):
-        shp = x.shape
         if act_dtype is not None:
             x = x.to(act_dtype).float()
-        x2 = x.reshape(-1, shp[-1]).numpy()
+        # the torch twins of the numpy laws (pinned bit-exact against them), threaded
         if quant == "fp8":
-            wq, ws = ofp8.quantize_rowwise(w.numpy())
-            y = ofp8.fp8_linear(x2, wq, ws, None if b is None else b.numpy())
-        elif quant == "mx":
-            wq, ws = omx.quantize_mx(w.numpy())
-            y = omx.mx_linear(x2, wq, ws, None if b is None else b.numpy())
-        else:
-            raise ValueError(quant)
-        return torch.from_numpy(np.ascontiguousarray(y)).reshape(*shp[:-1], w.shape[0])
+            return ofp8.fp8_linear_torch(x, w, b)
+        y = omx.fake_quantize_mx_torch(x) @ omx.fake_quantize_mx_torch(w).T
+        return y if b is None else y + b
 
     return lin
 
@@ -176,20 +170,28 @@ def _rope(x, cos, sin):
 
 
 def double_block(w: dict, hidden, context, temb, cos, sin, shape: FluxShape,
-                 rms_law=ops.rms_norm_cpu_law, quant=None, act_dtype=None):
+                 rms_law=ops.rms_norm_cpu_law, quant=None, act_dtype=None, store=None,
+                 mods=None):
     """modeling_flux.py:796-867 with NeuronFluxAttention (:1190-1462). Returns (context, hidden).
-    `quant` ("fp8" / "mx") quantizes every block linear but the adaLN ones."""
+    `quant` ("fp8" / "mx") quantizes every block linear but the adaLN ones. `store` (a dtype)
+    rounds every activation the device keeps in memory to it (modulation vectors, LayerNorm
+    outputs, projections before and after q/k norm + RoPE, attention output, MLP hidden, the
+    residual stream); `mods` = (image [1, 6D], context [1, 6D]) replaces the computed
+    modulation vectors."""
     L = ops.linear
     Q = qlinear(quant, act_dtype)
-    emb = L(torch.nn.functional.silu(temb), w["norm1.linear.weight"], w["norm1.linear.bias"])
+    R = ops.rounder(store)
+    silu_t = torch.nn.functional.silu(temb)
+    if mods is None:
+        mods = (L(silu_t, w["norm1.linear.weight"], w["norm1.linear.bias"]),
+                L(silu_t, w["norm1_context.linear.weight"], w["norm1_context.linear.bias"]))
+    emb, cemb = R(mods[0]), R(mods[1])
     sh_msa, sc_msa, g_msa, sh_mlp, sc_mlp, g_mlp = emb.chunk(6, dim=1)
-    cemb = L(torch.nn.functional.silu(temb), w["norm1_context.linear.weight"],
-             w["norm1_context.linear.bias"])
     c_sh_msa, c_sc_msa, c_g_msa, c_sh_mlp, c_sc_mlp, c_g_mlp = cemb.chunk(6, dim=1)
-    nx = ops.ada_modulate(hidden, sh_msa, sc_msa)
-    nc = ops.ada_modulate(context, c_sh_msa, c_sc_msa)
+    nx = R(ops.ada_modulate(hidden, sh_msa, sc_msa))
+    nc = R(ops.ada_modulate(context, c_sh_msa, c_sc_msa))
 
-    a = lambda n, x: Q(x, w[f"attn.{n}.weight"], w[f"attn.{n}.bias"])  # noqa: E731
+    a = lambda n, x: R(Q(x, w[f"attn.{n}.weight"], w[f"attn.{n}.bias"]))  # noqa: E731
     q, k, v = _heads(a("to_q", nx), shape), _heads(a("to_k", nx), shape), _heads(a("to_v", nx), shape)
     q = rms_law(q, w["attn.norm_q.weight"], 1e-6)
     k = rms_law(k, w["attn.norm_k.weight"], 1e-6)
@@ -200,25 +202,25 @@ def double_block(w: dict, hidden, context, temb, cos, sin, shape: FluxShape,
     q = torch.cat([cq, q], dim=2)
     k = torch.cat([ck, k], dim=2)
     v = torch.cat([cv, v], dim=2)
-    q, k = _rope(q, cos, sin), _rope(k, cos, sin)
-    o = _attend(q, k, v, shape)
+    q, k = R(_rope(q, cos, sin)), R(_rope(k, cos, sin))
+    o = R(_attend(q, k, v, shape))
     st = context.shape[1]
     c_attn, x_attn = o[:, :st], o[:, st:]
-    x_attn = a("to_out.0", x_attn)
-    c_attn = a("to_add_out", c_attn)
+    x_attn = Q(x_attn, w["attn.to_out.0.weight"], w["attn.to_out.0.bias"])
+    c_attn = Q(c_attn, w["attn.to_add_out.weight"], w["attn.to_add_out.bias"])
 
-    hidden = hidden + g_msa[:, None] * x_attn
-    nx2 = ops.ada_modulate(hidden, sh_mlp, sc_mlp)
-    ff = Q(ops.gelu_tanh(Q(nx2, w["ff.net.0.proj.weight"], w["ff.net.0.proj.bias"])),
+    hidden = R(hidden + g_msa[:, None] * x_attn)
+    nx2 = R(ops.ada_modulate(hidden, sh_mlp, sc_mlp))
+    ff = Q(R(ops.gelu_tanh(Q(nx2, w["ff.net.0.proj.weight"], w["ff.net.0.proj.bias"]))),
            w["ff.net.2.weight"], w["ff.net.2.bias"])
-    hidden = hidden + g_mlp[:, None] * ff
+    hidden = R(hidden + g_mlp[:, None] * ff)
 
-    context = context + c_g_msa[:, None] * c_attn
-    nc2 = ops.ada_modulate(context, c_sh_mlp, c_sc_mlp)
-    cff = Q(ops.gelu_tanh(Q(nc2, w["ff_context.net.0.proj.weight"],
-                            w["ff_context.net.0.proj.bias"])),
+    context = R(context + c_g_msa[:, None] * c_attn)
+    nc2 = R(ops.ada_modulate(context, c_sh_mlp, c_sc_mlp))
+    cff = Q(R(ops.gelu_tanh(Q(nc2, w["ff_context.net.0.proj.weight"],
+                              w["ff_context.net.0.proj.bias"]))),
             w["ff_context.net.2.weight"], w["ff_context.net.2.bias"])
-    context = context + c_g_mlp[:, None] * cff
+    context = R(context + c_g_mlp[:, None] * cff)
     return context, hidden
 
 
@@ -232,30 +234,33 @@ def _attend(q, k, v, shape: FluxShape):
 
 
 def single_block(w: dict, hidden, temb, cos, sin, shape: FluxShape, rms_law=ops.rms_norm_cpu_law,
-                 quant=None, act_dtype=None):
+                 quant=None, act_dtype=None, store=None, mods=None):
     """modeling_flux.py:696-736: proj_out over [attn | mlp] as two column halves + bias. Under
     `quant` the proj_out is quantized as the one [D, D + mlp] linear the device runs (the fp8
     per-channel scale spans both halves; for MXFP8 it equals quantizing the halves separately,
-    the attention half's K being a whole number of 512-wide swizzle tiles)."""
+    the attention half's K being a whole number of 512-wide swizzle tiles). `store` and `mods`
+    ([1, 3D]) as in double_block."""
     L = ops.linear
     Q = qlinear(quant, act_dtype)
+    R = ops.rounder(store)
     d = shape.hidden
-    emb = L(torch.nn.functional.silu(temb), w["norm.linear.weight"], w["norm.linear.bias"])
-    shift, scale, gate = emb.chunk(3, dim=1)
-    nh = ops.ada_modulate(hidden, shift, scale)
-    mlp = ops.gelu_tanh(Q(nh, w["proj_mlp.weight"], w["proj_mlp.bias"]))
-    a = lambda n: Q(nh, w[f"attn.{n}.weight"], w[f"attn.{n}.bias"])  # noqa: E731
+    if mods is None:
+        mods = L(torch.nn.functional.silu(temb), w["norm.linear.weight"], w["norm.linear.bias"])
+    shift, scale, gate = R(mods).chunk(3, dim=1)
+    nh = R(ops.ada_modulate(hidden, shift, scale))
+    mlp = R(ops.gelu_tanh(Q(nh, w["proj_mlp.weight"], w["proj_mlp.bias"])))
+    a = lambda n: R(Q(nh, w[f"attn.{n}.weight"], w[f"attn.{n}.bias"]))  # noqa: E731
     q, k, v = _heads(a("to_q"), shape), _heads(a("to_k"), shape), _heads(a("to_v"), shape)
     q = rms_law(q, w["attn.norm_q.weight"], 1e-6)
     k = rms_law(k, w["attn.norm_k.weight"], 1e-6)
-    q, k = _rope(q, cos, sin), _rope(k, cos, sin)
-    o = _attend(q, k, v, shape)
+    q, k = R(_rope(q, cos, sin)), R(_rope(k, cos, sin))
+    o = R(_attend(q, k, v, shape))
     wp = w["proj_out.weight"]
     if quant is None:
         out = L(o, wp[:, :d]) + L(mlp, wp[:, d:])
     else:
         out = Q(torch.cat([o, mlp], dim=-1), wp)
-    return hidden + gate[:, None] * (out + w["proj_out.bias"])
+    return R(hidden + gate[:, None] * (out + w["proj_out.bias"]))
 
 
 # ------------------------------------------------------------------------------------ model

@@ -50,3 +50,32 @@ def fp8_linear(x: np.ndarray, wq: np.ndarray, ws: np.ndarray, bias=None) -> np.n
     if bias is not None:
         y = y + np.asarray(bias, dtype=np.float32)
     return y.reshape(*x.shape[:-1], wq.shape[0]).astype(np.float32)
+
+
+def fake_quantize_rowwise_torch(x):
+    """quantize_rowwise then dequantize_rowwise in torch's threaded element-wise ops, the same
+    law step for step (e4m3 through torch's float8_e4m3fn cast, pinned equal to e4m3_encode).
+    Returns (dequantized codes [R, K] fp32 without the scale, scales [R]); pinned bit-exact
+    against the numpy functions (tests/test_oracle_fp8.py)."""
+    import torch
+
+    x = x.to(torch.float32)
+    amax = x.abs().amax(dim=-1)
+    a = torch.clamp_min(amax, float(TINY))
+    scale = a / float(E4M3_MAX)
+    inv = float(E4M3_MAX) / a
+    q = (x * inv[..., None]).clamp(-float(E4M3_MAX), float(E4M3_MAX)).to(torch.float8_e4m3fn)
+    return q.to(torch.float32), scale
+
+
+def fp8_linear_torch(x, w, bias=None):
+    """fp8_linear on torch fp32 operands, quantizing both rows-wise here: what the per-token x
+    per-channel fp8 GEMM computes for activations x [..., K] and weights w [N, K]."""
+    x2 = x.reshape(-1, x.shape[-1])
+    xq, xs = fake_quantize_rowwise_torch(x2)
+    wq, ws = fake_quantize_rowwise_torch(w)
+    y = (xq @ wq.T) * xs[:, None] * ws[None, :]
+    if bias is not None:
+        y = y + bias
+    return y.reshape(*x.shape[:-1], w.shape[0])
+

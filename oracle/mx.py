@@ -129,3 +129,36 @@ def mx_linear(x: np.ndarray, wq: np.ndarray, ws: np.ndarray, bias=None) -> np.nd
     if bias is not None:
         y = y + np.asarray(bias, dtype=np.float32)
     return y.reshape(*x.shape[:-1], wq.shape[0]).astype(np.float32)
+
+
+# ------------------------------------------------------------- torch twin for large blocks
+def _e8m0_values_torch(s):
+    """2^(s - 127) in fp32 for uint8 scales s (as int32), built from the bit pattern: exact,
+    including s = 0 (the subnormal 2^-127)."""
+    import torch
+
+    bits = torch.where(s > 0, s << 23, torch.full_like(s, 0x400000))
+    return bits.view(torch.float32)
+
+
+def fake_quantize_mx_torch(t):
+    """quantize_mx then dequantize_mx of a torch fp32 [..., K] tensor, in torch's threaded
+    element-wise ops: the same block law step for step (swizzle, exponent-field maxima,
+    IEEE fp32 divide, clamp, RNE e4m3 through torch's float8_e4m3fn cast, which is pinned equal
+    to e4m3_encode on every rounding boundary). Pinned bit-exact against the numpy functions
+    above (tests/test_oracle_mx.py); the block oracles use it for their large linears."""
+    import torch
+
+    t = t.to(torch.float32)
+    k = t.shape[-1]
+    perm = torch.from_numpy(swizzle_perm(k))
+    sw = t.index_select(-1, perm).reshape(*t.shape[:-1], k // BLOCK, BLOCK).contiguous()
+    e = (sw.view(torch.int32) >> 23) & 0xFF
+    s = (e.amax(dim=-1) - E4M3_MAX_EXP).clamp(0, 255)
+    value = _e8m0_values_torch(s.to(torch.int32))[..., None]
+    q = (sw / value).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+    deq = (q.to(torch.float32) * value).reshape(*t.shape[:-1], k)
+    out = torch.empty_like(deq)
+    out.index_copy_(-1, perm, deq)
+    return out
+

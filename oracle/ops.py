@@ -35,6 +35,15 @@ def attention(q, k, v, *, scale=None, causal=False, attention_mask=None, bound_m
     return torch.matmul(probs, v)
 
 
+def rounder(dtype=None):
+    """Identity, or a round trip through ``dtype`` (returned in fp32): the oracle blocks apply it
+    wherever a device that stores its activations in ``dtype`` rounds them, so a quantized
+    linear downstream sees the same inputs on both sides."""
+    if dtype is None:
+        return lambda x: x
+    return lambda x: x.to(dtype).float()
+
+
 def rms_norm_cpu_law(x, weight, eps):
     """difflet/backends/cpu/ops_impl/norm.py:19-22: fp32 variance, cast to x's dtype before
     +eps, normalise and apply the weight in x's dtype."""

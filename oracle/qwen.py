@@ -150,81 +150,119 @@ def _heads(x, shape: QwenShape):
     return x.view(b, s, shape.heads, shape.head_dim).transpose(1, 2)
 
 
+def _masked_joint_attention(q_img, k_img, v_img, q_txt, k_txt, v_txt, valid: int):
+    """modeling_qwen_image.py:493-552 at cp = 1: keys and queries ordered [image | text], every
+    query attends to the key prefix [0, S_img + valid) through the op's bounds (bound_min 0,
+    bound_max S_img + valid), heads folded into the batch; the output is put back in
+    [text | image] order. In [B, H, S, d]; out [B, H, S_txt + S_img, d]."""
+    q = torch.cat([q_img, q_txt], dim=2)
+    k = torch.cat([k_img, k_txt], dim=2)
+    v = torch.cat([v_img, v_txt], dim=2)
+    b, h, s_q, d = q.shape
+    n_img = q_img.shape[2]
+    bound_max = torch.full((b * h, s_q, 1), n_img + int(valid), dtype=torch.int32)
+    out = ops.attention(q.reshape(b * h, s_q, d), k.reshape(b * h, -1, d),
+                        v.reshape(b * h, -1, d), scale=1 / math.sqrt(d),
+                        bound_min=torch.zeros_like(bound_max), bound_max=bound_max)
+    out = out.reshape(b, h, s_q, d)
+    return torch.cat([out[:, :, n_img:], out[:, :, :n_img]], dim=2)
+
+
 def block(w: dict, hidden, context, temb, cos, sin, shape: QwenShape, quant=None,
-          act_dtype=None):
+          act_dtype=None, store=None, mods=None, text_valid_len=None):
     """One joint block; returns (context, hidden). `quant` = "mx" puts the MX targets through
     the MXFP8 law; `act_dtype` rounds their activations first (a bf16 device quantizes the bf16
-    tensor)."""
+    tensor). `store` (a dtype) rounds every activation the device keeps in memory to it;
+    `mods` = (image [1, 6D], text [1, 6D]) replaces the computed modulation vectors.
+    `text_valid_len` (an int) masks the text keys from that index on, the reference's masked
+    joint attention for a right-padded prompt (modeling_qwen_image.py:493-552)."""
     L = ops.linear
     Q = qlinear(quant, act_dtype)
+    R = ops.rounder(store)
     lin = lambda n, x: (Q if n in MX_TARGETS else L)(x, w[f"{n}.weight"], w[f"{n}.bias"])  # noqa: E731
     silu_t = torch.nn.functional.silu(temb)
-    img_mod = L(silu_t, w["img_mod.1.weight"], w["img_mod.1.bias"])
-    txt_mod = L(silu_t, w["txt_mod.1.weight"], w["txt_mod.1.bias"])
-    i_sh1, i_sc1, i_g1, i_sh2, i_sc2, i_g2 = img_mod.chunk(6, dim=1)
-    t_sh1, t_sc1, t_g1, t_sh2, t_sc2, t_g2 = txt_mod.chunk(6, dim=1)
+    if mods is None:
+        mods = (L(silu_t, w["img_mod.1.weight"], w["img_mod.1.bias"]),
+                L(silu_t, w["txt_mod.1.weight"], w["txt_mod.1.bias"]))
+    i_sh1, i_sc1, i_g1, i_sh2, i_sc2, i_g2 = R(mods[0]).chunk(6, dim=1)
+    t_sh1, t_sc1, t_g1, t_sh2, t_sc2, t_g2 = R(mods[1]).chunk(6, dim=1)
 
-    nx = ops.ada_modulate(hidden, i_sh1, i_sc1)
-    nc = ops.ada_modulate(context, t_sh1, t_sc1)
-    q, k, v = (_heads(lin(f"attn.{n}", nx), shape) for n in ("to_q", "to_k", "to_v"))
-    cq, ck, cv = (_heads(lin(f"attn.{n}", nc), shape)
+    nx = R(ops.ada_modulate(hidden, i_sh1, i_sc1))
+    nc = R(ops.ada_modulate(context, t_sh1, t_sc1))
+    q, k, v = (_heads(R(lin(f"attn.{n}", nx)), shape) for n in ("to_q", "to_k", "to_v"))
+    cq, ck, cv = (_heads(R(lin(f"attn.{n}", nc)), shape)
                   for n in ("add_q_proj", "add_k_proj", "add_v_proj"))
     q = ops.rms_norm_fp32(q, w["attn.norm_q.weight"], 1e-6)
     k = ops.rms_norm_fp32(k, w["attn.norm_k.weight"], 1e-6)
     cq = ops.rms_norm_fp32(cq, w["attn.norm_added_q.weight"], 1e-6)
     ck = ops.rms_norm_fp32(ck, w["attn.norm_added_k.weight"], 1e-6)
     st = context.shape[1]
-    rope = lambda x, c, s: ops.apply_rotary_emb_fp32(x, c[None, None], s[None, None])  # noqa: E731
-    q = torch.cat([rope(cq, cos[:st], sin[:st]), rope(q, cos[st:], sin[st:])], dim=2)
-    k = torch.cat([rope(ck, cos[:st], sin[:st]), rope(k, cos[st:], sin[st:])], dim=2)
-    v = torch.cat([cv, v], dim=2)
-    b, hh, s, d = q.shape
-    o = ops.attention(q.reshape(b * hh, s, d), k.reshape(b * hh, s, d), v.reshape(b * hh, s, d),
-                      scale=1 / math.sqrt(d))
-    o = o.reshape(b, hh, s, d).transpose(1, 2).reshape(b, s, hh * d)
+    rope = lambda x, c, s: R(ops.apply_rotary_emb_fp32(x, c[None, None], s[None, None]))  # noqa: E731
+    q_img, k_img = rope(q, cos[st:], sin[st:]), rope(k, cos[st:], sin[st:])
+    q_txt, k_txt = rope(cq, cos[:st], sin[:st]), rope(ck, cos[:st], sin[:st])
+    b, hh, _, d = q.shape
+    if text_valid_len is None:
+        qj, kj, vj = (torch.cat(p, dim=2) for p in ((q_txt, q_img), (k_txt, k_img), (cv, v)))
+        s = qj.shape[2]
+        o = ops.attention(qj.reshape(b * hh, s, d), kj.reshape(b * hh, s, d),
+                          vj.reshape(b * hh, s, d), scale=1 / math.sqrt(d)).reshape(b, hh, s, d)
+    else:
+        o = _masked_joint_attention(q_img, k_img, v, q_txt, k_txt, cv, int(text_valid_len))
+        s = o.shape[2]
+    o = R(o.transpose(1, 2).reshape(b, s, hh * d))
     c_attn = lin("attn.to_add_out", o[:, :st])
     x_attn = lin("attn.to_out.0", o[:, st:])
 
-    hidden = hidden + i_g1[:, None] * x_attn
-    context = context + t_g1[:, None] * c_attn
-    nx2 = ops.ada_modulate(hidden, i_sh2, i_sc2)
-    hidden = hidden + i_g2[:, None] * lin("img_mlp.net.2", ops.gelu_tanh(lin("img_mlp.net.0.proj", nx2)))
-    nc2 = ops.ada_modulate(context, t_sh2, t_sc2)
-    context = context + t_g2[:, None] * lin("txt_mlp.net.2", ops.gelu_tanh(lin("txt_mlp.net.0.proj", nc2)))
+    hidden = R(hidden + i_g1[:, None] * x_attn)
+    context = R(context + t_g1[:, None] * c_attn)
+    nx2 = R(ops.ada_modulate(hidden, i_sh2, i_sc2))
+    hidden = R(hidden + i_g2[:, None] * lin("img_mlp.net.2",
+                                            R(ops.gelu_tanh(lin("img_mlp.net.0.proj", nx2)))))
+    nc2 = R(ops.ada_modulate(context, t_sh2, t_sc2))
+    context = R(context + t_g2[:, None] * lin("txt_mlp.net.2",
+                                              R(ops.gelu_tanh(lin("txt_mlp.net.0.proj", nc2)))))
     return context, hidden
 
 
 # ------------------------------------------------------------------------------------ model
-def time_embed(ew: dict, timestep, model_dtype=torch.float32):
+def time_embed(ew: dict, timestep, model_dtype=torch.float32, store=None):
     """The timestep projection: the model casts t / 1000 to its dtype, the sinusoid scales it
-    by 1000 (256 channels, cos first, shift 0), then linear_1 - SiLU - linear_2."""
+    by 1000 (256 channels, cos first, shift 0), then linear_1 - SiLU - linear_2. `store`
+    rounds the sinusoid and both linears' outputs as a device holding them in that dtype."""
     L = ops.linear
+    R = ops.rounder(store)
     t = timestep.to(model_dtype).float() * 1000.0
-    tp = ops.timestep_embedding(t, 256, flip_sin_to_cos=True, downscale_freq_shift=0)
-    h = L(tp, ew["time_text_embed.timestep_embedder.linear_1.weight"],
-          ew["time_text_embed.timestep_embedder.linear_1.bias"])
-    return L(torch.nn.functional.silu(h), ew["time_text_embed.timestep_embedder.linear_2.weight"],
-             ew["time_text_embed.timestep_embedder.linear_2.bias"])
+    tp = R(ops.timestep_embedding(t, 256, flip_sin_to_cos=True, downscale_freq_shift=0))
+    h = R(L(tp, ew["time_text_embed.timestep_embedder.linear_1.weight"],
+            ew["time_text_embed.timestep_embedder.linear_1.bias"]))
+    return R(L(torch.nn.functional.silu(h), ew["time_text_embed.timestep_embedder.linear_2.weight"],
+               ew["time_text_embed.timestep_embedder.linear_2.bias"]))
 
 
 def forward(shape: QwenShape, seed: int, latents, text, timestep, img_hw, weights=None,
-            dtype=torch.bfloat16, model_dtype=torch.float32, quant=None, act_dtype=None):
+            dtype=torch.bfloat16, model_dtype=torch.float32, quant=None, act_dtype=None,
+            text_valid_len=None, store=None):
     """One denoise step: latents [B, h*w, in_ch] (packed 2x2 patches), text [B, S_txt,
     txt_dim] (the text encoder's hidden states), timestep t / 1000 [B] -> [B, h*w, out_ch].
-    Blocks are drawn one at a time unless `weights` = (embed, [block...]) is given."""
+    Blocks are drawn one at a time unless `weights` = (embed, [block...]) is given.
+    `text_valid_len` masks a right-padded prompt's padding keys in every block (the
+    reference's text_valid_len path, modeling_qwen_image.py:579-601,738-739). `store` rounds
+    what a device keeps in that dtype, as in block()."""
     ew = weights[0] if weights else embed_weights(shape, seed, dtype=dtype)
     L = ops.linear
-    hidden = L(latents, ew["img_in.weight"], ew["img_in.bias"])
-    context = L(ops.rms_norm_fp32(text, ew["txt_norm.weight"], 1e-6), ew["txt_in.weight"],
-                ew["txt_in.bias"])
-    temb = time_embed(ew, timestep, model_dtype)
+    R = ops.rounder(store)
+    hidden = R(L(latents, ew["img_in.weight"], ew["img_in.bias"]))
+    context = R(L(R(ops.rms_norm_fp32(text, ew["txt_norm.weight"], 1e-6)), ew["txt_in.weight"],
+                  ew["txt_in.bias"]))
+    temb = time_embed(ew, timestep, model_dtype, store)
     cos, sin = pos_embed(img_hw[0], img_hw[1], text.shape[1], shape.axes, shape.theta)
     for i in range(shape.n_blocks):
         w = weights[1][i] if weights else block_weights(shape, seed, i, dtype=dtype)
-        context, hidden = block(w, hidden, context, temb, cos, sin, shape, quant, act_dtype)
-    emb = L(torch.nn.functional.silu(temb), ew["norm_out.linear.weight"], ew["norm_out.linear.bias"])
+        context, hidden = block(w, hidden, context, temb, cos, sin, shape, quant, act_dtype,
+                                store=store, text_valid_len=text_valid_len)
+    emb = R(L(torch.nn.functional.silu(temb), ew["norm_out.linear.weight"], ew["norm_out.linear.bias"]))
     scale, shift = emb.chunk(2, dim=1)  # AdaLayerNormContinuous: scale first
-    hidden = ops.layer_norm(hidden) * (1 + scale)[:, None] + shift[:, None]
+    hidden = R(ops.layer_norm(hidden) * (1 + scale)[:, None] + shift[:, None])
     return L(hidden, ew["proj_out.weight"], ew["proj_out.bias"])
 
 

@@ -145,38 +145,43 @@ def _attend(q, k, v, shape: WanShape):
     return o.reshape(b, h, s, d).transpose(1, 2).reshape(b, s, h * d)
 
 
-def block(w: dict, hidden, text, tproj, cos, sin, shape: WanShape, quant=None, act_dtype=None):
+def block(w: dict, hidden, text, tproj, cos, sin, shape: WanShape, quant=None, act_dtype=None,
+          store=None):
     """hidden [B, S, D], text [B, S_txt, D] (embedded), tproj [B, 6, D] -> hidden. `quant`
     ("mx") applies the MX law to the reference's Wan targets (difflet/quant/targets.py:259-263:
-    the cross-attention's q/k/v and both FFN linears), the rest in fp32."""
+    the cross-attention's q/k/v and both FFN linears), the rest in fp32. `store` (a dtype)
+    rounds every activation the device keeps in memory to it, and the two gates, which the
+    device holds in that dtype; the shift / scale vectors stay fp32 as on the device."""
     from oracle.flux import qlinear
 
     L = ops.linear
     Q = qlinear(quant, act_dtype)
+    R = ops.rounder(store)
     b, s, d = hidden.shape
     mods = w["scale_shift_table"] + tproj
     sh, sc, g, c_sh, c_sc, c_g = mods.chunk(6, dim=1)
+    g, c_g = R(g), R(c_g)
     # self-attention
-    nh = ops.layer_norm(hidden) * (1 + sc) + sh
-    q = ops.rms_norm_fp32(L(nh, w["attn1.to_q.weight"], w["attn1.to_q.bias"]), w["attn1.norm_q.weight"], 1e-6)
-    k = ops.rms_norm_fp32(L(nh, w["attn1.to_k.weight"], w["attn1.to_k.bias"]), w["attn1.norm_k.weight"], 1e-6)
-    v = L(nh, w["attn1.to_v.weight"], w["attn1.to_v.bias"])
-    rot = lambda x: ops.apply_rotary_emb(x.view(b, s, shape.heads, shape.head_dim),  # noqa: E731
-                                         cos[None, :, None], sin[None, :, None]).reshape(b, s, d)
+    nh = R(ops.layer_norm(hidden) * (1 + sc) + sh)
+    q = ops.rms_norm_fp32(R(L(nh, w["attn1.to_q.weight"], w["attn1.to_q.bias"])), w["attn1.norm_q.weight"], 1e-6)
+    k = ops.rms_norm_fp32(R(L(nh, w["attn1.to_k.weight"], w["attn1.to_k.bias"])), w["attn1.norm_k.weight"], 1e-6)
+    v = R(L(nh, w["attn1.to_v.weight"], w["attn1.to_v.bias"]))
+    rot = lambda x: R(ops.apply_rotary_emb(x.view(b, s, shape.heads, shape.head_dim),  # noqa: E731
+                                           cos[None, :, None], sin[None, :, None]).reshape(b, s, d))
     q, k = rot(q), rot(k)
-    o = L(_attend(q, k, v, shape), w["attn1.to_out.0.weight"], w["attn1.to_out.0.bias"])
-    hidden = hidden + o * g
+    o = L(R(_attend(q, k, v, shape)), w["attn1.to_out.0.weight"], w["attn1.to_out.0.bias"])
+    hidden = R(hidden + o * g)
     # cross-attention to the text
-    nh = torch.nn.functional.layer_norm(hidden, (d,), w["norm2.weight"], w["norm2.bias"], 1e-6)
-    q = ops.rms_norm_fp32(Q(nh, w["attn2.to_q.weight"], w["attn2.to_q.bias"]), w["attn2.norm_q.weight"], 1e-6)
-    k = ops.rms_norm_fp32(Q(text, w["attn2.to_k.weight"], w["attn2.to_k.bias"]), w["attn2.norm_k.weight"], 1e-6)
-    v = Q(text, w["attn2.to_v.weight"], w["attn2.to_v.bias"])
-    hidden = hidden + L(_attend(q, k, v, shape), w["attn2.to_out.0.weight"], w["attn2.to_out.0.bias"])
+    nh = R(torch.nn.functional.layer_norm(hidden, (d,), w["norm2.weight"], w["norm2.bias"], 1e-6))
+    q = R(ops.rms_norm_fp32(R(Q(nh, w["attn2.to_q.weight"], w["attn2.to_q.bias"])), w["attn2.norm_q.weight"], 1e-6))
+    k = R(ops.rms_norm_fp32(R(Q(text, w["attn2.to_k.weight"], w["attn2.to_k.bias"])), w["attn2.norm_k.weight"], 1e-6))
+    v = R(Q(text, w["attn2.to_v.weight"], w["attn2.to_v.bias"]))
+    hidden = R(hidden + L(R(_attend(q, k, v, shape)), w["attn2.to_out.0.weight"], w["attn2.to_out.0.bias"]))
     # feed-forward
-    nh = ops.layer_norm(hidden) * (1 + c_sc) + c_sh
-    ff = Q(ops.gelu_tanh(Q(nh, w["ffn.net_in.weight"], w["ffn.net_in.bias"])),
+    nh = R(ops.layer_norm(hidden) * (1 + c_sc) + c_sh)
+    ff = Q(R(ops.gelu_tanh(Q(nh, w["ffn.net_in.weight"], w["ffn.net_in.bias"]))),
            w["ffn.net_out.weight"], w["ffn.net_out.bias"])
-    return hidden + ff * c_g
+    return R(hidden + ff * c_g)
 
 
 # ------------------------------------------------------------------------------------ model

@@ -142,3 +142,93 @@ def test_compile_repeated_blocks(gpu):
     e = _rel(y1, y0)
     print(f"per-block compiled model vs eager rel L2 {e:.2e}", flush=True)
     assert e < 5e-3
+
+
+# ------------------------------------------------ compiled FLUX single block vs the oracle
+class FluxSingleOnOps(nn.Module):
+    """FLUX's single-stream block (difflet/models/flux/modeling_flux.py:696-736) written on the
+    rocm op modules: adaLN-Zero-Single from SiLU(temb), LayerNorm, q/k/v and the MLP, per-head
+    RMSNorm, the fp32 RoPE law, attention, one proj_out over [attn | mlp], gated residual."""
+
+    def __init__(self, d, heads, mlp, dev):
+        super().__init__()
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        self.heads = heads
+        self.norm_linear = ColumnParallelLinear(d, 3 * d, **bf)
+        self.norm = LayerNorm(d, eps=1e-6, elementwise_affine=False)
+        self.to_q, self.to_k, self.to_v = (ColumnParallelLinear(d, d, **bf) for _ in range(3))
+        self.proj_mlp = ColumnParallelLinear(d, mlp, **bf)
+        self.norm_q, self.norm_k = RMSNorm(128).to(dev), RMSNorm(128).to(dev)
+        self.proj_out = RowParallelLinear(d + mlp, d, **bf)
+
+    def load_oracle(self, w):
+        names = {"norm_linear": "norm.linear", "to_q": "attn.to_q", "to_k": "attn.to_k",
+                 "to_v": "attn.to_v", "proj_mlp": "proj_mlp", "proj_out": "proj_out"}
+        with torch.no_grad():
+            for mine, theirs in names.items():
+                getattr(self, mine).weight.copy_(w[f"{theirs}.weight"])
+                getattr(self, mine).bias.copy_(w[f"{theirs}.bias"])
+            self.norm_q.weight.copy_(w["attn.norm_q.weight"])
+            self.norm_k.weight.copy_(w["attn.norm_k.weight"])
+
+    def forward(self, x, temb, cos, sin):
+        from difflet_amd.backends.rocm.ops_impl.embeddings import apply_rotary_emb_fp32
+
+        b, s, d = x.shape
+        shift, scale, gate = self.norm_linear(F.silu(temb)).chunk(3, dim=1)
+        nh = self.norm(x) * (1 + scale[:, None]) + shift[:, None]
+        mlp = F.gelu(self.proj_mlp(nh), approximate="tanh")
+        heads = lambda t: t.view(b, s, self.heads, 128).transpose(1, 2)  # noqa: E731
+        q = apply_rotary_emb_fp32(self.norm_q(heads(self.to_q(nh))), cos, sin)
+        k = apply_rotary_emb_fp32(self.norm_k(heads(self.to_k(nh))), cos, sin)
+        o = attention(q, k, heads(self.to_v(nh)), scale=1.0 / math.sqrt(128))
+        o = o.transpose(1, 2).reshape(b, s, d)
+        return x + gate[:, None] * self.proj_out(torch.cat([o, mlp], dim=-1))
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp8"])
+def test_compiled_flux_single_block_matches_the_oracle(gpu, kind):
+    """The compiled op-module block at FLUX width (3072, 24 heads, MLP 12288) on 128 + 16 x 16
+    tokens against oracle.flux.single_block on the same weights: rel L2 <= 1e-2 against the
+    fp32 block (bf16), <= 3e-2 against the oracle of the per-channel fp8 law with bf16
+    activations (fp8 twins on every linear but the adaLN one)."""
+    from difflet_amd.quant.linear import prepare_fp8_kernels_, quantize_module_
+    from difflet_amd.quant.spec import RocmQuantSpec
+    from oracle import flux as oflux
+    from oracle import ops
+
+    shape = oflux.FluxShape(n_double=1, n_single=1)
+    w = oflux.single_block_weights(shape, 5, 0)
+    g = torch.Generator().manual_seed(5)
+    st, hw = 128, (16, 16)
+    s = st + hw[0] * hw[1]
+    x = torch.randn(1, s, shape.hidden, generator=g).bfloat16().float()
+    temb = torch.randn(1, shape.hidden, generator=g).bfloat16().float()
+    cos, sin = ops.flux_pos_embed(ops.flux_ids(st, *hw))
+    blk = FluxSingleOnOps(shape.hidden, shape.heads, shape.mlp, gpu).eval()
+    blk.load_oracle(w)
+    if kind == "fp8":
+        spec = RocmQuantSpec(targets=(r"to_q", r"to_k", r"to_v", r"proj_mlp", r"proj_out"),
+                             format="fp8_rowwise")
+        assert len(quantize_module_(blk, spec, from_dense=True)) == 5
+        prepare_fp8_kernels_(blk)
+    args = (x.to(gpu, torch.bfloat16), temb.to(gpu, torch.bfloat16), cos.to(gpu), sin.to(gpu))
+    print(f"compiled FLUX single block ({kind}) vs oracle", flush=True)
+    with torch.no_grad():
+        torch._dynamo.reset()
+        y = torch.compile(blk, fullgraph=True, mode="default")(*args)
+        mods = blk.norm_linear(F.silu(args[1])).float().cpu()
+    torch.cuda.synchronize()
+    full = oflux.single_block(w, x, temb, cos, sin, shape)
+    if kind == "bf16":
+        e = _rel(y.cpu(), full)
+        print(f"compiled bf16 block vs fp32 oracle rel L2 {e:.3e}", flush=True)
+        assert e < 1e-2
+        return
+    ref = oflux.single_block(w, x, temb, cos, sin, shape, quant="fp8", act_dtype=torch.bfloat16,
+                             store=torch.bfloat16, mods=mods)
+    e, fmt_dev, fmt_ref = _rel(y.cpu(), ref), _rel(y.cpu(), full), _rel(ref, full)
+    print(f"compiled fp8 block vs same-law oracle rel L2 {e:.3e}; format error device "
+          f"{fmt_dev:.3e}, oracle {fmt_ref:.3e}", flush=True)
+    assert e < 3e-2
+    assert abs(fmt_dev - fmt_ref) < 0.1 * fmt_ref

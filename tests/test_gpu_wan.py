@@ -78,8 +78,10 @@ def test_wan_reduced_depth_step_matches_fp32_oracle(gpu):
 
 def test_wan_block_mx_matches_the_oracle_of_the_same_law(gpu):
     """The reference's MXFP8 Wan targets (cross-attention q/k/v, both FFN linears) on the MX
-    GEMM, against the oracle block with the MX law on the same linears (bf16 activations
-    quantized), at width 1024 (8 heads), FFN 2816, a 2 x 8 x 8 grid and 64 text tokens."""
+    GEMM, against the oracle block with the MX law on the same linears and the device's bf16
+    rounding points (rel L2 <= 3e-2), at width 1024 (8 heads), FFN 2816, a 2 x 8 x 8 grid and
+    64 text tokens; the device's error against the unquantized block equals the oracle's own
+    within 10 %."""
     print("wan block, mx", flush=True)
     kw = dict(hidden=1024, heads=8, ffn=2816, n_blocks=1)
     shape = owan.WanShape(**kw)
@@ -95,7 +97,8 @@ def test_wan_block_mx_matches_the_oracle_of_the_same_law(gpu):
     tproj = (torch.randn(1, 6, shape.hidden, generator=g) * 0.5).bfloat16().float()
     cos, sin = owan.rope_tables(grid, shape)
     bw = {k[len("blocks.0."):]: v.float() for k, v in w.items() if k.startswith("blocks.0.")}
-    ref = owan.block(bw, hidden, text, tproj, cos, sin, shape, quant="mx", act_dtype=torch.bfloat16)
+    ref = owan.block(bw, hidden, text, tproj, cos, sin, shape, quant="mx", act_dtype=torch.bfloat16,
+                     store=torch.bfloat16)
     ref_bf16 = owan.block(bw, hidden, text, tproj, cos, sin, shape)
     bufs = dit._buffers(s, st)
     bufs["h"].copy_(hidden[0].to(gpu, torch.bfloat16))
@@ -109,8 +112,8 @@ def test_wan_block_mx_matches_the_oracle_of_the_same_law(gpu):
     fmt_dev, fmt_ref = rel_l2(bufs["h"], ref_bf16[0]), rel_l2(ref, ref_bf16)
     print(f"mx block rel L2 vs the MX oracle {e:.3e}; format error device {fmt_dev:.3e}, "
           f"oracle {fmt_ref:.3e}", flush=True)
-    assert e < 4e-2
-    assert abs(fmt_dev - fmt_ref) <= 0.1 * fmt_ref + 1e-2
+    assert e < 3e-2
+    assert abs(fmt_dev - fmt_ref) <= 0.1 * fmt_ref
 
 
 def test_wan_step_from_mxfp8_directory_equals_quantize_at_load(gpu, tmp_path):

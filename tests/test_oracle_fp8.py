@@ -62,3 +62,24 @@ def test_fp8_linear_is_the_scaled_integer_product():
     assert np.allclose(y, manual, rtol=1e-5, atol=1e-5)
     exact = x @ w.T + b
     assert np.linalg.norm(y - exact) / np.linalg.norm(exact) < 0.06
+
+
+def test_torch_twin_of_the_row_law_is_bit_exact():
+    """fake_quantize_rowwise_torch / fp8_linear_torch (the threaded twins the block oracles
+    use) equal the numpy law bit for bit: codes, scales and the linear's output."""
+    import torch
+
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((9, 256)) * np.exp2(rng.integers(-30, 30, size=(9, 1)))).astype(np.float32)
+    x[4] = 0.0
+    x[5, :3] = [448.0, -1e-30, 3e-39]
+    q, s = ofp8.quantize_rowwise(x)
+    tq, ts = ofp8.fake_quantize_rowwise_torch(torch.from_numpy(x))
+    assert np.array_equal(tq.numpy(), omx.e4m3_decode(q))
+    assert np.array_equal(ts.numpy().view(np.uint32), s.view(np.uint32))
+    w = (rng.standard_normal((40, 256)) * 0.02).astype(np.float32)
+    b = rng.standard_normal(40).astype(np.float32)
+    wq, ws = ofp8.quantize_rowwise(w)
+    want = ofp8.fp8_linear(x, wq, ws, b)
+    got = ofp8.fp8_linear_torch(torch.from_numpy(x), torch.from_numpy(w), torch.from_numpy(b))
+    assert np.allclose(got.numpy(), want, rtol=1e-6, atol=1e-6)

@@ -101,3 +101,116 @@ def test_mx_targets_are_the_qwen_image_targets():
     names = {k.rsplit(".", 1)[0] for k, _ in oqwen.block_params(SMALL) if k.endswith(".weight")}
     for n in names:
         assert match(f"transformer_blocks.7.{n}") == (n in oqwen.MX_TARGETS), n
+
+
+# ------------------------------------------------ unit gates: a plain transformer block
+def _unit_gate_weights(seed):
+    """Zero modulation weights, biases that give shift = scale = 0 and gate = 1 on both
+    streams; random q/k norm weights so the norm's affine step is exercised too."""
+    w = oqwen.block_weights(SMALL, seed, 0, dtype=torch.float32)
+    d = SMALL.hidden
+    for part in ("img_mod.1", "txt_mod.1"):
+        w[f"{part}.weight"].zero_()
+        b = torch.zeros(6 * d)
+        b[2 * d:3 * d] = 1.0  # gate 1
+        b[5 * d:6 * d] = 1.0  # gate 2
+        w[f"{part}.bias"] = b
+    g = torch.Generator().manual_seed(seed)
+    for n in ("norm_q", "norm_k", "norm_added_q", "norm_added_k"):
+        w[f"attn.{n}.weight"] = 0.5 + torch.rand(128, generator=g)
+    return w
+
+
+def _plain_qwen_block(w, x, c, cos, sin):
+    """Pre-LN joint block from torch primitives: F.layer_norm, F.rms_norm, RoPE as complex
+    multiplication, F.scaled_dot_product_attention over [text | image], F.gelu(tanh) MLPs."""
+    import torch.nn.functional as F
+
+    d, st = SMALL.hidden, c.shape[1]
+    heads = lambda t: t.view(1, -1, 2, 128).transpose(1, 2)  # noqa: E731
+    lin = lambda t, n: F.linear(t, w[f"{n}.weight"], w[f"{n}.bias"])  # noqa: E731
+    ln = lambda t: F.layer_norm(t, (d,), eps=1e-6)  # noqa: E731
+    rms = lambda t, n: F.rms_norm(t, (128,), w[f"attn.{n}.weight"], 1e-6)  # noqa: E731
+    ang = torch.atan2(sin[:, 0::2], cos[:, 0::2])
+
+    def rope(t):
+        z = torch.view_as_complex(t.reshape(*t.shape[:-1], 64, 2).contiguous())
+        return torch.view_as_real(z * torch.polar(torch.ones_like(ang), ang)).reshape(t.shape)
+
+    nx, nc = ln(x), ln(c)
+    q = torch.cat([rms(heads(lin(nc, "attn.add_q_proj")), "norm_added_q"),
+                   rms(heads(lin(nx, "attn.to_q")), "norm_q")], dim=2)
+    k = torch.cat([rms(heads(lin(nc, "attn.add_k_proj")), "norm_added_k"),
+                   rms(heads(lin(nx, "attn.to_k")), "norm_k")], dim=2)
+    v = torch.cat([heads(lin(nc, "attn.add_v_proj")), heads(lin(nx, "attn.to_v"))], dim=2)
+    o = F.scaled_dot_product_attention(rope(q), rope(k), v).transpose(1, 2).reshape(1, -1, d)
+    x = x + lin(o[:, st:], "attn.to_out.0")
+    c = c + lin(o[:, :st], "attn.to_add_out")
+    mlp = lambda t, s: lin(F.gelu(lin(ln(t), f"{s}.net.0.proj"), approximate="tanh"), f"{s}.net.2")  # noqa: E731
+    return c + mlp(c, "txt_mlp"), x + mlp(x, "img_mlp")
+
+
+def _unit_gate_case(seed=11):
+    w = _unit_gate_weights(seed)
+    hidden, context, temb = _inputs(seed)
+    cos, sin = oqwen.pos_embed(1, 7, 5)
+    return w, hidden, context, temb, cos, sin
+
+
+def test_unit_gates_make_the_block_a_plain_transformer_block():
+    """Zero shift / scale and unit gates reduce the block (attention and both MLPs) to a plain
+    pre-LN joint transformer block computed from torch's own primitives."""
+    w, hidden, context, temb, cos, sin = _unit_gate_case()
+    c_ref, h_ref = _plain_qwen_block(w, hidden, context, cos, sin)
+    c2, h2 = oqwen.block(w, hidden, context, temb, cos, sin, SMALL)
+    assert torch.allclose(h2, h_ref, atol=1e-5, rtol=1e-5)
+    assert torch.allclose(c2, c_ref, atol=1e-5, rtol=1e-5)
+
+
+def test_planted_exact_gelu_is_seen_by_the_plain_block(monkeypatch):
+    """The unit-gate check fails an oracle whose MLP takes the exact GELU."""
+    w, hidden, context, temb, cos, sin = _unit_gate_case()
+    c_ref, h_ref = _plain_qwen_block(w, hidden, context, cos, sin)
+    monkeypatch.setattr(ops, "gelu_tanh", lambda x: torch.nn.functional.gelu(x))
+    c2, h2 = oqwen.block(w, hidden, context, temb, cos, sin, SMALL)
+    assert not torch.allclose(h2, h_ref, atol=1e-5, rtol=1e-5)
+    assert not torch.allclose(c2, c_ref, atol=1e-5, rtol=1e-5)
+
+
+def test_planted_swapped_chunk_order_is_seen_by_the_plain_block():
+    """Modulation vectors read in another chunk order (scale where the gate belongs) fail the
+    unit-gate check: the block then scales LN(x) by 2 and closes both gates."""
+    w, hidden, context, temb, cos, sin = _unit_gate_case()
+    c_ref, h_ref = _plain_qwen_block(w, hidden, context, cos, sin)
+    d = SMALL.hidden
+    silu = torch.nn.functional.silu(temb)
+    mods = [ops.linear(silu, w[f"{p}.weight"], w[f"{p}.bias"]) for p in ("img_mod.1", "txt_mod.1")]
+    swapped = [torch.cat([m[:, :d], m[:, 2 * d:3 * d], m[:, d:2 * d], m[:, 3 * d:]], dim=1)
+               for m in mods]
+    c2, h2 = oqwen.block(w, hidden, context, temb, cos, sin, SMALL, mods=tuple(swapped))
+    assert not torch.allclose(h2, h_ref, atol=1e-3)
+    # the vectors in their own order reproduce the check
+    c3, h3 = oqwen.block(w, hidden, context, temb, cos, sin, SMALL, mods=tuple(mods))
+    assert torch.allclose(h3, h_ref, atol=1e-5, rtol=1e-5)
+
+
+def test_masked_text_keys_equal_the_trimmed_prompt():
+    """The reference's masked joint attention (keys [image | text] bounded at S_img + valid)
+    gives the image stream, and the valid text rows, that the prompt cut to its valid rows
+    gives: masked keys take no weight and padded queries influence nothing."""
+    w = oqwen.block_weights(SMALL, 13, 0, dtype=torch.float32)
+    hidden, context, temb = _inputs(13, st=9)
+    cos, sin = oqwen.pos_embed(1, 7, 9)
+    valid = 4
+    c_m, h_m = oqwen.block(w, hidden, context, temb, cos, sin, SMALL, text_valid_len=valid)
+    cos_t = torch.cat([cos[:valid], cos[9:]])
+    sin_t = torch.cat([sin[:valid], sin[9:]])
+    c_t, h_t = oqwen.block(w, hidden, context[:, :valid], temb, cos_t, sin_t, SMALL)
+    assert torch.allclose(h_m, h_t, atol=1e-5, rtol=1e-5)
+    assert torch.allclose(c_m[:, :valid], c_t, atol=1e-5, rtol=1e-5)
+    # and it differs from attending to the padding
+    _, h_u = oqwen.block(w, hidden, context, temb, cos, sin, SMALL)
+    assert not torch.allclose(h_u, h_m, atol=1e-3)
+    # a fully valid prompt is the unmasked block
+    _, h_f = oqwen.block(w, hidden, context, temb, cos, sin, SMALL, text_valid_len=9)
+    assert torch.allclose(h_f, h_u, atol=1e-5, rtol=1e-5)

@@ -77,3 +77,112 @@ def test_cross_attention_with_one_text_token_adds_its_projected_value():
     v = L(text, w["attn2.to_v.weight"], w["attn2.to_v.bias"])
     ref = hidden + L(v, w["attn2.to_out.0.weight"], w["attn2.to_out.0.bias"])
     assert torch.allclose(out, ref, atol=1e-5)
+
+
+# ------------------------------------------------ unit gates: a plain transformer block
+def _unit_gate_case(seed=21, s=6, st=4):
+    """Zero shift / scale and unit gates (table + proj), random affine norm2 and random q/k
+    RMSNorm weights over the whole width."""
+    w = owan.block_weights(SMALL, seed, 0, dtype=torch.float32)
+    hidden, text, tproj = _block_inputs(seed, s=s, st=st)
+    table = torch.zeros(1, 6, SMALL.hidden)
+    table[:, 2] = 1.0
+    table[:, 5] = 1.0
+    w["scale_shift_table"] = table - tproj
+    g = torch.Generator().manual_seed(seed)
+    for a in ("attn1", "attn2"):
+        for n in ("norm_q", "norm_k"):
+            w[f"{a}.{n}.weight"] = 0.5 + torch.rand(SMALL.hidden, generator=g)
+    w["norm2.weight"] = 0.5 + torch.rand(SMALL.hidden, generator=g)
+    w["norm2.bias"] = 0.1 * torch.randn(SMALL.hidden, generator=g)
+    cos, sin = owan.rope_tables((1, 2, 3), SMALL)
+    return w, hidden, text, tproj, cos, sin
+
+
+def _plain_wan_block(w, x, text, cos, sin):
+    """Wan's block with unit gates and no modulation, from torch primitives: F.rms_norm over the
+    whole width (across heads), RoPE as complex multiplication of consecutive pairs,
+    F.scaled_dot_product_attention, affine F.layer_norm before the cross-attention, then
+    LayerNorm and a GELU(tanh) FFN (modeling_wan.py:564-578,720-763)."""
+    import torch.nn.functional as F
+
+    d = SMALL.hidden
+    heads = lambda t: t.view(1, -1, 2, 128).transpose(1, 2)  # noqa: E731
+    merge = lambda t: t.transpose(1, 2).reshape(1, -1, d)  # noqa: E731
+    lin = lambda t, n: F.linear(t, w[f"{n}.weight"], w[f"{n}.bias"])  # noqa: E731
+    rms = lambda t, n: F.rms_norm(t, (d,), w[f"{n}.weight"], 1e-6)  # noqa: E731
+    ang = torch.atan2(sin[:, 1::2], cos[:, 0::2])
+
+    def rope(t):  # [1, S, D] as heads
+        h = heads(t)
+        z = torch.view_as_complex(h.reshape(*h.shape[:-1], 64, 2).contiguous())
+        return torch.view_as_real(z * torch.polar(torch.ones_like(ang), ang)).reshape(h.shape)
+
+    n1 = F.layer_norm(x, (d,), eps=1e-6)
+    q = rope(rms(lin(n1, "attn1.to_q"), "attn1.norm_q"))
+    k = rope(rms(lin(n1, "attn1.to_k"), "attn1.norm_k"))
+    x = x + lin(merge(F.scaled_dot_product_attention(q, k, heads(lin(n1, "attn1.to_v")))),
+                "attn1.to_out.0")
+    n2 = F.layer_norm(x, (d,), w["norm2.weight"], w["norm2.bias"], 1e-6)
+    q = heads(rms(lin(n2, "attn2.to_q"), "attn2.norm_q"))
+    k = heads(rms(lin(text, "attn2.to_k"), "attn2.norm_k"))
+    x = x + lin(merge(F.scaled_dot_product_attention(q, k, heads(lin(text, "attn2.to_v")))),
+                "attn2.to_out.0")
+    ff = lin(F.gelu(lin(F.layer_norm(x, (d,), eps=1e-6), "ffn.net_in"), approximate="tanh"),
+             "ffn.net_out")
+    return x + ff
+
+
+def test_unit_gates_make_the_block_a_plain_transformer_block():
+    """Self-attention (across-heads RMSNorm, stride-2 RoPE), the affine norm2 and
+    cross-attention, and the FFN, against torch's own primitives."""
+    w, hidden, text, tproj, cos, sin = _unit_gate_case()
+    ref = _plain_wan_block(w, hidden, text, cos, sin)
+    out = owan.block(w, hidden, text, tproj, cos, sin, SMALL)
+    assert torch.allclose(out, ref, atol=1e-5, rtol=1e-5)
+
+
+def test_planted_exact_gelu_is_seen_by_the_plain_block(monkeypatch):
+    w, hidden, text, tproj, cos, sin = _unit_gate_case()
+    ref = _plain_wan_block(w, hidden, text, cos, sin)
+    monkeypatch.setattr(ops, "gelu_tanh", lambda x: torch.nn.functional.gelu(x))
+    assert not torch.allclose(owan.block(w, hidden, text, tproj, cos, sin, SMALL), ref,
+                              atol=1e-5, rtol=1e-5)
+
+
+def test_planted_per_head_rms_norm_is_seen_by_the_plain_block(monkeypatch):
+    """An oracle that normalises q and k per head (FLUX's law) instead of across all heads
+    fails the check."""
+    w, hidden, text, tproj, cos, sin = _unit_gate_case()
+    ref = _plain_wan_block(w, hidden, text, cos, sin)
+    across = ops.rms_norm_fp32
+
+    def per_head(x, weight, eps):
+        h = x.unflatten(-1, (-1, 128))
+        y = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)
+        return y.flatten(-2) * weight
+
+    monkeypatch.setattr(ops, "rms_norm_fp32", per_head)
+    assert not torch.allclose(owan.block(w, hidden, text, tproj, cos, sin, SMALL), ref, atol=1e-4)
+    monkeypatch.setattr(ops, "rms_norm_fp32", across)
+    assert torch.allclose(owan.block(w, hidden, text, tproj, cos, sin, SMALL), ref, atol=1e-5,
+                          rtol=1e-5)
+
+
+def test_planted_swapped_chunk_order_is_seen_by_the_plain_block():
+    """timestep_proj with its gate and scale chunks exchanged (an oracle reading the six
+    vectors in another order) fails the check."""
+    w, hidden, text, tproj, cos, sin = _unit_gate_case()
+    ref = _plain_wan_block(w, hidden, text, cos, sin)
+    mods = w["scale_shift_table"] + tproj
+    swapped = mods[:, [0, 2, 1, 3, 4, 5]] - w["scale_shift_table"]
+    assert not torch.allclose(owan.block(w, hidden, text, swapped, cos, sin, SMALL), ref, atol=1e-3)
+
+
+def test_planted_per_head_rope_table_offset_is_seen():
+    """RoPE applied with the table of the wrong token (rows shifted by one) fails the check:
+    the self-attention path is not left unpinned by the gates."""
+    w, hidden, text, tproj, cos, sin = _unit_gate_case()
+    ref = _plain_wan_block(w, hidden, text, cos, sin)
+    out = owan.block(w, hidden, text, tproj, cos.roll(1, 0), sin.roll(1, 0), SMALL)
+    assert not torch.allclose(out, ref, atol=1e-4)
