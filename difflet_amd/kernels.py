@@ -238,7 +238,7 @@ def _check_epilogue_operands(p: Problem, i: int, kind: str, n: int, k: int,
     if epilogue == _lib.EPI_GATE_RESIDUAL:
         if p.gate is None or p.residual is None:
             raise ValueError(f"problem {i}: the gate/residual epilogue needs gate and residual")
-        rpb = p.rows_per_batch or m
+        rpb = p.rows_per_batch or max(m, 1)
         batches = max(1, -(-m // rpb))
         g = p.gate if p.gate.dim() == 2 else p.gate.reshape(1, -1)
         if g.dtype != torch.bfloat16:
@@ -297,6 +297,8 @@ def gemm_grouped(problems: Sequence[Problem], *, kind: str = "bf16",
     bytes, which lets poorly filled launches cut tiles along K. On MI355X at the DiT shapes the
     cut tiles measure slower than whole ones: workgroups that start mid-tile no longer share
     K slices of A and W through their XCD's L2."""
+    # a problem without rows has nothing to compute (and an empty tensor may have no address)
+    problems = [p for p in problems if p.a.shape[0] > 0]
     if not problems:
         return
     n, k = problems[0].w.shape[0], problems[0].w.shape[1]
@@ -503,6 +505,8 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float) -> torch.
     x2 = _rows2d(x, "rms_norm")
     rows, dim = x2.shape
     y = torch.empty((rows, dim), dtype=x.dtype, device=dev)
+    if rows == 0:
+        return y.reshape(x.shape)
     wdt = _dt(weight) if weight is not None else _lib.F32
     check(lib().difflet_rocm_rms_norm(_ptr(x2), x2.stride(0), _ptr(y), dim, _dt(x2), rows, dim,
                                       _ptr(weight), wdt, float(eps), _stream(dev)), "rms_norm")

@@ -129,3 +129,13 @@ def test_the_c_abi_bounds_the_rope_rows_itself():
                                     None)
     assert st == _lib.EINVAL
     assert b"RoPE rows up to 320 of a 319-row table" in lib.difflet_rocm_last_error()
+
+
+def test_problems_without_rows_are_dropped_before_any_check():
+    """A grouped launch whose text part is empty (an empty prompt) runs its other problems; a
+    launch with no rows at all returns at once (an empty tensor may have no address)."""
+    empty = Problem(_bf16(0, K), _bf16(N, K), _bf16(0, N), gate=_bf16(1, N),
+                    residual=_bf16(0, N))
+    kernels.gemm_grouped([empty], epilogue=_lib.EPI_GATE_RESIDUAL)
+    with pytest.raises(ValueError, match=DEVICE_MSG):
+        kernels.gemm_grouped([empty, _gated()], epilogue=_lib.EPI_GATE_RESIDUAL)
