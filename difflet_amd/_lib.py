@@ -71,6 +71,9 @@ SIGNATURES: dict[str, tuple] = {
         _i64p, _i64p, _i64p, _i64p, _f32, _i32, _vp, _i32, _i64p, _vp, _vp, _i64p, _vp, _i64,
         _vp]),
     "difflet_rocm_attention_workspace_bytes": (_i64, []),
+    "difflet_rocm_attention_noalloc": (_i32, [
+        _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64,
+        _i64p, _i64p, _i64p, _i64p, _f32, _i32, _vp, _i32, _i64p, _vp, _vp, _i64p, _vp]),
     "difflet_rocm_gemm_workspace_bytes": (_i64, []),
     "difflet_rocm_gemm_bf16": (_i32, [_i32, ctypes.POINTER(GemmProblem), _i64, _i64, _i32,
                                       _i64, _vp, _i64, ctypes.POINTER(GemmQk), _vp]),

@@ -33,6 +33,8 @@
 // Masking follows the reference: masked scores become the lowest finite float (so a fully
 // masked row averages V, as softmax over equal finfo.min scores does); keys past seq_k do not
 // exist and take -inf.
+#include <mutex>
+
 #include "common.hpp"
 #include <float.h>
 
@@ -720,16 +722,25 @@ extern "C" int64_t difflet_rocm_attention_workspace_bytes(void) {
   return cus > 0 ? att_workspace_bytes(cus) : 0;
 }
 
-extern "C" int difflet_rocm_attention(const void* q, const void* k, const void* v, void* o,
-                                      int dtype, int64_t batch, int64_t heads, int64_t seq_q,
-                                      int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
-                                      const int64_t* k_strides, const int64_t* v_strides,
-                                      const int64_t* o_strides, float scale, int causal,
-                                      const void* mask, int mask_dtype,
-                                      const int64_t* mask_strides, const int32_t* bound_min,
-                                      const int32_t* bound_max, const int64_t* bound_strides,
-                                      void* workspace, int64_t workspace_bytes,
-                                      difflet_stream_t stream) {
+// Counters of the split schedule back to zero before a launch that uses them (a fill kernel,
+// not a memset node, so the pair can be captured into a graph).
+__global__ void att_zero_counters(int* __restrict__ ctr, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) ctr[i] = 0;
+}
+
+// The body of both attention entry points. clear_counters: zero the workspace's counters on
+// the stream before a split-schedule launch (the caller-owned workspace is zeroed once by its
+// owner and left zeroed by the kernels; the library's own scratch is cleared every time).
+static int attention_impl(const char* name, const void* q, const void* k, const void* v,
+                          void* o, int dtype, int64_t batch, int64_t heads, int64_t seq_q,
+                          int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
+                          const int64_t* k_strides, const int64_t* v_strides,
+                          const int64_t* o_strides, float scale, int causal, const void* mask,
+                          int mask_dtype, const int64_t* mask_strides, const int32_t* bound_min,
+                          const int32_t* bound_max, const int64_t* bound_strides,
+                          void* workspace, int64_t workspace_bytes, bool clear_counters,
+                          difflet_stream_t stream) {
   DLT_REQUIRE(q && k && v && o && q_strides && k_strides && v_strides && o_strides,
               DIFFLET_EINVAL, "attention: null pointer");
   DLT_REQUIRE(dtype == DIFFLET_BF16 || dtype == DIFFLET_F16, DIFFLET_EUNSUPPORTED,
@@ -811,6 +822,13 @@ extern "C" int difflet_rocm_attention(const void* q, const void* k, const void* 
       args.split_units = total * ((seq_k + BLOCK_N - 1) / BLOCK_N);
       args.ws = (uint8_t*)workspace;
       grid = dim3((unsigned)cus);
+      if (clear_counters) {
+        const int n = (int)total;  // one counter per query tile
+        hipLaunchKernelGGL(att_zero_counters, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                           s, reinterpret_cast<int*>(workspace), n);
+        const int st = dlt_check_launch(name);
+        if (st != DIFFLET_OK) return st;
+      }
     }
   }
   if (dtype == DIFFLET_BF16) {
@@ -822,5 +840,83 @@ extern "C" int difflet_rocm_attention(const void* q, const void* k, const void* 
     else if (masked) hipLaunchKernelGGL((attn_fwd_kernel<f16, true>), grid, dim3(256), 0, s, args);
     else hipLaunchKernelGGL((attn_fwd_kernel<f16, false>), grid, dim3(256), 0, s, args);
   }
-  return dlt_check_launch("attention");
+  return dlt_check_launch(name);
+}
+
+extern "C" int difflet_rocm_attention(const void* q, const void* k, const void* v, void* o,
+                                      int dtype, int64_t batch, int64_t heads, int64_t seq_q,
+                                      int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
+                                      const int64_t* k_strides, const int64_t* v_strides,
+                                      const int64_t* o_strides, float scale, int causal,
+                                      const void* mask, int mask_dtype,
+                                      const int64_t* mask_strides, const int32_t* bound_min,
+                                      const int32_t* bound_max, const int64_t* bound_strides,
+                                      void* workspace, int64_t workspace_bytes,
+                                      difflet_stream_t stream) {
+  return attention_impl("attention", q, k, v, o, dtype, batch, heads, seq_q, seq_k, head_dim,
+                        q_strides, k_strides, v_strides, o_strides, scale, causal, mask,
+                        mask_dtype, mask_strides, bound_min, bound_max, bound_strides, workspace,
+                        workspace_bytes, false, stream);
+}
+
+// ---- attention that allocates nothing: the split schedule's workspace is this file's static
+// device array. Each device holds its own copy (69.2 MB, for up to 256 compute units) from
+// module load until the process ends; every call on a device shares it, so calls that overlap
+// in time on one device race (one stream, or calls ordered by events, is safe).
+constexpr int ATT_SCRATCH_GROUPS = 256;
+constexpr int64_t ATT_SCRATCH_BYTES = ATT_CTR_BYTES + 2 * (int64_t)ATT_SCRATCH_GROUPS * ATT_SLOT_BYTES;
+static __device__ __align__(256) uint8_t scratch[ATT_SCRATCH_BYTES];
+
+// The device address of `scratch` on the current device, looked up once per device with that
+// device current (in host code the array's name is not a device address).
+static void* att_scratch_ptr(int* err) {
+  static std::mutex mu;
+  static void* ptrs[64] = {nullptr};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    *err = 1;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (ptrs[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      dlt_set_error("attention_noalloc: hipGetSymbolAddress of the scratch array failed on "
+                    "device %d: %s", dev, hipGetErrorString(e));
+      *err = 2;
+      return nullptr;
+    }
+    ptrs[dev] = p;
+  }
+  return ptrs[dev];
+}
+
+extern "C" int difflet_rocm_attention_noalloc(const void* q, const void* k, const void* v,
+                                              void* o, int dtype, int64_t batch, int64_t heads,
+                                              int64_t seq_q, int64_t seq_k, int64_t head_dim,
+                                              const int64_t* q_strides, const int64_t* k_strides,
+                                              const int64_t* v_strides, const int64_t* o_strides,
+                                              float scale, int causal, const void* mask,
+                                              int mask_dtype, const int64_t* mask_strides,
+                                              const int32_t* bound_min, const int32_t* bound_max,
+                                              const int64_t* bound_strides,
+                                              difflet_stream_t stream) {
+  const int cus = att_device_cus();
+  DLT_REQUIRE(cus > 0, DIFFLET_ELAUNCH, "attention_noalloc: no device");
+  DLT_REQUIRE(cus <= ATT_SCRATCH_GROUPS, DIFFLET_EUNSUPPORTED,
+              "attention_noalloc: the device has %d compute units; the static scratch holds the "
+              "split schedule of at most %d (%lld bytes)", cus, ATT_SCRATCH_GROUPS,
+              (long long)ATT_SCRATCH_BYTES);
+  int err = 0;
+  void* ws = att_scratch_ptr(&err);
+  if (err == 1) {
+    dlt_set_error("attention_noalloc: no current device");
+    return DIFFLET_ELAUNCH;
+  }
+  if (err) return DIFFLET_ELAUNCH;
+  return attention_impl("attention_noalloc", q, k, v, o, dtype, batch, heads, seq_q, seq_k,
+                        head_dim, q_strides, k_strides, v_strides, o_strides, scale, causal,
+                        mask, mask_dtype, mask_strides, bound_min, bound_max, bound_strides, ws,
+                        att_workspace_bytes(cus), true, stream);
 }

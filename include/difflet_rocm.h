@@ -83,6 +83,26 @@ int difflet_rocm_attention(const void* q, const void* k, const void* v, void* o,
  * reference, whose attention calls torch's SDPA (difflet/backends/cuda/ops_impl/attention.py:41-86). */
 int64_t difflet_rocm_attention_workspace_bytes(void);
 
+/* difflet_rocm_attention with no workspace argument, allocating nothing: no counterpart in the
+ * reference. It is for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc). Same arguments, semantics and
+ * results as difflet_rocm_attention given a workspace (the same kernels and schedule). The
+ * split schedule's workspace is instead a static device array of the library: 69.2 MB per
+ * device (16 KiB of counters + 2 x 132 KiB for each of up to 256 compute units), held from
+ * module load until the process ends; a device with more compute units is refused
+ * (DIFFLET_EUNSUPPORTED). Its address is looked up on a device's first call, so make that
+ * first call outside capture. The counters are cleared on the stream by a small fill kernel
+ * before each split launch. Every call on one device shares the array: calls that may overlap
+ * in time on one device (different streams without ordering) race. */
+int difflet_rocm_attention_noalloc(const void* q, const void* k, const void* v, void* o,
+                                   int dtype, int64_t batch, int64_t heads, int64_t seq_q,
+                                   int64_t seq_k, int64_t head_dim, const int64_t* q_strides,
+                                   const int64_t* k_strides, const int64_t* v_strides,
+                                   const int64_t* o_strides, float scale, int causal,
+                                   const void* mask, int mask_dtype, const int64_t* mask_strides,
+                                   const int32_t* bound_min, const int32_t* bound_max,
+                                   const int64_t* bound_strides, difflet_stream_t stream);
+
 /* ------------------------------------------------------------------------------------------
  * GEMM with fused epilogues: for each problem p, C_p = epilogue(A_p W_p^T + bias_p).
  * Replaces F.linear in difflet/backends/_torch_megatron/linear.py:120-126,189-202 (and the
