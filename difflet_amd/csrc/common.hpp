@@ -158,12 +158,15 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 // ------------------------------------------------------------------ math
 // GELU with the tanh approximation, 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), with tanh
 // written through exp: tanh(u) = 1 - 2 / (exp(2u) + 1), which saturates cleanly at +-1.
+// 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), written as x sigmoid(2u) =
+// x / (1 + 2^(x (c0 + c1 x^2))) with c0 = -2 sqrt(2/pi) log2(e), c1 = 0.044715 c0: the same
+// function in five VALU operations and two transcendentals. Large negative x gives 2^+inf = inf
+// and x * 0; large positive x gives x.
 __device__ __forceinline__ float gelu_tanh(float x) {
-  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
-  const float k1 = 0.044715f;
-  float u = k0 * (x + k1 * x * x * x);
-  float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(__expf(2.0f * u) + 1.0f);
-  return 0.5f * x * (1.0f + t);
+  constexpr float c0 = -2.302208198144325f;  // -2 * 0.7978845608028654 * 1.4426950408889634
+  constexpr float c1 = c0 * 0.044715f;
+  const float e = __builtin_amdgcn_exp2f(x * __builtin_fmaf(x * x, c1, c0));
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
 

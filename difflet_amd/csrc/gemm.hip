@@ -31,6 +31,7 @@
 // is remapped so each XCD gets a contiguous run of tiles, and tiles run in groups of 8 tile rows
 // so the W and A panels of neighbouring tiles stay L2-resident.
 #include <algorithm>
+#include <type_traits>
 #include <vector>
 
 #include "common.hpp"
@@ -107,13 +108,24 @@ struct GemmArgs {
   const float* rope_sin;
 };
 
-// KT: K elements per stage. WN: wavefronts along N (two along M). Every type runs 8 wavefronts
-// of 128 x 64 (measured against 4 of 128 x 128: +10-20 % for fp8, +0-6 % for bf16, and 128
-// accumulators leave room for the split-tile code without spills).
+// KT: K elements per stage, KTB its bytes per row, NSLOT the stages the LDS ring holds. WN:
+// wavefronts along N (two along M). Every type runs 8 wavefronts of 128 x 64 (measured against 4
+// of 128 x 128: +10-20 % for fp8, +0-6 % for bf16, and 128 accumulators leave room for the
+// split-tile code without spills). bf16 and fp8 stage 128 bytes of each row (two slots of
+// 64 KB): a direct-to-LDS load then fetches 8 rows x 128 B, one whole line per row, which moves
+// data from L2 into LDS 1.5x faster than 16 rows x 64 B (measured on FLUX's shapes: the loads
+// alone of fp8 W1 take 123 against 193 us). MXFP8 keeps 64-byte stages in four slots, the
+// geometry its E8M0 scale ring is laid out for.
 template <Elem E> struct ElemTraits;
-template <> struct ElemTraits<Elem::BF16> { static constexpr int KT = 32, BYTES = 2, WN = 4; };
-template <> struct ElemTraits<Elem::FP8> { static constexpr int KT = 64, BYTES = 1, WN = 4; };
-template <> struct ElemTraits<Elem::MX> { static constexpr int KT = 64, BYTES = 1, WN = 4; };
+template <> struct ElemTraits<Elem::BF16> {
+  static constexpr int KT = 64, BYTES = 2, WN = 4, KTB = 128, NSLOT = 2;
+};
+template <> struct ElemTraits<Elem::FP8> {
+  static constexpr int KT = 128, BYTES = 1, WN = 4, KTB = 128, NSLOT = 2;
+};
+template <> struct ElemTraits<Elem::MX> {
+  static constexpr int KT = 64, BYTES = 1, WN = 4, KTB = 64, NSLOT = 4;
+};
 
 
 // A stage row is 64 bytes = 4 chunks of 16. Chunk c of row r sits at c ^ swz(r), swz(r) =
@@ -153,23 +165,34 @@ __device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 2)) &
 __device__ __forceinline__ int lds_off(int row, int chunk) {
   return row * KT_BYTES + ((chunk ^ swz(row)) << 4);
 }
+// A 128-byte stage row is 8 chunks of 16; chunk c of row r sits at c ^ swz8(r), swz8(r) =
+// (r & 7) ^ ((r >> 3) & 1). A fragment read takes one logical chunk of 32 consecutive rows: any 8
+// aligned consecutive rows land in 8 distinct 16-byte bank groups (an LDS serving 8 lanes over
+// 32 banks per cycle), and any 16 aligned consecutive rows in 16 distinct ones of the 256-byte
+// period (16 lanes over 64 banks): even and odd rows each see all 8 chunk positions.
+__device__ __forceinline__ int swz8(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+__device__ __forceinline__ int lds_off8(int row, int chunk) {
+  return row * 128 + ((chunk ^ swz8(row)) << 4);
+}
 
 // WN = ElemTraits<E>::WN wavefronts along N, 2 along M: 128 WN threads.
 template <Elem E, int EPI, int WN, bool QK>
 __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) {
   constexpr int KT = ElemTraits<E>::KT;
   constexpr int EB = ElemTraits<E>::BYTES;
+  constexpr int KTB = ElemTraits<E>::KTB, NSLOT = ElemTraits<E>::NSLOT;
   constexpr int WN_WAVES = WN, NWAVES = 2 * WN;
   constexpr int WTN = BN / WN_WAVES, TJ = WTN / 32;  // wave tile 128 x WTN: 4 x TJ MFMA tiles
-  constexpr int SLABS = 32 / NWAVES;  // 1 KB LDS slabs one wave loads per stage
-  // LDS: the stage ring [stage][A|W] and (MX) the E8M0 scales of 8 stages (16 bytes) per row, a
-  // ring of 3 such blocks [slot][A|W][row]. One LDS variable: with two, the compiler gives their
-  // accesses alias scopes and then drains all loads (vmcnt(0)) before each LDS read that follows
-  // a direct-to-LDS load.
-  constexpr int RING_BYTES = STAGES * 2 * BM * KT_BYTES;
+  constexpr int SLABS = 2 * BM * KTB / 1024 / NWAVES;  // 1 KB LDS slabs one wave loads per stage
+  // LDS: the stage ring [slot][A|W] (128 KB) and (MX) the E8M0 scales of 8 stages (16 bytes) per
+  // row, a ring of 3 such blocks [slot][A|W][row]. One LDS variable: with two, the compiler
+  // gives their accesses alias scopes and then drains all loads (vmcnt(0)) before each LDS read
+  // that follows a direct-to-LDS load.
+  constexpr int RING_BYTES = NSLOT * 2 * BM * KTB;
   constexpr int SC_BYTES = E == Elem::MX ? 3 * 2 * BM * 16 : 0;
+  static_assert(RING_BYTES == 128 * 1024, "the epilogues stage a 256 x 256 bf16 tile in the ring");
   __shared__ __attribute__((aligned(16))) uint8_t lds[RING_BYTES + SC_BYTES];
-  auto& smem = *reinterpret_cast<uint8_t(*)[STAGES][2][BM * KT_BYTES]>(lds);
+  auto& smem = *reinterpret_cast<uint8_t(*)[NSLOT][2][BM * KTB]>(lds);
   auto& smem_sc = *reinterpret_cast<uint32_t(*)[3][2][BM][4]>(lds + RING_BYTES);
 
   const int tid = threadIdx.x;
@@ -243,7 +266,14 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
 #pragma unroll
   for (int i = 0; i < SA; ++i) {
     const int p = (wave * SA + i) * 64 + lane;
-    const int r = p >> 2, ch = (p & 3) ^ swz(r);
+    int r, ch;
+    if constexpr (KTB == 128) {  // 8 rows x 8 chunks per slab
+      r = p >> 3;
+      ch = (p & 7) ^ swz8(r);
+    } else {  // 16 rows x 4 chunks per slab
+      r = p >> 2;
+      ch = (p & 3) ^ swz(r);
+    }
     a_off[i] = (uint32_t)(r * a_row_bytes) + ch * 16;
     w_off[i] = (uint32_t)(r * w_row_bytes) + ch * 16;
   }
@@ -269,7 +299,7 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
   // part `part` (of 4) of stage kt's loads: a quarter of this wave's slabs, A slabs first (MX:
   // with part 0, wave kt % 8 also loads part kt % 8 of the next scale block)
   auto issue_part = [&](int kt, int st, int part) {
-    const uint32_t kb = (uint32_t)(kbeg + kt) * KT_BYTES;  // kt counts from the range start
+    const uint32_t kb = (uint32_t)(kbeg + kt) * KTB;  // kt counts from the range start
 #pragma unroll
     for (int s = part * SLABS / 4; s < (part + 1) * SLABS / 4; ++s) {
       if (s < SA)
@@ -384,70 +414,158 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
     for (int i = 0; i < 4; ++i) mma_row(f, h, i);
   };
 
-  // prologue: stages 0 .. STAGES-2 of the range in flight, then wait for stage 0. Past the last
-  // K stage the loads re-read the last stage (in bounds) into the free ring slot: every
-  // iteration then issues and waits alike, and the loop body is one straight-line block.
-  // (Stage numbers count from the range start, which for MX is a multiple of 8 stages, so the
-  // scale blocks keep their alignment.)
-  if constexpr (E == Elem::MX) {  // scale block 0, one part per wave, ahead of stage 0
+  if constexpr (KTB == 128) {
+    // ---- bf16 / fp8: 128-byte stages in two LDS slots. A stage is NKS MFMA K steps (bf16 4 of
+    // 16 elements, fp8 2 of 64); fragments of the next K step are read while the current one's
+    // MFMAs run (two register sets). Before the last K step of stage kt every wave waits for its
+    // loads of stage kt + 1 (the only ones in flight) and for its own reads of this stage, and
+    // one barrier then publishes stage kt + 1 and frees this slot; the loads of stage kt + 2
+    // into it go out with the last K step's MFMAs, so each stage has a whole stage to land.
+    constexpr int NKS = E == Elem::BF16 ? 4 : 2;
+    constexpr int NA = E == Elem::BF16 ? 1 : 2;  // 16-byte LDS reads per fragment
+    // A fragments roll: tile i's fragment of the next K step is read into its registers right
+    // after tile i's MFMAs of this step issue; W fragments alternate between two sets. With 128
+    // accumulators that keeps a wave within 256 registers (two whole sets spill).
+    i32x4 fa[4][2], fw[2][4][2];  // [tile][part]; fw[set][tile j < TJ][part]
+    auto read_a = [&](int st, int ks, int i) {
+      const uint8_t* sA = smem[st][0];
+      const int r = wm * 128 + i * 32 + frow;
 #pragma unroll
-    for (int p = wave; p < 8; p += NWAVES) issue_scales(0, p);
-  }
+      for (int h = 0; h < NA; ++h)
+        fa[i][h] = *reinterpret_cast<const i32x4*>(sA + lds_off8(r, 2 * NA * ks + 2 * h + fhalf));
+    };
+    auto read_w = [&](int st, int ks, int set) {
+      const uint8_t* sW = smem[st][1];
 #pragma unroll
-  for (int s0 = 0; s0 < STAGES - 1; ++s0) issue_stage(min(s0, nkt - 1), s0);
-  {
-    constexpr int c = 2 * LOADS_PER_STAGE;
-    __builtin_amdgcn_s_waitcnt(0x0f70 | (c & 15) | ((c >> 4) << 14));
-  }
-  __syncthreads();
-  Frags f0, f1;
-  read_a(0, 0, f0);
-  read_w(0, 0, 0, f0);
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int st = kt % STAGES;
-    // half 0 of stage kt; meanwhile read half 1's fragments
-    if constexpr (E == Elem::BF16) {
-      read_a1(st, f1);
-      read_w(st, 1, kt, f1);
-      mma_half(f0, 0);
-      interleave3<4 * TJ, 4 + TJ, 0>();
-    } else {
-      read_w(st, 1, kt, f1);
+      for (int j = 0; j < TJ; ++j) {
+        const int r = wn * WTN + j * 32 + frow;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        f1.a[i][0] = f0.a[i][0];
-        f1.a[i][1] = f0.a[i][1];
-        f1.sa[i] = f0.sa[i];
+        for (int h = 0; h < NA; ++h)
+          fw[set][j][h] =
+              *reinterpret_cast<const i32x4*>(sW + lds_off8(r, 2 * NA * ks + 2 * h + fhalf));
       }
-      mma_half(f0, 0);
-      interleave3<2 * TJ, TJ, 0>();
+    };
+    auto mma_tile = [&](int set, int i) {
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        if constexpr (E == Elem::BF16) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8, fw[set][j][0]), __builtin_bit_cast(bf16x8, fa[i][0]),
+              acc[i][j], 0, 0, 0);
+        } else {
+          const i32x8 w8 = {fw[set][j][0][0], fw[set][j][0][1], fw[set][j][0][2], fw[set][j][0][3],
+                            fw[set][j][1][0], fw[set][j][1][1], fw[set][j][1][2], fw[set][j][1][3]};
+          const i32x8 a8 = {fa[i][0][0], fa[i][0][1], fa[i][0][2], fa[i][0][3],
+                            fa[i][1][0], fa[i][1][1], fa[i][1][2], fa[i][1][3]};
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w8, a8, acc[i][j], 0, 0, 0,
+                                                                      0, 0, 0);
+        }
+      }
+    };
+    issue_stage(0, 0);
+    if (nkt > 1) {
+      issue_stage(1, 1);
+      constexpr int c = LOADS_PER_STAGE;  // stage 0 landed, stage 1 may be in flight
+      __builtin_amdgcn_s_waitcnt(0x0f70 | (c & 15) | ((c >> 4) << 14));
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0f70);
     }
-    // stage kt + 1 must have landed (stage kt + 2 may still be in flight), then the barrier
-    // publishes it to every wave and frees stage kt - 1 for stage kt + STAGES - 1
+    __syncthreads();
+    read_w(0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) read_a(0, 0, i);
+    for (int kt = 0; kt < nkt; ++kt) {
+      const int st = kt & 1;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const int set = ks & 1;
+        const bool last = ks == NKS - 1;
+        // the next K step: of this stage, or the first of stage kt + 1 (past the range's last
+        // stage it reads stale LDS that nothing uses)
+        const int nst = last ? (st ^ 1) : st, nks = last ? 0 : ks + 1;
+        const bool loads = last && kt + 2 < nkt;
+        if (last) {
+          // stage kt + 1 has landed (only its loads are in flight) and this wave's reads of
+          // slot st are done; the barrier publishes the one and frees the other
+          __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+          stage_barrier();
+        }
+        read_w(nst, nks, set ^ 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          mma_tile(set, i);
+          read_a(nst, nks, i);
+          if (loads) issue_part(kt + 2, st, i);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+  } else {
+  // prologue: stages 0 .. STAGES-2 of the range in flight, then wait for stage 0. Past the last
+    // K stage the loads re-read the last stage (in bounds) into the free ring slot: every
+    // iteration then issues and waits alike, and the loop body is one straight-line block.
+    // (Stage numbers count from the range start, which for MX is a multiple of 8 stages, so the
+    // scale blocks keep their alignment.)
+    if constexpr (E == Elem::MX) {  // scale block 0, one part per wave, ahead of stage 0
+  #pragma unroll
+      for (int p = wave; p < 8; p += NWAVES) issue_scales(0, p);
+    }
+  #pragma unroll
+    for (int s0 = 0; s0 < STAGES - 1; ++s0) issue_stage(min(s0, nkt - 1), s0);
     {
-      constexpr int c = LOADS_PER_STAGE;
+      constexpr int c = 2 * LOADS_PER_STAGE;
       __builtin_amdgcn_s_waitcnt(0x0f70 | (c & 15) | ((c >> 4) << 14));
     }
-    stage_barrier();
-    // half 1 of stage kt in four parts, each one A tile's MFMAs, that tile's fragments of
-    // stage kt + 1 (unused after the last stage) and a quarter of stage kt + 3's loads: the
-    // loads then trickle into the vector-memory pipe instead of arriving as one burst
-    const int nst = (kt + 1) % STAGES;
-    const int lk = min(kt + STAGES - 1, nkt - 1), ls = (kt + STAGES - 1) % STAGES;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      mma_row(f1, 1, i);
-      read_a_i(nst, kt + 1, f0, i);
+    __syncthreads();
+    Frags f0, f1;
+    read_a(0, 0, f0);
+    read_w(0, 0, 0, f0);
+    for (int kt = 0; kt < nkt; ++kt) {
+      const int st = kt % STAGES;
+      // half 0 of stage kt; meanwhile read half 1's fragments
       if constexpr (E == Elem::BF16) {
-        if (i < TJ) read_w_j(nst, 0, kt + 1, f0, i);
+        read_a1(st, f1);
+        read_w(st, 1, kt, f1);
+        mma_half(f0, 0);
+        interleave3<4 * TJ, 4 + TJ, 0>();
       } else {
-        if (i < TJ / 2) read_w_j(nst, 0, kt + 1, f0, i);
+        read_w(st, 1, kt, f1);
+  #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f1.a[i][0] = f0.a[i][0];
+          f1.a[i][1] = f0.a[i][1];
+          f1.sa[i] = f0.sa[i];
+        }
+        mma_half(f0, 0);
+        interleave3<2 * TJ, TJ, 0>();
       }
-      issue_part(lk, ls, i);
-      __builtin_amdgcn_sched_barrier(0);
+      // stage kt + 1 must have landed (stage kt + 2 may still be in flight), then the barrier
+      // publishes it to every wave and frees stage kt - 1 for stage kt + STAGES - 1
+      {
+        constexpr int c = LOADS_PER_STAGE;
+        __builtin_amdgcn_s_waitcnt(0x0f70 | (c & 15) | ((c >> 4) << 14));
+      }
+      stage_barrier();
+      // half 1 of stage kt in four parts, each one A tile's MFMAs, that tile's fragments of
+      // stage kt + 1 (unused after the last stage) and a quarter of stage kt + 3's loads: the
+      // loads then trickle into the vector-memory pipe instead of arriving as one burst
+      const int nst = (kt + 1) % STAGES;
+      const int lk = min(kt + STAGES - 1, nkt - 1), ls = (kt + STAGES - 1) % STAGES;
+  #pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        mma_row(f1, 1, i);
+        read_a_i(nst, kt + 1, f0, i);
+        if constexpr (E == Elem::BF16) {
+          if (i < TJ) read_w_j(nst, 0, kt + 1, f0, i);
+        } else {
+          if (i < TJ / 2) read_w_j(nst, 0, kt + 1, f0, i);
+        }
+        issue_part(lk, ls, i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // the trailing re-reads land before the workgroup ends
   }
-  __builtin_amdgcn_s_waitcnt(0x0f70);  // the trailing re-reads land before the workgroup ends
 
   // ---- a tile cut between split workgroups c0 .. c1: the last to arrive finishes it.
   // Partial sums move through the workspace with device-scope (sc1) loads and stores, which
@@ -628,6 +746,90 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
 #pragma unroll
         for (int e = 0; e < 4; ++e) st[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
         *reinterpret_cast<u32x4*>(reinterpret_cast<bf16*>(P.c) + m * P.ldc + n0 + ch * 8) = st;
+      }
+    }
+    continue;  // this tile is stored
+  }
+  if constexpr (EPI != DIFFLET_EPI_GATE_RESIDUAL) {
+    // Plain and GELU tiles go out through the idle LDS ring: each wave writes its values (the
+    // same fp32 math and bf16 rounding as a direct store) as [256 rows][32 chunks of 16 bytes],
+    // chunk c of row r at c ^ (r & 31); then each half-wave stores one row of the tile, 16 bytes
+    // per lane, 512 contiguous bytes. Stored straight from the accumulators, a wave instruction
+    // covers 32 rows x 16 bytes, and the plain and GELU epilogues took 25-30 % of the fp8 GEMMs.
+    uint8_t* tile = lds;
+    const float* wsc = reinterpret_cast<const float*>(P.w_scale);
+    // the 4 row scales (fp8) for the whole tile; a W tile's column vectors while it is stored
+    float sa[4] = {1.f, 1.f, 1.f, 1.f};
+    if constexpr (E == Elem::FP8)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t m = m0 + wm * 128 + i * 32 + frow;
+        sa[i] = m < M ? reinterpret_cast<const float*>(P.a_scale)[m] : 0.f;
+      }
+    __syncthreads();  // every wave's last fragment reads of the ring are done
+    // GELU on columns >= act_col_start: a tile lies wholly on one side (uniform branch) or
+    // straddles it (per-column select, no branch)
+    auto stage = [&](auto gelu_mode) {
+      constexpr int G = decltype(gelu_mode)::value;  // 0 none, 1 every column, 2 per column
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        u32x2 bv[4];
+        f32x4 wv[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t n = n0 + wn * WTN + j * 32 + q * 8 + fhalf * 4;
+          const bool nok = n < N;
+          bv[q] = (P.bias && nok) ? *reinterpret_cast<const u32x2*>(P.bias + n) : u32x2{0u, 0u};
+          if constexpr (E == Elem::FP8)
+            wv[q] = nok ? *reinterpret_cast<const f32x4*>(wsc + n) : f32x4{};
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = wm * 128 + i * 32 + frow;  // tile row
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int cl = wn * WTN + j * 32 + q * 8 + fhalf * 4;  // tile column of the 4 values
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v[e] = acc[i][j][q * 4 + e];
+              if constexpr (E == Elem::FP8) v[e] = v[e] * (sa[i] * wv[q][e]);
+              v[e] += bf16bits_to_f32(e & 1 ? bv[q][e >> 1] >> 16 : bv[q][e >> 1] & 0xffffu);
+              if constexpr (G == 1) v[e] = gelu_tanh(v[e]);
+              if constexpr (G == 2) {
+                const float g = gelu_tanh(v[e]);
+                v[e] = n0 + cl + e >= args.act_col_start ? g : v[e];
+              }
+            }
+            const u32x2 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            *reinterpret_cast<u32x2*>(tile + r * 512 + (((cl >> 3) ^ (r & 31)) << 4) + (cl & 7) * 2) = o;
+          }
+        }
+      }
+    };
+    if constexpr (EPI == DIFFLET_EPI_GELU) {
+      if (n0 >= args.act_col_start) stage(std::integral_constant<int, 1>{});
+      else if (n0 + BN > args.act_col_start) stage(std::integral_constant<int, 2>{});
+      else stage(std::integral_constant<int, 0>{});
+    } else {
+      stage(std::integral_constant<int, 0>{});
+    }
+    __syncthreads();
+    const int ch = lane & 31, half = lane >> 5;  // 16-byte chunk of the row, which row of two
+    const int64_t n = n0 + ch * 8;
+    // 16-byte stores need 16-byte aligned rows; otherwise two 8-byte halves (N % 4 == 0)
+    const bool wide = (((uintptr_t)P.c & 15) == 0) && (P.ldc % 8 == 0);
+    for (int r = wave * 2 + half; r < BM; r += 2 * NWAVES) {
+      const int64_t m = m0 + r;
+      if (m >= M) break;  // rows only grow
+      if (n >= N) continue;
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(tile + r * 512 + ((ch ^ (r & 31)) << 4));
+      bf16* dst = reinterpret_cast<bf16*>(P.c) + m * P.ldc + n;
+      if (wide && n + 8 <= N) {
+        *reinterpret_cast<u32x4*>(dst) = raw;
+      } else {
+        *reinterpret_cast<u32x2*>(dst) = u32x2{raw[0], raw[1]};
+        if (n + 4 < N) *reinterpret_cast<u32x2*>(dst + 4) = u32x2{raw[2], raw[3]};
       }
     }
     continue;  // this tile is stored
