@@ -170,6 +170,22 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 }
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
 
+// Sum over each row of 16 lanes, result in all 16, by DPP lane moves (no LDS round trip):
+// quad_perm [1,0,3,2] and [2,3,0,1] give each lane its quad's sum, row_half_mirror (lane i of
+// 8 takes lane 7 - i) adds the neighbouring quad, row_mirror (i takes 15 - i) the other half.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float sum16_dpp(float v) {
+  v += dpp_move<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_move<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_move<0x141>(v);  // row_half_mirror
+  v += dpp_move<0x140>(v);  // row_mirror
+  return v;
+}
+
 // ------------------------------------------------------------------ buffer resources
 // Raw buffer loads: an out-of-range offset reads zero, which is how GEMM and attention tiles
 // handle ragged M / N / sequence edges without branches.

@@ -507,10 +507,10 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
     // (Stage numbers count from the range start, which for MX is a multiple of 8 stages, so the
     // scale blocks keep their alignment.)
     if constexpr (E == Elem::MX) {  // scale block 0, one part per wave, ahead of stage 0
-  #pragma unroll
+#pragma unroll
       for (int p = wave; p < 8; p += NWAVES) issue_scales(0, p);
     }
-  #pragma unroll
+#pragma unroll
     for (int s0 = 0; s0 < STAGES - 1; ++s0) issue_stage(min(s0, nkt - 1), s0);
     {
       constexpr int c = 2 * LOADS_PER_STAGE;
@@ -530,7 +530,7 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
         interleave3<4 * TJ, 4 + TJ, 0>();
       } else {
         read_w(st, 1, kt, f1);
-  #pragma unroll
+#pragma unroll
         for (int i = 0; i < 4; ++i) {
           f1.a[i][0] = f0.a[i][0];
           f1.a[i][1] = f0.a[i][1];
@@ -551,7 +551,7 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
       // loads then trickle into the vector-memory pipe instead of arriving as one burst
       const int nst = (kt + 1) % STAGES;
       const int lk = min(kt + STAGES - 1, nkt - 1), ls = (kt + STAGES - 1) % STAGES;
-  #pragma unroll
+#pragma unroll
       for (int i = 0; i < 4; ++i) {
         mma_row(f1, 1, i);
         read_a_i(nst, kt + 1, f0, i);
@@ -663,93 +663,6 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
   if constexpr (QK)
     qk_tile = (n0 >= args.q_col && n0 < (int64_t)args.q_col + args.qk_cols) ||
               (n0 >= args.k_col && n0 < (int64_t)args.k_col + args.qk_cols);
-  if constexpr (QK) if (qk_tile) {
-    // The tile's bf16 output (the plain GEMM's values) goes through the idle LDS ring as
-    // [256 rows][32 chunks of 16 bytes], chunk c of row r at c ^ (r & 31); then each half-wave
-    // takes one row: 16 lanes per 128-column head reduce its sum of squares with xor shuffles,
-    // scale by rsqrt(mean + eps) and the norm weights, rotate and store 16 bytes per lane.
-    const bf16* nw = (n0 >= args.q_col && n0 < (int64_t)args.q_col + args.qk_cols) ? P.nq : P.nk;
-    uint8_t* tile = lds;
-    __syncthreads();  // every wave's last fragment reads of the ring are done
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = wm * 128 + i * 32 + frow;  // tile row
-      const int64_t mc = min(m0 + r, (int64_t)M - 1);
-      float sa = 1.f;
-      if constexpr (E == Elem::FP8) sa = reinterpret_cast<const float*>(P.a_scale)[mc];
-#pragma unroll
-      for (int j = 0; j < TJ; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int cl = wn * WTN + j * 32 + q * 8 + fhalf * 4;  // tile column of the 4 values
-          const int64_t n = n0 + cl;  // < N: the q/k columns lie inside N
-          const u32x2 bv = P.bias ? *reinterpret_cast<const u32x2*>(P.bias + n) : u32x2{0u, 0u};
-          f32x4 wsv = {1.f, 1.f, 1.f, 1.f};
-          if constexpr (E == Elem::FP8) wsv = *reinterpret_cast<const f32x4*>(ws + n);
-          float v[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            v[e] = acc[i][j][q * 4 + e];
-            if constexpr (E == Elem::FP8) v[e] = v[e] * (sa * wsv[e]);
-            v[e] += bf16bits_to_f32(e & 1 ? bv[e >> 1] >> 16 : bv[e >> 1] & 0xffffu);
-          }
-          const u32x2 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-          *reinterpret_cast<u32x2*>(tile + r * 512 + (((cl >> 3) ^ (r & 31)) << 4) + (cl & 7) * 2) = o;
-        }
-    }
-    __syncthreads();
-    const int ch = lane & 31, half = lane >> 5;  // 16-byte chunk of the row, which row of two
-    const int d = (ch & 15) * 8;                 // column within the head
-    const u32x4 wraw = nw ? *reinterpret_cast<const u32x4*>(nw + d)
-                          : u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
-    for (int r = wave * 2 + half; r < BM; r += 2 * NWAVES) {
-      const int64_t m = m0 + r;
-      const u32x4 raw = *reinterpret_cast<const u32x4*>(tile + r * 512 + ((ch ^ (r & 31)) << 4));
-      float v[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[2 * e] = bf16bits_to_f32(raw[e] & 0xffffu);
-        v[2 * e + 1] = bf16bits_to_f32(raw[e] >> 16);
-      }
-      float ss = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o, 64);
-      const float rs = 1.0f / __builtin_sqrtf(ss / 128.0f + args.qk_eps);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[2 * e] = v[2 * e] * rs * bf16bits_to_f32(wraw[e] & 0xffffu);
-        v[2 * e + 1] = v[2 * e + 1] * rs * bf16bits_to_f32(wraw[e] >> 16);
-      }
-      if (m < M) {
-        const int64_t rr = P.rope_row0 + m;
-        const float* cp = args.rope_cos + rr * 128 + d;
-        const float* sp = args.rope_sin + rr * 128 + d;
-        float c[8], sn[8];
-        *reinterpret_cast<f32x4*>(c) = *reinterpret_cast<const f32x4*>(cp);
-        *reinterpret_cast<f32x4*>(c + 4) = *reinterpret_cast<const f32x4*>(cp + 4);
-        *reinterpret_cast<f32x4*>(sn) = *reinterpret_cast<const f32x4*>(sp);
-        *reinterpret_cast<f32x4*>(sn + 4) = *reinterpret_cast<const f32x4*>(sp + 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float a0 = v[2 * e], b0 = v[2 * e + 1];
-          if (args.rope_law == 0) {
-            v[2 * e] = a0 * c[2 * e] - b0 * sn[2 * e];
-            v[2 * e + 1] = b0 * c[2 * e + 1] + a0 * sn[2 * e + 1];
-          } else {
-            v[2 * e] = a0 * c[2 * e] - b0 * sn[2 * e + 1];
-            v[2 * e + 1] = a0 * sn[2 * e + 1] + b0 * c[2 * e];
-          }
-        }
-        u32x4 st;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) st[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
-        *reinterpret_cast<u32x4*>(reinterpret_cast<bf16*>(P.c) + m * P.ldc + n0 + ch * 8) = st;
-      }
-    }
-    continue;  // this tile is stored
-  }
   if constexpr (EPI != DIFFLET_EPI_GATE_RESIDUAL) {
     // Plain and GELU tiles go out through the idle LDS ring: each wave writes its values (the
     // same fp32 math and bf16 rounding as a direct store) as [256 rows][32 chunks of 16 bytes],
@@ -815,6 +728,83 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
       stage(std::integral_constant<int, 0>{});
     }
     __syncthreads();
+    if constexpr (QK) if (qk_tile) {
+      // fused q/k RMSNorm + RoPE: this tile's 256 columns are two heads of q or of k (the
+      // staged values are the plain GEMM's bf16 output); each half-wave takes one row, 16 lanes
+      // per 128-column head reduce its sum of squares with xor shuffles, scale by
+      // rsqrt(mean + eps) and the norm weights, rotate and store 16 bytes per lane
+      const bf16* nw = (n0 >= args.q_col && n0 < (int64_t)args.q_col + args.qk_cols) ? P.nq : P.nk;
+      {
+        const int ch = lane & 31, half = lane >> 5;  // 16-byte chunk of the row, which row of two
+        const int d = (ch & 15) * 8;                 // column within the head
+        const u32x4 wraw = nw ? *reinterpret_cast<const u32x4*>(nw + d)
+                              : u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+        // each half-wave takes rows wave * 2 + half + 16 t; batches of RB rows issue all their
+        // LDS and RoPE-table loads before any arithmetic (one latency per batch, not per row;
+        // the accumulators are dead here, so the registers are free)
+        constexpr int RB = 4, SLOTS = BM / (2 * NWAVES);
+        const bool law0 = args.rope_law == 0;
+#pragma unroll 1
+        for (int t0 = 0; t0 < SLOTS; t0 += RB) {
+          u32x4 raw[RB];
+          f32x4 c[RB][2], sn[RB][2];
+#pragma unroll
+          for (int b = 0; b < RB; ++b) {
+            const int r = wave * 2 + half + (t0 + b) * 2 * NWAVES;
+            const int64_t mc = min(m0 + r, (int64_t)M - 1);  // rows past M read a valid table row
+            raw[b] = *reinterpret_cast<const u32x4*>(tile + r * 512 + ((ch ^ (r & 31)) << 4));
+            const int64_t rr = P.rope_row0 + mc;
+            const float* cp = args.rope_cos + rr * 128 + d;
+            const float* sp = args.rope_sin + rr * 128 + d;
+            c[b][0] = *reinterpret_cast<const f32x4*>(cp);
+            c[b][1] = *reinterpret_cast<const f32x4*>(cp + 4);
+            sn[b][0] = *reinterpret_cast<const f32x4*>(sp);
+            sn[b][1] = *reinterpret_cast<const f32x4*>(sp + 4);
+          }
+#pragma unroll
+          for (int b = 0; b < RB; ++b) {
+            const int r = wave * 2 + half + (t0 + b) * 2 * NWAVES;
+            const int64_t m = m0 + r;
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v[2 * e] = bf16bits_to_f32(raw[b][e] & 0xffffu);
+              v[2 * e + 1] = bf16bits_to_f32(raw[b][e] >> 16);
+            }
+            float ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+            ss = sum16_dpp(ss);  // 16 lanes hold one head of one row
+            const float rs = __builtin_amdgcn_rsqf(ss * (1.0f / 128.0f) + args.qk_eps);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v[2 * e] = v[2 * e] * rs * bf16bits_to_f32(wraw[e] & 0xffffu);
+              v[2 * e + 1] = v[2 * e + 1] * rs * bf16bits_to_f32(wraw[e] >> 16);
+            }
+            const float* cf = reinterpret_cast<const float*>(&c[b][0]);
+            const float* sf = reinterpret_cast<const float*>(&sn[b][0]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float a0 = v[2 * e], b0 = v[2 * e + 1];
+              if (law0) {
+                v[2 * e] = a0 * cf[2 * e] - b0 * sf[2 * e];
+                v[2 * e + 1] = b0 * cf[2 * e + 1] + a0 * sf[2 * e + 1];
+              } else {
+                v[2 * e] = a0 * cf[2 * e] - b0 * sf[2 * e + 1];
+                v[2 * e + 1] = a0 * sf[2 * e + 1] + b0 * cf[2 * e];
+              }
+            }
+            if (m < M) {
+              u32x4 st;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) st[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+              *reinterpret_cast<u32x4*>(reinterpret_cast<bf16*>(P.c) + m * P.ldc + n0 + ch * 8) = st;
+            }
+          }
+        }
+      }
+      continue;  // this tile is stored
+    }
     const int ch = lane & 31, half = lane >> 5;  // 16-byte chunk of the row, which row of two
     const int64_t n = n0 + ch * 8;
     // 16-byte stores need 16-byte aligned rows; otherwise two 8-byte halves (N % 4 == 0)
