@@ -176,7 +176,10 @@ __device__ __forceinline__ int lds_off8(int row, int chunk) {
 }
 
 // WN = ElemTraits<E>::WN wavefronts along N, 2 along M: 128 WN threads.
-template <Elem E, int EPI, int WN, bool QK>
+// SPLIT: the launch uses the split schedule (workgroups may own several tiles or parts of
+// them). Whole-tile launches (SPLIT false, the DiT steps) hold no state across tiles, so the
+// K loop's addressing and the epilogue do not compete for registers with a tile loop.
+template <Elem E, int EPI, int WN, bool QK, bool SPLIT>
 __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) {
   constexpr int KT = ElemTraits<E>::KT;
   constexpr int EB = ElemTraits<E>::BYTES;
@@ -205,9 +208,9 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
   const SkPlan& plan = args.sk;
   const int nk = args.k / KT, nu = plan.nu;
   int bid = blockIdx.x;
-  int s_self = -1;  // split workgroup index
+  [[maybe_unused]] int s_self = -1;  // split workgroup index
   int64_t u_lo, u_hi;
-  if (bid < plan.dp) {  // XCD-contiguous runs of tiles
+  if (!SPLIT || bid < plan.dp) {  // XCD-contiguous runs of tiles
     if ((plan.dp & 7) == 0) bid = (bid & 7) * (plan.dp >> 3) + (bid >> 3);
     u_lo = (int64_t)bid * nu;
     u_hi = u_lo + nu;
@@ -217,9 +220,11 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
     u_hi = (int64_t)plan.dp * nu + sk_lo(plan, s_self + 1);
   }
   // the split-tile flag lives in the LDS ring, idle when it is used (one LDS variable, above)
-  volatile int& sk_flag = *reinterpret_cast<volatile int*>(lds);
+  [[maybe_unused]] volatile int& sk_flag = *reinterpret_cast<volatile int*>(lds);
 
-  for (int64_t u = u_lo; u < u_hi;) {
+  bool more = true;  // whole-tile launches run the body once
+  for (int64_t u = u_lo; more && u < u_hi;) {
+  if constexpr (!SPLIT) more = false;
   const int tt = (int)(u / nu);  // tile
   const int ub = (int)(u - (int64_t)tt * nu), ue = (int)(min(u_hi, (int64_t)(tt + 1) * nu) - (int64_t)tt * nu);
   // its K stages [kbeg, kend) run here; the loop below counts them from 0
@@ -571,7 +576,7 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
   // Partial sums move through the workspace with device-scope (sc1) loads and stores, which
   // the L2 of another XCD cannot serve stale; a store is complete (vmcnt) before its workgroup
   // counts itself, so a count read at device scope orders them without cache-wide fences.
-  if (kbeg != 0 || kend != nk) {
+  if constexpr (SPLIT) if (kbeg != 0 || kend != nk) {
     const int tl = tt - plan.dp;  // tile index within the split part
     const int64_t x0 = (int64_t)tl * nu;
     const int c0 = sk_owner(plan, x0), c1 = sk_owner(plan, x0 + nu - 1);
@@ -1068,26 +1073,31 @@ static int gemm_launch(const char* name, int nproblems, const difflet_gemm_probl
   args.ws = (uint8_t*)workspace;
   constexpr int NT = ElemTraits<E>::WN;
   dim3 grid((unsigned)(args.sk.dp + args.sk.groups)), block(128 * NT);
+  const bool split = args.sk.groups > 0;
+  auto go = [&](auto epi, auto fused) {
+    constexpr int EP = decltype(epi)::value;
+    constexpr bool Q = decltype(fused)::value;
+    if (split)
+      hipLaunchKernelGGL((gemm_kernel<E, EP, NT, Q, true>), grid, block, 0, stream, args);
+    else
+      hipLaunchKernelGGL((gemm_kernel<E, EP, NT, Q, false>), grid, block, 0, stream, args);
+  };
+  using std::integral_constant;
   switch (epilogue * 2 + (qk ? 1 : 0)) {
     case 2 * DIFFLET_EPI_NONE:
-      hipLaunchKernelGGL((gemm_kernel<E, DIFFLET_EPI_NONE, NT, false>), grid, block, 0, stream,
-                         args);
+      go(integral_constant<int, DIFFLET_EPI_NONE>{}, std::false_type{});
       break;
     case 2 * DIFFLET_EPI_NONE + 1:
-      hipLaunchKernelGGL((gemm_kernel<E, DIFFLET_EPI_NONE, NT, true>), grid, block, 0, stream,
-                         args);
+      go(integral_constant<int, DIFFLET_EPI_NONE>{}, std::true_type{});
       break;
     case 2 * DIFFLET_EPI_GELU:
-      hipLaunchKernelGGL((gemm_kernel<E, DIFFLET_EPI_GELU, NT, false>), grid, block, 0, stream,
-                         args);
+      go(integral_constant<int, DIFFLET_EPI_GELU>{}, std::false_type{});
       break;
     case 2 * DIFFLET_EPI_GELU + 1:
-      hipLaunchKernelGGL((gemm_kernel<E, DIFFLET_EPI_GELU, NT, true>), grid, block, 0, stream,
-                         args);
+      go(integral_constant<int, DIFFLET_EPI_GELU>{}, std::true_type{});
       break;
     default:
-      hipLaunchKernelGGL((gemm_kernel<E, DIFFLET_EPI_GATE_RESIDUAL, NT, false>), grid, block, 0,
-                         stream, args);
+      go(integral_constant<int, DIFFLET_EPI_GATE_RESIDUAL>{}, std::false_type{});
       break;
   }
   return dlt_check_launch(name);

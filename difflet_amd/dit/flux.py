@@ -141,6 +141,9 @@ class FluxDiT(JointDiT):
                        for i in range(cfg.n_single)]
         self._bufs: dict = {}
         self._rope: dict = {}
+        #: per linear kind, whether the single block's q/k RMSNorm + RoPE runs in the W1 GEMM's
+        #: epilogue (else as one launch after it)
+        self.fuse_single_qk = {"bf16": True, "fp8": True, "mx": True}
         #: optional timing hook: probe(name) returns a context manager recording HIP events
         #: around a launch on the current stream (used by the benchmark, None otherwise)
         self.probe = None
@@ -169,14 +172,21 @@ class FluxDiT(JointDiT):
 
     def single_block(self, i: int, bufs, mod, cos, sin):
         blk = self.single[i]
-        d = self.cfg.hidden
+        c = self.cfg
+        d = c.hidden
         h, n, big = bufs["h"], bufs["n"], bufs["big"]
         sh, sc, g = self._mods(mod, self.mod_off[("s", i)], 3)
         p = self._ln(bufs, slice(0, h.shape[0]), sc, sh, blk.w1.kind == "fp8")
-        # [k | v | q | mlp]: GELU on the MLP columns, q/k RMSNorm + RoPE in the same epilogue
+        # [k | v | q | mlp]: GELU on the MLP columns, q/k RMSNorm + RoPE in the same epilogue or
+        # in one launch after it (self.fuse_single_qk)
+        fuse = self.fuse_single_qk[blk.w1.kind]
         self._gemm("gemm.single.w1",
                    [blk.w1.problem(n, big, prepared=p, norm_q=blk.nq, norm_k=blk.nk)],
-                   blk.w1.kind, _lib.EPI_GELU, 3 * d, qk=self._qk_epilogue(2 * d, 0, cos, sin))
+                   blk.w1.kind, _lib.EPI_GELU, 3 * d,
+                   qk=self._qk_epilogue(2 * d, 0, cos, sin) if fuse else None)
+        if not fuse:
+            kernels.qk_norm_rope(big, heads=c.heads, head_dim=c.head_dim, q_off=2 * d, k_off=0,
+                                 wq=blk.nq, wk=blk.nk, eps=EPS, cos=cos, sin=sin, law=0)
         self._attn(big, 2 * d, 0, d)
         self._gemm("gemm.single.w2", [blk.w2.problem(big[:, 2 * d:], h, gate=g, residual=h)],
                    blk.w2.kind, _lib.EPI_GATE_RESIDUAL)
