@@ -12,8 +12,10 @@ attention.py:8-48; the CUDA twin difflet/backends/cuda/ops_impl/attention.py:41-
 * Inputs ``(B, H, S, D)`` or ``(B*H, S, D)``, any strides with a contiguous last dim; softmax in
   fp32, output in ``v``'s dtype.
 
-The kernel runs bf16 and fp16 at head_dim 128; other dtypes / head dims raise
-NotImplementedError (no silent fallback to another implementation).
+The kernels run bf16 and fp16 on the matrix cores and fp32 on the vector ALUs (an fp32 model
+computes in fp32, as the reference's CPU op does), at head_dim 128 (the DiTs) or 64 (the T5 /
+UMT5 text encoders); other dtypes / head dims raise NotImplementedError (no silent fallback to
+another implementation).
 
 The context-parallel forms run their cp = 1 degenerate case (plain attention over the local,
 here whole, sequence: difflet/backends/cpu/ops_impl/attention.py:55-143); cp > 1 raises.
@@ -25,7 +27,8 @@ import torch
 
 from difflet_amd.backends.rocm.ops_impl import library
 
-_SUPPORTED = (torch.bfloat16, torch.float16)
+_SUPPORTED = (torch.bfloat16, torch.float16, torch.float32)
+_HEAD_DIMS = (64, 128)
 
 
 def _check(q, k, v):
@@ -34,9 +37,9 @@ def _check(q, k, v):
             raise ValueError(f"rocm attention takes device tensors, got one on {t.device}")
     if q.dtype not in _SUPPORTED:
         raise NotImplementedError(
-            f"rocm attention runs bf16 / fp16 on the HIP kernel; got {q.dtype}")
-    if q.shape[-1] != 128:
-        raise NotImplementedError(f"rocm attention supports head_dim 128, got {q.shape[-1]}")
+            f"rocm attention runs bf16 / fp16 / fp32 on the HIP kernels; got {q.dtype}")
+    if q.shape[-1] not in _HEAD_DIMS:
+        raise NotImplementedError(f"rocm attention supports head_dim 64 and 128, got {q.shape[-1]}")
 
 
 def attention(q, k, v, *, scale: float | None = None, causal: bool = False,
@@ -49,7 +52,7 @@ def attention(q, k, v, *, scale: float | None = None, causal: bool = False,
         raise ValueError("attention_mask and bounds are mutually exclusive")
     _check(q, k, v)
     scale = 1.0 if scale is None else float(scale)
-    if attention_mask is not None and attention_mask.dtype not in (torch.bool,) + _SUPPORTED + (torch.float32,):
+    if attention_mask is not None and attention_mask.dtype not in (torch.bool,) + _SUPPORTED:
         attention_mask = attention_mask.to(q.dtype)
     return library.attention(q, k, v, scale, bool(causal), attention_mask, bound_min, bound_max)
 

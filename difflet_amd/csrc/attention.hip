@@ -34,6 +34,7 @@
 // masked row averages V, as softmax over equal finfo.min scores does); keys past seq_k do not
 // exist and take -inf.
 #include <mutex>
+#include <type_traits>
 
 #include "common.hpp"
 #include <float.h>
@@ -138,11 +139,17 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
 }
 
-template <typename T, bool MASKED>
+// D: head dim, 128 or 64 (T5 / UMT5 encoders). The K tile's row pitch is D * 2 + 16 bytes.
+template <typename T, bool MASKED, int D>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
   typedef typename MfmaT<T>::frag frag;
-  __shared__ __attribute__((aligned(16))) uint8_t sk[2][BLOCK_N * K_PITCH];
-  __shared__ __attribute__((aligned(16))) uint8_t sv[2][HD * VT_PITCH];
+  constexpr int KP = D * 2 + 16;      // K row pitch
+  constexpr int NC = D / 16;          // Q fragments (16 dims each)
+  constexpr int NDT = D / 32;         // 32-dim output tiles
+  constexpr int KCH = D / 8;          // 16-byte chunks per K row
+  __shared__ __attribute__((aligned(16))) uint8_t sk[2][BLOCK_N * KP];
+  __shared__ __attribute__((aligned(16))) uint8_t sv[2][D * VT_PITCH];
+  auto kofs = [](int row, int chunk) { return row * KP + (chunk << 4); };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 31, g = lane >> 5;
@@ -163,12 +170,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
   const int64_t qrow = a.qs[2] * 2, krow = a.ks[2] * 2, vrow = a.vs[2] * 2;
 
   // ---- Q fragments (second MFMA operand): lane holds q row my_q, dims 16c + 8g .. +8
-  frag qf[8];
+  frag qf[NC];
   {
     const __amdgpu_buffer_rsrc_t rq =
         make_rsrc(qp, (uint32_t)min((int64_t)a.seq_q * qrow, (int64_t)0xffffffff));
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
+    for (int c = 0; c < NC; ++c) {
       // rows past seq_q lie past the resource's range and read zero
       qf[c] = __builtin_bit_cast(frag, buf_load16(rq, (uint32_t)(my_q * qrow) + (c * 16 + g * 8) * 2));
     }
@@ -179,24 +186,31 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
   const __amdgpu_buffer_rsrc_t rv =
       make_rsrc(vp, (uint32_t)min((int64_t)a.seq_k * vrow, (int64_t)0xffffffff));
 
-  // staging: K rows (t/16 + 16 i), chunk t % 16; V keys 4 (t % 16) + i, dims 8 (t / 16) .. +8
-  const int kr = tid >> 4, kc = tid & 15;
+  // staging: K rows (t / KCH + (256 / KCH) i), chunk t % KCH; V keys 4 (t % 16) + i, dims
+  // 8 (t / 16) .. +8 (threads past the head's D / 8 dim groups move no V)
+  constexpr int KRI = 256 / KCH, NKI = BLOCK_N / KRI;  // K rows per pass, passes
+  const int kr = tid / KCH, kc = tid % KCH;
   const int vkg = tid & 15, vdg = tid >> 4;
+  const bool v_on = vdg < D / 8;
   const int vt_pos = vt_quad_pos(vkg) * 8;  // byte offset of this thread's key quad in a V^T row
-  u32x4 gk[4], gv[4];
+  u32x4 gk[NKI], gv[4];
   auto load_tile = [&](int j0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = j0 + kr + 16 * i;
+    for (int i = 0; i < NKI; ++i) {
+      const int key = j0 + kr + KRI * i;
       gk[i] = buf_load16(rk, (uint32_t)(key * krow) + kc * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
       const int vkey = j0 + vkg * 4 + i;
-      gv[i] = buf_load16(rv, (uint32_t)(vkey * vrow) + vdg * 16);
+      gv[i] = v_on ? buf_load16(rv, (uint32_t)(vkey * vrow) + vdg * 16) : u32x4{0u, 0u, 0u, 0u};
     }
   };
   auto store_tile = [&](int st) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<u32x4*>(&sk[st][k_off(kr + 16 * i, kc)]) = gk[i];
+    for (int i = 0; i < NKI; ++i)
+      *reinterpret_cast<u32x4*>(&sk[st][kofs(kr + KRI * i, kc)]) = gk[i];
+    if (!v_on) return;
     // transpose: for each of the 8 dims, the 4 keys' 16-bit values side by side
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
@@ -210,9 +224,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
     }
   };
 
-  f32x16 acc[4];
+  f32x16 acc[NDT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) acc[i] = f32x16{};
+  for (int i = 0; i < NDT; ++i) acc[i] = f32x16{};
   float m_run = -INFINITY, l_run = 0.f;
 
   int bmin = 0, bmax = a.seq_k;
@@ -237,9 +251,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
     for (int kt2 = 0; kt2 < 2; ++kt2) {
       s[kt2] = f32x16{};
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
+      for (int c = 0; c < NC; ++c) {
         const frag kf =
-            *reinterpret_cast<const frag*>(&sk[st][k_off(kt2 * 32 + col, c * 2 + g)]);
+            *reinterpret_cast<const frag*>(&sk[st][kofs(kt2 * 32 + col, c * 2 + g)]);
         s[kt2] = MfmaT<T>::mma(kf, qf[c], s[kt2]);
       }
     }
@@ -306,7 +320,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
     l_run = l_run * alpha + ls;
     if (__any(alpha != 1.0f)) {  // the running max moved for some query of this wave
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < NDT; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][v] *= alpha;
     }
@@ -322,7 +336,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
         for (int u = 0; u < 4; ++u) pb[u] = pp[kt2][hh * 4 + u];
         const frag pf = __builtin_bit_cast(frag, pb);
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
+        for (int dt = 0; dt < NDT; ++dt) {
           const frag vf = *reinterpret_cast<const frag*>(
               &sv[st][(dt * 32 + col) * VT_PITCH + (base + g * 8) * 2]);
           acc[dt] = MfmaT<T>::mma(vf, pf, acc[dt]);
@@ -339,7 +353,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
   if (my_q < a.seq_q) {
     T* op = reinterpret_cast<T*>(a.o) + b * a.os[0] + h * a.os[1] + (int64_t)my_q * a.os[2];
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         u32x2 w;
@@ -722,6 +736,101 @@ extern "C" int64_t difflet_rocm_attention_workspace_bytes(void) {
   return cus > 0 ? att_workspace_bytes(cus) : 0;
 }
 
+// ---- fp32 inputs (models run in fp32, as the reference's CPU op computes them): scores,
+// softmax and P V in fp32 on the VALU, one query per lane, 256 queries per workgroup. K and V
+// tiles of 32 keys go through LDS and are read by every lane at the same address (broadcast).
+// Online softmax per lane over each tile; masks, bounds, causal and scale as the MFMA kernels.
+constexpr int F32_TILE = 32;
+template <int D>
+__global__ __launch_bounds__(256, 1) void attn_f32_kernel(const AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) float skk[F32_TILE][D];
+  __shared__ __attribute__((aligned(16))) float svv[F32_TILE][D];
+  const int tid = threadIdx.x;
+  const int bh = blockIdx.x / a.q_tiles, qt = blockIdx.x % a.q_tiles;
+  const int b = bh / a.heads, h = bh % a.heads;
+  const int my_q = qt * 256 + tid;
+  const bool qok = my_q < a.seq_q;
+  const float* qp = reinterpret_cast<const float*>(a.q) + b * a.qs[0] + h * a.qs[1];
+  const float* kp = reinterpret_cast<const float*>(a.k) + b * a.ks[0] + h * a.ks[1];
+  const float* vp = reinterpret_cast<const float*>(a.v) + b * a.vs[0] + h * a.vs[1];
+  float q[D], o[D];
+#pragma unroll
+  for (int d = 0; d < D; d += 4) {
+    const f32x4 x = qok ? *reinterpret_cast<const f32x4*>(qp + (int64_t)my_q * a.qs[2] + d)
+                        : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      q[d + e] = x[e];
+      o[d + e] = 0.f;
+    }
+  }
+  int bmin = 0, bmax = a.seq_k;
+  if (a.bmin && qok) {
+    bmin = a.bmin[b * a.bs[0] + h * a.bs[1] + (int64_t)my_q * a.bs[2]];
+    bmax = a.bmax[b * a.bs[0] + h * a.bs[1] + (int64_t)my_q * a.bs[2]];
+  }
+  const float scale = a.scale_log2 / LOG2E;
+  float m_run = -INFINITY, l_run = 0.f;
+  for (int j0 = 0; j0 < a.seq_k; j0 += F32_TILE) {
+    __syncthreads();  // the previous tile's reads are done
+    for (int i = tid; i < F32_TILE * D / 4; i += 256) {
+      const int key = j0 + i / (D / 4), d = (i % (D / 4)) * 4;
+      f32x4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
+      if (key < a.seq_k) {
+        kv = *reinterpret_cast<const f32x4*>(kp + (int64_t)key * a.ks[2] + d);
+        vv = *reinterpret_cast<const f32x4*>(vp + (int64_t)key * a.vs[2] + d);
+      }
+      *reinterpret_cast<f32x4*>(&skk[i / (D / 4)][d]) = kv;
+      *reinterpret_cast<f32x4*>(&svv[i / (D / 4)][d]) = vv;
+    }
+    __syncthreads();
+    float sc[F32_TILE];
+    float mx = -INFINITY;
+#pragma unroll 4
+    for (int j = 0; j < F32_TILE; ++j) {
+      const int key = j0 + j;
+      float dot = 0.f;
+#pragma unroll
+      for (int d = 0; d < D; ++d) dot += q[d] * skk[j][d];
+      float x = dot * scale;
+      bool masked = key < bmin || key >= bmax || (a.causal && key > my_q);
+      if (a.mask && !masked && key < a.seq_k && qok) {
+        const int64_t mo = b * a.ms[0] + h * a.ms[1] + (int64_t)my_q * a.ms[2] +
+                           (int64_t)key * a.ms[3];
+        if (a.mask_dtype == DIFFLET_BOOL) masked = reinterpret_cast<const uint8_t*>(a.mask)[mo] == 0;
+        else if (a.mask_dtype == DIFFLET_F32) x += reinterpret_cast<const float*>(a.mask)[mo];
+        else if (a.mask_dtype == DIFFLET_BF16) x += bf16_to_f32(reinterpret_cast<const bf16*>(a.mask)[mo]);
+        else x += (float)reinterpret_cast<const f16*>(a.mask)[mo];
+      }
+      x = masked ? -FLT_MAX : x;
+      if (key >= a.seq_k) x = -INFINITY;  // keys past seq_k do not exist
+      sc[j] = x;
+      mx = fmaxf(mx, x);
+    }
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = __expf(m_run - m_use);
+    m_run = m_new;
+    l_run *= alpha;
+#pragma unroll
+    for (int d = 0; d < D; ++d) o[d] *= alpha;
+#pragma unroll 4
+    for (int j = 0; j < F32_TILE; ++j) {
+      const float p = __expf(sc[j] - m_use);
+      l_run += p;
+#pragma unroll
+      for (int d = 0; d < D; ++d) o[d] += p * svv[j][d];
+    }
+  }
+  if (qok) {
+    float* op = reinterpret_cast<float*>(a.o) + b * a.os[0] + h * a.os[1] + (int64_t)my_q * a.os[2];
+    const float inv = 1.0f / l_run;
+#pragma unroll
+    for (int d = 0; d < D; d += 4)
+      *reinterpret_cast<f32x4*>(op + d) = f32x4{o[d] * inv, o[d + 1] * inv, o[d + 2] * inv, o[d + 3] * inv};
+  }
+}
+
 // Counters of the split schedule back to zero before a launch that uses them (a fill kernel,
 // not a memset node, so the pair can be captured into a graph).
 __global__ void att_zero_counters(int* __restrict__ ctr, int n) {
@@ -743,10 +852,10 @@ static int attention_impl(const char* name, const void* q, const void* k, const 
                           difflet_stream_t stream) {
   DLT_REQUIRE(q && k && v && o && q_strides && k_strides && v_strides && o_strides,
               DIFFLET_EINVAL, "attention: null pointer");
-  DLT_REQUIRE(dtype == DIFFLET_BF16 || dtype == DIFFLET_F16, DIFFLET_EUNSUPPORTED,
-              "attention: dtype %d unsupported (bf16 and fp16 only)", dtype);
-  DLT_REQUIRE(head_dim == HD, DIFFLET_EUNSUPPORTED, "attention: head_dim %lld unsupported (128)",
-              (long long)head_dim);
+  DLT_REQUIRE(dtype == DIFFLET_BF16 || dtype == DIFFLET_F16 || dtype == DIFFLET_F32,
+              DIFFLET_EUNSUPPORTED, "attention: dtype %d unsupported (bf16, fp16, fp32)", dtype);
+  DLT_REQUIRE(head_dim == HD || head_dim == 64, DIFFLET_EUNSUPPORTED,
+              "attention: head_dim %lld unsupported (128 or 64)", (long long)head_dim);
   DLT_REQUIRE(batch >= 0 && heads >= 0 && seq_q >= 0 && seq_k >= 0, DIFFLET_EINVAL,
               "attention: negative size");
   DLT_REQUIRE(seq_q < (1 << 24) && seq_k < (1 << 24) && batch * heads < (1 << 24),
@@ -761,15 +870,16 @@ static int attention_impl(const char* name, const void* q, const void* k, const 
               DIFFLET_EINVAL, "attention: bad mask");
   const int64_t* ss[4] = {q_strides, k_strides, v_strides, o_strides};
   const void* ps[4] = {q, k, v, o};
+  const int64_t elem_align = dtype == DIFFLET_F32 ? 4 : 8;  // elements per 16 bytes
   for (int i = 0; i < 4; ++i) {
-    DLT_REQUIRE(ss[i][2] % 8 == 0 && ss[i][1] % 8 == 0 && ss[i][0] % 8 == 0 &&
-                    ((uintptr_t)ps[i] & 15) == 0,
-                DIFFLET_EINVAL, "attention: rows must be 16-byte aligned (strides %% 8 == 0)");
+    DLT_REQUIRE(ss[i][2] % elem_align == 0 && ss[i][1] % elem_align == 0 &&
+                    ss[i][0] % elem_align == 0 && ((uintptr_t)ps[i] & 15) == 0,
+                DIFFLET_EINVAL, "attention: rows must be 16-byte aligned");
   }
   // queries up to one workgroup tile (256) and keys up to two K/V tiles past the end are
   // addressed (and read as zero through the buffer range check), so those byte offsets must
-  // fit 32 bits
-  DLT_REQUIRE((seq_q + 256) * q_strides[2] * 2 < (1LL << 32) &&
+  // fit 32 bits (the fp32 kernel uses 64-bit addresses)
+  DLT_REQUIRE(dtype == DIFFLET_F32 || (seq_q + 256) * q_strides[2] * 2 < (1LL << 32) &&
                   (seq_k + 128) * k_strides[2] * 2 < (1LL << 32) &&
                   (seq_k + 128) * v_strides[2] * 2 < (1LL << 32),
               DIFFLET_EUNSUPPORTED, "attention: one head's sequence exceeds 4 GiB");
@@ -794,7 +904,7 @@ static int attention_impl(const char* name, const void* q, const void* k, const 
   // kernel pays a few tiles of pipeline fill, so short key sequences (cross-attention to text)
   // run the single-group kernel
   const bool masked = causal || mask || bound_min || !(scale > 0.0f);
-  const bool pingpong = !masked && seq_k > 1024;
+  const bool pingpong = head_dim == HD && !masked && seq_k > 1024;
   const int qblock = pingpong ? 2 * BLOCK_M : BLOCK_M;  // queries per workgroup
   args.q_tiles = (int)((seq_q + qblock - 1) / qblock);
   const int64_t total = (int64_t)args.q_tiles * batch * heads;
@@ -811,6 +921,17 @@ static int attention_impl(const char* name, const void* q, const void* k, const 
   if (bound_min)
     for (int i = 0; i < 3; ++i) args.bs[i] = bound_strides[i];
   hipStream_t s = (hipStream_t)stream;
+  if (dtype == DIFFLET_F32) {
+    args.q_tiles = (int)((seq_q + 255) / 256);
+    const int64_t t32 = (int64_t)args.q_tiles * batch * heads;
+    DLT_REQUIRE(t32 < (1LL << 31), DIFFLET_EUNSUPPORTED, "%s: too many tiles", name);
+    args.total = (int)t32;
+    if (head_dim == 64)
+      hipLaunchKernelGGL((attn_f32_kernel<64>), dim3((unsigned)t32), dim3(256), 0, s, args);
+    else
+      hipLaunchKernelGGL((attn_f32_kernel<128>), dim3((unsigned)t32), dim3(256), 0, s, args);
+    return dlt_check_launch(name);
+  }
   dim3 grid((unsigned)total);
   if (pingpong && workspace) {
     // split schedule when the last wave of workgroups would leave > 10 % of the CUs idle
@@ -831,14 +952,22 @@ static int attention_impl(const char* name, const void* q, const void* k, const 
       }
     }
   }
+  auto fwd = [&](auto t, auto d) {
+    using TT = decltype(t);
+    constexpr int DD = decltype(d)::value;
+    if (masked) hipLaunchKernelGGL((attn_fwd_kernel<TT, true, DD>), grid, dim3(256), 0, s, args);
+    else hipLaunchKernelGGL((attn_fwd_kernel<TT, false, DD>), grid, dim3(256), 0, s, args);
+  };
+  using D64 = std::integral_constant<int, 64>;
+  using D128 = std::integral_constant<int, 128>;
   if (dtype == DIFFLET_BF16) {
     if (pingpong) hipLaunchKernelGGL((attn_pp_kernel<bf16>), grid, dim3(512), 0, s, args);
-    else if (masked) hipLaunchKernelGGL((attn_fwd_kernel<bf16, true>), grid, dim3(256), 0, s, args);
-    else hipLaunchKernelGGL((attn_fwd_kernel<bf16, false>), grid, dim3(256), 0, s, args);
+    else if (head_dim == 64) fwd(bf16{}, D64{});
+    else fwd(bf16{}, D128{});
   } else {
     if (pingpong) hipLaunchKernelGGL((attn_pp_kernel<f16>), grid, dim3(512), 0, s, args);
-    else if (masked) hipLaunchKernelGGL((attn_fwd_kernel<f16, true>), grid, dim3(256), 0, s, args);
-    else hipLaunchKernelGGL((attn_fwd_kernel<f16, false>), grid, dim3(256), 0, s, args);
+    else if (head_dim == 64) fwd(f16{}, D64{});
+    else fwd(f16{}, D128{});
   }
   return dlt_check_launch(name);
 }

@@ -50,7 +50,7 @@ def test_ops_attention_forms(gpu):
     ref_u = ops.attention(qf, keys, vals, scale=sc)
     assert rel_l2(torch.cat([oi, ot], dim=2), ref_u) < 1e-2
     with pytest.raises(NotImplementedError):
-        A.attention(q.float().to(gpu), k.float().to(gpu), v.float().to(gpu))
+        A.attention(q.double().to(gpu), k.double().to(gpu), v.double().to(gpu))
 
 
 @pytest.mark.parametrize("m,k,n", [(3, 3072, 500), (300, 256, 128), (77, 100, 30)])

@@ -688,3 +688,75 @@ def test_attention_matches_the_reference_cpu_op_vectors(gpu):
         e = rel_l2(out, want)
         print(f"  rel L2 {e:.3e}", flush=True)
         assert e < 2e-2, name
+
+
+def test_attention_fp32_matches_the_reference_cpu_op_vectors(gpu):
+    """fp32 inputs run the fp32 kernel: every contract form against the reference CPU op's own
+    fp32 output (tests/golden/attention_reference.json), to fp32 summation-order error."""
+    import json
+    from pathlib import Path
+
+    from tests.golden.make_attention_golden import cases, decode
+
+    g = json.loads((Path(__file__).parent / "golden" / "attention_reference.json").read_text())
+    for name, ((q, k, v), kw) in cases(torch.float32).items():
+        print(f"fp32 attention vs reference vectors: {name}", flush=True)
+        kw = {key: (val.to(gpu) if torch.is_tensor(val) else val) for key, val in kw.items()}
+        kw.setdefault("scale", 1.0)
+        out = kernels.attention(q.to(gpu), k.to(gpu), v.to(gpu), **kw)
+        torch.cuda.synchronize()
+        want = decode(g[f"{name}.float32"])
+        assert out.dtype == torch.float32 and tuple(out.shape) == tuple(want.shape), name
+        e = rel_l2(out, want)
+        assert e < 1e-5, f"{name}: rel L2 {e:.3e}"
+
+
+# the T5 / UMT5 text encoders' attention: head_dim 64, unscaled scores plus a relative-position
+# bias (an additive [1, H, S, S] mask), key padding as a bool mask; ragged query/key counts
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("b,h,sq,sk", [(1, 2, 1, 1), (2, 3, 77, 77), (1, 4, 512, 512),
+                                       (1, 2, 300, 1100)])
+def test_attention_head_dims_and_fp32(gpu, dtype, d, b, h, sq, sk):
+    print(f"attention d={d} {dtype} b={b} h={h} sq={sq} sk={sk}", flush=True)
+    g = torch.Generator().manual_seed(d + sq + sk)
+    q, k, v = _attn_case(g, b, h, sq, sk, d=d, dtype=dtype)
+    qf, kf, vf = q.float(), k.float(), v.float()
+    tol = 2e-5 if dtype == torch.float32 else 1e-2
+    s = 1 / math.sqrt(d)
+    out = kernels.attention(q.to(gpu), k.to(gpu), v.to(gpu), scale=s)
+    assert out.dtype == dtype and out.shape == q.shape
+    assert rel_l2(out, ops.attention(qf, kf, vf, scale=s)) < tol
+    bias = torch.randn(1, h, sq, sk, generator=g) * 3.0
+    ref = ops.attention(qf, kf, vf, scale=1.0, attention_mask=bias)
+    out = kernels.attention(q.to(gpu), k.to(gpu), v.to(gpu), scale=1.0,
+                            attention_mask=bias.to(gpu))
+    assert rel_l2(out, ref) < tol
+    keep = torch.ones(b, 1, 1, sk, dtype=torch.bool)
+    keep[..., sk - sk // 3:] = False
+    keep[..., 0] = True
+    ref = ops.attention(qf, kf, vf, scale=s, attention_mask=keep)
+    out = kernels.attention(q.to(gpu), k.to(gpu), v.to(gpu), scale=s, attention_mask=keep.to(gpu))
+    assert rel_l2(out, ref) < tol
+    if sq == sk:
+        ref = ops.attention(qf, kf, vf, scale=s, causal=True)
+        out = kernels.attention(q.to(gpu), k.to(gpu), v.to(gpu), scale=s, causal=True)
+        assert rel_l2(out, ref) < tol
+
+
+def test_attention_fp32_bounds_strides_and_empty_windows(gpu):
+    """The fp32 kernel on column views of one [S, 3 H D] buffer with per-query key windows, an
+    empty window averaging v."""
+    g = torch.Generator().manual_seed(31)
+    s, h, d = 333, 3, 64
+    buf = torch.randn(s, 3 * h * d, generator=g)
+    views = [buf[:, i * h * d:(i + 1) * h * d].reshape(s, h, d).transpose(0, 1) for i in range(3)]
+    bmin = torch.randint(0, 100, (h, s, 1), generator=g, dtype=torch.int32)
+    bmax = bmin + torch.randint(1, 200, (h, s, 1), generator=g, dtype=torch.int32)
+    bmax[1, :7] = bmin[1, :7]
+    ref = ops.attention(*views, scale=0.1, bound_min=bmin, bound_max=bmax)
+    gb = buf.to(gpu)
+    gv = [gb[:, i * h * d:(i + 1) * h * d].reshape(s, h, d).transpose(0, 1) for i in range(3)]
+    out = kernels.attention(*gv, scale=0.1, bound_min=bmin.to(gpu), bound_max=bmax.to(gpu))
+    assert rel_l2(out, ref) < 2e-5
+    assert rel_l2(out[1, :7].cpu(), views[2][1].mean(dim=0).expand(7, -1)) < 2e-5
