@@ -107,6 +107,12 @@ SIGNATURES: dict[str, tuple] = {
                                  _i32, _vp]),
     "difflet_rocm_timestep_embedding": (_i32, [_vp, _vp, _i32, _i64, _i64, _i32, _f32, _f32,
                                                _f32, _vp]),
+    "difflet_rocm_gemm_f32": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _i64,
+                                     _i64, _i64, _vp]),
+    "difflet_rocm_gated_gelu": (_i32, [_vp, _i64, _vp, _i64, _i32, _i64, _i64, _vp]),
+    "difflet_rocm_embedding": (_i32, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp]),
+    "difflet_rocm_relative_bias": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i64, _i64, _vp,
+                                          _i64, _vp, _vp]),
 }
 
 _lib = None

@@ -72,6 +72,27 @@ def _(x, w, bias, out_features):
     return x.new_empty((x.shape[0], out_features), dtype=torch.bfloat16)
 
 
+@torch.library.custom_op("difflet_rocm::linear_f32", mutates_args=())
+def linear_f32(x: Tensor, w: Tensor, bias: Optional[Tensor], out_features: int) -> Tensor:
+    """y [M, out_features] fp32 = x [M, K'] @ w[:out_features, :K']^T + bias on the fp32 GEMM,
+    where w [N', K'] may be the zero-padded weight (K' and N' multiples of 4)."""
+    m, kx = x.shape
+    n_pad, k_pad = w.shape
+    if m == 0:
+        return x.new_empty((0, out_features), dtype=torch.float32)
+    if kx != k_pad:
+        x = F.pad(x, (0, k_pad - kx))
+    if bias is not None and bias.shape[0] != n_pad:
+        bias = F.pad(bias, (0, n_pad - bias.shape[0]))
+    y = kernels.gemm_f32(x.contiguous(), w, None if bias is None else bias.contiguous())
+    return y if n_pad == out_features else y[:, :out_features].contiguous()
+
+
+@linear_f32.register_fake
+def _(x, w, bias, out_features):
+    return x.new_empty((x.shape[0], out_features), dtype=torch.float32)
+
+
 @torch.library.custom_op("difflet_rocm::fp8_linear", mutates_args=())
 def fp8_linear(x: Tensor, w_kernel: Tensor, w_scale: Tensor, bias: Optional[Tensor],
                mx: bool) -> Tensor:

@@ -6,9 +6,11 @@ Same constructors, attributes, state dicts and bias semantics as the CPU twins
 ``(x @ W^T, bias)``; ``reduce_output`` / ``gather_output`` / ``input_is_parallel`` /
 ``reduce_dtype`` are accepted and have no effect at tp = 1.
 
-The matmul: bf16 weights; up to 8 rows of input go through the GEMV kernel (the modulation and
-timestep linears, HBM-bound on W), more through the tiled GEMM. A K that is not a multiple of
-64 or an N not a multiple of 4 is zero-padded once on the weight (and per call on the input).
+The matmul: bf16 weights run the bf16 kernels, up to 8 rows of input through the GEMV kernel
+(the modulation and timestep linears, HBM-bound on W), more through the tiled GEMM; fp32
+weights (a model loaded in fp32, such as the T5 encoders' fp32 option) run the fp32
+matrix-core GEMM, in fp32 throughout as F.linear does. A K or N off the kernel's multiples (64
+and 4 for bf16, 4 and 4 for fp32) is zero-padded once on the weight (and per call on the input).
 """
 
 from __future__ import annotations
@@ -47,7 +49,8 @@ class _RocmLinearBase(nn.Module):
     def _weight_for_gemm(self):
         w = self.weight
         k, n = self.in_features, self.out_features
-        kp, np_ = -(-k // 64) * 64, -(-n // 4) * 4
+        kq = 64 if w.dtype == torch.bfloat16 else 4
+        kp, np_ = -(-k // kq) * kq, -(-n // 4) * 4
         if kp == k and np_ == n:
             return w.detach(), k, n
         key = (w.data_ptr(), w._version)
@@ -61,8 +64,10 @@ class _RocmLinearBase(nn.Module):
         w = self.weight
         if x.device.type != "cuda" or w.device.type != "cuda":
             raise ValueError("rocm linear takes device tensors")
+        if w.dtype == torch.float32:
+            return self._matmul_f32(x, bias)
         if w.dtype != torch.bfloat16:
-            raise NotImplementedError(f"rocm linear runs bf16 weights, got {w.dtype}")
+            raise NotImplementedError(f"rocm linear runs bf16 or fp32 weights, got {w.dtype}")
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
         if x2.dtype != torch.bfloat16:
@@ -75,6 +80,17 @@ class _RocmLinearBase(nn.Module):
         # zero-padded to its tile multiples (built once, only for odd shapes)
         wg = w.detach() if library._gemv_fits(m, self.in_features) else self._weight_for_gemm()[0]
         y = library.linear(x2, wg, b, self.out_features)
+        return y.reshape(*shape[:-1], self.out_features).to(x.dtype)
+
+
+    def _matmul_f32(self, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1]).to(torch.float32)
+        m = x2.shape[0]
+        if m == 0:
+            return x.new_empty(*shape[:-1], self.out_features)
+        b = None if bias is None else bias.detach().to(torch.float32)
+        y = library.linear_f32(x2, self._weight_for_gemm()[0], b, self.out_features)
         return y.reshape(*shape[:-1], self.out_features).to(x.dtype)
 
 

@@ -70,6 +70,22 @@ struct AttnArgs {
   uint8_t* ws;
 };
 
+// One additive-mask entry (fp32, bf16 or fp16) at element offset mo.
+__device__ inline float load_mask(const AttnArgs& a, int64_t mo) {
+  if (a.mask_dtype == DIFFLET_F32) return reinterpret_cast<const float*>(a.mask)[mo];
+  if (a.mask_dtype == DIFFLET_BF16) return bf16_to_f32(reinterpret_cast<const bf16*>(a.mask)[mo]);
+  return (float)reinterpret_cast<const f16*>(a.mask)[mo];
+}
+
+// score + mask * unit (unit converts the mask to the score's units). A finite fill such as
+// finfo.min stays finite, as the reference's score + mask does in fp32: a sum that overflows
+// from a finite mask value is clamped to the lowest float, so a row whose every key carries the
+// fill averages v instead of dividing zero by zero. A -inf mask entry stays -inf.
+__device__ inline float add_mask(float x, float add, float unit) {
+  const float y = __builtin_fmaf(add, unit, x);
+  return (y == -INFINITY && add != -INFINITY) ? -FLT_MAX : y;
+}
+
 // Split schedule of the ping-pong kernel, for launches whose last wave of workgroups would leave
 // many compute units idle: one workgroup per compute unit, each taking an equal contiguous range
 // of the (query tile, key tile) units, query-tile-major. A query tile cut between workgroups
@@ -276,12 +292,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
                                (int64_t)key * a.ms[3];
             if (a.mask_dtype == DIFFLET_BOOL) {
               masked = reinterpret_cast<const uint8_t*>(a.mask)[mo] == 0;
-            } else if (a.mask_dtype == DIFFLET_F32) {
-              x += reinterpret_cast<const float*>(a.mask)[mo] * LOG2E;
-            } else if (a.mask_dtype == DIFFLET_BF16) {
-              x += bf16_to_f32(reinterpret_cast<const bf16*>(a.mask)[mo]) * LOG2E;
             } else {
-              x += (float)reinterpret_cast<const f16*>(a.mask)[mo] * LOG2E;
+              x = add_mask(x, load_mask(a, mo), LOG2E);
             }
           }
           s[kt2][v] = masked ? -FLT_MAX : x;
@@ -798,9 +810,7 @@ __global__ __launch_bounds__(256, 1) void attn_f32_kernel(const AttnArgs a) {
         const int64_t mo = b * a.ms[0] + h * a.ms[1] + (int64_t)my_q * a.ms[2] +
                            (int64_t)key * a.ms[3];
         if (a.mask_dtype == DIFFLET_BOOL) masked = reinterpret_cast<const uint8_t*>(a.mask)[mo] == 0;
-        else if (a.mask_dtype == DIFFLET_F32) x += reinterpret_cast<const float*>(a.mask)[mo];
-        else if (a.mask_dtype == DIFFLET_BF16) x += bf16_to_f32(reinterpret_cast<const bf16*>(a.mask)[mo]);
-        else x += (float)reinterpret_cast<const f16*>(a.mask)[mo];
+        else x = add_mask(x, load_mask(a, mo), 1.0f);
       }
       x = masked ? -FLT_MAX : x;
       if (key >= a.seq_k) x = -INFINITY;  // keys past seq_k do not exist

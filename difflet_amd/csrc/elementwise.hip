@@ -8,6 +8,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include <float.h>
 
 namespace dlt {
 
@@ -564,6 +565,75 @@ __global__ __launch_bounds__(256) void gelu_kernel(const T* __restrict__ x, T* _
     Elt<T>::store(y + i, gelu_tanh(Elt<T>::load(x + i)));
 }
 
+// ------------------------------------------------------------------ gated GELU
+// y[r, c] = gelu_tanh(x[r, c]) * x[r, f + c]: the T5 / UMT5 gated FFN's act(wi_0 h) * wi_1 h,
+// both projections computed by one GEMM into the two halves of x's rows.
+template <typename T>
+__global__ __launch_bounds__(256) void gated_gelu_kernel(const T* __restrict__ x, int64_t ldx,
+                                                         T* __restrict__ y, int64_t ldy,
+                                                         int64_t rows, int64_t f) {
+  const int64_t nvr = f / 8;
+  const int64_t nv = rows * nvr;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nv;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / nvr, c = (i % nvr) * 8;
+    float g[8], l[8];
+    V8<T>::load(x + r * ldx + c, g);
+    V8<T>::load(x + r * ldx + f + c, l);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) g[j] = gelu_tanh(g[j]) * l[j];
+    V8<T>::store(y + r * ldy + c, g);
+  }
+}
+
+// ------------------------------------------------------------------ embedding rows
+// out[i, :] = table[ids[i], :] as raw 16-byte pieces (any element type); an id outside
+// [0, table_rows) gives a zero row instead of a read past the table.
+__global__ __launch_bounds__(256) void embedding_kernel(const int64_t* __restrict__ ids,
+                                                        int64_t n, const uint8_t* __restrict__ table,
+                                                        int64_t table_rows, int64_t ldt,
+                                                        uint8_t* __restrict__ out, int64_t ldo,
+                                                        int64_t row_bytes) {
+  const int64_t nvr = row_bytes / 16;
+  const int64_t nv = n * nvr;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nv;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / nvr, c = (i % nvr) * 16;
+    const int64_t id = ids[r];
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (id >= 0 && id < table_rows) v = *reinterpret_cast<const u32x4*>(table + id * ldt + c);
+    *reinterpret_cast<u32x4*>(out + r * ldo + c) = v;
+  }
+}
+
+// ------------------------------------------------------------------ relative position bias
+// out[b, h, q, k] = table[bucket[k - q + seq_q - 1], h] (fp32), or the lowest float where
+// key k of batch element b is padding (key_keep[b, k] == 0): the T5 bias plus the additive
+// padding mask. A bucket outside [0, num_buckets) gives NaN rather than a read past the table.
+template <typename TT>
+__global__ __launch_bounds__(256) void relative_bias_kernel(
+    const int32_t* __restrict__ bucket, int num_buckets, const TT* __restrict__ table,
+    int64_t heads, int64_t batch, int64_t seq_q, int64_t seq_k,
+    const uint8_t* __restrict__ keep, int64_t keep_stride, float* __restrict__ out) {
+  const int64_t total = batch * heads * seq_q * seq_k;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t k = i % seq_k;
+    const int64_t q = (i / seq_k) % seq_q;
+    const int64_t bh = i / (seq_k * seq_q);
+    const int64_t h = bh % heads, b = bh / heads;
+    float v;
+    if (keep && keep[b * keep_stride + k] == 0) {
+      v = -FLT_MAX;
+    } else {
+      const int bk = bucket[k - q + seq_q - 1];
+      v = (bk >= 0 && bk < num_buckets) ? Elt<TT>::load(table + (int64_t)bk * heads + h)
+                                        : __builtin_nanf("");
+    }
+    out[i] = v;
+  }
+}
+
 // ------------------------------------------------------------------ gate * x + residual
 template <typename T, typename TG>
 __global__ __launch_bounds__(256) void gate_residual_kernel(
@@ -1010,6 +1080,65 @@ extern "C" int difflet_rocm_gate_residual(const void* residual, const void* x,
                          s, (const T*)residual, (const T*)x, (const TG*)gate, (T*)y, rows,
                          dim, gate_stride, rows_per_batch)));
   return dlt_check_launch("gate_residual");
+}
+
+extern "C" int difflet_rocm_gated_gelu(const void* x, int64_t ldx, void* y, int64_t ldy,
+                                       int dtype, int64_t rows, int64_t f,
+                                       difflet_stream_t stream) {
+  DLT_REQUIRE(x && y && rows >= 0 && f > 0, DIFFLET_EINVAL, "gated_gelu: bad arguments");
+  DLT_REQUIRE(f % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && ldx >= 2 * f && ldy >= f &&
+                  aligned16(x) && aligned16(y),
+              DIFFLET_EINVAL,
+              "gated_gelu: f and the row strides must be multiples of 8 (ldx >= 2 f, ldy >= f), "
+              "pointers 16-byte aligned");
+  if (rows == 0) return DIFFLET_OK;
+  int64_t blocks = (rows * f / 8 + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  DLT_DISPATCH_FLOAT(dtype, T,
+    hipLaunchKernelGGL((gated_gelu_kernel<T>), dim3((unsigned)blocks), dim3(256), 0,
+                       (hipStream_t)stream, (const T*)x, ldx, (T*)y, ldy, rows, f));
+  return dlt_check_launch("gated_gelu");
+}
+
+extern "C" int difflet_rocm_embedding(const int64_t* ids, int64_t n, const void* table,
+                                      int64_t table_rows, int64_t ldt_bytes, void* out,
+                                      int64_t ldo_bytes, int64_t row_bytes,
+                                      difflet_stream_t stream) {
+  DLT_REQUIRE(n >= 0 && table_rows > 0 && row_bytes > 0, DIFFLET_EINVAL,
+              "embedding: bad sizes");
+  if (n == 0) return DIFFLET_OK;
+  DLT_REQUIRE(ids && table && out, DIFFLET_EINVAL, "embedding: null pointer");
+  DLT_REQUIRE(row_bytes % 16 == 0 && ldt_bytes % 16 == 0 && ldo_bytes % 16 == 0 &&
+                  ldt_bytes >= row_bytes && ldo_bytes >= row_bytes && aligned16(table) &&
+                  aligned16(out),
+              DIFFLET_EINVAL, "embedding: rows must be 16-byte multiples and aligned");
+  int64_t blocks = (n * (row_bytes / 16) + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(embedding_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                     ids, n, (const uint8_t*)table, table_rows, ldt_bytes, (uint8_t*)out,
+                     ldo_bytes, row_bytes);
+  return dlt_check_launch("embedding");
+}
+
+extern "C" int difflet_rocm_relative_bias(const int32_t* buckets, int num_buckets,
+                                          const void* table, int table_dtype, int64_t heads,
+                                          int64_t batch, int64_t seq_q, int64_t seq_k,
+                                          const uint8_t* key_keep, int64_t keep_stride,
+                                          float* out, difflet_stream_t stream) {
+  DLT_REQUIRE(num_buckets > 0 && heads > 0 && batch >= 0 && seq_q >= 0 && seq_k >= 0,
+              DIFFLET_EINVAL, "relative_bias: bad sizes");
+  const int64_t total = batch * heads * seq_q * seq_k;
+  if (total == 0) return DIFFLET_OK;
+  DLT_REQUIRE(buckets && table && out, DIFFLET_EINVAL, "relative_bias: null pointer");
+  DLT_REQUIRE(!key_keep || keep_stride >= seq_k, DIFFLET_EINVAL,
+              "relative_bias: keep_stride shorter than seq_k");
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  DLT_DISPATCH_FLOAT(table_dtype, TT,
+    hipLaunchKernelGGL((relative_bias_kernel<TT>), dim3((unsigned)blocks), dim3(256), 0,
+                       (hipStream_t)stream, buckets, num_buckets, (const TT*)table, heads, batch,
+                       seq_q, seq_k, key_keep, keep_stride, out));
+  return dlt_check_launch("relative_bias");
 }
 
 template <typename T>

@@ -616,3 +616,92 @@ def timestep_embedding(t: torch.Tensor, dim: int, *, flip_sin_to_cos: bool,
                                                 float(max_period), _stream(dev)),
           "timestep_embedding")
     return y
+
+
+# ------------------------------------------------------------------------ text encoders
+def gemm_f32(a: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, *,
+             residual: torch.Tensor | None = None, out: torch.Tensor | None = None
+             ) -> torch.Tensor:
+    """A W^T (+ bias) (+ residual) in fp32 on the matrix cores: a [M, K], w [N, K], bias [N],
+    residual and out [M, N] (residual may be out). K and N multiples of 4."""
+    for name, t in (("a", a), ("w", w), ("bias", bias), ("residual", residual), ("out", out)):
+        if t is not None and t.dtype != torch.float32:
+            raise TypeError(f"gemm_f32: {name} must be fp32, got {t.dtype}")
+    if a.dim() != 2 or w.dim() != 2 or a.shape[1] != w.shape[1]:
+        raise ValueError(f"gemm_f32: a {tuple(a.shape)} and w {tuple(w.shape)} do not chain")
+    m, k = a.shape
+    n = w.shape[0]
+    if k % 4 or n % 4:
+        raise ValueError(f"gemm_f32: K ({k}) and N ({n}) must be multiples of 4")
+    if bias is not None and (bias.dim() != 1 or bias.shape[0] != n or bias.stride(0) != 1):
+        raise ValueError(f"gemm_f32: bias must be a contiguous [{n}] vector")
+    for name, t in (("residual", residual), ("out", out)):
+        if t is not None and (t.dim() != 2 or tuple(t.shape) != (m, n) or t.stride(1) != 1):
+            raise ValueError(f"gemm_f32: {name} must be [{m}, {n}] with contiguous rows")
+    dev = _on_gpu(a, w, bias, residual, out)
+    a2 = a if a.stride(1) == 1 and a.stride(0) % 4 == 0 else a.contiguous()
+    w2 = w if w.stride(1) == 1 and w.stride(0) % 4 == 0 else w.contiguous()
+    y = out if out is not None else torch.empty((m, n), dtype=torch.float32, device=dev)
+    check(lib().difflet_rocm_gemm_f32(_ptr(a2), a2.stride(0), _ptr(w2), w2.stride(0), _ptr(bias),
+                                      _ptr(residual),
+                                      residual.stride(0) if residual is not None else 0,
+                                      _ptr(y), y.stride(0), m, n, k, _stream(dev)), "gemm_f32")
+    return y
+
+
+def gated_gelu(x: torch.Tensor, f: int, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """gelu_tanh(x[:, :f]) * x[:, f:2f] for x [rows, >= 2f] with contiguous rows."""
+    if x.dim() != 2 or x.stride(1) != 1 or x.shape[1] < 2 * f:
+        raise ValueError(f"gated_gelu: x must be [rows, >= {2 * f}] with contiguous rows")
+    dev = _on_gpu(x, out)
+    y = out if out is not None else torch.empty((x.shape[0], f), dtype=x.dtype, device=dev)
+    if y.dtype != x.dtype or tuple(y.shape) != (x.shape[0], f) or y.stride(1) != 1:
+        raise ValueError("gated_gelu: out must match x's dtype and be [rows, f]")
+    check(lib().difflet_rocm_gated_gelu(_ptr(x), x.stride(0), _ptr(y), y.stride(0), _dt(x),
+                                        x.shape[0], f, _stream(dev)), "gated_gelu")
+    return y
+
+
+def embedding(ids: torch.Tensor, table: torch.Tensor) -> torch.Tensor:
+    """table[ids] for int64 ids (any shape) and a [rows, dim] table with contiguous rows. Ids
+    outside [0, rows) raise IndexError, as F.embedding does (checked before the gather)."""
+    if ids.dtype != torch.int64:
+        raise TypeError(f"embedding: ids must be int64, got {ids.dtype}")
+    if table.dim() != 2 or table.stride(1) != 1:
+        raise ValueError("embedding: table must be [rows, dim] with contiguous rows")
+    if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= table.shape[0]):
+        raise IndexError(f"embedding: ids outside [0, {table.shape[0]})")
+    dev = _on_gpu(table)
+    flat = ids.reshape(-1).to(dev).contiguous()
+    es = table.element_size()
+    y = torch.empty((flat.shape[0], table.shape[1]), dtype=table.dtype, device=dev)
+    check(lib().difflet_rocm_embedding(_ptr(flat), flat.shape[0], _ptr(table), table.shape[0],
+                                       table.stride(0) * es, _ptr(y), y.stride(0) * es,
+                                       table.shape[1] * es, _stream(dev)), "embedding")
+    return y.reshape(*ids.shape, table.shape[1])
+
+
+def relative_bias(buckets: torch.Tensor, table: torch.Tensor, *, batch: int, seq_q: int,
+                  seq_k: int, key_keep: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 [batch, heads, seq_q, seq_k] T5 position bias: table[buckets[k - q + seq_q - 1]]
+    per head (table [num_buckets, heads]); keys with key_keep[b, k] == 0 get the lowest float.
+    buckets: int32 [seq_q + seq_k - 1], values in [0, num_buckets)."""
+    if buckets.dtype != torch.int32 or buckets.dim() != 1 or buckets.shape[0] != seq_q + seq_k - 1:
+        raise ValueError(f"relative_bias: buckets must be int32 [{seq_q + seq_k - 1}]")
+    if table.dim() != 2 or not table.is_contiguous():
+        raise ValueError("relative_bias: table must be a contiguous [num_buckets, heads]")
+    if key_keep is not None and (tuple(key_keep.shape) != (batch, seq_k)
+                                 or key_keep.dtype not in (torch.bool, torch.uint8)):
+        raise ValueError(f"relative_bias: key_keep must be bool/uint8 [{batch}, {seq_k}]")
+    dev = _on_gpu(buckets, table, key_keep)
+    keep = None
+    if key_keep is not None:
+        keep = key_keep.contiguous()
+        keep = keep.view(torch.uint8) if keep.dtype == torch.bool else keep
+    nb, heads = table.shape
+    y = torch.empty((batch, heads, seq_q, seq_k), dtype=torch.float32, device=dev)
+    check(lib().difflet_rocm_relative_bias(_ptr(buckets.contiguous()), nb, _ptr(table), _dt(table),
+                                           heads, batch, seq_q, seq_k, _ptr(keep),
+                                           keep.stride(0) if keep is not None else 0, _ptr(y),
+                                           _stream(dev)), "relative_bias")
+    return y

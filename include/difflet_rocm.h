@@ -320,6 +320,46 @@ int difflet_rocm_timestep_embedding(const float* t, void* y, int dtype, int64_t 
                                     int64_t dim, int flip_sin_to_cos, float downscale_freq_shift,
                                     float scale, float max_period, difflet_stream_t stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Text encoders (T5-XXL for FLUX, UMT5-XXL for Wan): the steps before the denoise loop.
+ * ---------------------------------------------------------------------------------------- */
+/* C[m, :n] = A[m, :k] W[:n, :k]^T (+ bias[n]) (+ residual[m, n]), every operand fp32, on the
+ * fp32 matrix cores: the linears of a model loaded in fp32, which the reference runs as
+ * F.linear (ColumnParallelLinear / RowParallelLinear, difflet/backends/cpu/ops_impl/
+ * linear.py:9-41; the T5 FFN keeps `wo` in fp32: difflet/models/flux/t5/modeling_t5.py:139-149).
+ * k and n multiples of 4, leading dimensions multiples of 4, pointers 16-byte aligned; residual
+ * may alias c. */
+int difflet_rocm_gemm_f32(const float* a, int64_t lda, const float* w, int64_t ldw,
+                          const float* bias, const float* residual, int64_t ldr, float* c,
+                          int64_t ldc, int64_t m, int64_t n, int64_t k, difflet_stream_t stream);
+
+/* y[r, c] = gelu_tanh(x[r, c]) * x[r, f + c] for c < f: the gated FFN's act(wi_0(h)) * wi_1(h)
+ * with gelu_new (difflet/models/flux/t5/modeling_t5.py:133-136,
+ * difflet/models/wan/umt5/modeling_umt5.py:125-128), both projections in one [rows, 2 f]
+ * buffer. f, ldx and ldy multiples of 8. */
+int difflet_rocm_gated_gelu(const void* x, int64_t ldx, void* y, int64_t ldy, int dtype,
+                            int64_t rows, int64_t f, difflet_stream_t stream);
+
+/* out[i, :] = table[ids[i], :] for n int64 ids, rows of row_bytes bytes (any element type);
+ * strides in bytes. ParallelEmbedding at tp = 1 (F.embedding: difflet/backends/cpu/ops_impl/
+ * linear.py:44-53). The reference raises on an id outside [0, table_rows); the caller checks
+ * the ids, and the kernel writes a zero row for such an id rather than reading past the table. */
+int difflet_rocm_embedding(const int64_t* ids, int64_t n, const void* table, int64_t table_rows,
+                           int64_t ldt_bytes, void* out, int64_t ldo_bytes, int64_t row_bytes,
+                           difflet_stream_t stream);
+
+/* The T5 relative position bias with the key padding folded in, fp32 [batch, heads, seq_q,
+ * seq_k]: out[b, h, q, k] = table[buckets[k - q + seq_q - 1], h] (table [num_buckets, heads]
+ * in table_dtype), or the lowest finite float where key_keep[b, k] == 0 (key_keep null: no
+ * padding). buckets[j] is the bucket of relative position j - (seq_q - 1) (compute_bias and
+ * _relative_position_bucket: difflet/models/flux/t5/modeling_t5.py:200-269,
+ * difflet/models/wan/umt5/modeling_umt5.py:196-242; the padding mask of modeling_umt5.py:
+ * 354-358). A bucket outside [0, num_buckets) gives NaN. */
+int difflet_rocm_relative_bias(const int32_t* buckets, int num_buckets, const void* table,
+                               int table_dtype, int64_t heads, int64_t batch, int64_t seq_q,
+                               int64_t seq_k, const uint8_t* key_keep, int64_t keep_stride,
+                               float* out, difflet_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

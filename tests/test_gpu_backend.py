@@ -74,6 +74,26 @@ def test_ops_linear_modules(gpu, m, k, n):
     assert rel_l2(y, F.linear(x.float(), row.weight.float().cpu())) < 4e-3
 
 
+@pytest.mark.parametrize("m,k,n", [(3, 3072, 500), (300, 256, 128), (77, 100, 30), (512, 4096, 10240)])
+def test_ops_linear_modules_fp32_weights(gpu, m, k, n):
+    """fp32 weights run the fp32 GEMM (K / N off multiples of 4 padded on the weight), fp32
+    math as F.linear does."""
+    from difflet_amd.backends.rocm.ops_impl import linear as L
+
+    g = torch.Generator().manual_seed(m + k + 1)
+    x = torch.randn(2, m, k, generator=g)
+    col = L.ColumnParallelLinear(k, n, bias=True, gather_output=False, dtype=torch.float32)
+    row = L.RowParallelLinear(k, n, bias=False, skip_bias_add=True, dtype=torch.float32)
+    ref = F.linear(x.double(), col.weight.double(), col.bias.double())
+    col, row = col.to(gpu), row.to(gpu)
+    out = col(x.to(gpu))
+    assert out.dtype == torch.float32 and out.shape == (2, m, n)
+    assert rel_l2(out, ref) < 1e-5
+    y, b = row(x.to(gpu))
+    assert b is None
+    assert rel_l2(y, F.linear(x.double(), row.weight.double().cpu())) < 1e-5
+
+
 def test_ops_norms_and_rotary(gpu):
     from difflet_amd.backends.rocm.ops_impl import embeddings as E
     from difflet_amd.backends.rocm.ops_impl import norm as N
