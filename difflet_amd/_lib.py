@@ -113,6 +113,12 @@ SIGNATURES: dict[str, tuple] = {
     "difflet_rocm_embedding": (_i32, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp]),
     "difflet_rocm_relative_bias": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i64, _i64, _vp,
                                           _i64, _vp, _vp]),
+    "difflet_rocm_group_norm_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
+    "difflet_rocm_group_norm": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _f32,
+                                       _i32, _vp, _i64, _vp]),
+    "difflet_rocm_im2col3x3": (_i32, [_vp, _i32, _i64, _i64, _i64, _i32, _i64, _i64, _vp, _i64,
+                                      _i64, _vp]),
+    "difflet_rocm_softmax_rows": (_i32, [_vp, _i64, _vp, _i64, _i32, _i64, _i64, _f32, _vp]),
 }
 
 _lib = None

@@ -33,7 +33,7 @@ extern "C" const char* difflet_rocm_version(void) {
   return "difflet-rocm " DIFFLET_ROCM_VERSION " (gfx950)";
 }
 
-extern "C" int difflet_rocm_abi_version(void) { return 6; }
+extern "C" int difflet_rocm_abi_version(void) { return 7; }
 
 extern "C" int difflet_rocm_device_count(void) {
   int n = 0;

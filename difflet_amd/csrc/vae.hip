@@ -1,0 +1,319 @@
+// Kernels of the VAE decoder (diffusers' 2D Decoder as the reference builds it for FLUX:
+// difflet/models/flux/vae/modeling_vae.py:107-117, difflet/backends/neuron/flux/vae.py:25-36):
+// GroupNorm over channels-last activations, the im2col gather of a 3x3 convolution (with the
+// nearest 2x upsampling of Upsample2D folded into its addressing), and the row softmax of the
+// mid-block attention. The convolutions and linears themselves run on the GEMMs.
+//
+// Activations are channels-last: [batch][pixels][channels], pixels row-major (y * W + x).
+//
+// GroupNorm runs in three passes over the activation: per-chunk, per-channel sums (of x, then of
+// (x - mean)^2), each merged per (batch, group) in double precision, then the normalization
+// with the affine weights (and SiLU) applied elementwise. Two passes for the variance keep it
+// free of the E[x^2] - E[x]^2 cancellation; both statistics are the population ones of
+// F.group_norm.
+
+#include <hip/hip_runtime.h>
+
+#include <float.h>
+#include <stdint.h>
+
+#include "common.hpp"
+#include "difflet_rocm.h"
+
+namespace dlt {
+
+// 8 consecutive values as fp32, from bf16 (16 bytes) or fp32 (32 bytes)
+template <typename T> struct Vec8;
+template <> struct Vec8<bf16> {
+  static __device__ __forceinline__ void load(const bf16* p, float* v) {
+    const u32x4 r = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = bf16bits_to_f32(r[i] & 0xffffu);
+      v[2 * i + 1] = bf16bits_to_f32(r[i] >> 16);
+    }
+  }
+  static __device__ __forceinline__ void store(bf16* p, const float* v) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+    *reinterpret_cast<u32x4*>(p) = r;
+  }
+};
+template <> struct Vec8<float> {
+  static __device__ __forceinline__ void load(const float* p, float* v) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = a[i];
+      v[4 + i] = b[i];
+    }
+  }
+  static __device__ __forceinline__ void store(float* p, const float* v) {
+    *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+  }
+};
+
+// ---- GroupNorm pass 1 / 2: per-channel sums over a chunk of pixels. Thread t handles channels
+// 8 (t % tpp) .. + 8 of pixel t / tpp of each pass (tpp = C / 8 threads per pixel); the
+// workgroup's threads that share channels are summed through LDS. mean == nullptr: sums of x;
+// else sums of (x - mean[b][group])^2. partial: [batch][chunks][C].
+template <typename T>
+__global__ __launch_bounds__(256) void gn_stats_kernel(const T* __restrict__ x, int64_t pixels,
+                                                       int channels, int groups, int64_t chunk,
+                                                       const float* __restrict__ mean,
+                                                       float* __restrict__ partial) {
+  __shared__ float red[256][9];
+  const int tid = threadIdx.x, tpp = channels / 8, ppass = 256 / tpp;
+  const int b = blockIdx.y, ck = blockIdx.x;
+  const int cv = tid % tpp, pr = tid / tpp;
+  const bool active = pr < ppass;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float mu[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const int cpg = channels / groups;
+  if (mean && active)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mu[i] = mean[b * groups + (cv * 8 + i) / cpg];
+  const int64_t p0 = ck * chunk, p1 = min(p0 + chunk, pixels);
+  const T* xb = x + (int64_t)b * pixels * channels;
+  if (active)
+    for (int64_t p = p0 + pr; p < p1; p += ppass) {
+      float v[8];
+      Vec8<T>::load(xb + p * channels + cv * 8, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float d = v[i] - mu[i];
+        acc[i] += mean ? d * d : v[i];
+      }
+    }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) red[tid][i] = active ? acc[i] : 0.f;
+  __syncthreads();
+  if (tid < tpp) {
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < ppass; ++r)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s[i] += red[r * tpp + tid][i];
+    float* out = partial + ((int64_t)b * gridDim.x + ck) * channels + tid * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = s[i];
+  }
+}
+
+// One thread per (batch, group): the chunks' partial sums merged in double. mode 0: the mean;
+// mode 1: rstd = 1 / sqrt(var + eps) from the sums of squared deviations.
+__global__ void gn_reduce_kernel(const float* __restrict__ partial, int batch, int chunks,
+                                 int channels, int groups, int64_t pixels, int mode, float eps,
+                                 float* __restrict__ out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= batch * groups) return;
+  const int b = i / groups, gi = i % groups, cpg = channels / groups;
+  double s = 0.0;
+  for (int c = 0; c < chunks; ++c) {
+    const float* row = partial + ((int64_t)b * chunks + c) * channels + gi * cpg;
+    for (int k = 0; k < cpg; ++k) s += (double)row[k];
+  }
+  const double n = (double)pixels * (double)cpg;
+  out[i] = mode == 0 ? (float)(s / n) : (float)(1.0 / __builtin_sqrt(s / n + (double)eps));
+}
+
+// y = (x - mean) * rstd * weight + bias, then SiLU when act == 1
+template <typename T>
+__global__ __launch_bounds__(256) void gn_apply_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                       int64_t pixels, int channels, int groups,
+                                                       const float* __restrict__ mean,
+                                                       const float* __restrict__ rstd,
+                                                       const float* __restrict__ w,
+                                                       const float* __restrict__ bias, int act,
+                                                       int batch) {
+  const int nv = channels / 8;
+  const int64_t total = (int64_t)batch * pixels * nv;
+  const int cpg = channels / groups;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * 256) {
+    const int cv = (int)(i % nv);
+    const int b = (int)(i / ((int64_t)pixels * nv));
+    float v[8];
+    Vec8<T>::load(x + i * 8, v);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int c = cv * 8 + k, gi = b * groups + c / cpg;
+      float o = (v[k] - mean[gi]) * rstd[gi];
+      o = o * (w ? w[c] : 1.f) + (bias ? bias[c] : 0.f);
+      if (act == 1) o = o / (1.0f + __expf(-o));
+      v[k] = o;
+    }
+    Vec8<T>::store(y + i * 8, v);
+  }
+}
+
+// ---- im2col of a 3x3 convolution with padding 1 over a channels-last image [H][W][C], for the
+// output pixels row0 .. row0 + rows - 1: row r of the [rows][ldo] output holds, for output pixel
+// row0 + r = (y, x) and tap t = 3 ky + kx, the C channels of the input pixel (y + ky - 1,
+// x + kx - 1), zero outside the image; columns 9 C .. kpad - 1 are zero.
+// up == 1: the input is first upsampled 2x by nearest neighbour (Ho = 2 H), i.e. the pixel read
+// is ((y + ky - 1) / 2, (x + kx - 1) / 2). Each thread moves 16 bytes.
+template <typename T>
+__global__ __launch_bounds__(256) void im2col3x3_kernel(const T* __restrict__ x, int h, int w,
+                                                        int channels, int up, int64_t row0,
+                                                        int64_t rows, T* __restrict__ out,
+                                                        int64_t ldo, int kpad) {
+  constexpr int EV = 16 / sizeof(T);  // elements per 16 bytes
+  const int ho = h << up, wo = w << up;
+  const int nv = kpad / EV;           // 16-byte pieces per output row
+  const int64_t total = rows * nv;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / nv;           // row of out; pixel row0 + r of the image
+    const int col = (int)(i % nv) * EV;
+    const int y = (int)((row0 + r) / wo), xx = (int)((row0 + r) % wo);
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (col < 9 * channels) {
+      const int t = col / channels, c = col % channels;
+      const int yy = y + t / 3 - 1, xs = xx + t % 3 - 1;
+      if (yy >= 0 && yy < ho && xs >= 0 && xs < wo)
+        v = *reinterpret_cast<const u32x4*>(x + ((int64_t)(yy >> up) * w + (xs >> up)) * channels + c);
+    }
+    *reinterpret_cast<u32x4*>(out + r * ldo + col) = v;
+  }
+}
+
+// ---- softmax over rows of fp32 scores: p = exp(s * scale - max) / sum, written in T. One
+// workgroup per row.
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_rows_kernel(const float* __restrict__ s,
+                                                           int64_t lds, T* __restrict__ p,
+                                                           int64_t ldp, int64_t cols,
+                                                           float scale) {
+  __shared__ float red[4];
+  const float* row = s + (int64_t)blockIdx.x * lds;
+  T* prow = p + (int64_t)blockIdx.x * ldp;
+  float mx = -INFINITY;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) mx = fmaxf(mx, row[c] * scale);
+  mx = block_max<4>(mx, red);
+  float sum = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) sum += __expf(row[c] * scale - mx);
+  sum = block_sum<4>(sum, red);
+  const float inv = 1.0f / sum;
+  for (int64_t c = threadIdx.x; c < cols; c += 256)
+    Elt<T>::store(prow + c, __expf(row[c] * scale - mx) * inv);
+}
+
+}  // namespace dlt
+
+using namespace dlt;
+
+#define DLT_DISPATCH_BF16_F32(dt, T, ...)                                          \
+  switch (dt) {                                                                    \
+    case DIFFLET_BF16: { typedef bf16 T; __VA_ARGS__; break; }                     \
+    case DIFFLET_F32: { typedef float T; __VA_ARGS__; break; }                     \
+    default: dlt_set_error("unsupported dtype %d (bf16 or fp32)", (int)(dt));       \
+      return DIFFLET_EUNSUPPORTED;                                                 \
+  }
+
+static bool vae_aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// chunking of the GroupNorm statistics: at most 512 chunks per image, each a multiple of the
+// pixels one pass of 256 threads covers
+static int64_t gn_chunk(int64_t pixels, int channels) {
+  const int64_t ppass = 256 / (channels / 8);
+  int64_t chunk = (pixels + 511) / 512;
+  chunk = (chunk + ppass - 1) / ppass * ppass;
+  return chunk < ppass ? ppass : chunk;
+}
+
+extern "C" int64_t difflet_rocm_group_norm_workspace_bytes(int64_t batch, int64_t pixels,
+                                                           int64_t channels, int64_t groups) {
+  if (batch <= 0 || pixels <= 0 || channels <= 0 || groups <= 0) return 0;
+  const int64_t chunks = (pixels + gn_chunk(pixels, (int)channels) - 1) / gn_chunk(pixels, (int)channels);
+  return (batch * chunks * channels + 2 * batch * groups) * 4;
+}
+
+extern "C" int difflet_rocm_group_norm(const void* x, void* y, int dtype, int64_t batch,
+                                       int64_t pixels, int64_t channels, int64_t groups,
+                                       const float* weight, const float* bias, float eps, int act,
+                                       void* workspace, int64_t workspace_bytes,
+                                       difflet_stream_t stream) {
+  DLT_REQUIRE(batch >= 0 && pixels >= 0 && groups > 0 && channels > 0, DIFFLET_EINVAL,
+              "group_norm: bad sizes");
+  DLT_REQUIRE(channels % groups == 0 && channels % 8 == 0 && channels <= 2048, DIFFLET_EINVAL,
+              "group_norm: channels (%lld) must be a multiple of 8 and of groups (%lld), <= 2048",
+              (long long)channels, (long long)groups);
+  DLT_REQUIRE(act == 0 || act == 1, DIFFLET_EINVAL, "group_norm: act must be 0 or 1");
+  if (batch * pixels == 0) return DIFFLET_OK;
+  DLT_REQUIRE(x && y && workspace, DIFFLET_EINVAL, "group_norm: null pointer");
+  DLT_REQUIRE(vae_aligned16(x) && vae_aligned16(y) && vae_aligned16(workspace), DIFFLET_EINVAL,
+              "group_norm: pointers must be 16-byte aligned");
+  DLT_REQUIRE(batch < 65536, DIFFLET_EUNSUPPORTED, "group_norm: batch too large");
+  const int64_t need = difflet_rocm_group_norm_workspace_bytes(batch, pixels, channels, groups);
+  DLT_REQUIRE(workspace_bytes >= need, DIFFLET_EINVAL,
+              "group_norm: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
+              (long long)need);
+  const int64_t chunk = gn_chunk(pixels, (int)channels);
+  const int chunks = (int)((pixels + chunk - 1) / chunk);
+  float* partial = reinterpret_cast<float*>(workspace);
+  float* mean = partial + batch * chunks * channels;
+  float* rstd = mean + batch * groups;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 sgrid((unsigned)chunks, (unsigned)batch);
+  const unsigned rblocks = (unsigned)((batch * groups + 63) / 64);
+  int64_t ablocks = (batch * pixels * (channels / 8) + 255) / 256;
+  if (ablocks > 65536) ablocks = 65536;
+  DLT_DISPATCH_BF16_F32(dtype, T,
+    hipLaunchKernelGGL((gn_stats_kernel<T>), sgrid, dim3(256), 0, s, (const T*)x, pixels,
+                       (int)channels, (int)groups, chunk, (const float*)nullptr, partial);
+    hipLaunchKernelGGL(gn_reduce_kernel, dim3(rblocks), dim3(64), 0, s, partial, (int)batch,
+                       chunks, (int)channels, (int)groups, pixels, 0, eps, mean);
+    hipLaunchKernelGGL((gn_stats_kernel<T>), sgrid, dim3(256), 0, s, (const T*)x, pixels,
+                       (int)channels, (int)groups, chunk, (const float*)mean, partial);
+    hipLaunchKernelGGL(gn_reduce_kernel, dim3(rblocks), dim3(64), 0, s, partial, (int)batch,
+                       chunks, (int)channels, (int)groups, pixels, 1, eps, rstd);
+    hipLaunchKernelGGL((gn_apply_kernel<T>), dim3((unsigned)ablocks), dim3(256), 0, s,
+                       (const T*)x, (T*)y, pixels, (int)channels, (int)groups, mean, rstd, weight,
+                       bias, act, (int)batch));
+  return dlt_check_launch("group_norm");
+}
+
+extern "C" int difflet_rocm_im2col3x3(const void* x, int dtype, int64_t height, int64_t width,
+                                      int64_t channels, int upsample, int64_t row0, int64_t rows,
+                                      void* out, int64_t ldo, int64_t kpad,
+                                      difflet_stream_t stream) {
+  DLT_REQUIRE(height > 0 && width > 0 && channels > 0 && (upsample == 0 || upsample == 1),
+              DIFFLET_EINVAL, "im2col3x3: bad sizes");
+  DLT_REQUIRE(x && out, DIFFLET_EINVAL, "im2col3x3: null pointer");
+  const int ev = dtype == DIFFLET_F32 ? 4 : 8;
+  DLT_REQUIRE(channels % ev == 0 && kpad % ev == 0 && kpad >= 9 * channels && ldo >= kpad &&
+                  ldo % ev == 0 && vae_aligned16(x) && vae_aligned16(out),
+              DIFFLET_EINVAL,
+              "im2col3x3: channels, kpad and ldo must be multiples of %d (16 bytes), kpad >= 9 C, "
+              "pointers aligned", ev);
+  const int64_t ho = height << upsample, wo = width << upsample;
+  DLT_REQUIRE(ho * wo < (1LL << 31) && 9 * channels < (1LL << 30), DIFFLET_EUNSUPPORTED,
+              "im2col3x3: image too large");
+  DLT_REQUIRE(row0 >= 0 && rows >= 0 && row0 + rows <= ho * wo, DIFFLET_EINVAL,
+              "im2col3x3: rows [%lld, %lld) outside the %lld output pixels", (long long)row0,
+              (long long)(row0 + rows), (long long)(ho * wo));
+  if (rows == 0) return DIFFLET_OK;
+  int64_t blocks = (rows * (kpad / ev) + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  DLT_DISPATCH_BF16_F32(dtype, T,
+    hipLaunchKernelGGL((im2col3x3_kernel<T>), dim3((unsigned)blocks), dim3(256), 0,
+                       (hipStream_t)stream, (const T*)x, (int)height, (int)width, (int)channels,
+                       upsample, row0, rows, (T*)out, ldo, (int)kpad));
+  return dlt_check_launch("im2col3x3");
+}
+
+extern "C" int difflet_rocm_softmax_rows(const float* s, int64_t lds, void* p, int64_t ldp,
+                                         int dtype, int64_t rows, int64_t cols, float scale,
+                                         difflet_stream_t stream) {
+  DLT_REQUIRE(rows >= 0 && cols > 0 && lds >= cols && ldp >= cols, DIFFLET_EINVAL,
+              "softmax_rows: bad sizes");
+  if (rows == 0) return DIFFLET_OK;
+  DLT_REQUIRE(s && p, DIFFLET_EINVAL, "softmax_rows: null pointer");
+  DLT_REQUIRE(rows < (1LL << 31), DIFFLET_EUNSUPPORTED, "softmax_rows: too many rows");
+  DLT_DISPATCH_BF16_F32(dtype, T,
+    hipLaunchKernelGGL((softmax_rows_kernel<T>), dim3((unsigned)rows), dim3(256), 0,
+                       (hipStream_t)stream, s, lds, (T*)p, ldp, cols, scale));
+  return dlt_check_launch("softmax_rows");
+}

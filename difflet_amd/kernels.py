@@ -705,3 +705,70 @@ def relative_bias(buckets: torch.Tensor, table: torch.Tensor, *, batch: int, seq
                                            keep.stride(0) if keep is not None else 0, _ptr(y),
                                            _stream(dev)), "relative_bias")
     return y
+
+
+# ------------------------------------------------------------------------ VAE decoder
+_GN_WORKSPACE: dict[int, torch.Tensor] = {}
+
+
+def group_norm(x: torch.Tensor, groups: int, weight: torch.Tensor | None,
+               bias: torch.Tensor | None, eps: float, *, silu: bool = False,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """GroupNorm (+ SiLU) of channels-last x [batch, pixels, C] (bf16 or fp32) with fp32 affine
+    vectors; statistics in fp32 / double, two passes."""
+    if x.dim() != 3 or not x.is_contiguous():
+        raise ValueError("group_norm: x must be a contiguous [batch, pixels, channels]")
+    b, p, c = x.shape
+    for name, t in (("weight", weight), ("bias", bias)):
+        if t is not None and (t.dtype != torch.float32 or t.shape != (c,) or not t.is_contiguous()):
+            raise ValueError(f"group_norm: {name} must be a contiguous fp32 [{c}]")
+    if c % groups or c % 8:
+        raise ValueError(f"group_norm: {c} channels are not a multiple of 8 and of {groups} groups")
+    dev = _on_gpu(x, weight, bias, out)
+    y = out if out is not None else torch.empty_like(x)
+    need = int(lib().difflet_rocm_group_norm_workspace_bytes(b, p, c, groups))
+    i = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _GN_WORKSPACE.get(i)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+        _GN_WORKSPACE[i] = ws
+    check(lib().difflet_rocm_group_norm(_ptr(x), _ptr(y), _dt(x), b, p, c, groups, _ptr(weight),
+                                        _ptr(bias), float(eps), int(bool(silu)), _ptr(ws),
+                                        ws.numel(), _stream(dev)), "group_norm")
+    return y
+
+
+def im2col3x3(x: torch.Tensor, *, upsample: bool = False, kpad: int | None = None,
+              row0: int = 0, rows: int | None = None,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """[H, W, C] channels-last image -> [rows, kpad] rows of the 9 taps' channels around output
+    pixels row0 .. row0 + rows - 1 (all by default; zero padding, and nearest 2x upsampling
+    first when upsample)."""
+    if x.dim() != 3 or not x.is_contiguous():
+        raise ValueError("im2col3x3: x must be a contiguous [height, width, channels]")
+    h, w, c = x.shape
+    ev = 4 if x.dtype == torch.float32 else 8
+    kpad = kpad if kpad is not None else -(-9 * c // ev) * ev
+    dev = _on_gpu(x, out)
+    up = int(bool(upsample))
+    total = (h << up) * (w << up)
+    rows = total - row0 if rows is None else rows
+    y = out if out is not None else torch.empty((rows, kpad), dtype=x.dtype, device=dev)
+    if y.dtype != x.dtype or y.shape[0] != rows or y.shape[1] < kpad or y.stride(1) != 1:
+        raise ValueError(f"im2col3x3: out must be [{rows}, >= {kpad}] of x's dtype")
+    check(lib().difflet_rocm_im2col3x3(_ptr(x), _dt(x), h, w, c, up, row0, rows, _ptr(y),
+                                       y.stride(0), kpad, _stream(dev)), "im2col3x3")
+    return y
+
+
+def softmax_rows(s: torch.Tensor, scale: float, *, dtype: torch.dtype = torch.float32,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """softmax(s * scale) over the last dim of fp32 scores [rows, cols], written in dtype."""
+    if s.dtype != torch.float32 or s.dim() != 2 or s.stride(1) != 1:
+        raise ValueError("softmax_rows: s must be fp32 [rows, cols] with contiguous rows")
+    dev = _on_gpu(s, out)
+    p = out if out is not None else torch.empty(s.shape, dtype=dtype, device=dev)
+    check(lib().difflet_rocm_softmax_rows(_ptr(s), s.stride(0), _ptr(p), p.stride(0), _dt(p),
+                                          s.shape[0], s.shape[1], float(scale), _stream(dev)),
+          "softmax_rows")
+    return p

@@ -360,6 +360,40 @@ int difflet_rocm_relative_bias(const int32_t* buckets, int num_buckets, const vo
                                int64_t seq_k, const uint8_t* key_keep, int64_t keep_stride,
                                float* out, difflet_stream_t stream);
 
+/* ------------------------------------------------------------------------------------------
+ * VAE decoder (FLUX's: diffusers' 2D Decoder, difflet/models/flux/vae/modeling_vae.py:107-117,
+ * difflet/backends/neuron/flux/vae.py:25-36). Channels-last activations [batch][pixels][C].
+ * ---------------------------------------------------------------------------------------- */
+/* Bytes of workspace difflet_rocm_group_norm needs for these sizes. */
+int64_t difflet_rocm_group_norm_workspace_bytes(int64_t batch, int64_t pixels, int64_t channels,
+                                                int64_t groups);
+
+/* GroupNorm over channels-last x (bf16 or fp32): per (batch, group) mean and population
+ * variance in fp32 / double, y = (x - mean) / sqrt(var + eps) * weight + bias (fp32 vectors,
+ * either may be null), then SiLU when act == 1. PatchedGroupNorm / nn.GroupNorm + SiLU of the
+ * decoder's resnets and output (modeling_vae.py:39-68: F.group_norm in fp32). channels a
+ * multiple of 8 and of groups, <= 2048; y may alias x. */
+int difflet_rocm_group_norm(const void* x, void* y, int dtype, int64_t batch, int64_t pixels,
+                            int64_t channels, int64_t groups, const float* weight,
+                            const float* bias, float eps, int act, void* workspace,
+                            int64_t workspace_bytes, difflet_stream_t stream);
+
+/* im2col of a 3x3, padding 1 convolution over one channels-last image [height][width][C]
+ * (bf16 or fp32), for output pixels row0 .. row0 + rows - 1: out [rows][ldo], row r = the 9
+ * taps' C channels (tap 3 ky + kx) around output pixel row0 + r = (y, x), zero outside the
+ * image, columns 9 C .. kpad zero. upsample == 1 first doubles the image by nearest neighbour
+ * (Upsample2D's interpolate before its conv), so Ho = 2 height. The GEMM of out with the weight
+ * [Cout][ky][kx][C] is that range of the convolution (nn.Conv2d(k=3, padding=1)). */
+int difflet_rocm_im2col3x3(const void* x, int dtype, int64_t height, int64_t width,
+                           int64_t channels, int upsample, int64_t row0, int64_t rows, void* out,
+                           int64_t ldo, int64_t kpad, difflet_stream_t stream);
+
+/* p[r, :] = softmax(s[r, :] * scale) for fp32 scores, p in dtype (bf16 or fp32): the mid-block
+ * attention's upcast softmax (one head of 512 channels, whose head width the flash kernels do
+ * not take). */
+int difflet_rocm_softmax_rows(const float* s, int64_t lds, void* p, int64_t ldp, int dtype,
+                              int64_t rows, int64_t cols, float scale, difflet_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

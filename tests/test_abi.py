@@ -30,7 +30,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     lib = _lib.load()
     for name in declared_symbols():
         assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
-    assert lib.difflet_rocm_abi_version() == 6
+    assert lib.difflet_rocm_abi_version() == 7
     assert b"gfx950" in lib.difflet_rocm_version()
 
 
