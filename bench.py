@@ -1,7 +1,7 @@
 """Benchmark: one DiT denoise step on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload flux|qwen|wan|weights|compile]
+                    [--workload flux|qwen|wan|weights|compile|t5|umt5|vae]
                     [--kinds bf16,fp8] [--no-cpu] [--calibrate-copy]
 
 flux (default): the full FLUX.1-dev-shaped transformer forward of one denoise step, batch 1,
@@ -21,7 +21,13 @@ per-channel fp8 and MXFP8; `value` is the summed quantizer time in ms, K timed c
 compile: one FLUX single block (4608 tokens, hidden 3072, 24 x 128 heads, MLP 12288) written
 with the op modules, one HIP kernel per op, run eagerly and under torch.compile(fullgraph=True);
 `value` is the compiled block's ms.
-Weights are random N(0, 0.02) drawn on the device (norm weights ones); inputs N(0, 1).
+t5 / umt5: the text encoder before the denoise loop, FLUX's T5-XXL / Wan's UMT5-XXL (24 blocks,
+4096 wide, 64 x 64 heads, gated FFN 10240) on one 512-token prompt (UMT5: 300 real tokens, the
+rest padding under the mask), bf16 and fp32; `value` is the bf16 encode in ms.
+vae: FLUX's VAE decoder after the loop, a 128 x 128 x 16 latent to a 1024 x 1024 image, bf16
+and fp32; `value` is the bf16 decode in ms.
+Weights are random N(0, 0.02) drawn on the device (norm weights ones); inputs N(0, 1); the
+encoders and the decoder draw their weights with their initializations' scales.
 
 Each step starts with its inputs resident in HBM. W untimed warmup steps, then K steps
 bracketed by torch.cuda.synchronize(); per-step times from HIP events on the step stream.
@@ -73,7 +79,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="flux",
-                    choices=("flux", "qwen", "wan", "weights", "compile"))
+                    choices=("flux", "qwen", "wan", "weights", "compile", "t5", "umt5", "vae"))
     ap.add_argument("--kinds", default=None,
                     help="comma list (flux: bf16,fp8 by default; qwen: mx,bf16)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -570,6 +576,116 @@ def run_compile(args, torch, log):
     return 0
 
 
+def t5_flops(cfg, s):
+    """Matrix FLOPs of one encode of s tokens: q/k/v/o, the gated FFN, scores and P V."""
+    d, inner, f = cfg.d_model, cfg.inner_dim, cfg.d_ff
+    per_layer = 2 * s * (4 * d * inner + 3 * d * f) + 4 * s * s * inner
+    return cfg.num_layers * per_layer
+
+
+def vae_flops(cfg, h, w):
+    """Matrix FLOPs of one decode of an h x w latent: every convolution (9 taps, or 1 for the
+    shortcuts) at its resolution, the mid-block attention's projections, scores and P V."""
+    from difflet_amd.vae import decoder as dvae
+
+    shapes = dvae.param_shapes(cfg)
+    top = cfg.block_out_channels[-1]
+    px = h * w
+    total = 2 * px * 9 * cfg.latent_channels * top  # conv_in
+    total += 2 * px * (4 * top * top) + 4 * px * px * top  # attention
+    res = {"mid_block": px}
+    scale = 1
+    for i, j, cin, cout, up in dvae._plan(cfg):
+        res[f"up_blocks.{i}"] = px * scale * scale
+        if up:
+            scale *= 2
+    for name, shp in shapes.items():
+        if not name.endswith(".weight") or len(shp) != 4 or name.startswith("decoder.conv_in"):
+            continue
+        blk = next((k for k in res if f"decoder.{k}." in name), None)
+        pix = res[blk] if blk else px * scale * scale  # conv_out at the full resolution
+        if ".upsamplers." in name:
+            pix *= 4
+        total += 2 * pix * shp[0] * shp[1] * shp[2] * shp[3]
+    return total
+
+
+def _time(fn, steps, warmup, torch):
+    for _ in range(max(warmup, 1)):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    times = []
+    for _ in range(steps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+    return sum(times) / len(times), sorted(times)[len(times) // 2]
+
+
+def run_stage(args, torch, log):
+    """The steps either side of the denoise loop: the T5 / UMT5 encoders and the VAE decoder,
+    bf16 and fp32, whole-stage time and its matrix FLOP rate against the MFMA peak."""
+    dev = torch.device("cuda")
+    res = {}
+    if args.workload in ("t5", "umt5"):
+        from difflet_amd.text.t5 import T5_XXL, UMT5_XXL, T5Encoder, random_param_source
+
+        cfg = T5_XXL if args.workload == "t5" else UMT5_XXL
+        s = 512
+        ids = torch.randint(0, cfg.vocab_size, (1, s), generator=torch.Generator().manual_seed(SEED)).to(dev)
+        mask = None
+        if cfg.per_layer_bias:
+            mask = torch.ones(1, s, dtype=torch.long, device=dev)
+            mask[:, 300:] = 0
+        flops = t5_flops(cfg, s)
+        name = "T5-XXL" if args.workload == "t5" else "UMT5-XXL"
+        workload = f"{name} text encoder, 24 blocks, d_model 4096, 64 x 64 heads, d_ff 10240, 512 tokens"
+        for dt in (torch.bfloat16, torch.float32):
+            enc = T5Encoder(cfg, random_param_source(cfg, SEED, dev, torch.float32), dtype=dt, device=dev)
+            ms, med = _time(lambda: enc(ids, mask), args.steps, args.warmup, torch)
+            res[str(dt).split(".")[1]] = {"ms": round(ms, 3), "median_ms": round(med, 3),
+                                          "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+            log(f"[{args.workload}] {dt}: {ms:.2f} ms")
+            del enc
+            torch.cuda.empty_cache()
+    else:
+        from difflet_amd.vae import decoder as dvae
+
+        cfg = dvae.FLUX_VAE
+        z = torch.randn(1, 16, 128, 128, generator=torch.Generator().manual_seed(SEED)).to(dev)
+        flops = vae_flops(cfg, 128, 128)
+        workload = "FLUX.1 VAE decoder, 128 x 128 x 16 latent -> 1024 x 1024 RGB"
+        for dt in (torch.bfloat16, torch.float32):
+            dec = dvae.VaeDecoder(cfg, dvae.random_param_source(cfg, SEED, dev), dtype=dt, device=dev)
+            ms, med = _time(lambda: dec.decode(z), args.steps, args.warmup, torch)
+            res[str(dt).split(".")[1]] = {"ms": round(ms, 3), "median_ms": round(med, 3),
+                                          "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+            log(f"[vae] {dt}: {ms:.2f} ms")
+            del dec
+            torch.cuda.empty_cache()
+    head = res["bfloat16"]
+    line = {
+        "metric": f"{args.workload} stage ms (bf16, fp32) at 1 GPU",
+        "value": head["ms"], "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": head["ms"], "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: random-init weights drawn on the device, random token ids / latents",
+        "config": {"workload": workload, "matrix_gflop": round(flops / 1e9, 1)},
+        "roofline": {"bound": "mfma", "achieved": head["tflops"], "peak": 2500.0,
+                     "unit": "TFLOP/s", "frac": round(head["tflops"] / 2500.0, 4),
+                     "traffic": None, "kernel": "whole stage (matrix FLOPs / stage time)"},
+        "by_dtype": res,
+    }
+    if "float32" in res:
+        line["by_dtype"]["float32"]["frac_of_fp32_peak"] = round(res["float32"]["tflops"] / 157.3, 4)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -590,6 +706,8 @@ def main():
         return run_weights(args, torch, log)
     if args.workload == "compile":
         return run_compile(args, torch, log)
+    if args.workload in ("t5", "umt5", "vae"):
+        return run_stage(args, torch, log)
     wl = WORKLOADS[args.workload]()
     kinds = [k for k in (args.kinds or ",".join(wl.kinds)).split(",") if k]
     if args.calibrate_copy:

@@ -749,18 +749,19 @@ extern "C" int64_t difflet_rocm_attention_workspace_bytes(void) {
 }
 
 // ---- fp32 inputs (models run in fp32, as the reference's CPU op computes them): scores,
-// softmax and P V in fp32 on the VALU, one query per lane, 256 queries per workgroup. K and V
-// tiles of 32 keys go through LDS and are read by every lane at the same address (broadcast).
+// softmax and P V in fp32 on the VALU, one query per lane, 256 queries per workgroup (64 when
+// 256 would leave most compute units idle). K and V tiles of 32 keys go through LDS and are read
+// by every lane at the same address (broadcast).
 // Online softmax per lane over each tile; masks, bounds, causal and scale as the MFMA kernels.
 constexpr int F32_TILE = 32;
-template <int D>
-__global__ __launch_bounds__(256, 1) void attn_f32_kernel(const AttnArgs a) {
+template <int D, int NQ>  // NQ: queries (threads) per workgroup, 64 or 256
+__global__ __launch_bounds__(NQ, 1) void attn_f32_kernel(const AttnArgs a) {
   __shared__ __attribute__((aligned(16))) float skk[F32_TILE][D];
   __shared__ __attribute__((aligned(16))) float svv[F32_TILE][D];
   const int tid = threadIdx.x;
   const int bh = blockIdx.x / a.q_tiles, qt = blockIdx.x % a.q_tiles;
   const int b = bh / a.heads, h = bh % a.heads;
-  const int my_q = qt * 256 + tid;
+  const int my_q = qt * NQ + tid;
   const bool qok = my_q < a.seq_q;
   const float* qp = reinterpret_cast<const float*>(a.q) + b * a.qs[0] + h * a.qs[1];
   const float* kp = reinterpret_cast<const float*>(a.k) + b * a.ks[0] + h * a.ks[1];
@@ -785,7 +786,7 @@ __global__ __launch_bounds__(256, 1) void attn_f32_kernel(const AttnArgs a) {
   float m_run = -INFINITY, l_run = 0.f;
   for (int j0 = 0; j0 < a.seq_k; j0 += F32_TILE) {
     __syncthreads();  // the previous tile's reads are done
-    for (int i = tid; i < F32_TILE * D / 4; i += 256) {
+    for (int i = tid; i < F32_TILE * D / 4; i += NQ) {
       const int key = j0 + i / (D / 4), d = (i % (D / 4)) * 4;
       f32x4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
       if (key < a.seq_k) {
@@ -932,14 +933,18 @@ static int attention_impl(const char* name, const void* q, const void* k, const 
     for (int i = 0; i < 3; ++i) args.bs[i] = bound_strides[i];
   hipStream_t s = (hipStream_t)stream;
   if (dtype == DIFFLET_F32) {
-    args.q_tiles = (int)((seq_q + 255) / 256);
+    const int cus = att_device_cus();
+    const bool narrow = (int64_t)((seq_q + 255) / 256) * batch * heads < 2 * (cus > 0 ? cus : 256);
+    const int nq = narrow ? 64 : 256;
+    args.q_tiles = (int)((seq_q + nq - 1) / nq);
     const int64_t t32 = (int64_t)args.q_tiles * batch * heads;
     DLT_REQUIRE(t32 < (1LL << 31), DIFFLET_EUNSUPPORTED, "%s: too many tiles", name);
     args.total = (int)t32;
-    if (head_dim == 64)
-      hipLaunchKernelGGL((attn_f32_kernel<64>), dim3((unsigned)t32), dim3(256), 0, s, args);
-    else
-      hipLaunchKernelGGL((attn_f32_kernel<128>), dim3((unsigned)t32), dim3(256), 0, s, args);
+    const dim3 g32((unsigned)t32);
+    if (head_dim == 64 && narrow) hipLaunchKernelGGL((attn_f32_kernel<64, 64>), g32, dim3(64), 0, s, args);
+    else if (head_dim == 64) hipLaunchKernelGGL((attn_f32_kernel<64, 256>), g32, dim3(256), 0, s, args);
+    else if (narrow) hipLaunchKernelGGL((attn_f32_kernel<128, 64>), g32, dim3(64), 0, s, args);
+    else hipLaunchKernelGGL((attn_f32_kernel<128, 256>), g32, dim3(256), 0, s, args);
     return dlt_check_launch(name);
   }
   dim3 grid((unsigned)total);

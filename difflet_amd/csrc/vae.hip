@@ -101,50 +101,66 @@ __global__ __launch_bounds__(256) void gn_stats_kernel(const T* __restrict__ x, 
   }
 }
 
-// One thread per (batch, group): the chunks' partial sums merged in double. mode 0: the mean;
-// mode 1: rstd = 1 / sqrt(var + eps) from the sums of squared deviations.
-__global__ void gn_reduce_kernel(const float* __restrict__ partial, int batch, int chunks,
-                                 int channels, int groups, int64_t pixels, int mode, float eps,
-                                 float* __restrict__ out) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= batch * groups) return;
+// One workgroup per (batch, group): the chunks' partial sums of the group's channels merged in
+// double (each thread strides over (chunk, channel) pairs, then a tree through LDS). mode 0: the
+// mean; mode 1: rstd = 1 / sqrt(var + eps) from the sums of squared deviations.
+__global__ __launch_bounds__(256) void gn_reduce_kernel(const float* __restrict__ partial,
+                                                        int batch, int chunks, int channels,
+                                                        int groups, int64_t pixels, int mode,
+                                                        float eps, float* __restrict__ out) {
+  __shared__ double red[256];
+  const int i = blockIdx.x;  // b * groups + g
   const int b = i / groups, gi = i % groups, cpg = channels / groups;
   double s = 0.0;
-  for (int c = 0; c < chunks; ++c) {
-    const float* row = partial + ((int64_t)b * chunks + c) * channels + gi * cpg;
-    for (int k = 0; k < cpg; ++k) s += (double)row[k];
+  for (int e = threadIdx.x; e < chunks * cpg; e += 256) {
+    const int c = e / cpg, k = e % cpg;
+    s += (double)partial[((int64_t)b * chunks + c) * channels + gi * cpg + k];
   }
-  const double n = (double)pixels * (double)cpg;
-  out[i] = mode == 0 ? (float)(s / n) : (float)(1.0 / __builtin_sqrt(s / n + (double)eps));
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const double n = (double)pixels * (double)cpg;
+    out[i] = mode == 0 ? (float)(red[0] / n) : (float)(1.0 / __builtin_sqrt(red[0] / n + (double)eps));
+  }
 }
 
-// y = (x - mean) * rstd * weight + bias, then SiLU when act == 1
+// y = (x - mean) * rstd * weight + bias, then SiLU when act == 1. Thread t of a workgroup keeps
+// channels 8 (t % nv) .. + 8 (nv = C / 8 vectors per pixel) for all its pixels, with the scale
+// rstd * weight and shift bias - mean * scale of its 8 channels computed once; blockIdx.y is the
+// batch element.
 template <typename T>
 __global__ __launch_bounds__(256) void gn_apply_kernel(const T* __restrict__ x, T* __restrict__ y,
                                                        int64_t pixels, int channels, int groups,
                                                        const float* __restrict__ mean,
                                                        const float* __restrict__ rstd,
                                                        const float* __restrict__ w,
-                                                       const float* __restrict__ bias, int act,
-                                                       int batch) {
-  const int nv = channels / 8;
-  const int64_t total = (int64_t)batch * pixels * nv;
-  const int cpg = channels / groups;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * 256) {
-    const int cv = (int)(i % nv);
-    const int b = (int)(i / ((int64_t)pixels * nv));
+                                                       const float* __restrict__ bias, int act) {
+  const int nv = channels / 8, ppb = 256 / nv;  // pixels per workgroup pass
+  const int cv = threadIdx.x % nv, pr = threadIdx.x / nv;
+  if (pr >= ppb) return;
+  const int b = blockIdx.y, cpg = channels / groups;
+  float sc[8], sh[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int c = cv * 8 + k, gi = b * groups + c / cpg;
+    sc[k] = rstd[gi] * (w ? w[c] : 1.f);
+    sh[k] = (bias ? bias[c] : 0.f) - mean[gi] * sc[k];
+  }
+  const int64_t base = (int64_t)b * pixels * channels + cv * 8;
+  for (int64_t p = (int64_t)blockIdx.x * ppb + pr; p < pixels; p += (int64_t)gridDim.x * ppb) {
     float v[8];
-    Vec8<T>::load(x + i * 8, v);
+    Vec8<T>::load(x + base + p * channels, v);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const int c = cv * 8 + k, gi = b * groups + c / cpg;
-      float o = (v[k] - mean[gi]) * rstd[gi];
-      o = o * (w ? w[c] : 1.f) + (bias ? bias[c] : 0.f);
+      float o = __builtin_fmaf(v[k], sc[k], sh[k]);
       if (act == 1) o = o / (1.0f + __expf(-o));
       v[k] = o;
     }
-    Vec8<T>::store(y + i * 8, v);
+    Vec8<T>::store(y + base + p * channels, v);
   }
 }
 
@@ -257,21 +273,22 @@ extern "C" int difflet_rocm_group_norm(const void* x, void* y, int dtype, int64_
   float* rstd = mean + batch * groups;
   hipStream_t s = (hipStream_t)stream;
   const dim3 sgrid((unsigned)chunks, (unsigned)batch);
-  const unsigned rblocks = (unsigned)((batch * groups + 63) / 64);
-  int64_t ablocks = (batch * pixels * (channels / 8) + 255) / 256;
-  if (ablocks > 65536) ablocks = 65536;
+  const unsigned rblocks = (unsigned)(batch * groups);
+  const int64_t ppb = 256 / (channels / 8);
+  int64_t ablocks = (pixels + ppb - 1) / ppb;
+  if (ablocks > 4096) ablocks = 4096;
+  const dim3 agrid((unsigned)ablocks, (unsigned)batch);
   DLT_DISPATCH_BF16_F32(dtype, T,
     hipLaunchKernelGGL((gn_stats_kernel<T>), sgrid, dim3(256), 0, s, (const T*)x, pixels,
                        (int)channels, (int)groups, chunk, (const float*)nullptr, partial);
-    hipLaunchKernelGGL(gn_reduce_kernel, dim3(rblocks), dim3(64), 0, s, partial, (int)batch,
+    hipLaunchKernelGGL(gn_reduce_kernel, dim3(rblocks), dim3(256), 0, s, partial, (int)batch,
                        chunks, (int)channels, (int)groups, pixels, 0, eps, mean);
     hipLaunchKernelGGL((gn_stats_kernel<T>), sgrid, dim3(256), 0, s, (const T*)x, pixels,
                        (int)channels, (int)groups, chunk, (const float*)mean, partial);
-    hipLaunchKernelGGL(gn_reduce_kernel, dim3(rblocks), dim3(64), 0, s, partial, (int)batch,
+    hipLaunchKernelGGL(gn_reduce_kernel, dim3(rblocks), dim3(256), 0, s, partial, (int)batch,
                        chunks, (int)channels, (int)groups, pixels, 1, eps, rstd);
-    hipLaunchKernelGGL((gn_apply_kernel<T>), dim3((unsigned)ablocks), dim3(256), 0, s,
-                       (const T*)x, (T*)y, pixels, (int)channels, (int)groups, mean, rstd, weight,
-                       bias, act, (int)batch));
+    hipLaunchKernelGGL((gn_apply_kernel<T>), agrid, dim3(256), 0, s, (const T*)x, (T*)y, pixels,
+                       (int)channels, (int)groups, mean, rstd, weight, bias, act));
   return dlt_check_launch("group_norm");
 }
 
