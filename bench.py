@@ -1,7 +1,7 @@
 """Benchmark: one DiT denoise step on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload flux|qwen|wan|weights|compile|t5|umt5|vae]
+                    [--workload flux|qwen|wan|weights|compile|t5|umt5|vae|wanvae]
                     [--kinds bf16,fp8] [--no-cpu] [--calibrate-copy]
 
 flux (default): the full FLUX.1-dev-shaped transformer forward of one denoise step, batch 1,
@@ -26,6 +26,8 @@ t5 / umt5: the text encoder before the denoise loop, FLUX's T5-XXL / Wan's UMT5-
 rest padding under the mask), bf16 and fp32; `value` is the bf16 encode in ms.
 vae: FLUX's VAE decoder after the loop, a 128 x 128 x 16 latent to a 1024 x 1024 image, bf16
 and fp32; `value` is the bf16 decode in ms.
+wanvae: Wan 2.2's 3D causal VAE decoder after the loop, a 21 x 60 x 104 x 16 latent to 81
+frames of 480 x 832, bf16 and fp32; `value` is the bf16 decode in ms.
 Weights are random N(0, 0.02) drawn on the device (norm weights ones); inputs N(0, 1); the
 encoders and the decoder draw their weights with their initializations' scales.
 
@@ -79,7 +81,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="flux",
-                    choices=("flux", "qwen", "wan", "weights", "compile", "t5", "umt5", "vae"))
+                    choices=("flux", "qwen", "wan", "weights", "compile", "t5", "umt5", "vae",
+                             "wanvae"))
     ap.add_argument("--kinds", default=None,
                     help="comma list (flux: bf16,fp8 by default; qwen: mx,bf16)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -610,6 +613,35 @@ def vae_flops(cfg, h, w):
     return total
 
 
+def wan_vae_flops(cfg, t, h, w):
+    """Matrix FLOPs of one decode of a t x h x w latent by Wan's causal decoder: every
+    convolution at its resolution over the frames it runs on (the time convolutions skip the
+    first latent frame), the mid-block attention's projections, scores and P V per frame."""
+    from difflet_amd.vae import wan as dwan
+
+    dims, z = cfg.dims, cfg.z_dim
+    px, frames = h * w, t
+    total = 2 * t * px * z * z + 2 * t * px * 27 * z * dims[0]  # post_quant_conv, conv_in
+    c0 = dims[0]
+    total += 2 * 2 * (2 * t * px * 27 * c0 * c0)                 # mid-block resnets
+    total += t * (2 * px * c0 * 4 * c0 + 4 * px * px * c0)         # attention
+    for _, cin, cout, mode in dwan.plan(cfg):
+        c = cin
+        for _ in range(cfg.num_res_blocks + 1):
+            total += 2 * frames * px * 27 * (c * cout + cout * cout)
+            if c != cout:
+                total += 2 * frames * px * c * cout
+            c = cout
+        if mode == "upsample3d":
+            total += 2 * (frames - 1) * px * 3 * cout * 2 * cout
+            frames = 1 + 2 * (frames - 1)
+        if mode is not None:
+            px *= 4
+            total += 2 * frames * px * 9 * cout * (cout // 2)
+    total += 2 * frames * px * 27 * dims[-1] * cfg.out_channels
+    return total
+
+
 def _time(fn, steps, warmup, torch):
     for _ in range(max(warmup, 1)):
         fn()
@@ -651,6 +683,23 @@ def run_stage(args, torch, log):
                                           "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
             log(f"[{args.workload}] {dt}: {ms:.2f} ms")
             del enc
+            torch.cuda.empty_cache()
+    elif args.workload == "wanvae":
+        from difflet_amd.vae import wan as dwan
+
+        cfg = dwan.WAN_VAE
+        z = torch.randn(1, 16, 21, 60, 104, generator=torch.Generator().manual_seed(SEED)).to(dev)
+        flops = wan_vae_flops(cfg, 21, 60, 104)
+        workload = ("Wan 2.2 VAE decoder (3D causal), 21 x 60 x 104 x 16 latent -> 81 frames of "
+                    "480 x 832 RGB")
+        for dt in (torch.bfloat16, torch.float32):
+            dec = dwan.WanVaeDecoder(cfg, dwan.random_param_source(cfg, SEED, dev), dtype=dt,
+                                     device=dev)
+            ms, med = _time(lambda: dec.decode(z), args.steps, args.warmup, torch)
+            res[str(dt).split(".")[1]] = {"ms": round(ms, 3), "median_ms": round(med, 3),
+                                          "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+            log(f"[wanvae] {dt}: {ms:.2f} ms")
+            del dec
             torch.cuda.empty_cache()
     else:
         from difflet_amd.vae import decoder as dvae
@@ -706,7 +755,7 @@ def main():
         return run_weights(args, torch, log)
     if args.workload == "compile":
         return run_compile(args, torch, log)
-    if args.workload in ("t5", "umt5", "vae"):
+    if args.workload in ("t5", "umt5", "vae", "wanvae"):
         return run_stage(args, torch, log)
     wl = WORKLOADS[args.workload]()
     kinds = [k for k in (args.kinds or ",".join(wl.kinds)).split(",") if k]

@@ -216,6 +216,117 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* __restri
     Elt<T>::store(prow + c, __expf(row[c] * scale - mx) * inv);
 }
 
+// ---- Wan's 3D causal VAE decoder (difflet/models/wan/vae/modeling_vae.py).
+//
+// Frames are channels-last too: frame f of a chunk is [pixels][channels] at a frame address
+// base(f) = (f / fpb) * fstride + (f % fpb) * sub with pixel stride ld. fpb = 2 reads the time
+// convolution's [t][pixels][2C] output as the frames it interleaves (frame 2t = channels
+// [0, C) of frame t, frame 2t + 1 = channels [C, 2C)) without a copy.
+
+// im2col of a causal (kt, ks, ks) convolution, kt in {1, 3}, ks in {1, 3}, spatial padding ks / 2
+// and temporal padding kt - 1 frames in front: for output frame t of the chunk and output pixel
+// (y, x), tap (dt, ky, kx) reads frame t + dt - (kt - 1) at pixel (y + ky - ks / 2, x + kx -
+// ks / 2), zero outside the image; a frame before the chunk (-2 or -1) comes from the two-frame
+// cache [2][pixels][C] of the convolution's input (zeros when cache is null). Row r of out holds
+// output row row0 + r = t * Ho * Wo + y * Wo + x; columns ((dt * ks + ky) * ks + kx) * C + c,
+// zero from kt ks^2 C to kpad. up == 1 doubles each frame by nearest neighbour first.
+template <typename T>
+__global__ __launch_bounds__(256) void im2col_causal_kernel(
+    const T* __restrict__ x, int64_t fstride, int fpb, int64_t sub, int64_t ld,
+    const T* __restrict__ cache, int h, int w, int channels, int kt, int ks, int up,
+    int64_t row0, int64_t rows, T* __restrict__ out, int64_t ldo, int kpad) {
+  constexpr int EV = 16 / sizeof(T);
+  const int ho = h << up, wo = w << up;
+  const int64_t po = (int64_t)ho * wo, pin = (int64_t)h * w;
+  const int taps = kt * ks * ks, half = ks >> 1;
+  const int nv = kpad / EV;
+  const int64_t total = rows * nv;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / nv;
+    const int col = (int)(i % nv) * EV;
+    const int64_t R = row0 + r;
+    const int t = (int)(R / po);
+    const int p = (int)(R % po);
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (col < taps * channels) {
+      const int tap = col / channels, c = col % channels;
+      const int dt = tap / (ks * ks), rem = tap % (ks * ks);
+      const int yy = p / wo + rem / ks - half, xs = p % wo + rem % ks - half;
+      const int f = t + dt - (kt - 1);
+      if (yy >= 0 && yy < ho && xs >= 0 && xs < wo) {
+        const int64_t pix = (int64_t)(yy >> up) * w + (xs >> up);
+        const T* src = nullptr;
+        if (f >= 0)
+          src = x + (int64_t)(f / fpb) * fstride + (int64_t)(f % fpb) * sub + pix * ld + c;
+        else if (cache)
+          src = cache + ((int64_t)(f + 2) * pin + pix) * channels + c;
+        if (src) v = *reinterpret_cast<const u32x4*>(src);
+      }
+    }
+    *reinterpret_cast<u32x4*>(out + r * ldo + col) = v;
+  }
+}
+
+// WanRMSNorm over the channels of each pixel, then SiLU when act == 1 (modeling_vae.py:154-160):
+// y = x * sqrt(C) / max(||x||_2, eps) * gamma, in fp32, rounded once. LPR lanes share a pixel
+// row, each holding NV vectors of 8 channels (channels <= 8 * LPR * NV).
+template <typename T, int LPR, int NV>
+__global__ __launch_bounds__(256) void rms_channels_kernel(const T* __restrict__ x, int64_t ldx,
+                                                           T* __restrict__ y, int64_t ldy,
+                                                           int64_t rows, int channels,
+                                                           const float* __restrict__ gamma,
+                                                           float eps, int act) {
+  const int lane = threadIdx.x % LPR;
+  const int nvec = channels / 8;
+  const float root = __builtin_sqrtf((float)channels);
+  for (int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LPR; row < rows;
+       row += (int64_t)gridDim.x * (256 / LPR)) {
+    float v[NV][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int vi = lane + j * LPR;
+      if (vi < nvec) {
+        Vec8<T>::load(x + row * ldx + vi * 8, v[j]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) ss = __builtin_fmaf(v[j][k], v[j][k], ss);
+      }
+    }
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, LPR);
+    const float scale = root / fmaxf(__builtin_sqrtf(ss), eps);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int vi = lane + j * LPR;
+      if (vi < nvec) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          float o = v[j][k] * scale * gamma[vi * 8 + k];
+          if (act == 1) o = o / (1.0f + __expf(-o));
+          v[j][k] = o;
+        }
+        Vec8<T>::store(y + row * ldy + vi * 8, v[j]);
+      }
+    }
+  }
+}
+
+// Channels-last rows [n][ld] (the first `channels` columns used) -> channel-first planes
+// out[c][n], each value clamped to [lo, hi]: one thread per row.
+template <typename T>
+__global__ __launch_bounds__(256) void rows_to_planes_kernel(const T* __restrict__ x, int64_t ld,
+                                                             int64_t n, int channels,
+                                                             T* __restrict__ out, float lo,
+                                                             float hi) {
+  for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < n;
+       q += (int64_t)gridDim.x * 256)
+    for (int c = 0; c < channels; ++c) {
+      const float v = Elt<T>::load(x + q * ld + c);  // NaN passes, as torch.clamp keeps it
+      Elt<T>::store(out + (int64_t)c * n + q, v < lo ? lo : (v > hi ? hi : v));
+    }
+}
+
 }  // namespace dlt
 
 using namespace dlt;
@@ -333,4 +444,91 @@ extern "C" int difflet_rocm_softmax_rows(const float* s, int64_t lds, void* p, i
     hipLaunchKernelGGL((softmax_rows_kernel<T>), dim3((unsigned)rows), dim3(256), 0,
                        (hipStream_t)stream, s, lds, (T*)p, ldp, cols, scale));
   return dlt_check_launch("softmax_rows");
+}
+
+extern "C" int difflet_rocm_im2col_causal(const void* x, int64_t frame_stride,
+                                          int64_t frames_per_block, int64_t sub_stride,
+                                          int64_t pixel_stride, const void* cache, int dtype,
+                                          int64_t height, int64_t width, int64_t channels,
+                                          int64_t kt, int64_t ks, int upsample, int64_t row0,
+                                          int64_t rows, void* out, int64_t ldo, int64_t kpad,
+                                          difflet_stream_t stream) {
+  DLT_REQUIRE(height > 0 && width > 0 && channels > 0 && (upsample == 0 || upsample == 1) &&
+                  (kt == 1 || kt == 3) && (ks == 1 || ks == 3) &&
+                  (frames_per_block == 1 || frames_per_block == 2),
+              DIFFLET_EINVAL, "im2col_causal: bad sizes or taps (kt, ks in {1, 3})");
+  DLT_REQUIRE(x && out, DIFFLET_EINVAL, "im2col_causal: null pointer");
+  const int ev = dtype == DIFFLET_F32 ? 4 : 8;
+  const int64_t k = kt * ks * ks * channels;
+  DLT_REQUIRE(channels % ev == 0 && kpad % ev == 0 && kpad >= k && ldo >= kpad && ldo % ev == 0 &&
+                  pixel_stride >= channels && pixel_stride % ev == 0 && sub_stride % ev == 0 &&
+                  frame_stride % ev == 0 && vae_aligned16(x) && vae_aligned16(out) &&
+                  (!cache || vae_aligned16(cache)),
+              DIFFLET_EINVAL,
+              "im2col_causal: channels, strides, kpad and ldo must be multiples of %d (16 bytes), "
+              "kpad >= kt ks^2 C, pointers aligned", ev);
+  const int64_t ho = height << upsample, wo = width << upsample;
+  DLT_REQUIRE(ho * wo < (1LL << 31) && k < (1LL << 30), DIFFLET_EUNSUPPORTED,
+              "im2col_causal: frame too large");
+  DLT_REQUIRE(row0 >= 0 && rows >= 0 && (row0 + rows) / (ho * wo) < (1LL << 31), DIFFLET_EINVAL,
+              "im2col_causal: bad row range");
+  if (rows == 0) return DIFFLET_OK;
+  int64_t blocks = (rows * (kpad / ev) + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  DLT_DISPATCH_BF16_F32(dtype, T,
+    hipLaunchKernelGGL((im2col_causal_kernel<T>), dim3((unsigned)blocks), dim3(256), 0,
+                       (hipStream_t)stream, (const T*)x, frame_stride, (int)frames_per_block,
+                       sub_stride, pixel_stride, (const T*)cache, (int)height, (int)width,
+                       (int)channels, (int)kt, (int)ks, upsample, row0, rows, (T*)out, ldo,
+                       (int)kpad));
+  return dlt_check_launch("im2col_causal");
+}
+
+template <typename T, int LPR, int NV>
+static void launch_rms_channels(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
+                                int channels, const float* gamma, float eps, int act,
+                                hipStream_t s) {
+  int64_t blocks = (rows * LPR + 255) / 256;
+  if (blocks > 16384) blocks = 16384;
+  hipLaunchKernelGGL((rms_channels_kernel<T, LPR, NV>), dim3((unsigned)blocks), dim3(256), 0, s,
+                     (const T*)x, ldx, (T*)y, ldy, rows, channels, gamma, eps, act);
+}
+
+extern "C" int difflet_rocm_rms_norm_channels(const void* x, int64_t ldx, void* y, int64_t ldy,
+                                              int dtype, int64_t rows, int64_t channels,
+                                              const float* gamma, float eps, int act,
+                                              difflet_stream_t stream) {
+  DLT_REQUIRE(rows >= 0 && channels > 0 && channels % 8 == 0 && channels <= 2048 &&
+                  ldx >= channels && ldy >= channels && (act == 0 || act == 1) && eps > 0.f,
+              DIFFLET_EINVAL,
+              "rms_norm_channels: channels (%lld) must be a multiple of 8, <= 2048, "
+              "row strides >= channels, act 0 or 1, eps > 0", (long long)channels);
+  if (rows == 0) return DIFFLET_OK;
+  DLT_REQUIRE(x && y && gamma, DIFFLET_EINVAL, "rms_norm_channels: null pointer");
+  const int ev = dtype == DIFFLET_F32 ? 4 : 8;
+  DLT_REQUIRE(ldx % ev == 0 && ldy % ev == 0 && vae_aligned16(x) && vae_aligned16(y),
+              DIFFLET_EINVAL, "rms_norm_channels: rows must be 16-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  const int nvec = (int)(channels / 8);
+  DLT_DISPATCH_BF16_F32(dtype, T,
+    if (nvec <= 16) launch_rms_channels<T, 16, 1>(x, ldx, y, ldy, rows, (int)channels, gamma, eps, act, s);
+    else if (nvec <= 32) launch_rms_channels<T, 32, 1>(x, ldx, y, ldy, rows, (int)channels, gamma, eps, act, s);
+    else if (nvec <= 64) launch_rms_channels<T, 64, 1>(x, ldx, y, ldy, rows, (int)channels, gamma, eps, act, s);
+    else launch_rms_channels<T, 64, 4>(x, ldx, y, ldy, rows, (int)channels, gamma, eps, act, s));
+  return dlt_check_launch("rms_norm_channels");
+}
+
+extern "C" int difflet_rocm_rows_to_planes(const void* x, int64_t ld, int dtype, int64_t n,
+                                           int64_t channels, void* out, float lo, float hi,
+                                           difflet_stream_t stream) {
+  DLT_REQUIRE(n >= 0 && channels > 0 && ld >= channels && lo <= hi, DIFFLET_EINVAL,
+              "rows_to_planes: bad sizes");
+  if (n == 0) return DIFFLET_OK;
+  DLT_REQUIRE(x && out, DIFFLET_EINVAL, "rows_to_planes: null pointer");
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  DLT_DISPATCH_BF16_F32(dtype, T,
+    hipLaunchKernelGGL((rows_to_planes_kernel<T>), dim3((unsigned)blocks), dim3(256), 0,
+                       (hipStream_t)stream, (const T*)x, ld, n, (int)channels, (T*)out, lo, hi));
+  return dlt_check_launch("rows_to_planes");
 }

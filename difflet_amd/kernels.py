@@ -772,3 +772,84 @@ def softmax_rows(s: torch.Tensor, scale: float, *, dtype: torch.dtype = torch.fl
                                           s.shape[0], s.shape[1], float(scale), _stream(dev)),
           "softmax_rows")
     return p
+
+
+# ------------------------------------------------------------------------ Wan's 3D VAE decoder
+def im2col_causal(x: torch.Tensor, hw: tuple[int, int], channels: int, *, kt: int, ks: int,
+                  kpad: int, upsample: bool = False, cache: torch.Tensor | None = None,
+                  frames_per_block: int = 1, frame_stride: int | None = None,
+                  sub_stride: int = 0, pixel_stride: int | None = None, row0: int = 0,
+                  rows: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Rows of a causal (kt, ks, ks) convolution over the frames held in x (contiguous; frame f
+    at element (f // frames_per_block) * frame_stride + (f % frames_per_block) * sub_stride,
+    pixels pixel_stride apart; by default [frames, H * W, channels]), frames -2 and -1 from
+    cache [2, H * W, channels] (zeros when None): [rows, kpad], output rows row0 .. row0 + rows
+    - 1 (default: every frame of x) at the (upsampled) output resolution."""
+    h, w = hw
+    if not x.is_contiguous():
+        raise ValueError("im2col_causal: x must be contiguous")
+    pix = h * w
+    ld = channels if pixel_stride is None else pixel_stride
+    fpb = frames_per_block
+    fs = pix * ld if frame_stride is None else frame_stride
+    up = int(bool(upsample))
+    po = (h << up) * (w << up)
+    if rows is None:
+        if frame_stride is not None or fpb != 1:
+            raise ValueError("im2col_causal: give rows when the frames are strided")
+        rows = (x.numel() // (pix * ld)) * po - row0
+    dev = _on_gpu(x, cache, out)
+    if row0 < 0 or rows < 0:
+        raise ValueError("im2col_causal: bad row range")
+    if rows:
+        # every element the rows read lies inside x (and cache)
+        last = (row0 + rows - 1) // po
+        end = (last // fpb) * fs + (last % fpb) * sub_stride + (pix - 1) * ld + channels
+        if end > x.numel() or channels > ld:
+            raise ValueError(f"im2col_causal: frames 0..{last} of {h}x{w}x{channels} overrun x "
+                             f"({x.numel()} elements)")
+    if cache is not None and (cache.dtype != x.dtype or tuple(cache.shape) != (2, pix, channels)
+                              or not cache.is_contiguous()):
+        raise ValueError(f"im2col_causal: cache must be a contiguous [2, {pix}, {channels}] of "
+                         "x's dtype")
+    y = out if out is not None else torch.empty((rows, kpad), dtype=x.dtype, device=dev)
+    if y.dtype != x.dtype or y.shape[0] != rows or y.shape[1] < kpad or y.stride(1) != 1:
+        raise ValueError(f"im2col_causal: out must be [{rows}, >= {kpad}] of x's dtype")
+    check(lib().difflet_rocm_im2col_causal(_ptr(x), fs, fpb, sub_stride, ld, _ptr(cache), _dt(x),
+                                           h, w, channels, kt, ks, up, row0, rows, _ptr(y),
+                                           y.stride(0), kpad, _stream(dev)), "im2col_causal")
+    return y
+
+
+def rms_norm_channels(x: torch.Tensor, gamma: torch.Tensor, *, eps: float = 1e-12,
+                      silu: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
+    """WanRMSNorm over the last dim of rows x [rows, C] (bf16 or fp32, unit stride along C):
+    x sqrt(C) / max(||x||, eps) * gamma (fp32 [C]), then SiLU when silu."""
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("rms_norm_channels: x must be [rows, channels] with unit column stride")
+    rows, c = x.shape
+    if gamma.dtype != torch.float32 or gamma.numel() != c or not gamma.is_contiguous():
+        raise ValueError(f"rms_norm_channels: gamma must be a contiguous fp32 [{c}]")
+    dev = _on_gpu(x, gamma, out)
+    y = out if out is not None else torch.empty_like(x)
+    if y.shape != x.shape or y.dtype != x.dtype or y.stride(1) != 1:
+        raise ValueError("rms_norm_channels: out must match x")
+    check(lib().difflet_rocm_rms_norm_channels(_ptr(x), x.stride(0), _ptr(y), y.stride(0), _dt(x),
+                                               rows, c, _ptr(gamma), float(eps), int(bool(silu)),
+                                               _stream(dev)), "rms_norm_channels")
+    return y
+
+
+def rows_to_planes(x: torch.Tensor, channels: int, *, lo: float = float("-inf"),
+                   hi: float = float("inf"), out: torch.Tensor | None = None) -> torch.Tensor:
+    """[n, >= channels] rows -> [channels, n] planes, clamped to [lo, hi]."""
+    if x.dim() != 2 or x.stride(1) != 1 or x.shape[1] < channels:
+        raise ValueError(f"rows_to_planes: x must be [n, >= {channels}] with unit column stride")
+    n = x.shape[0]
+    dev = _on_gpu(x, out)
+    y = out if out is not None else torch.empty((channels, n), dtype=x.dtype, device=dev)
+    if y.dtype != x.dtype or y.numel() != channels * n or not y.is_contiguous():
+        raise ValueError(f"rows_to_planes: out must be a contiguous [{channels}, {n}] of x's dtype")
+    check(lib().difflet_rocm_rows_to_planes(_ptr(x), x.stride(0), _dt(x), n, channels, _ptr(y),
+                                            float(lo), float(hi), _stream(dev)), "rows_to_planes")
+    return y

@@ -394,6 +394,44 @@ int difflet_rocm_im2col3x3(const void* x, int dtype, int64_t height, int64_t wid
 int difflet_rocm_softmax_rows(const float* s, int64_t lds, void* p, int64_t ldp, int dtype,
                               int64_t rows, int64_t cols, float scale, difflet_stream_t stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Wan's 3D causal VAE decoder (WanVAEDecoderModel, difflet/models/wan/vae/modeling_vae.py:509-560;
+ * the same decoder serves Qwen-Image's one latent frame). Frames channels-last, decoded one
+ * latent frame (chunk) at a time, each causal convolution keeping the last two frames of its
+ * input as the next chunk's cache (modeling_vae.py:121-134, 225-268).
+ * ---------------------------------------------------------------------------------------- */
+/* im2col of a causal (kt, ks, ks) convolution, kt and ks in {1, 3} (WanCausalConv3d with
+ * padding (kt - 1, ks / 2, ks / 2) front-only in time, modeling_vae.py:95-134; ks = 3, kt = 1 is
+ * the resampler's nn.Conv2d(3, padding=1) per frame, with upsample == 1 its nearest 2x first,
+ * :163-226). Chunk frame f lies at x + (f / frames_per_block) * frame_stride + (f %
+ * frames_per_block) * sub_stride, pixel stride pixel_stride (elements); frames_per_block 2 reads
+ * the time convolution's [t][pixels][2C] output as its interleaved frames 2t, 2t + 1
+ * (modeling_vae.py:219-221). Frames -2 and -1 come from cache [2][height * width][channels]
+ * (zeros when cache is null: the first chunk's zero padding). out [rows][ldo]: row r is output
+ * row row0 + r = (frame, y, x) of the chunk at the output resolution, columns ((dt ks + ky) ks +
+ * kx) C + c, zero from kt ks^2 C to kpad; the GEMM with the weight [Cout][kt][ks][ks][C] is that
+ * range of the convolution. channels, strides, kpad, ldo multiples of 16 bytes. */
+int difflet_rocm_im2col_causal(const void* x, int64_t frame_stride, int64_t frames_per_block,
+                               int64_t sub_stride, int64_t pixel_stride, const void* cache,
+                               int dtype, int64_t height, int64_t width, int64_t channels,
+                               int64_t kt, int64_t ks, int upsample, int64_t row0, int64_t rows,
+                               void* out, int64_t ldo, int64_t kpad, difflet_stream_t stream);
+
+/* WanRMSNorm over the channels of each row (pixel), then SiLU when act == 1
+ * (modeling_vae.py:137-160, F.normalize in fp32): y = x sqrt(C) / max(||x||_2, eps) * gamma
+ * (fp32 gamma [C]), bf16 or fp32 rows of stride ldx / ldy; channels a multiple of 8, <= 2048; y
+ * may alias x. */
+int difflet_rocm_rms_norm_channels(const void* x, int64_t ldx, void* y, int64_t ldy, int dtype,
+                                   int64_t rows, int64_t channels, const float* gamma, float eps,
+                                   int act, difflet_stream_t stream);
+
+/* out[c][q] = clamp(x[q][c], lo, hi) for q < n, c < channels (x rows of stride ld): the
+ * decoder's channels-last output as the [C][frames * pixels] planes of a [B, C, T, H, W] video,
+ * with the final clamp to [-1, 1] (modeling_vae.py:557). */
+int difflet_rocm_rows_to_planes(const void* x, int64_t ld, int dtype, int64_t n,
+                                int64_t channels, void* out, float lo, float hi,
+                                difflet_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
