@@ -164,37 +164,6 @@ __global__ __launch_bounds__(256) void gn_apply_kernel(const T* __restrict__ x, 
   }
 }
 
-// ---- im2col of a 3x3 convolution with padding 1 over a channels-last image [H][W][C], for the
-// output pixels row0 .. row0 + rows - 1: row r of the [rows][ldo] output holds, for output pixel
-// row0 + r = (y, x) and tap t = 3 ky + kx, the C channels of the input pixel (y + ky - 1,
-// x + kx - 1), zero outside the image; columns 9 C .. kpad - 1 are zero.
-// up == 1: the input is first upsampled 2x by nearest neighbour (Ho = 2 H), i.e. the pixel read
-// is ((y + ky - 1) / 2, (x + kx - 1) / 2). Each thread moves 16 bytes.
-template <typename T>
-__global__ __launch_bounds__(256) void im2col3x3_kernel(const T* __restrict__ x, int h, int w,
-                                                        int channels, int up, int64_t row0,
-                                                        int64_t rows, T* __restrict__ out,
-                                                        int64_t ldo, int kpad) {
-  constexpr int EV = 16 / sizeof(T);  // elements per 16 bytes
-  const int ho = h << up, wo = w << up;
-  const int nv = kpad / EV;           // 16-byte pieces per output row
-  const int64_t total = rows * nv;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * 256) {
-    const int64_t r = i / nv;           // row of out; pixel row0 + r of the image
-    const int col = (int)(i % nv) * EV;
-    const int y = (int)((row0 + r) / wo), xx = (int)((row0 + r) % wo);
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (col < 9 * channels) {
-      const int t = col / channels, c = col % channels;
-      const int yy = y + t / 3 - 1, xs = xx + t % 3 - 1;
-      if (yy >= 0 && yy < ho && xs >= 0 && xs < wo)
-        v = *reinterpret_cast<const u32x4*>(x + ((int64_t)(yy >> up) * w + (xs >> up)) * channels + c);
-    }
-    *reinterpret_cast<u32x4*>(out + r * ldo + col) = v;
-  }
-}
-
 // ---- softmax over rows of fp32 scores: p = exp(s * scale - max) / sum, written in T. One
 // workgroup per row.
 template <typename T>
@@ -223,48 +192,66 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* __restri
 // convolution's [t][pixels][2C] output as the frames it interleaves (frame 2t = channels
 // [0, C) of frame t, frame 2t + 1 = channels [C, 2C)) without a copy.
 
-// im2col of a causal (kt, ks, ks) convolution, kt in {1, 3}, ks in {1, 3}, spatial padding ks / 2
-// and temporal padding kt - 1 frames in front: for output frame t of the chunk and output pixel
-// (y, x), tap (dt, ky, kx) reads frame t + dt - (kt - 1) at pixel (y + ky - ks / 2, x + kx -
-// ks / 2), zero outside the image; a frame before the chunk (-2 or -1) comes from the two-frame
-// cache [2][pixels][C] of the convolution's input (zeros when cache is null). Row r of out holds
+// ---- im2col of a convolution over channels-last frames: a causal (kt, ks, ks) kernel, kt and
+// ks in {1, 3}, spatial padding ks / 2 and temporal padding kt - 1 frames in front (kt = 1,
+// ks = 3: a 3x3 Conv2d per frame). For output frame t of the chunk and output pixel (y, x),
+// tap (dt, ky, kx) reads frame t + dt - (kt - 1) at pixel (y + ky - ks / 2, x + kx - ks / 2),
+// zero outside the frame; a frame before the chunk (-2 or -1) comes from the two-frame cache
+// [2][pixels][C] of the convolution's input (zeros when cache is null). Row r of out holds
 // output row row0 + r = t * Ho * Wo + y * Wo + x; columns ((dt * ks + ky) * ks + kx) * C + c,
 // zero from kt ks^2 C to kpad. up == 1 doubles each frame by nearest neighbour first.
+//
+// A gather bound by its stores (a row of K columns from K / C source pixels). Each workgroup
+// first tabulates its columns' (tap, channel) in LDS, one entry per 16-byte chunk; then each
+// wave takes one output row at a time (its frame and pixel computed once per row) and its lanes
+// copy consecutive 16-byte chunks, so every store instruction writes 1 KB in one piece.
+constexpr int IM2COL_MAX_TAB = 8192;  // chunks with data per row (LDS: 32 KB)
 template <typename T>
-__global__ __launch_bounds__(256) void im2col_causal_kernel(
+__global__ __launch_bounds__(256) void im2col_rows_kernel(
     const T* __restrict__ x, int64_t fstride, int fpb, int64_t sub, int64_t ld,
     const T* __restrict__ cache, int h, int w, int channels, int kt, int ks, int up,
     int64_t row0, int64_t rows, T* __restrict__ out, int64_t ldo, int kpad) {
   constexpr int EV = 16 / sizeof(T);
+  extern __shared__ uint32_t tab[];
   const int ho = h << up, wo = w << up;
   const int64_t po = (int64_t)ho * wo, pin = (int64_t)h * w;
-  const int taps = kt * ks * ks, half = ks >> 1;
-  const int nv = kpad / EV;
-  const int64_t total = rows * nv;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * 256) {
-    const int64_t r = i / nv;
-    const int col = (int)(i % nv) * EV;
+  const int half = ks >> 1;
+  const int nk = kt * ks * ks * channels / EV;  // chunks with data
+  const int nv = kpad / EV;                     // chunks per output row
+  for (int j = threadIdx.x; j < nk; j += 256) {
+    const int col = j * EV, tap = col / channels, c = col - tap * channels;
+    const int dt = tap / (ks * ks), rem = tap - dt * ks * ks, ky = rem / ks, kx = rem - ky * ks;
+    tab[j] = ((uint32_t)dt << 28) | ((uint32_t)ky << 24) | ((uint32_t)kx << 20) | (uint32_t)c;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  for (int64_t r = (int64_t)blockIdx.x * 4 + wv; r < rows; r += (int64_t)gridDim.x * 4) {
     const int64_t R = row0 + r;
     const int t = (int)(R / po);
-    const int p = (int)(R % po);
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (col < taps * channels) {
-      const int tap = col / channels, c = col % channels;
-      const int dt = tap / (ks * ks), rem = tap % (ks * ks);
-      const int yy = p / wo + rem / ks - half, xs = p % wo + rem % ks - half;
-      const int f = t + dt - (kt - 1);
-      if (yy >= 0 && yy < ho && xs >= 0 && xs < wo) {
-        const int64_t pix = (int64_t)(yy >> up) * w + (xs >> up);
-        const T* src = nullptr;
-        if (f >= 0)
-          src = x + (int64_t)(f / fpb) * fstride + (int64_t)(f % fpb) * sub + pix * ld + c;
-        else if (cache)
-          src = cache + ((int64_t)(f + 2) * pin + pix) * channels + c;
-        if (src) v = *reinterpret_cast<const u32x4*>(src);
+    const int p = (int)(R - (int64_t)t * po);
+    const int oy = p / wo, ox = p - oy * wo;
+    T* dst = out + r * ldo;
+    for (int j = lane; j < nv; j += 64) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (j < nk) {
+        const uint32_t e = tab[j];
+        const int dt = (int)(e >> 28), ky = (int)(e >> 24) & 15, kx = (int)(e >> 20) & 15;
+        const int c = (int)(e & 0xfffffu);
+        const int f = t + dt - (kt - 1);
+        const int yy = oy + ky - half, xs = ox + kx - half;
+        if (yy >= 0 && yy < ho && xs >= 0 && xs < wo) {
+          const int64_t pix = (int64_t)(yy >> up) * w + (xs >> up);
+          const T* src = nullptr;
+          if (f >= 0)
+            src = x + (int64_t)(f / fpb) * fstride + (int64_t)(f % fpb) * sub + pix * ld + c;
+          else if (cache)
+            src = cache + ((int64_t)(f + 2) * pin + pix) * channels + c;
+          if (src) v = *reinterpret_cast<const u32x4*>(src);
+        }
       }
+      *reinterpret_cast<u32x4*>(dst + j * EV) = v;
     }
-    *reinterpret_cast<u32x4*>(out + r * ldo + col) = v;
   }
 }
 
@@ -423,12 +410,16 @@ extern "C" int difflet_rocm_im2col3x3(const void* x, int dtype, int64_t height, 
               "im2col3x3: rows [%lld, %lld) outside the %lld output pixels", (long long)row0,
               (long long)(row0 + rows), (long long)(ho * wo));
   if (rows == 0) return DIFFLET_OK;
-  int64_t blocks = (rows * (kpad / ev) + 255) / 256;
+  DLT_REQUIRE(9 * channels / ev <= IM2COL_MAX_TAB, DIFFLET_EUNSUPPORTED,
+              "im2col3x3: too many channels");
+  int64_t blocks = (rows + 3) / 4;
   if (blocks > 65536) blocks = 65536;
+  const size_t tab_bytes = (size_t)(9 * channels / ev) * 4;
   DLT_DISPATCH_BF16_F32(dtype, T,
-    hipLaunchKernelGGL((im2col3x3_kernel<T>), dim3((unsigned)blocks), dim3(256), 0,
-                       (hipStream_t)stream, (const T*)x, (int)height, (int)width, (int)channels,
-                       upsample, row0, rows, (T*)out, ldo, (int)kpad));
+    hipLaunchKernelGGL((im2col_rows_kernel<T>), dim3((unsigned)blocks), dim3(256), tab_bytes,
+                       (hipStream_t)stream, (const T*)x, (int64_t)0, 1, (int64_t)0, channels,
+                       (const T*)nullptr, (int)height, (int)width, (int)channels, 1, 3, upsample,
+                       row0, rows, (T*)out, ldo, (int)kpad));
   return dlt_check_launch("im2col3x3");
 }
 
@@ -473,10 +464,12 @@ extern "C" int difflet_rocm_im2col_causal(const void* x, int64_t frame_stride,
   DLT_REQUIRE(row0 >= 0 && rows >= 0 && (row0 + rows) / (ho * wo) < (1LL << 31), DIFFLET_EINVAL,
               "im2col_causal: bad row range");
   if (rows == 0) return DIFFLET_OK;
-  int64_t blocks = (rows * (kpad / ev) + 255) / 256;
+  DLT_REQUIRE(k / ev <= IM2COL_MAX_TAB, DIFFLET_EUNSUPPORTED, "im2col_causal: too many columns");
+  int64_t blocks = (rows + 3) / 4;
   if (blocks > 65536) blocks = 65536;
+  const size_t tab_bytes = (size_t)(k / ev) * 4;
   DLT_DISPATCH_BF16_F32(dtype, T,
-    hipLaunchKernelGGL((im2col_causal_kernel<T>), dim3((unsigned)blocks), dim3(256), 0,
+    hipLaunchKernelGGL((im2col_rows_kernel<T>), dim3((unsigned)blocks), dim3(256), tab_bytes,
                        (hipStream_t)stream, (const T*)x, frame_stride, (int)frames_per_block,
                        sub_stride, pixel_stride, (const T*)cache, (int)height, (int)width,
                        (int)channels, (int)kt, (int)ks, upsample, row0, rows, (T*)out, ldo,
