@@ -62,31 +62,40 @@ struct GemmProblemDev {
   int64_t rope_row0;  // RoPE table row of row 0
 };
 
-// Split schedule (stream-K). Tiles [0, dp) run one per workgroup. The other S tiles are cut
-// along K: their S * nk (tile, K stage) units, tile-major, are dealt to `groups` workgroups in
-// contiguous ranges [lo(s), lo(s + 1)), lo(s) = s * units / groups, so every workgroup ends at
-// the same time whatever S is. A tile cut between workgroups c0 .. c1 is finished by the last of
-// them to arrive: each other one stores its fp32 accumulators to a workspace slot and counts
-// itself in the tile's counter; the last adds the slots in contributor order (a fixed order: the
-// result does not depend on which one arrives last) and runs the epilogue. Nobody waits.
+// Split schedule. Tiles [0, dp) run one per workgroup. The other S < cus tiles (the last,
+// poorly filled wave) are cut along K, in units of `gran` K stages (nu units per tile), over
+// the nx = 8 XCDs as a whole: workgroups are dealt to the XCDs round-robin, so split workgroup
+// s runs on XCD c = s % 8 as its member r = s / 8 of g = cus / 8. The S tiles form
+// ng = ceil(S / g) groups of g consecutive tiles; XCD c takes the contiguous range
+// [lo(c), lo(c + 1)) of the ng * nu (group, unit) pairs, lo(c) = c * ng * nu / 8, and its
+// member r runs tile (group * g + r) of every group in it (nothing where that is past S). The g
+// workgroups of an XCD thus walk K in lockstep over g neighbouring tiles, as whole tiles do, and
+// share each K slice of their A and W panels through the XCD's L2; a range spans at most two
+// groups (ng <= 8). A tile cut between XCDs c0 .. c1 is finished by the last contributor to
+// arrive: each other one stores its fp32 accumulators in its workspace slot and counts itself in
+// the tile's counter; the last adds the slots in XCD order (a fixed order: the result does not
+// depend on who arrives last) and runs the epilogue. Nobody waits.
 struct SkPlan {
-  int dp;         // data-parallel tiles (workgroups 0 .. dp - 1)
-  int groups;     // split workgroups after them (0: no split part)
-  int nu;         // units per tile: K stages in granules of `gran` (the last may be shorter)
-  int gran;       // K stages per unit (MX: 8, one block of E8M0 scales per row)
-  int64_t units;  // S * nu
+  int dp;      // data-parallel tiles (workgroups 0 .. dp - 1)
+  int groups;  // split workgroups after them (0: no split part; else nx * g)
+  int nu;      // units per tile: K stages in granules of `gran` (the last may be shorter)
+  int gran;    // K stages per unit (MX: 8, one block of E8M0 scales per row)
+  int S;       // cut tiles
+  int g;       // tiles per group = workgroups per XCD
+  int nx;      // XCDs
+  int64_t units;  // ng * nu
 };
-__host__ __device__ inline int64_t sk_lo(const SkPlan& p, int s) {
-  return (int64_t)s * p.units / p.groups;
+__host__ __device__ inline int64_t sk_lo(const SkPlan& p, int c) {
+  return (int64_t)c * p.units / p.nx;
 }
-// the split workgroup whose range holds unit x (0 <= x < units)
+// the XCD whose range holds (group, unit) pair x (0 <= x < units)
 __host__ __device__ inline int sk_owner(const SkPlan& p, int64_t x) {
-  return (int)(((x + 1) * p.groups - 1) / p.units);
+  return (int)(((x + 1) * p.nx - 1) / p.units);
 }
-// workspace slot of workgroup c's part of split tile tl: 0 for the first tile of c's range,
-// 1 for its last (a range holds at most two cut tiles)
-__host__ __device__ inline int sk_slot(const SkPlan& p, int c, int tl) {
-  return 2 * c + (sk_lo(p, c) >= (int64_t)tl * p.nu ? 0 : 1);
+// workspace slot of member r of XCD c for its piece of group gi: two per workgroup, 0 for the
+// first group of c's range, 1 for the second
+__host__ __device__ inline int sk_slot(const SkPlan& p, int c, int r, int gi) {
+  return 2 * (c * p.g + r) + (sk_lo(p, c) >= (int64_t)gi * p.nu ? 0 : 1);
 }
 constexpr int64_t SK_CTR_BYTES = 16384;        // one int counter per split tile
 constexpr int SK_MAX_TILES = (int)(SK_CTR_BYTES / 4);
@@ -204,33 +213,41 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN_WAVES, wn = wave % WN_WAVES;
 
-  // ---- work: one whole tile (data-parallel part), or a range of (tile, K stage) units
+  // ---- work: one whole tile (data-parallel part), or a range of (group, K unit) pairs
   const SkPlan& plan = args.sk;
   const int nk = args.k / KT, nu = plan.nu;
   int bid = blockIdx.x;
-  [[maybe_unused]] int s_self = -1;  // split workgroup index
-  int64_t u_lo, u_hi;
-  if (!SPLIT || bid < plan.dp) {  // XCD-contiguous runs of tiles
+  [[maybe_unused]] int c_self = -1, r_self = 0;  // split workgroups: XCD and member
+  int64_t u_lo = 0, u_hi = 1;                     // one piece, or pairs [u_lo, u_hi)
+  if (!SPLIT || bid < plan.dp) {                  // XCD-contiguous runs of tiles
     if ((plan.dp & 7) == 0) bid = (bid & 7) * (plan.dp >> 3) + (bid >> 3);
-    u_lo = (int64_t)bid * nu;
-    u_hi = u_lo + nu;
   } else {
-    s_self = bid - plan.dp;
-    u_lo = (int64_t)plan.dp * nu + sk_lo(plan, s_self);
-    u_hi = (int64_t)plan.dp * nu + sk_lo(plan, s_self + 1);
+    c_self = (bid - plan.dp) % plan.nx;
+    r_self = (bid - plan.dp) / plan.nx;
+    u_lo = sk_lo(plan, c_self);
+    u_hi = sk_lo(plan, c_self + 1);
   }
   // the split-tile flag lives in the LDS ring, idle when it is used (one LDS variable, above)
   [[maybe_unused]] volatile int& sk_flag = *reinterpret_cast<volatile int*>(lds);
 
-  bool more = true;  // whole-tile launches run the body once
-  for (int64_t u = u_lo; more && u < u_hi;) {
-  if constexpr (!SPLIT) more = false;
-  const int tt = (int)(u / nu);  // tile
-  const int ub = (int)(u - (int64_t)tt * nu), ue = (int)(min(u_hi, (int64_t)(tt + 1) * nu) - (int64_t)tt * nu);
+  for (int64_t u = u_lo; u < u_hi;) {
+  int tt, ub, ue;  // tile, and the units [ub, ue) of it that run here
+  if (!SPLIT || c_self < 0) {
+    tt = bid, ub = 0, ue = nu;
+    u = u_hi;
+  } else {
+    const int gi = (int)(u / nu);
+    const int64_t g0 = (int64_t)gi * nu;
+    ub = (int)(u - g0);
+    ue = (int)(min(u_hi, g0 + nu) - g0);
+    if (u != u_lo) __syncthreads();  // the previous piece's last LDS reads are done
+    u = g0 + ue;
+    const int tl = gi * plan.g + r_self;
+    if (tl >= plan.S) continue;  // past the last cut tile: nothing to run in this group
+    tt = plan.dp + tl;
+  }
   // its K stages [kbeg, kend) run here; the loop below counts them from 0
   const int kbeg = ub * plan.gran, kend = min(ue * plan.gran, nk), nkt = kend - kbeg;
-  if (u != u_lo) __syncthreads();  // the previous tile's last LDS reads are done
-  u += ue - ub;
 
   // ---- tile -> problem, grouped raster
   int p = 0;
@@ -572,13 +589,14 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
     __builtin_amdgcn_s_waitcnt(0x0f70);  // the trailing re-reads land before the workgroup ends
   }
 
-  // ---- a tile cut between split workgroups c0 .. c1: the last to arrive finishes it.
+  // ---- a tile cut between XCDs c0 .. c1: the last contributor to arrive finishes it.
   // Partial sums move through the workspace with device-scope (sc1) loads and stores, which
   // the L2 of another XCD cannot serve stale; a store is complete (vmcnt) before its workgroup
   // counts itself, so a count read at device scope orders them without cache-wide fences.
   if constexpr (SPLIT) if (kbeg != 0 || kend != nk) {
     const int tl = tt - plan.dp;  // tile index within the split part
-    const int64_t x0 = (int64_t)tl * nu;
+    const int gi = tl / plan.g;    // its group
+    const int64_t x0 = (int64_t)gi * nu;
     const int c0 = sk_owner(plan, x0), c1 = sk_owner(plan, x0 + nu - 1);
     const int nc = c1 - c0 + 1;
     int* ctr = reinterpret_cast<int*>(args.ws) + tl;
@@ -589,12 +607,12 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
     // lane's 16 bytes vary across the wave, the rest is a scalar offset
     const uint32_t vo = (uint32_t)lane * 16;
     auto soff = [&](int c, int i, int j, int q) {
-      return (uint32_t)(sk_slot(plan, c, tl) * SK_SLOT_BYTES) +
+      return (uint32_t)(sk_slot(plan, c, r_self, gi) * SK_SLOT_BYTES) +
              (uint32_t)(((wave * (4 * TJ) + i * TJ + j) * 4 + q) * 1024);
     };
     // With two contributors (a + b == b + a) or as the first one, this workgroup's own
     // accumulators can stay in registers and still be summed in contributor order
-    const bool own_in_regs = nc == 2 || s_self == c0;
+    const bool own_in_regs = nc == 2 || c_self == c0;
     bool last = false;
     __syncthreads();  // every wave's loads into the ring have landed (the flag is in slot 0)
     if (own_in_regs) {
@@ -614,7 +632,7 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
             const f32x4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
                              acc[i][j][4 * q + 3]};
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, vo,
-                                                   soff(s_self, i, j, q), SC1);
+                                                   soff(c_self, i, j, q), SC1);
           }
       __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the stores are complete
       __syncthreads();
@@ -632,7 +650,7 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
         for (int j = 0; j < TJ; ++j) acc[i][j] = f32x16{};
     }
     for (int c = c0; c <= c1; ++c) {
-      if (own_in_regs && c == s_self) continue;
+      if (own_in_regs && c == c_self) continue;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -926,22 +944,34 @@ static int64_t sk_workspace_bytes(int groups) {
 
 // The schedule of T tiles of nk K stages (cut in units of `gran` stages) on `cus` compute
 // units. Whole tiles while the last wave of workgroups would still be >= 92 % full; otherwise
-// all but one full wave run whole tiles and the remaining S tiles (one to two waves' worth) are
-// cut along K over `cus` workgroups, each taking at least SK_MIN_STAGES stages.
+// the full waves run whole tiles and the S tiles of the last one are cut over the XCDs (see
+// SkPlan), when each XCD's range is at least SK_MIN_STAGES stages and the cut takes a quarter
+// off the launch's K walk (waves * nu units on the busiest workgroup). The cut tiles' partial
+// sums go through memory: 256 KB out and back per cut, all CUs at once, which at ~6 TB/s costs
+// about as much as 10-20 % of a 3072-deep tile. On MI355X that pays on Qwen-Image's 336-tile
+// launches (FF2 MXFP8 365 -> 316 us, bf16 576 -> 483 us) and loses on FLUX's 216-, 648- and
+// 864-tile ones (out projection bf16 87 -> 101 us, FF1 fp8 169 -> 198 us), which this rule
+// leaves whole.
 static SkPlan sk_plan(int T, int nk, int gran, int cus, int64_t ws_bytes) {
   const int nu = (nk + gran - 1) / gran;
-  SkPlan pl = {T, 0, nu, gran, 0};
-  if (cus <= 0 || T <= 0) return pl;
+  SkPlan pl = {T, 0, nu, gran, 0, 0, 0, 0};
+  constexpr int NX = 8;
+  if (cus <= 0 || T <= 0 || cus % NX != 0) return pl;
   const int waves = (T + cus - 1) / cus;
   if ((double)T >= 0.92 * (double)waves * cus) return pl;
-  const int dp = (T / cus > 1 ? T / cus - 1 : 0) * cus;
-  const int S = T - dp;
-  const int64_t units = (int64_t)S * nu;
-  const int64_t min_units = std::max(1, SK_MIN_STAGES / gran);
-  const int groups = (int)std::min<int64_t>(cus, units / min_units);
-  if (S > SK_MAX_TILES || groups < 2 || ws_bytes < sk_workspace_bytes(groups)) return pl;
+  const int dp = (T / cus) * cus, S = T - dp, g = cus / NX;  // 0 < S < 0.92 cus
+  const int ng = (S + g - 1) / g;
+  const int64_t units = (int64_t)ng * nu;
+  const int64_t span = (units + NX - 1) / NX;
+  if (S > SK_MAX_TILES || ws_bytes < sk_workspace_bytes(cus) ||
+      units / NX < std::max(1, SK_MIN_STAGES / gran) ||
+      4 * (nu - span) < (int64_t)waves * nu)
+    return pl;
   pl.dp = dp;
-  pl.groups = groups;
+  pl.groups = cus;
+  pl.S = S;
+  pl.g = g;
+  pl.nx = NX;
   pl.units = units;
   return pl;
 }
@@ -1142,9 +1172,9 @@ extern "C" int difflet_rocm_gemm_mxfp8(int nproblems, const difflet_gemm_problem
 }
 
 // Host walk of the split schedule the kernels follow (same functions): every (tile, K stage)
-// runs on exactly one workgroup, each cut tile's contributors are the workgroups the kernels
-// sum, and no two cut tiles share a workspace slot. Returns 0, or the first violated check's
-// number; dp / groups receive the plan.
+// runs on exactly one workgroup, each cut tile's contributors are the XCDs the kernels sum, and
+// no two pieces share a workspace slot. Returns 0, or the first violated check's number;
+// dp / groups receive the plan.
 extern "C" int difflet_rocm_gemm_schedule_check(int tiles, int k_stages, int gran, int cus,
                                                 int64_t workspace_bytes, int* dp, int* groups) {
   if (tiles <= 0 || k_stages <= 0 || gran <= 0 || cus <= 0) return 1;
@@ -1152,39 +1182,47 @@ extern "C" int difflet_rocm_gemm_schedule_check(int tiles, int k_stages, int gra
   if (dp) *dp = pl.dp;
   if (groups) *groups = pl.groups;
   if (pl.groups == 0) return pl.dp == tiles ? 0 : 2;
-  if (pl.dp % cus != 0 || pl.dp + (int64_t)pl.units / pl.nu != tiles) return 3;
-  const int S = tiles - pl.dp;
+  const int S = pl.S;
+  if (pl.dp % cus != 0 || pl.dp + S != tiles || pl.groups != pl.nx * pl.g || pl.groups > cus ||
+      pl.units != (int64_t)((S + pl.g - 1) / pl.g) * pl.nu || pl.units > (int64_t)pl.nx * pl.nu)
+    return 3;
+  if (SK_CTR_BYTES + 2 * (int64_t)pl.groups * SK_SLOT_BYTES > workspace_bytes ||
+      S > SK_MAX_TILES)
+    return 4;
   std::vector<int> covered((size_t)S * k_stages, 0);  // per (tile, K stage)
   std::vector<int> slot_tile(2 * (size_t)pl.groups, -1);
-  for (int s = 0; s < pl.groups; ++s) {
-    const int64_t lo = sk_lo(pl, s), hi = sk_lo(pl, s + 1);
-    if (hi - lo < std::max(1, SK_MIN_STAGES / gran)) return 4;
-    for (int64_t u = lo; u < hi;) {  // the kernel's walk
-      const int tl = (int)(u / pl.nu);
-      const int ub = (int)(u - (int64_t)tl * pl.nu);
-      const int ue = (int)(std::min(hi, (int64_t)(tl + 1) * pl.nu) - (int64_t)tl * pl.nu);
+  for (int s = 0; s < pl.groups; ++s) {  // the kernel's walk
+    const int c = s % pl.nx, r = s / pl.nx;
+    const int64_t lo = sk_lo(pl, c), hi = sk_lo(pl, c + 1);
+    if (hi - lo < std::max(1, SK_MIN_STAGES / gran)) return 5;
+    for (int64_t u = lo; u < hi;) {
+      const int gi = (int)(u / pl.nu);
+      const int64_t g0 = (int64_t)gi * pl.nu;
+      const int ub = (int)(u - g0), ue = (int)(std::min(hi, g0 + pl.nu) - g0);
+      u = g0 + ue;
+      const int tl = gi * pl.g + r;
+      if (tl >= S) continue;
       const int kbeg = ub * gran, kend = std::min(ue * gran, k_stages);
-      if (kbeg >= kend) return 11;
+      if (kbeg >= kend) return 6;
       for (int k = kbeg; k < kend; ++k) covered[(size_t)tl * k_stages + k] += 1;
-      if (kbeg != 0 || kend != k_stages) {  // a cut tile
-        const int c0 = sk_owner(pl, (int64_t)tl * pl.nu);
-        const int c1 = sk_owner(pl, (int64_t)(tl + 1) * pl.nu - 1);
-        if (s < c0 || s > c1 || c1 == c0) return 5;
-        const int slot = sk_slot(pl, s, tl);
-        if (slot < 2 * s || slot > 2 * s + 1) return 6;
-        if (slot_tile[slot] != -1) return 7;
+      const int c0 = sk_owner(pl, g0), c1 = sk_owner(pl, g0 + pl.nu - 1);
+      if (c < c0 || c > c1) return 7;
+      if ((kbeg != 0 || kend != k_stages) != (c0 != c1)) return 8;
+      if (c0 != c1) {  // a cut tile: this piece's slot
+        const int slot = sk_slot(pl, c, r, gi);
+        if (slot != 2 * (c * pl.g + r) && slot != 2 * (c * pl.g + r) + 1) return 9;
+        if (slot_tile[slot] != -1) return 10;
         slot_tile[slot] = tl;
       }
-      u += ue - ub;
     }
   }
   for (int v : covered)
-    if (v != 1) return 8;
-  for (int tl = 0; tl < S; ++tl) {  // contributors per the formula own exactly the tile's units
-    const int64_t x0 = (int64_t)tl * pl.nu, x1 = x0 + pl.nu;
+    if (v != 1) return 11;
+  for (int gi = 0; gi * pl.g < S; ++gi) {  // the owners per the formula hold the group's pairs
+    const int64_t x0 = (int64_t)gi * pl.nu, x1 = x0 + pl.nu;
     const int c0 = sk_owner(pl, x0), c1 = sk_owner(pl, x1 - 1);
-    if (sk_lo(pl, c0) > x0 || sk_lo(pl, c1 + 1) < x1) return 9;
-    if (c0 < c1 && sk_lo(pl, c0 + 1) <= x0) return 10;
+    if (sk_lo(pl, c0) > x0 || sk_lo(pl, c1 + 1) < x1) return 12;
+    if (c0 < c1 && sk_lo(pl, c0 + 1) <= x0) return 13;
   }
   return 0;
 }

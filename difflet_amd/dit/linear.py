@@ -121,5 +121,7 @@ def linear_group(get, q, prefixes: list[str], kind: str, *,
 
 
 def run(problems, kind: str, epilogue: int = 0, act_col_start: int = 0, qk=None) -> None:
+    # the stream's split workspace: the kernels cut a launch's last wave of tiles along K where
+    # that pays (Qwen-Image's 336-tile projections) and run every other launch as whole tiles
     kernels.gemm_grouped(problems, kind=kind, epilogue=epilogue, act_col_start=act_col_start,
-                         qk=qk)
+                         qk=qk, workspace="shared")

@@ -186,7 +186,7 @@ _GEMM_FN = {"bf16": "difflet_rocm_gemm_bf16", "fp8": "difflet_rocm_gemm_fp8_roww
             "mx": "difflet_rocm_gemm_mxfp8"}
 
 
-_WORKSPACE: dict[int, torch.Tensor] = {}
+_WORKSPACE: dict[tuple[int, int], torch.Tensor] = {}
 _ATT_WORKSPACE: dict[tuple[int, int], torch.Tensor] = {}
 
 
@@ -206,15 +206,17 @@ def attention_workspace(dev: torch.device) -> torch.Tensor:
 
 
 def gemm_workspace(dev: torch.device) -> torch.Tensor:
-    """The device's shared split-GEMM workspace, zero-filled once on first use. It serves GEMMs
-    issued in order on one stream at a time; concurrent streams pass their own."""
+    """The split-GEMM workspace of the device's current stream, zero-filled once on first use
+    (every launch leaves its counters at zero). Launches on one stream run in order, so they can
+    share it; each stream gets its own, since launches on different streams may overlap."""
     i = dev.index if dev.index is not None else torch.cuda.current_device()
-    ws = _WORKSPACE.get(i)
+    key = (i, torch.cuda.current_stream(torch.device("cuda", i)).cuda_stream)
+    ws = _WORKSPACE.get(key)
     if ws is None:
         with torch.cuda.device(i):
             nbytes = int(lib().difflet_rocm_gemm_workspace_bytes())
         ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=torch.device("cuda", i))
-        _WORKSPACE[i] = ws
+        _WORKSPACE[key] = ws
     return ws
 
 
@@ -292,11 +294,11 @@ def gemm_grouped(problems: Sequence[Problem], *, kind: str = "bf16",
                  workspace: torch.Tensor | None | str = None,
                  qk: QkNormRope | None = None) -> None:
     """Runs up to 4 GEMMs sharing N, K and the epilogue in one launch (writes each p.c).
-    workspace: None (every tile whole on one workgroup, the default), "shared" (the device's,
-    see gemm_workspace) or a zero-filled uint8 tensor of difflet_rocm_gemm_workspace_bytes()
-    bytes, which lets poorly filled launches cut tiles along K. On MI355X at the DiT shapes the
-    cut tiles measure slower than whole ones: workgroups that start mid-tile no longer share
-    K slices of A and W through their XCD's L2."""
+    workspace: None (every tile whole on one workgroup, the default), "shared" (the current
+    stream's, see gemm_workspace) or a zero-filled uint8 tensor of
+    difflet_rocm_gemm_workspace_bytes() bytes, which lets a launch whose last wave of tiles
+    would be poorly filled cut those tiles along K over the XCDs when that takes a quarter off
+    its time (Qwen-Image's 336-tile projections; FLUX's launches stay whole)."""
     # a problem without rows has nothing to compute (and an empty tensor may have no address)
     problems = [p for p in problems if p.a.shape[0] > 0]
     if not problems:

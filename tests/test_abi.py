@@ -52,7 +52,7 @@ def test_error_paths_report_without_a_gpu():
 
 @pytest.mark.parametrize("cus", [256, 304, 80])
 def test_gemm_split_schedule_covers_every_stage_once(cus):
-    """The GEMMs' stream-K schedule, walked on the host with the kernels' own functions: every
+    """The GEMMs' split schedule, walked on the host with the kernels' own functions: every
     (tile, K stage) runs exactly once, cut tiles are summed from their true contributors, and
     no two cut tiles share a workspace slot."""
     import ctypes
@@ -85,14 +85,22 @@ def test_gemm_split_plan_at_the_step_shapes():
     lib = _lib.load()
     ws = 16384 + 2 * 256 * 256 * 256 * 4
     dp, groups = ctypes.c_int(), ctypes.c_int()
-    # a 216-tile launch on 256 CUs splits all of its tiles; a 1512-tile one (98 % full) splits none
+    # Qwen-Image's 336-tile launches run a wave of whole tiles and cut the last 80 over the
+    # 256 CUs; FLUX's 216-tile ones (the cut would save an eighth) and a 1512-tile one (98 %
+    # full) stay whole
+    assert lib.difflet_rocm_gemm_schedule_check(336, 48, 1, 256, ws, ctypes.byref(dp),
+                                                ctypes.byref(groups)) == 0
+    assert (dp.value, groups.value) == (256, 256)
+    assert lib.difflet_rocm_gemm_schedule_check(336, 192, 8, 256, ws, ctypes.byref(dp),
+                                                ctypes.byref(groups)) == 0
+    assert (dp.value, groups.value) == (256, 256)
     assert lib.difflet_rocm_gemm_schedule_check(216, 96, 1, 256, ws, ctypes.byref(dp),
                                                 ctypes.byref(groups)) == 0
-    assert (dp.value, groups.value) == (0, 256)
+    assert (dp.value, groups.value) == (216, 0)
     assert lib.difflet_rocm_gemm_schedule_check(1512, 96, 1, 256, ws, ctypes.byref(dp),
                                                 ctypes.byref(groups)) == 0
     assert (dp.value, groups.value) == (1512, 0)
     # without enough workspace nothing is split
-    assert lib.difflet_rocm_gemm_schedule_check(216, 96, 1, 256, 1 << 20, ctypes.byref(dp),
+    assert lib.difflet_rocm_gemm_schedule_check(336, 48, 1, 256, 1 << 20, ctypes.byref(dp),
                                                 ctypes.byref(groups)) == 0
-    assert (dp.value, groups.value) == (216, 0)
+    assert (dp.value, groups.value) == (336, 0)

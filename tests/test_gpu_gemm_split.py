@@ -44,9 +44,10 @@ def _reference(kind, a, w, b):
     return torch.from_numpy(omx.mx_linear(a.float().numpy(), wq, ws, b.float().numpy()))
 
 
-# (m, n, k): 216 tiles (all cut, two contributors each), 360 and 648 tiles (whole tiles first,
-# then one to two waves cut), 15 tiles of a short K (several contributors per tile)
-SHAPES = [(4608, 3072, 3072), (4608, 5120, 1024), (4608, 9216, 1024), (600, 1280, 3072)]
+# (m, n, k): 336 and 360 tiles (a wave of whole tiles, then the last 80 / 104 cut in groups of
+# 32 over the 8 XCDs, one or two XCDs per tile; fp8 at k = 1024 stays whole), 15 tiles of a
+# long K (one group cut over all 8 XCDs: eight contributors per tile)
+SHAPES = [(7168, 3072, 3072), (4608, 5120, 1024), (600, 1280, 8192)]
 
 
 @pytest.mark.parametrize("kind", ["bf16", "fp8", "mx"])
@@ -76,12 +77,13 @@ def test_split_gemm_equals_whole_tiles_and_reference(gpu, kind, m, n, k):
 
 @pytest.mark.parametrize("kind", ["bf16", "fp8"])
 def test_split_gemm_gate_residual_in_place_grouped(gpu, kind):
-    """FLUX's output projection shape: text and image problems in one launch (216 tiles, all
-    cut), gate * (acc + bias) + residual written over the residual."""
+    """Qwen-Image's output projection shape: text and image problems in one launch (1 + 27
+    row tiles x 12 = 336 tiles, the last 80 cut), gate * (acc + bias) + residual written over
+    the residual."""
     g = torch.Generator().manual_seed(11)
     n, k = 3072, 3072
     probs, refs = [], []
-    for m in (512, 4096):
+    for m in (256, 6889):
         a, w, b = rnd(g, m, k), rnd(g, n, k, std=0.05), rnd(g, n, std=0.1)
         gate, res = rnd(g, 1, n), rnd(g, m, n)
         aq, wq, sa, sw = _operands(kind, a, w, gpu)
