@@ -139,6 +139,46 @@ __device__ __forceinline__ int vt_quad_pos(int q) {
   return (q & ~3) | (r == 1 ? 2 : r == 2 ? 1 : r);
 }
 
+// Ping-pong kernel LDS: K and V tiles both row-major [64 keys][128 dims], filled by direct-to-LDS
+// buffer loads (the DMA writes each instruction's 64 lanes x 16 bytes to 1 KB of consecutive
+// 16-byte slots, so the layouts are slot maps with padding, not swizzles). K rows take 17 slots
+// (272 bytes, the same as k_off): a b128 fragment read of 16 consecutive keys at one chunk hits
+// 16 distinct bank groups. V rows take 20 slots (320 bytes) and are read through
+// ds_read_b64_tr_b16, which transposes within each 16-lane group: lane j of the group supplies
+// the address of 4 dims of key row j / 4, and lane i receives dim i of the 4 rows. A V^T operand
+// (8 keys of one dim per lane) is two such reads; their 32 lanes touch 4 rows x 8 chunks, at
+// bank groups 4 row + chunk (mod 16), all distinct.
+constexpr int PK_SLOTS = 17, PV_SLOTS = 20;
+constexpr int PK_BYTES = BLOCK_N * PK_SLOTS * 16, PV_BYTES = BLOCK_N * PV_SLOTS * 16;
+static_assert(PK_SLOTS * 16 == K_PITCH, "K fragment reads use k_off");
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// One direct-to-LDS load: 16 bytes per lane at byte offset voff of buffer r into LDS bytes
+// [lds_addr + 16 lane, + 16). Written as inline assembly so that the compiler does not track it:
+// the builtin makes it wait for every such load before the next LDS read of any address (it
+// cannot tell the tile being filled from the ones being read), which put each tile's whole
+// load latency in front of the next phase's fragment reads. The kernel waits for these loads
+// itself (vmcnt(0) before the barrier that publishes a tile); the compiler's own waits for the
+// loads it does track only grow stricter with untracked loads in flight.
+// r: the buffer resource's four words (rsrc_words).
+__device__ __forceinline__ void dma16(i32x4_t r, const uint8_t* lds_ptr, uint32_t voff) {
+  const uint32_t la = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds_ptr);
+  // s_nop 4: five wait states for a resource word a VALU instruction (v_readlane) may have just
+  // written; s_nop 0: one between the M0 write and the load that reads it
+  asm volatile("s_nop 4\n\ts_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(la), "v"(voff), "s"(r)
+               : "memory", "m0");
+}
+// The words of make_rsrc's resource: base address, stride 0, `bytes` records, the same flags.
+__device__ __forceinline__ i32x4_t rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return i32x4_t{(int)(uint32_t)a, (int)(uint32_t)((a >> 32) & 0xffffu), (int)bytes, 0x00020000};
+}
+
 // max / sum of x over lanes l and l ^ 32 (the two lanes holding one query's statistics).
 // v_permlane32_swap exchanges the upper half of its first operand with the lower half of its
 // second: given x twice, the two results hold {x, x of lane l ^ 32} in every lane, so their max
@@ -395,12 +435,24 @@ __device__ __forceinline__ void phase_barrier() {
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt / expcnt untouched
   asm volatile("s_barrier" ::: "memory");
 }
+// The same after this wave's direct-to-LDS loads have landed but for the last VM issued (they
+// complete in order): the barrier then publishes the tile the earlier ones filled.
+template <int VM>
+__device__ __forceinline__ void vm_phase_barrier() {
+  static_assert(VM >= 0 && VM < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt(0x0070 | VM);  // vmcnt(VM) lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
+}
 
 template <typename T>
 __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
   typedef typename MfmaT<T>::frag frag;
-  __shared__ __attribute__((aligned(16))) uint8_t sk[2][BLOCK_N * K_PITCH];
-  __shared__ __attribute__((aligned(16))) uint8_t sv[2][HD * VT_PITCH];
+  // one LDS variable (two K tiles, two V tiles, the split flag): with several, the compiler gives
+  // their accesses alias scopes and waits for every direct-to-LDS load before each LDS read
+  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * PK_BYTES + 3 * PV_BYTES + 16];
+  auto sk = [&](int st) { return lds + st * PK_BYTES; };
+  auto sv = [&](int st) { return lds + 3 * PK_BYTES + st * PV_BYTES; };
+  volatile int& last_flag = *reinterpret_cast<volatile int*>(lds + 3 * PK_BYTES + 3 * PV_BYTES);
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -408,7 +460,6 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
   const int gt = tid & 255;  // thread index within the group
   const int col = lane & 31, g = lane >> 5;
 
-  __shared__ int last_flag;
   const int ntiles = (a.seq_k + BLOCK_N - 1) / BLOCK_N;
   int bid = blockIdx.x;  // XCD-contiguous runs of query tiles (whole heads share an L2)
   if ((gridDim.x & 7) == 0) bid = (bid & 7) * (gridDim.x >> 3) + (bid >> 3);
@@ -435,48 +486,56 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
   const int64_t qrow = a.qs[2] * 2, krow = a.ks[2] * 2, vrow = a.vs[2] * 2;
 
   frag qf[8];  // Q fragments (second MFMA operand): row my_q, dims 16c + 8g .. +8
-  {
+  // Loaded after the prologue's tile loads and waited for with them (vmcnt(0)): the compiler
+  // tracks these loads but not the tile loads, and a wait for them still pending at the loop
+  // would sit in the loop body, where the hardware counter also holds the tile loads in flight.
+  auto load_q = [&]() {
     const __amdgpu_buffer_rsrc_t rq =
         make_rsrc(qp, (uint32_t)min((int64_t)a.seq_q * qrow, (int64_t)0xffffffff));
 #pragma unroll
     for (int c = 0; c < 8; ++c)
       qf[c] = __builtin_bit_cast(frag, buf_load16(rq, (uint32_t)(my_q * qrow) + (c * 16 + g * 8) * 2));
-  }
-  const __amdgpu_buffer_rsrc_t rk =
-      make_rsrc(kp, (uint32_t)min((int64_t)a.seq_k * krow, (int64_t)0xffffffff));
-  const __amdgpu_buffer_rsrc_t rv =
-      make_rsrc(vp, (uint32_t)min((int64_t)a.seq_k * vrow, (int64_t)0xffffffff));
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+  };
+  const i32x4_t rk = rsrc_words(kp, (uint32_t)min((int64_t)a.seq_k * krow, (int64_t)0xffffffff));
+  const i32x4_t rv = rsrc_words(vp, (uint32_t)min((int64_t)a.seq_k * vrow, (int64_t)0xffffffff));
 
-  // staging, 256 threads per tile: group B moves K (rows gt / 16 + 16 i, chunk gt % 16),
-  // group A moves V (keys 4 (gt % 16) + i, dims 8 (gt / 16) .. +8, transposed into V^T)
-  const int kr = gt >> 4, kc = gt & 15;
-  const int vkg = gt & 15, vdg = gt >> 4;
-  const int vt_pos = vt_quad_pos(vkg) * 8;
-  u32x4 stg[4];
-  auto load_k = [&](int j0) {
+  // staging by direct-to-LDS loads, 4 waves per tile: group B loads K, group A loads V. A tile
+  // of P slots per row is P instructions of 1 KB; wave wb of the group issues instructions
+  // n = wb + 4 i. Lane l of instruction n fills slot 64 n + l = (row, slot-in-row); the pad slots
+  // load the row's last chunk again (never read). Rows past seq_k load row seq_k - 1 (real,
+  // finite data: its keys are masked to -inf and its P is 0), so no LDS row is left stale. The
+  // whole offset goes in the per-lane offset, which the buffer's range check covers (the host
+  // keeps seq_k + 128 rows within 4 GiB).
+  const int wb = wave & 3;
+  const int pslots = grp_a ? PV_SLOTS : PK_SLOTS;
+  const uint32_t row_bytes = (uint32_t)(grp_a ? vrow : krow);
+  uint32_t rc[5];  // (row << 16) | byte offset in the row
 #pragma unroll
-    for (int i = 0; i < 4; ++i) stg[i] = buf_load16(rk, (uint32_t)((j0 + kr + 16 * i) * krow) + kc * 16);
+  for (int i = 0; i < 5; ++i) {
+    const int sl = (wb + 4 * i) * 64 + lane;
+    rc[i] = ((uint32_t)(sl / pslots) << 16) | (uint32_t)(min(sl % pslots, 15) * 16);
+  }
+  auto dma_voff = [&](int j0, int i) {
+    const uint32_t row = (uint32_t)min(j0 + (int)(rc[i] >> 16), a.seq_k - 1);
+    return row * row_bytes + (rc[i] & 0xffffu);
   };
-  auto store_k = [&](int st) {
+  auto dma_k = [&](int j0, int st) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(&sk[st][k_off(kr + 16 * i, kc)]) = stg[i];
+    for (int i = 0; i < 5; ++i)
+      if (wb + 4 * i < PK_SLOTS)
+        dma16(rk, sk(st) + (wb + 4 * i) * 1024, dma_voff(j0, i));
   };
-  auto load_v = [&](int j0) {
+  auto dma_v = [&](int j0, int st) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) stg[i] = buf_load16(rv, (uint32_t)((j0 + vkg * 4 + i) * vrow) + vdg * 16);
+    for (int i = 0; i < 5; ++i)
+      dma16(rv, sv(st) + (wb + 4 * i) * 1024, dma_voff(j0, i));
   };
-  auto store_v = [&](int st) {
-#pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      const int w = d >> 1, sh = (d & 1) * 16;
-      const uint32_t k0 = (stg[0][w] >> sh) & 0xffffu, k1 = (stg[1][w] >> sh) & 0xffffu;
-      const uint32_t k2 = (stg[2][w] >> sh) & 0xffffu, k3 = (stg[3][w] >> sh) & 0xffffu;
-      u32x2 pk;
-      pk[0] = k0 | (k1 << 16);
-      pk[1] = k2 | (k3 << 16);
-      *reinterpret_cast<u32x2*>(&sv[st][(vdg * 8 + d) * VT_PITCH + vt_pos]) = pk;
-    }
-  };
+  // V^T fragment reads: lane l of 16-lane group G supplies key row 4 g + (l >> 2) % 4 of the
+  // 8-key half and dims 32 dt + 16 (G % 2) + 4 (l % 4); it receives dim 32 dt + l % 32 of keys
+  // {4g .. 4g + 3} (first read) and {8 + 4g .. 8 + 4g + 3} (second), the order of its P values
+  const uint32_t vl = (uint32_t)((4 * g + ((lane >> 2) & 3)) * (PV_SLOTS * 16) +
+                                 32 * ((lane >> 4) & 1) + 8 * (lane & 3));
 
   f32x16 acc[4];
 #pragma unroll
@@ -486,53 +545,52 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
   float m_run = -INFINITY, l_run = 0.f;
   const float cmul = a.scale_log2;
 
-  // One MFMA phase: O^T += V^T P^T of the tile in sv[vst] (4 groups of 4 MFMAs, one per
-  // 16 keys), then S^T = K Q^T of the tile in sk[kst] (4 groups: two d-chunks for both 32-key
-  // blocks, so consecutive MFMAs are independent). The fragments of group i + 1 are read
-  // while group i's MFMAs run; sched_barrier keeps the compiler from pulling each read down
-  // next to its MFMA, where every MFMA would wait out a full LDS latency.
+  // One MFMA phase: O^T += V^T P^T of the tile in sv(vst), 16 MFMAs (steps 0-15: 16-key block
+  // gi = step / 4, output dims 32 dt, dt = step % 4, two transposing 8-byte reads each), then
+  // S^T = K Q^T of the tile in sk(kst), 16 MFMAs (steps 16-31: two d-chunks for both 32-key
+  // blocks per group of four, one 16-byte read each), so consecutive MFMAs are independent.
+  // Fragment reads run ahead of their MFMAs: 6 steps in the P V part (12 reads in flight: the
+  // LDS counter holds 15), 12 steps in the scores part; sched_barrier keeps the compiler from
+  // pulling each read down next to its MFMA, where every MFMA would wait out an LDS latency.
   auto mfma_phase = [&](int vst, int kst) {
-    frag fb[4][4];
-    auto load_group = [&](int gi, frag (&f)[4]) {
-      if (gi < 4) {
+    frag fr[16];  // ring: step t's fragment in fr[t % 16] (at most 13 steps in flight)
+    auto issue = [&](int t) {
+      if (t < 16) {
+        const int gi = t >> 2, dt = t & 3;
         const int base = (gi >> 1) * 32 + (gi & 1) * 16;
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-          f[dt] = *reinterpret_cast<const frag*>(
-              &sv[vst][(dt * 32 + col) * VT_PITCH + (base + g * 8) * 2]);
+        const uint8_t* p = sv(vst) + vl + base * (PV_SLOTS * 16) + dt * 64;
+        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)p);
+        const v4i16 hi =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(p + 8 * (PV_SLOTS * 16)));
+        const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+        fr[t & 15] = __builtin_bit_cast(frag, u32x4{l2[0], l2[1], h2[0], h2[1]});
       } else {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int kt2 = u & 1, c = 2 * (gi - 4) + (u >> 1);
-          f[u] = *reinterpret_cast<const frag*>(&sk[kst][k_off(kt2 * 32 + col, c * 2 + g)]);
-        }
+        const int u = (t - 16) & 3, kt2 = u & 1, c = 2 * ((t - 16) >> 2) + (u >> 1);
+        fr[t & 15] = *reinterpret_cast<const frag*>(sk(kst) + k_off(kt2 * 32 + col, c * 2 + g));
       }
     };
-    auto run_group = [&](int gi, const frag (&f)[4]) {
-      if (gi < 4) {
-        const int kt2 = gi >> 1, hh = gi & 1;
-        u32x4 pb;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) pb[u] = pp[kt2][hh * 4 + u];
-        const frag pf = __builtin_bit_cast(frag, pb);
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) acc[dt] = MfmaT<T>::mma(f[dt], pf, acc[dt]);
+    auto run = [&](int t) {
+      if (t < 16) {
+        const int gi = t >> 2, dt = t & 3, kt2 = gi >> 1, hh = gi & 1;
+        const u32x4 pb = {pp[kt2][hh * 4], pp[kt2][hh * 4 + 1], pp[kt2][hh * 4 + 2],
+                          pp[kt2][hh * 4 + 3]};
+        acc[dt] = MfmaT<T>::mma(fr[t & 15], __builtin_bit_cast(frag, pb), acc[dt]);
       } else {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int kt2 = u & 1, c = 2 * (gi - 4) + (u >> 1);
-          s[kt2] = MfmaT<T>::mma(f[u], qf[c], c == 0 ? f32x16{} : s[kt2]);
-        }
+        const int u = (t - 16) & 3, kt2 = u & 1, c = 2 * ((t - 16) >> 2) + (u >> 1);
+        s[kt2] = MfmaT<T>::mma(fr[t & 15], qf[c], c == 0 ? f32x16{} : s[kt2]);
       }
     };
-    load_group(0, fb[0]);
-    load_group(1, fb[1]);
-    load_group(2, fb[2]);
+    constexpr auto upto = [](int t) { return t < 16 ? t + 6 : (t + 12 < 31 ? t + 12 : 31); };
 #pragma unroll
-    for (int gi = 0; gi < 8; ++gi) {
-      if (gi < 5) load_group(gi + 3, fb[(gi + 3) & 3]);
+    for (int t = 0; t <= upto(0); ++t) issue(t);
+#pragma unroll
+    for (int t = 0; t < 32; ++t) {
+      if (t > 0) {
+#pragma unroll
+        for (int n = upto(t - 1) + 1; n <= upto(t); ++n) issue(n);
+      }
       __builtin_amdgcn_sched_barrier(0);
-      run_group(gi, fb[gi & 3]);
+      run(t);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -542,7 +600,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
       s[kt2] = f32x16{};
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
-        const frag kf = *reinterpret_cast<const frag*>(&sk[st][k_off(kt2 * 32 + col, c * 2 + g)]);
+        const frag kf = *reinterpret_cast<const frag*>(sk(st) + k_off(kt2 * 32 + col, c * 2 + g));
         s[kt2] = MfmaT<T>::mma(kf, qf[c], s[kt2]);
       }
     }
@@ -563,10 +621,23 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kt2][v]);
     mx = pair_max(mx);
-    const float m_new = fmaxf(m_run, mx * cmul);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    m_run = m_new;
+    // Lazy rescaling: the exponentials stay relative to m_run (scaled units) until some query
+    // of the wave sees a score more than 2^8 above it, so p <= 256 (exact in the fp32 sums, in
+    // range for the 16-bit P operand) and the output is rescaled on a few tiles, not on every
+    // tile where a running max grows. The result is the same softmax: O and l share the
+    // reference m_run, which the final normalization and the split merge divide out.
+    const float ms = mx * cmul;
+    if (__any(ms > m_run + 8.0f)) {
+      const float m_new = fmaxf(m_run, ms);
+      const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][v] *= alpha;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
     float ls = 0.f;
 #pragma unroll
     for (int kt2 = 0; kt2 < 2; ++kt2)
@@ -577,61 +648,75 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
         ls += p0 + p1;
         pp[kt2][v >> 1] = MfmaT<T>::pack2(p0, p1);
       }
-    l_run = l_run * alpha + ls;
-    if (__any(alpha != 1.0f)) {  // the running max moved for some query of this wave
+    l_run += ls;
+    // P is computed here, in the softmax phase: without the pins the compiler sinks the
+    // exponentials past the rescale branch into the next MFMA phase, where P is first read,
+    // and the MFMA wave then runs the softmax itself
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+    for (int kt2 = 0; kt2 < 2; ++kt2)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[i][v] *= alpha;
-    }
+      for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(pp[kt2][i]));
   };
 
   // The two groups run separate loops with the same barrier sequence (2 + 2 nt barriers), so
-  // each loop's registers are allocated for that group alone. Key tiles t0 .. t0 + nt - 1.
+  // each loop's registers are allocated for that group alone. Key tiles t0 .. t0 + nt - 1, in a
+  // ring of three K and three V buffers (tile j in buffer j mod 3). Loads in flight: K(j + 3) from
+  // B's softmax phase 2j + 1 to the barrier ending phase 2j + 4 (A's scores(j + 3) are phase
+  // 2j + 5); V(j + 2) from A's MFMA phase 2j + 1 to the barrier ending phase 2j + 4 (A's
+  // P V(j + 2) is phase 2j + 5). Each lands in the buffer whose last readers finished in phase
+  // 2j. Every iteration issues its loads, past the last tile too (their rows clamp to the last
+  // key, in bounds, and nobody reads them), so each barrier waits with one fixed vmcnt that lets
+  // the newest tile's loads (4 or 5 instructions per wave) stay in flight.
   const int k0 = t0 * BLOCK_N;
   if (grp_a) {
-    load_v(k0);
-    phase_barrier();  // prologue: B has K(t0), K(t0 + 1) in LDS
+    dma_v(k0, 0);
+    dma_v(k0 + BLOCK_N, 1);
+    load_q();
+    phase_barrier();  // prologue: B has K(t0) in LDS
     scores_only(0);
     phase_barrier();
+    // ring buffers of tiles j, j + 1, j + 2 (rotated, not j % 3: a division the compiler
+    // keeps in vector registers)
+    int r0 = 0, r1 = 1, r2 = 2;
     for (int jt = 0; jt < nt; ++jt) {
       const int j0 = k0 + jt * BLOCK_N;
-      softmax(j0);  // phase 2j
-      store_v(jt & 1);
-      if (jt + 1 < nt) load_v(j0 + BLOCK_N);
-      phase_barrier();
+      softmax(j0);             // phase 2j
+      vm_phase_barrier<5>();  // V(j) landed, V(j + 1) may be in flight
+      dma_v(j0 + 2 * BLOCK_N, r2);
       __builtin_amdgcn_s_setprio(1);  // phase 2j + 1 (past the last tile the scores read
-      mfma_phase(jt & 1, (jt + 1) & 1);  // the idle K buffer and go unused)
+      mfma_phase(r0, r1);             // an unused K buffer and go unused)
       __builtin_amdgcn_s_setprio(0);
       phase_barrier();
+      const int r = r0;
+      r0 = r1, r1 = r2, r2 = r;
     }
   } else {
-    load_k(k0);
-    store_k(0);
-    if (nt > 1) {
-      load_k(k0 + BLOCK_N);
-      store_k(1);
-    }
-    if (nt > 2) load_k(k0 + 2 * BLOCK_N);
-    // sv[1] is read as "tile -1" by the first P V (with P = 0): zeros, not stale LDS that
+    dma_k(k0, 0);
+    dma_k(k0 + BLOCK_N, 1);
+    dma_k(k0 + 2 * BLOCK_N, 2);
+    // sv(2) is read as "tile -1" by the first P V (with P = 0): zeros, not stale LDS that
     // could hold NaN patterns
-    for (int i = gt; i < HD * VT_PITCH / 16; i += 256)
-      *reinterpret_cast<u32x4*>(&sv[1][i * 16]) = u32x4{0u, 0u, 0u, 0u};
+    for (int i = gt; i < PV_BYTES / 16; i += 256)
+      *reinterpret_cast<u32x4*>(sv(2) + i * 16) = u32x4{0u, 0u, 0u, 0u};
+    load_q();               // with K(t0 .. t0 + 2) landed
     phase_barrier();
-    phase_barrier();  // A scores tile 0
+    phase_barrier();        // A scores tile 0
+    int rp = 2, r0 = 0, r1 = 1;  // ring buffers of tiles j - 1, j, j + 1
     for (int jt = 0; jt < nt; ++jt) {
       const int j0 = k0 + jt * BLOCK_N;
       __builtin_amdgcn_s_setprio(1);  // phase 2j (the first P V is of "tile -1": P = 0)
-      mfma_phase((jt - 1) & 1, jt & 1);
+      mfma_phase(rp, r0);
       __builtin_amdgcn_s_setprio(0);
+      vm_phase_barrier<4>();  // K(j + 1) landed, K(j + 2) may be in flight
+      softmax(j0);            // phase 2j + 1
+      dma_k(j0 + 3 * BLOCK_N, r0);
       phase_barrier();
-      softmax(j0);  // phase 2j + 1
-      if (jt + 2 < nt) store_k(jt & 1);
-      if (jt + 3 < nt) load_k(j0 + 3 * BLOCK_N);
-      phase_barrier();
+      const int r = rp;
+      rp = r0, r0 = r1, r1 = r;
     }
-    mfma_phase((nt - 1) & 1, nt & 1);  // phase 2n: the last P V (scores unused)
+    mfma_phase(rp, r0);  // phase 2n: the last P V (scores unused)
   }
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): no load into the LDS outlives the tile
 
   if (nt != ntiles) {
     // a query tile cut between split workgroups: store this part (device-scope sc1 stores,
