@@ -615,20 +615,37 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
           if (key >= a.seq_k) s[kt2][v] = -INFINITY;
         }
     }
-    float mx = -INFINITY;
+    // Lazy rescaling without a max on the common path: the exponentials are taken relative to
+    // the reference m_run (scaled units; m_run never exceeds the running max, so the largest
+    // score seen so far has p >= 1 and the sums cannot vanish). Only when some lane's sum
+    // reaches 2^20 (a score more than 20 above m_run: the first tile, where m_run is -inf and
+    // the sums are inf or NaN, or a large jump) does the wave find the tile's max, move m_run to
+    // it, rescale O and l and take the exponentials again. P up to 2^20 is exact in the fp32
+    // sums and in range for the 16-bit P operand (whose relative precision does not depend on
+    // the magnitude). The result is the same softmax: O and l share the reference m_run, which
+    // the final normalization and the split merge divide out.
+    auto exps = [&](float m_use) {  // P relative to m_use, and the lane's sum of it
+      float ls = 0.f;
 #pragma unroll
-    for (int kt2 = 0; kt2 < 2; ++kt2)
+      for (int kt2 = 0; kt2 < 2; ++kt2)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kt2][v]);
-    mx = pair_max(mx);
-    // Lazy rescaling: the exponentials stay relative to m_run (scaled units) until some query
-    // of the wave sees a score more than 2^8 above it, so p <= 256 (exact in the fp32 sums, in
-    // range for the 16-bit P operand) and the output is rescaled on a few tiles, not on every
-    // tile where a running max grows. The result is the same softmax: O and l share the
-    // reference m_run, which the final normalization and the split merge divide out.
-    const float ms = mx * cmul;
-    if (__any(ms > m_run + 8.0f)) {
-      const float m_new = fmaxf(m_run, ms);
+        for (int v = 0; v < 16; v += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt2][v], cmul, -m_use));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt2][v + 1], cmul, -m_use));
+          ls += p0 + p1;
+          pp[kt2][v >> 1] = MfmaT<T>::pack2(p0, p1);
+        }
+      return ls;
+    };
+    float ls = exps(m_run);
+    if (__any(!(ls < 0x1p20f))) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt2 = 0; kt2 < 2; ++kt2)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kt2][v]);
+      mx = pair_max(mx);
+      const float m_new = fmaxf(m_run, mx * cmul);
       const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
       m_run = m_new;
       l_run *= alpha;
@@ -636,18 +653,8 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][v] *= alpha;
+      ls = exps(m_run == -INFINITY ? 0.f : m_run);
     }
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
-    float ls = 0.f;
-#pragma unroll
-    for (int kt2 = 0; kt2 < 2; ++kt2)
-#pragma unroll
-      for (int v = 0; v < 16; v += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt2][v], cmul, -m_use));
-        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt2][v + 1], cmul, -m_use));
-        ls += p0 + p1;
-        pp[kt2][v >> 1] = MfmaT<T>::pack2(p0, p1);
-      }
     l_run += ls;
     // P is computed here, in the softmax phase: without the pins the compiler sinks the
     // exponentials past the rescale branch into the next MFMA phase, where P is first read,

@@ -401,6 +401,26 @@ def test_attention_split_schedule_on_two_streams(gpu):
         assert rel_l2(o, w) < 2e-3
 
 
+@pytest.mark.parametrize("ramp", [False, True])
+def test_attention_large_and_growing_scores(gpu, ramp):
+    """Scores far outside exp2's range (softmax scale folded: |s| up to ~60 in log2 units) and,
+    with the ramp, keys whose magnitude grows along the sequence, so the running max jumps by
+    more than 20 on later tiles: the ping-pong kernel's rescaling path against fp32."""
+    g = torch.Generator().manual_seed(31 + ramp)
+    b, h, sq, sk = 1, 2, 600, 2000
+    q, k, v = _attn_case(g, b, h, sq, sk)
+    q = (q.float() * 3).to(torch.bfloat16)
+    k = k.float() * 3
+    if ramp:
+        k = k * torch.linspace(0.2, 3.0, sk).view(1, 1, sk, 1)
+    k = k.to(torch.bfloat16)
+    scale = 1 / math.sqrt(128)
+    ref = ops.attention(q.float(), k.float(), v.float(), scale=scale)
+    out = kernels.attention(q.to(gpu), k.to(gpu), v.to(gpu), scale=scale)
+    assert torch.isfinite(out.float()).all()
+    assert rel_l2(out, ref) < 1e-2
+
+
 def test_attention_folded_heads_and_scale_one(gpu):
     g = torch.Generator().manual_seed(5)
     q, k, v = (rnd(g, 6, 96, 128, std=0.2) for _ in range(3))
