@@ -158,17 +158,19 @@ typedef struct difflet_gemm_qk {
 } difflet_gemm_qk;
 
 /* Workspace of the GEMMs below (all three take the same one). With a workspace, a launch whose
- * output tiles would leave the last wave of workgroups less than 92 % full cuts part of its tiles
- * along K over one workgroup per compute unit (stream-K); the workgroup finishing a cut tile
- * adds the fp32 partial sums of the others in a fixed order, so results are deterministic for
- * a given device. With workspace NULL (or too small) every tile runs whole on one workgroup.
- * The workspace must be zero-filled once when allocated; the GEMMs leave it zeroed. Launches
- * that may overlap in time (different streams) must not share one. Returns the bytes needed on
- * the current device: 16 KiB of counters + 2 x 256 KiB per compute unit. Measured on MI355X at
- * the DiT step's shapes, cut tiles run slower than whole ones (workgroups that start mid-tile
- * stop sharing K slices of A and W through their XCD's L2), so the step passes NULL. No
- * counterpart in the reference, whose linears call the vendor BLAS (torch.nn.functional.linear,
- * difflet/backends/cpu/ops_impl/linear.py:9-41). */
+ * output tiles would leave the last wave of workgroups less than 92 % full runs its full waves
+ * as whole tiles and cuts the last wave's tiles along K over the 8 XCDs: in groups of 32 tiles,
+ * each XCD takes a contiguous range of (group, K unit) pairs and its 32 workgroups walk the
+ * same K units of 32 neighbouring tiles together (whole-tile L2 sharing is kept). The cut is
+ * made only when it takes a quarter off the launch's K walk (Qwen-Image's 336-tile projections
+ * qualify; FLUX's 216-tile ones, which would save an eighth, stay whole). The workgroup
+ * finishing a cut tile adds the fp32 partial sums of the others in a fixed order, so results
+ * are deterministic for a given device. With workspace NULL (or too small) every tile runs
+ * whole on one workgroup. The workspace must be zero-filled once when allocated; the GEMMs
+ * leave it zeroed. Launches that may overlap in time (different streams) must not share one.
+ * Returns the bytes needed on the current device: 16 KiB of counters + 2 x 256 KiB per compute
+ * unit. No counterpart in the reference, whose linears call the vendor BLAS
+ * (torch.nn.functional.linear, difflet/backends/cpu/ops_impl/linear.py:9-41). */
 int64_t difflet_rocm_gemm_workspace_bytes(void);
 
 /* bf16 x bf16 -> fp32 accumulate -> bf16. k % 64 == 0. */
