@@ -2,12 +2,12 @@
 //
 // A [M, K] and W [N, K] are both K-contiguous (activations and nn.Linear weights as stored).
 // One kernel skeleton serves three element types:
-//   bf16  : v_mfma_f32_32x32x16_bf16, 32 K-elements (64 bytes) per K stage;
-//   fp8   : v_mfma_f32_32x32x64_f8f6f4 (e4m3), 64 K-elements per K stage, per-row scales of A
-//           and W applied in the epilogue (acc * sa[m] * sw[n]);
+//   bf16  : v_mfma_f32_32x32x16_bf16, 64 K-elements (128 bytes) per K stage, 4 MFMA K steps;
+//   fp8   : v_mfma_f32_32x32x64_f8f6f4 (e4m3), 128 K-elements per K stage, 2 K steps, per-row
+//           scales of A and W applied in the epilogue (acc * sa[m] * sw[n]);
 //   mxfp8 : v_mfma_scale_f32_32x32x64_f8f6f4 with one E8M0 scale per 32-element block of a
-//           row (the block split over the two lane groups, see the K loop), 64 K per K stage.
-// A K stage is therefore always 64 bytes per row, and the LDS geometry is shared.
+//           row (the block split over the two lane groups, see the K loop), 128 K per K stage.
+// A K stage is therefore always 128 bytes per row, and the LDS geometry is shared.
 //
 // Tiling: a workgroup owns a 256 x 256 tile of C: 8 wavefronts in a 2 x 4 grid, each 128 x 64 =
 // 4 x 2 MFMA tiles of 32 x 32 (128 fp32 accumulators per lane), two per SIMD, so one
@@ -17,15 +17,15 @@
 // row m = l % 32 and registers run along n in groups of 4 consecutive columns: the epilogue
 // reads bias / gate / residual and writes C in 8-byte pieces.
 //
-// LDS: a ring of 4 stages of (A tile + W tile) = 4 x 32 KB, filled by direct-to-LDS buffer
-// loads (no register round trip), 3 stages in flight. Rows are XOR-swizzled in 16-byte chunks
-// (swz below) so fragment reads are free of bank conflicts. Global loads are raw buffer loads:
-// rows past M (or N) read as zero, so ragged edges need no branches.
+// LDS: two stage slots of (A tile + W tile) = 2 x 64 KB, filled by direct-to-LDS buffer loads
+// (no register round trip) that each move 8 whole 128-byte rows; MXFP8 adds a 24 KB ring of
+// E8M0 scale blocks. Rows are XOR-swizzled in 16-byte chunks (swz8 below) so fragment reads are
+// free of bank conflicts. Global loads are raw buffer loads: rows past M (or N) read as zero, so
+// ragged edges need no branches.
 //
-// K loop: one straight-line body per stage, one barrier per stage. Half 0 of the stage's MFMAs
-// runs while half 1's fragments are read; half 1 runs in four parts, each interleaving one A
-// tile's MFMAs with the next stage's fragment reads and a quarter of the loads three stages
-// ahead, so no part of the memory pipe sees a burst.
+// K loop: one barrier per stage, placed before the stage's last K step: the fragments of the
+// next K step are read while the current one's MFMAs run, and the next stage's loads go out
+// with the last K step, a quarter per A tile, so each stage has a whole stage to land.
 //
 // Tile order: workgroup ids are spread round-robin over the 8 XCDs, each with its own L2. The id
 // is remapped so each XCD gets a contiguous run of tiles, and tiles run in groups of 8 tile rows
@@ -38,8 +38,7 @@
 
 namespace dlt {
 
-constexpr int BM = 256, BN = 256, KT_BYTES = 64;
-constexpr int STAGES = 4;  // K stages in LDS: 4 x (16 KB A + 16 KB W) = 128 KB, 3 in flight
+constexpr int BM = 256, BN = 256;
 constexpr int MAX_PROBLEMS = 4;
 constexpr int GROUP_M = 8;
 
@@ -79,7 +78,7 @@ struct SkPlan {
   int dp;      // data-parallel tiles (workgroups 0 .. dp - 1)
   int groups;  // split workgroups after them (0: no split part; else nx * g)
   int nu;      // units per tile: K stages in granules of `gran` (the last may be shorter)
-  int gran;    // K stages per unit (MX: 8, one block of E8M0 scales per row)
+  int gran;    // K stages per unit (MX: 4, one block of E8M0 scales per row)
   int S;       // cut tiles
   int g;       // tiles per group = workgroups per XCD
   int nx;      // XCDs
@@ -123,8 +122,8 @@ struct GemmArgs {
 // split-tile code without spills). bf16 and fp8 stage 128 bytes of each row (two slots of
 // 64 KB): a direct-to-LDS load then fetches 8 rows x 128 B, one whole line per row, which moves
 // data from L2 into LDS 1.5x faster than 16 rows x 64 B (measured on FLUX's shapes: the loads
-// alone of fp8 W1 take 123 against 193 us). MXFP8 keeps 64-byte stages in four slots, the
-// geometry its E8M0 scale ring is laid out for.
+// alone of fp8 W1 take 123 against 193 us). MXFP8 stages the same 128 bytes (128 codes) per row;
+// its E8M0 scales (4 bytes per row and stage) take a separate 24 KB ring.
 template <Elem E> struct ElemTraits;
 template <> struct ElemTraits<Elem::BF16> {
   static constexpr int KT = 64, BYTES = 2, WN = 4, KTB = 128, NSLOT = 2;
@@ -133,47 +132,15 @@ template <> struct ElemTraits<Elem::FP8> {
   static constexpr int KT = 128, BYTES = 1, WN = 4, KTB = 128, NSLOT = 2;
 };
 template <> struct ElemTraits<Elem::MX> {
-  static constexpr int KT = 64, BYTES = 1, WN = 4, KTB = 64, NSLOT = 4;
+  static constexpr int KT = 128, BYTES = 1, WN = 4, KTB = 128, NSLOT = 2;
 };
 
-
-// A stage row is 64 bytes = 4 chunks of 16. Chunk c of row r sits at c ^ swz(r), swz(r) =
-// ((r >> 1) ^ (r >> 2)) & 3: the rows an ds_read_b128 serves together (8 or 16 consecutive
-// rows, one logical chunk) then land in distinct bank groups whether the LDS serves 8 lanes
-// over 32 banks or 16 lanes over 64 banks per cycle.
-// Scheduling hint: NREAD LDS reads spread evenly among NMFMA MFMAs (the scheduler would otherwise
-// sink each read next to its first use and wait on it there).
-template <int NMFMA, int NREAD>
-__device__ __forceinline__ void interleave() {
-#pragma unroll
-  for (int r = 0; r < NREAD; ++r) {
-    __builtin_amdgcn_sched_group_barrier(0x008, NMFMA / NREAD, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);              // DS read
-  }
-}
-
-// NM MFMAs with ND LDS reads and NV vector-memory loads spread evenly among them.
-template <int NM, int ND, int NV, int R = 0>
-__device__ __forceinline__ void interleave3() {
-  if constexpr (R < NM) {
-    constexpr int d = (ND * (R + 1)) / NM - (ND * R) / NM;
-    constexpr int v = (NV * (R + 1)) / NM - (NV * R) / NM;
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if constexpr (d > 0) __builtin_amdgcn_sched_group_barrier(0x100, d, 0);
-    if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x020, v, 0);
-    interleave3<NM, ND, NV, R + 1>();
-  }
-}
 
 // Workgroup barrier without the LDS drain __syncthreads implies. At each use the only LDS reads
 // still in flight are of the stage being computed, which no load of this iteration overwrites;
 // the memory clobber keeps the compiler from moving LDS accesses across it.
 __device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
-__device__ __forceinline__ int lds_off(int row, int chunk) {
-  return row * KT_BYTES + ((chunk ^ swz(row)) << 4);
-}
 // A 128-byte stage row is 8 chunks of 16; chunk c of row r sits at c ^ swz8(r), swz8(r) =
 // (r & 7) ^ ((r >> 3) & 1). A fragment read takes one logical chunk of 32 consecutive rows: any 8
 // aligned consecutive rows land in 8 distinct 16-byte bank groups (an LDS serving 8 lanes over
@@ -182,6 +149,29 @@ __device__ __forceinline__ int lds_off(int row, int chunk) {
 __device__ __forceinline__ int swz8(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 __device__ __forceinline__ int lds_off8(int row, int chunk) {
   return row * 128 + ((chunk ^ swz8(row)) << 4);
+}
+
+// Scaled f8f6f4 MFMA whose E8M0 scales are byte oa of sw (first operand) and byte ob of sa
+// (second). The byte selects are instruction fields: callers pass values that are constant
+// after unrolling, and the switches fold away.
+template <int OA>
+__device__ __forceinline__ f32x16 mfma_mx_b(const i32x8& w, const i32x8& a, const f32x16& c,
+                                            uint32_t sw, int ob, uint32_t sa) {
+  switch (ob) {
+    case 0: return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, a, c, 0, 0, OA, (int)sw, 0, (int)sa);
+    case 1: return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, a, c, 0, 0, OA, (int)sw, 1, (int)sa);
+    case 2: return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, a, c, 0, 0, OA, (int)sw, 2, (int)sa);
+    default: return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, a, c, 0, 0, OA, (int)sw, 3, (int)sa);
+  }
+}
+__device__ __forceinline__ f32x16 mfma_mx(const i32x8& w, const i32x8& a, const f32x16& c,
+                                          int oa, uint32_t sw, int ob, uint32_t sa) {
+  switch (oa) {
+    case 0: return mfma_mx_b<0>(w, a, c, sw, ob, sa);
+    case 1: return mfma_mx_b<1>(w, a, c, sw, ob, sa);
+    case 2: return mfma_mx_b<2>(w, a, c, sw, ob, sa);
+    default: return mfma_mx_b<3>(w, a, c, sw, ob, sa);
+  }
 }
 
 // WN = ElemTraits<E>::WN wavefronts along N, 2 along M: 128 WN threads.
@@ -276,9 +266,9 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
   const __amdgpu_buffer_rsrc_t rw =
       make_rsrc(P.w + n0 * w_row_bytes, (uint32_t)min(w_valid, (int64_t)0xffffffff));
 
-  // Direct-to-LDS staging: a stage of one operand is 256 rows x 64 bytes = 16 KB = 16 slabs of
+  // Direct-to-LDS staging: a stage of one operand is 256 rows x 128 bytes = 32 KB = 32 slabs of
   // 1 KB; wave w fills slabs 4 w .. 4 w + 3. Lane l of load i writes slot p = (4 w + i) * 64 + l,
-  // i.e. row p / 4, physical chunk p % 4, so it loads logical chunk (p % 4) ^ swz(row) of that
+  // i.e. row p / 8, physical chunk p % 8, so it loads logical chunk (p % 8) ^ swz8(row) of that
   // row. Per-lane offsets are fixed; the stage's K offset goes in soffset.
   typedef __attribute__((address_space(3))) void lds_void;
   constexpr int SA = SLABS / 2;  // slabs of each operand per wave
@@ -288,22 +278,17 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
 #pragma unroll
   for (int i = 0; i < SA; ++i) {
     const int p = (wave * SA + i) * 64 + lane;
-    int r, ch;
-    if constexpr (KTB == 128) {  // 8 rows x 8 chunks per slab
-      r = p >> 3;
-      ch = (p & 7) ^ swz8(r);
-    } else {  // 16 rows x 4 chunks per slab
-      r = p >> 2;
-      ch = (p & 3) ^ swz(r);
-    }
+    const int r = p >> 3, ch = (p & 7) ^ swz8(r);  // 8 rows x 8 chunks per slab
     a_off[i] = (uint32_t)(r * a_row_bytes) + ch * 16;
     w_off[i] = (uint32_t)(r * w_row_bytes) + ch * 16;
   }
-  // MX scales: block q = the 16 scale bytes of stages 8 q .. 8 q + 7 of every row (K-blocks
-  // 16 q .. 16 q + 15), in ring slot q % 3. Block q + 1 is loaded in 8 parts of 64 rows while the
-  // stages of block q are issued: with stage s, wave s % 8 loads part s % 8 (A rows for parts
-  // 0-3, W rows for 4-7). A part lands before the stages that read it (it was issued with an
-  // earlier stage), and slot (q + 1) % 3 was last read by block q - 2. The whole offset goes in
+  // MX scales: block q = the 16 scale bytes of stages 4 q .. 4 q + 3 of every row (K-blocks
+  // 16 q .. 16 q + 15; stage s's 4 bytes are word s % 4), in ring slot q % 3. Block q + 1 is
+  // loaded in 8 parts of 64 rows (A rows for parts 0-3, W rows for 4-7) while the stages of
+  // block q are issued: with stage s, waves 2 (s % 4) and 2 (s % 4) + 1 load the parts of their
+  // own number. The loads of stage s land by the barrier that publishes stage s, two stages
+  // before block q + 1's first stage 4 q + 4 at the latest, and slot (q + 1) % 3 was last read
+  // by block q - 2, whose stages end before stage 4 q, the first to carry block q + 1. The whole offset goes in
   // the per-lane offset so the resource's range check covers it: bytes past the scale array
   // (rows past M / N, a last block shorter than 16 bytes) read zero.
   const int ksb = K / 32;  // scale row stride (blocks per row)
@@ -316,10 +301,11 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
     const uint32_t row = (p & 3) * 64 + lane;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(p < 4 ? rsa : rsw,
                                              (lds_void*)&smem_sc[blk % 3][p >> 2][(p & 3) * 64][0],
-                                             16, row * ksb + ((kbeg >> 3) + blk) * 16, 0, 0, 0);
+                                             16, row * ksb + ((kbeg >> 2) + blk) * 16, 0, 0, 0);
   };
   // part `part` (of 4) of stage kt's loads: a quarter of this wave's slabs, A slabs first (MX:
-  // with part 0, wave kt % 8 also loads part kt % 8 of the next scale block)
+  // with part 0, waves 2 (kt % 4) and 2 (kt % 4) + 1 also load their parts of the next scale
+  // block)
   auto issue_part = [&](int kt, int st, int part) {
     const uint32_t kb = (uint32_t)(kbeg + kt) * KTB;  // kt counts from the range start
 #pragma unroll
@@ -332,7 +318,7 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
             rw, (lds_void*)&smem[st][1][(wave * SA + s - SA) * 1024], 16, w_off[s - SA], kb, 0, 0);
     }
     if constexpr (E == Elem::MX) {
-      if (part == 0 && wave == (kt & 7) % NWAVES) issue_scales((kt >> 3) + 1, kt & 7);
+      if (part == 0 && (wave >> 1) == (kt & 3)) issue_scales((kt >> 2) + 1, wave);
     }
   };
   auto issue_stage = [&](int kt, int st) {
@@ -354,91 +340,10 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
   const int frow = lane & 31;  // fragment row within a 32-row MFMA tile
   const int fhalf = lane >> 5;
 
-  // A stage (64 bytes of K per row) is computed in two halves of equal MFMA time:
-  //   bf16: MFMA K step h (16 K), all 16 tiles, fragments of chunk 2 h + g;
-  //   fp8 / mx: one 64-K MFMA step; half h covers W tiles j in [h TJ / 2, (h + 1) TJ / 2). The f8f6f4 MFMA
-  //   takes K in lane-group halves: bytes 0-15 of both lane groups are one 32-K block (scaled by
-  //   the group-0 lane's scale), bytes 16-31 the other, so group g holds chunks g and 2 + g.
-  struct Frags {
-    i32x4 a[4][2], w[4][2];  // w[j], j < TJ used
-    uint32_t sa[4], sw[4];  // MX: this lane's scale bytes for its A rows / W rows
-  };
-  auto read_a_i = [&](int st, int kt, Frags& f, int i) {  // A fragment i of half 0
-    const uint8_t* sA = smem[st][0];
-    const int r = wm * 128 + i * 32 + frow;
-    if constexpr (E == Elem::BF16) {
-      f.a[i][0] = *reinterpret_cast<const i32x4*>(sA + lds_off(r, fhalf));
-    } else {
-      f.a[i][0] = *reinterpret_cast<const i32x4*>(sA + lds_off(r, fhalf));
-      f.a[i][1] = *reinterpret_cast<const i32x4*>(sA + lds_off(r, 2 + fhalf));
-    }
-    if constexpr (E == Elem::MX)
-      f.sa[i] = (smem_sc[(kt >> 3) % 3][0][r][(kt & 7) >> 1] >> ((kt & 1) * 16 + fhalf * 8)) & 0xffu;
-  };
-  auto read_a = [&](int st, int kt, Frags& f) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) read_a_i(st, kt, f, i);
-  };
-  auto read_a1 = [&](int st, Frags& f) {  // bf16: the A fragments of half 1
-    const uint8_t* sA = smem[st][0];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      f.a[i][0] = *reinterpret_cast<const i32x4*>(sA + lds_off(wm * 128 + i * 32 + frow, 2 + fhalf));
-  };
-  // W fragment j (bf16: K step h; fp8 / mx: tile j of the stage's one K step)
-  auto read_w_j = [&](int st, int h, int kt, Frags& f, int j) {
-    const uint8_t* sW = smem[st][1];
-    const int r = wn * WTN + j * 32 + frow;
-    if constexpr (E == Elem::BF16) {
-      f.w[j][0] = *reinterpret_cast<const i32x4*>(sW + lds_off(r, h * 2 + fhalf));
-    } else {
-      f.w[j][0] = *reinterpret_cast<const i32x4*>(sW + lds_off(r, fhalf));
-      f.w[j][1] = *reinterpret_cast<const i32x4*>(sW + lds_off(r, 2 + fhalf));
-      if constexpr (E == Elem::MX)
-        f.sw[j] = (smem_sc[(kt >> 3) % 3][1][r][(kt & 7) >> 1] >> ((kt & 1) * 16 + fhalf * 8)) & 0xffu;
-    }
-  };
-  auto read_w = [&](int st, int h, int kt, Frags& f) {
-    if constexpr (E == Elem::BF16) {
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) read_w_j(st, h, kt, f, j);
-    } else {
-#pragma unroll
-      for (int jj = 0; jj < TJ / 2; ++jj) read_w_j(st, h, kt, f, h * (TJ / 2) + jj);
-    }
-  };
-  auto mma_row = [&](const Frags& f, int h, int i) {  // the MFMAs of A tile i in half h
-#pragma unroll
-    for (int jj = 0; jj < (E == Elem::BF16 ? TJ : TJ / 2); ++jj) {
-      const int j = E == Elem::BF16 ? jj : h * (TJ / 2) + jj;
-      if constexpr (E == Elem::BF16) {
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            __builtin_bit_cast(bf16x8, f.w[j][0]), __builtin_bit_cast(bf16x8, f.a[i][0]),
-            acc[i][j], 0, 0, 0);
-      } else {
-        const i32x8 fw = {f.w[j][0][0], f.w[j][0][1], f.w[j][0][2], f.w[j][0][3],
-                          f.w[j][1][0], f.w[j][1][1], f.w[j][1][2], f.w[j][1][3]};
-        const i32x8 fa = {f.a[i][0][0], f.a[i][0][1], f.a[i][0][2], f.a[i][0][3],
-                          f.a[i][1][0], f.a[i][1][1], f.a[i][1][2], f.a[i][1][3]};
-        if constexpr (E == Elem::FP8) {
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw, fa, acc[i][j], 0, 0,
-                                                                      0, 0, 0, 0);
-        } else {
-          // group g scales block g of the stage
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-              fw, fa, acc[i][j], 0, 0, 0, (int)f.sw[j], 0, (int)f.sa[i]);
-        }
-      }
-    }
-  };
-  auto mma_half = [&](const Frags& f, int h) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) mma_row(f, h, i);
-  };
-
-  if constexpr (KTB == 128) {
-    // ---- bf16 / fp8: 128-byte stages in two LDS slots. A stage is NKS MFMA K steps (bf16 4 of
-    // 16 elements, fp8 2 of 64); fragments of the next K step are read while the current one's
+  static_assert(KTB == 128 && NSLOT == 2, "the K loop runs 128-byte stages in two slots");
+  {
+    // ---- 128-byte stages in two LDS slots. A stage is NKS MFMA K steps (bf16 4 of 16 elements,
+    // fp8 and MX 2 of 64); fragments of the next K step are read while the current one's
     // MFMAs run (two register sets). Before the last K step of stage kt every wave waits for its
     // loads of stage kt + 1 (the only ones in flight) and for its own reads of this stage, and
     // one barrier then publishes stage kt + 1 and frees this slot; the loads of stage kt + 2
@@ -448,16 +353,30 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
     // A fragments roll: tile i's fragment of the next K step is read into its registers right
     // after tile i's MFMAs of this step issue; W fragments alternate between two sets. With 128
     // accumulators that keeps a wave within 256 registers (two whole sets spill).
+    // MX: K step ks of a stage is K-blocks 2 ks (lane group 0's chunks) and 2 ks + 1 (group 1's),
+    // each lane passing its row's scale of its group's block: byte 2 ks + fhalf of the stage's
+    // scale word. The scales roll with the fragments they belong to, packed one byte per tile
+    // (the MFMA's scale byte select picks the tile's): A tile i in byte i of sa, W tile j of set
+    // s in byte j of sw[s]. Eight separate registers push the loop past 256 and spill.
     i32x4 fa[4][2], fw[2][4][2];  // [tile][part]; fw[set][tile j < TJ][part]
-    auto read_a = [&](int st, int ks, int i) {
+    [[maybe_unused]] uint32_t sa = 0, sw[2] = {0, 0};
+    auto scale_of = [&](int op, int r, int skt, int ks) {  // MX: operand op's scale for row r
+      return (uint32_t)(reinterpret_cast<const uint8_t*>(&smem_sc[(skt >> 2) % 3][op][r][skt & 3]) +
+                        fhalf)[2 * ks];
+    };
+    // fragments of K step ks of stage skt (counted from the range start), in ring slot st
+    auto read_a = [&](int st, int skt, int ks, int i) {
       const uint8_t* sA = smem[st][0];
       const int r = wm * 128 + i * 32 + frow;
 #pragma unroll
       for (int h = 0; h < NA; ++h)
         fa[i][h] = *reinterpret_cast<const i32x4*>(sA + lds_off8(r, 2 * NA * ks + 2 * h + fhalf));
+      if constexpr (E == Elem::MX)
+        sa = (sa & ~(0xffu << (8 * i))) | (scale_of(0, r, skt, ks) << (8 * i));
     };
-    auto read_w = [&](int st, int ks, int set) {
+    auto read_w = [&](int st, int skt, int ks, int set) {
       const uint8_t* sW = smem[st][1];
+      if constexpr (E == Elem::MX) sw[set] = 0;
 #pragma unroll
       for (int j = 0; j < TJ; ++j) {
         const int r = wn * WTN + j * 32 + frow;
@@ -465,6 +384,7 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
         for (int h = 0; h < NA; ++h)
           fw[set][j][h] =
               *reinterpret_cast<const i32x4*>(sW + lds_off8(r, 2 * NA * ks + 2 * h + fhalf));
+        if constexpr (E == Elem::MX) sw[set] |= scale_of(1, r, skt, ks) << (8 * j);
       }
     };
     auto mma_tile = [&](int set, int i) {
@@ -479,11 +399,23 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
                             fw[set][j][1][0], fw[set][j][1][1], fw[set][j][1][2], fw[set][j][1][3]};
           const i32x8 a8 = {fa[i][0][0], fa[i][0][1], fa[i][0][2], fa[i][0][3],
                             fa[i][1][0], fa[i][1][1], fa[i][1][2], fa[i][1][3]};
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w8, a8, acc[i][j], 0, 0, 0,
-                                                                      0, 0, 0);
+          if constexpr (E == Elem::FP8)
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w8, a8, acc[i][j], 0, 0,
+                                                                        0, 0, 0, 0);
+          else
+          {
+            acc[i][j] = mfma_mx(w8, a8, acc[i][j], j, sw[set], i, sa);
+            // pinned here: left free, the scaled MFMAs sink below the next step's fragment
+            // reads, whose registers then all live at once and spill
+            asm volatile("" : "+v"(acc[i][j]));
+          }
         }
       }
     };
+    if constexpr (E == Elem::MX) {  // scale block 0, one part per wave, ahead of stage 0
+#pragma unroll
+      for (int p = wave; p < 8; p += NWAVES) issue_scales(0, p);
+    }
     issue_stage(0, 0);
     if (nkt > 1) {
       issue_stage(1, 1);
@@ -493,9 +425,9 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
       __builtin_amdgcn_s_waitcnt(0x0f70);
     }
     __syncthreads();
-    read_w(0, 0, 0);
+    read_w(0, 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) read_a(0, 0, i);
+    for (int i = 0; i < 4; ++i) read_a(0, 0, 0, i);
     for (int kt = 0; kt < nkt; ++kt) {
       const int st = kt & 1;
 #pragma unroll
@@ -504,7 +436,7 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
         const bool last = ks == NKS - 1;
         // the next K step: of this stage, or the first of stage kt + 1 (past the range's last
         // stage it reads stale LDS that nothing uses)
-        const int nst = last ? (st ^ 1) : st, nks = last ? 0 : ks + 1;
+        const int nst = last ? (st ^ 1) : st, nkt_s = last ? kt + 1 : kt, nks = last ? 0 : ks + 1;
         const bool loads = last && kt + 2 < nkt;
         if (last) {
           // stage kt + 1 has landed (only its loads are in flight) and this wave's reads of
@@ -512,81 +444,16 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
           __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
           stage_barrier();
         }
-        read_w(nst, nks, set ^ 1);
+        read_w(nst, nkt_s, nks, set ^ 1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           mma_tile(set, i);
-          read_a(nst, nks, i);
+          read_a(nst, nkt_s, nks, i);
           if (loads) issue_part(kt + 2, st, i);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
-  } else {
-  // prologue: stages 0 .. STAGES-2 of the range in flight, then wait for stage 0. Past the last
-    // K stage the loads re-read the last stage (in bounds) into the free ring slot: every
-    // iteration then issues and waits alike, and the loop body is one straight-line block.
-    // (Stage numbers count from the range start, which for MX is a multiple of 8 stages, so the
-    // scale blocks keep their alignment.)
-    if constexpr (E == Elem::MX) {  // scale block 0, one part per wave, ahead of stage 0
-#pragma unroll
-      for (int p = wave; p < 8; p += NWAVES) issue_scales(0, p);
-    }
-#pragma unroll
-    for (int s0 = 0; s0 < STAGES - 1; ++s0) issue_stage(min(s0, nkt - 1), s0);
-    {
-      constexpr int c = 2 * LOADS_PER_STAGE;
-      __builtin_amdgcn_s_waitcnt(0x0f70 | (c & 15) | ((c >> 4) << 14));
-    }
-    __syncthreads();
-    Frags f0, f1;
-    read_a(0, 0, f0);
-    read_w(0, 0, 0, f0);
-    for (int kt = 0; kt < nkt; ++kt) {
-      const int st = kt % STAGES;
-      // half 0 of stage kt; meanwhile read half 1's fragments
-      if constexpr (E == Elem::BF16) {
-        read_a1(st, f1);
-        read_w(st, 1, kt, f1);
-        mma_half(f0, 0);
-        interleave3<4 * TJ, 4 + TJ, 0>();
-      } else {
-        read_w(st, 1, kt, f1);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          f1.a[i][0] = f0.a[i][0];
-          f1.a[i][1] = f0.a[i][1];
-          f1.sa[i] = f0.sa[i];
-        }
-        mma_half(f0, 0);
-        interleave3<2 * TJ, TJ, 0>();
-      }
-      // stage kt + 1 must have landed (stage kt + 2 may still be in flight), then the barrier
-      // publishes it to every wave and frees stage kt - 1 for stage kt + STAGES - 1
-      {
-        constexpr int c = LOADS_PER_STAGE;
-        __builtin_amdgcn_s_waitcnt(0x0f70 | (c & 15) | ((c >> 4) << 14));
-      }
-      stage_barrier();
-      // half 1 of stage kt in four parts, each one A tile's MFMAs, that tile's fragments of
-      // stage kt + 1 (unused after the last stage) and a quarter of stage kt + 3's loads: the
-      // loads then trickle into the vector-memory pipe instead of arriving as one burst
-      const int nst = (kt + 1) % STAGES;
-      const int lk = min(kt + STAGES - 1, nkt - 1), ls = (kt + STAGES - 1) % STAGES;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        mma_row(f1, 1, i);
-        read_a_i(nst, kt + 1, f0, i);
-        if constexpr (E == Elem::BF16) {
-          if (i < TJ) read_w_j(nst, 0, kt + 1, f0, i);
-        } else {
-          if (i < TJ / 2) read_w_j(nst, 0, kt + 1, f0, i);
-        }
-        issue_part(lk, ls, i);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // the trailing re-reads land before the workgroup ends
   }
 
   // ---- a tile cut between XCDs c0 .. c1: the last contributor to arrive finishes it.
@@ -1098,7 +965,7 @@ static int gemm_launch(const char* name, int nproblems, const difflet_gemm_probl
     args.rope_cos = qk->cos;
     args.rope_sin = qk->sin;
   }
-  args.sk = sk_plan((int)tiles, (int)(k / KT), E == Elem::MX ? 8 : 1,
+  args.sk = sk_plan((int)tiles, (int)(k / KT), E == Elem::MX ? 4 : 1,
                     workspace ? device_cus() : 0, workspace ? workspace_bytes : 0);
   args.ws = (uint8_t*)workspace;
   constexpr int NT = ElemTraits<E>::WN;

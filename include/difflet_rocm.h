@@ -199,7 +199,7 @@ int difflet_rocm_gemm_mxfp8(int nproblems, const difflet_gemm_problem* problems,
                             difflet_stream_t stream);
 
 /* Host-side check of the split schedule the GEMMs use for `tiles` output tiles of `k_stages`
- * K stages, cut in units of `gran` stages (1; 8 for MXFP8), on `cus` compute units with
+ * K stages, cut in units of `gran` stages (1; 4 for MXFP8), on `cus` compute units with
  * `workspace_bytes` of workspace: each (tile, stage) runs on exactly one workgroup, and cut
  * tiles are summed from the right contributors and slots. Returns 0 or the number of the failed
  * check; *dp / *groups receive the whole-tile count and the number of split workgroups. Runs on
