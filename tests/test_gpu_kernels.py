@@ -315,12 +315,17 @@ def test_gemm_fp8_rowwise_matches_oracle(gpu, m, n, k):
     assert rel_l2(c, torch.from_numpy(ref)) < 4e-3  # same codes; fp32 sum order + bf16 out
 
 
-@pytest.mark.parametrize("m,n,k", [(256, 256, 128), (300, 520, 384), (1030, 1024, 3072)])
+# K of 1 to 24 stages of 128: scale blocks of four stages, the last one partial at k = 384,
+# 640 and 1152 (the scale ring's 16-byte rows then end inside the next row's bytes)
+@pytest.mark.parametrize("m,n,k", [(256, 256, 128), (300, 520, 384), (200, 384, 640),
+                                   (513, 260, 1152), (1030, 1024, 3072)])
 def test_gemm_mxfp8_matches_fake_quant_linear(gpu, m, n, k):
     print(f"gemm_mx m={m} n={n} k={k}", flush=True)
     g = torch.Generator().manual_seed(m * 3 + k)
     a, w, b = rnd(g, m, k), rnd(g, n, k, std=0.05), rnd(g, n, std=0.1)
     a[0, 7] = 50.0  # an outlier block
+    a[1, k - 5] = -30.0  # in the last block of row 1
+    w[3, k // 2 + 1] = 2.0  # a weight block with its own scale
     wq, ws = kernels.quantize_mxfp8(w.to(gpu), swizzled=True)
     aq, as_ = kernels.quantize_mxfp8(a.to(gpu), swizzled=True)
     c = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
