@@ -75,11 +75,11 @@ def test_split_gemm_equals_whole_tiles_and_reference(gpu, kind, m, n, k):
     assert int(torch.count_nonzero(ctr)) == 0  # every counter back at zero
 
 
-@pytest.mark.parametrize("kind", ["bf16", "fp8"])
+@pytest.mark.parametrize("kind", ["bf16", "fp8", "mx"])
 def test_split_gemm_gate_residual_in_place_grouped(gpu, kind):
     """Qwen-Image's output projection shape: text and image problems in one launch (1 + 27
     row tiles x 12 = 336 tiles, the last 80 cut), gate * (acc + bias) + residual written over
-    the residual."""
+    the residual. MXFP8 runs this epilogue on the split in the Qwen-Image step's FF2."""
     g = torch.Generator().manual_seed(11)
     n, k = 3072, 3072
     probs, refs = [], []
