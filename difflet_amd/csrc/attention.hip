@@ -108,6 +108,8 @@ __host__ __device__ inline int att_owner(int64_t units, int groups, int64_t x) {
 template <typename T> struct MfmaT;
 template <> struct MfmaT<bf16> {
   typedef bf16x8 frag;
+  // lazy-rescale limit of the ping-pong softmax: every P below it is a finite 16-bit operand
+  static constexpr float kLazyLimit = 0x1p20f;
   static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
@@ -120,6 +122,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 template <> struct MfmaT<f16> {
   typedef f16x8 frag;
+  static constexpr float kLazyLimit = 0x1p15f;  // fp16's largest finite value is 65504
   static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
@@ -618,12 +621,13 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
     // Lazy rescaling without a max on the common path: the exponentials are taken relative to
     // the reference m_run (scaled units; m_run never exceeds the running max, so the largest
     // score seen so far has p >= 1 and the sums cannot vanish). Only when some lane's sum
-    // reaches 2^20 (a score more than 20 above m_run: the first tile, where m_run is -inf and
-    // the sums are inf or NaN, or a large jump) does the wave find the tile's max, move m_run to
-    // it, rescale O and l and take the exponentials again. P up to 2^20 is exact in the fp32
-    // sums and in range for the 16-bit P operand (whose relative precision does not depend on
-    // the magnitude). The result is the same softmax: O and l share the reference m_run, which
-    // the final normalization and the split merge divide out.
+    // reaches the type's limit (2^20 for bf16, 2^15 for fp16: a score more than 20 or 15 above
+    // m_run, the first tile, where m_run is -inf and the sums are inf or NaN, or a large jump)
+    // does the wave find the tile's max, move m_run to it, rescale O and l and take the
+    // exponentials again. Every P then stays below the limit: exact in the fp32 sums and finite
+    // in the 16-bit P operand (bf16 reaches 3.4e38, fp16 only 65504; the relative precision of
+    // either does not depend on the magnitude). The result is the same softmax: O and l share
+    // the reference m_run, which the final normalization and the split merge divide out.
     auto exps = [&](float m_use) {  // P relative to m_use, and the lane's sum of it
       float ls = 0.f;
 #pragma unroll
@@ -638,7 +642,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
       return ls;
     };
     float ls = exps(m_run);
-    if (__any(!(ls < 0x1p20f))) {
+    if (__any(!(ls < MfmaT<T>::kLazyLimit))) {
       float mx = -INFINITY;
 #pragma unroll
       for (int kt2 = 0; kt2 < 2; ++kt2)

@@ -710,7 +710,7 @@ def relative_bias(buckets: torch.Tensor, table: torch.Tensor, *, batch: int, seq
 
 
 # ------------------------------------------------------------------------ VAE decoder
-_GN_WORKSPACE: dict[int, torch.Tensor] = {}
+_GN_WORKSPACE: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def group_norm(x: torch.Tensor, groups: int, weight: torch.Tensor | None,
@@ -729,11 +729,15 @@ def group_norm(x: torch.Tensor, groups: int, weight: torch.Tensor | None,
     dev = _on_gpu(x, weight, bias, out)
     y = out if out is not None else torch.empty_like(x)
     need = int(lib().difflet_rocm_group_norm_workspace_bytes(b, p, c, groups))
+    # one workspace per (device, stream), as for the GEMM and attention workspaces: launches on
+    # one stream run in order and can share it, and a grown one replaces the old on the stream
+    # that allocated it, so the allocator reuses the old block only after its last reader
     i = dev.index if dev.index is not None else torch.cuda.current_device()
-    ws = _GN_WORKSPACE.get(i)
+    key = (i, torch.cuda.current_stream(torch.device("cuda", i)).cuda_stream)
+    ws = _GN_WORKSPACE.get(key)
     if ws is None or ws.numel() < need:
-        ws = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
-        _GN_WORKSPACE[i] = ws
+        ws = torch.empty(max(need, 256), dtype=torch.uint8, device=torch.device("cuda", i))
+        _GN_WORKSPACE[key] = ws
     check(lib().difflet_rocm_group_norm(_ptr(x), _ptr(y), _dt(x), b, p, c, groups, _ptr(weight),
                                         _ptr(bias), float(eps), int(bool(silu)), _ptr(ws),
                                         ws.numel(), _stream(dev)), "group_norm")

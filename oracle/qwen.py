@@ -14,10 +14,15 @@ its published algorithm: img_in, txt_norm (RMSNorm) + txt_in, the timestep proje
 (sinusoid of 256 channels, flip_sin_to_cos, shift 0, scale 1000, then linear-SiLU-linear),
 AdaLN-Continuous norm_out (scale first) and proj_out; the 3-axis RoPE table of QwenEmbedRope
 with scale_rope (image height / width positions centred on zero, text positions from
-max(h // 2, w // 2)), angles computed in fp32. These model-level pieces and the RMSNorm
-rounding order of diffusers (normalise in fp32, round to the weight dtype, multiply by the
-weight) are parity unpinned: no fixture of the reference covers them, and the device and this
-oracle consume the same tables and weights. The oracle computes the fp32 RMSNorm law.
+max(h // 2, w // 2)), angles computed in fp32. No fixture of the reference covers these
+model-level pieces; tests/test_oracle_qwen.py pins time_embed, embed_text, final_layer and
+forward's composition by reductions to torch primitives and closed forms (identity linears,
+distinct scale / shift vectors), each with a planted mistake that fails it (sin-first
+sinusoid, a cast after the 1000 scale, LayerNorm for txt_norm, shift-first AdaLN-Continuous).
+Parity unpinned: the RMSNorm rounding order of diffusers in bf16 (normalise in fp32, round to
+the weight dtype, multiply by the weight; the oracle computes the fp32 law) and the
+pos_embed table beyond its closed form (test_rope_table_closed_form restates the published
+rule; the device and this oracle consume the same table).
 
 MXFP8 (config: every targeted linear, QWEN_IMAGE_TARGETS of difflet/quant/targets.py:117-121):
 q/k/v, the added q/k/v and both MLPs take FakeQuantMXLinear's law (difflet/quant/
@@ -252,14 +257,31 @@ def forward(shape: QwenShape, seed: int, latents, text, timestep, img_hw, weight
     L = ops.linear
     R = ops.rounder(store)
     hidden = R(L(latents, ew["img_in.weight"], ew["img_in.bias"]))
-    context = R(L(R(ops.rms_norm_fp32(text, ew["txt_norm.weight"], 1e-6)), ew["txt_in.weight"],
-                  ew["txt_in.bias"]))
+    context = embed_text(ew, text, store)
     temb = time_embed(ew, timestep, model_dtype, store)
     cos, sin = pos_embed(img_hw[0], img_hw[1], text.shape[1], shape.axes, shape.theta)
     for i in range(shape.n_blocks):
         w = weights[1][i] if weights else block_weights(shape, seed, i, dtype=dtype)
         context, hidden = block(w, hidden, context, temb, cos, sin, shape, quant, act_dtype,
                                 store=store, text_valid_len=text_valid_len)
+    return final_layer(ew, hidden, temb, store)
+
+
+def embed_text(ew: dict, text, store=None):
+    """txt_norm (RMSNorm over the text encoder's width, eps 1e-6, the fp32 law) then txt_in:
+    text [B, S_txt, txt_dim] -> [B, S_txt, D]. `store` rounds the normalised text and the
+    result as a device holding them in that dtype."""
+    R = ops.rounder(store)
+    n = R(ops.rms_norm_fp32(text, ew["txt_norm.weight"], 1e-6))
+    return R(ops.linear(n, ew["txt_in.weight"], ew["txt_in.bias"]))
+
+
+def final_layer(ew: dict, hidden, temb, store=None):
+    """AdaLayerNormContinuous norm_out (difflet/layers/normalization.py:150-190: emb =
+    linear(SiLU(temb)), chunked scale first, then shift; LayerNorm without affine, eps 1e-6)
+    and proj_out: hidden [B, S_img, D], temb [B, D] -> [B, S_img, out_ch]."""
+    L = ops.linear
+    R = ops.rounder(store)
     emb = R(L(torch.nn.functional.silu(temb), ew["norm_out.linear.weight"], ew["norm_out.linear.bias"]))
     scale, shift = emb.chunk(2, dim=1)  # AdaLayerNormContinuous: scale first
     hidden = R(ops.layer_norm(hidden) * (1 + scale)[:, None] + shift[:, None])

@@ -24,7 +24,11 @@ parallelism:
                                      unpatchify)
 FP32LayerNorm, Timesteps / TimestepEmbedding and PixArtAlphaTextProjection come from diffusers
 0.38.0 (absent here); their published algorithms are the closed forms above (F.layer_norm in
-fp32, the sinusoid, two linears around an activation).
+fp32, the sinusoid, two linears around an activation). tests/test_oracle_wan.py pins condition,
+final_layer and forward's composition by reductions to torch primitives and closed forms
+(identity linears, distinct shift / scale rows), each with a planted mistake that fails it
+(exact GELU in the text projection, a sin-first sinusoid, t cast to bf16 before the sinusoid,
+shift and scale exchanged).
 
 Weights: N(0, std) per block from torch.Generator(seed + block index) in spec order, rounded to
 the model dtype; RMSNorm / LayerNorm weights ones, the LayerNorm bias zero.
@@ -218,11 +222,18 @@ def forward(shape: WanShape, seed: int, latents, timestep, text, weights=None,
     for i in range(shape.n_blocks):
         wb = weights[1][i] if weights else block_weights(shape, seed, i, dtype=dtype)
         hidden = block(wb, hidden, txt, tproj, cos, sin, shape)
-    shift, scale = (ew["scale_shift_table"] + temb[:, None]).chunk(2, dim=1)
-    hidden = ops.layer_norm(hidden) * (1 + scale) + shift
-    out = ops.linear(hidden, ew["proj_out.weight"], ew["proj_out.bias"])
+    out = final_layer(ew, hidden, temb)
     out = out.reshape(b, *grid, pt, ph, pw, -1).permute(0, 7, 1, 4, 2, 5, 3, 6)
     return out.flatten(6, 7).flatten(4, 5).flatten(2, 3)
+
+
+def final_layer(ew: dict, hidden, temb):
+    """norm_out + proj_out (:1031-1044): (shift, scale) = scale_shift_table + temb, in that
+    chunk order; fp32 LayerNorm without affine, x (1 + scale) + shift, then proj_out.
+    hidden [B, S, D], temb [B, D] -> [B, S, out_ch * prod(patch)]."""
+    shift, scale = (ew["scale_shift_table"] + temb[:, None]).chunk(2, dim=1)
+    hidden = ops.layer_norm(hidden) * (1 + scale) + shift
+    return ops.linear(hidden, ew["proj_out.weight"], ew["proj_out.bias"])
 
 
 def synthetic_inputs(shape: WanShape, seed: int, latent_fhw, txt_len, batch: int = 1):

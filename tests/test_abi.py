@@ -100,6 +100,15 @@ def test_gemm_split_plan_at_the_step_shapes():
     assert lib.difflet_rocm_gemm_schedule_check(1512, 96, 1, 256, ws, ctypes.byref(dp),
                                                 ctypes.byref(groups)) == 0
     assert (dp.value, groups.value) == (1512, 0)
+    # MXFP8 (units of 4 K stages of 128) with a shorter last unit: K = 2816 (22 stages, the last
+    # unit 2) at Qwen-Image's 336 tiles, K = 7808 (61 stages, the last unit 1) on 15 tiles;
+    # both split, as the device tests of these shapes assume
+    assert lib.difflet_rocm_gemm_schedule_check(336, 22, 4, 256, ws, ctypes.byref(dp),
+                                                ctypes.byref(groups)) == 0
+    assert (dp.value, groups.value) == (256, 256)
+    assert lib.difflet_rocm_gemm_schedule_check(15, 61, 4, 256, ws, ctypes.byref(dp),
+                                                ctypes.byref(groups)) == 0
+    assert (dp.value, groups.value) == (0, 256)
     # without enough workspace nothing is split
     assert lib.difflet_rocm_gemm_schedule_check(336, 48, 1, 256, 1 << 20, ctypes.byref(dp),
                                                 ctypes.byref(groups)) == 0

@@ -75,6 +75,14 @@ def test_split_gemm_equals_whole_tiles_and_reference(gpu, kind, m, n, k):
     assert int(torch.count_nonzero(ctr)) == 0  # every counter back at zero
 
 
+# MXFP8 cuts K in units of 4 stages (one E8M0 block per row of 128 K); these K leave a shorter
+# last unit: 2816 = 22 stages at 336 tiles (the last unit 2 stages), 7808 = 61 stages on 15
+# tiles (the last unit 1 stage, eight contributors per tile). Both plans split (test_abi.py).
+@pytest.mark.parametrize("m,n,k", [(7168, 3072, 2816), (600, 1280, 7808)])
+def test_split_gemm_mx_with_a_short_last_unit(gpu, m, n, k):
+    test_split_gemm_equals_whole_tiles_and_reference(gpu, "mx", m, n, k)
+
+
 @pytest.mark.parametrize("kind", ["bf16", "fp8", "mx"])
 def test_split_gemm_gate_residual_in_place_grouped(gpu, kind):
     """Qwen-Image's output projection shape: text and image problems in one launch (1 + 27

@@ -426,6 +426,29 @@ def test_attention_large_and_growing_scores(gpu, ramp):
     assert rel_l2(out, ref) < 1e-2
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("jump", [15.5, 17.0, 19.5])
+def test_attention_late_key_beats_the_running_max(gpu, dtype, jump):
+    """One key on a late tile scores `jump` log2 units above every earlier key (scale 1: a
+    score of jump / log2(e)). Unrescaled its probability would be 2^jump, past fp16's 65504
+    from 2^16 on: the ping-pong kernel must rescale before packing P for fp16 as for bf16."""
+    g = torch.Generator().manual_seed(int(jump * 10))
+    b, h, sq, sk, hot = 1, 2, 300, 2000, 1500
+    q = torch.randn(b, h, sq, 128, generator=g) * 0.02
+    k = torch.randn(b, h, sk, 128, generator=g) * 0.02
+    v = torch.randn(b, h, sk, 128, generator=g)
+    q[..., 0] = 1.0
+    k[..., 0] = 0.0
+    k[:, :, hot, 0] = jump / math.log2(math.e)
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    ref = ops.attention(q.float(), k.float(), v.float(), scale=1.0)
+    out = kernels.attention(q.to(gpu), k.to(gpu), v.to(gpu), scale=1.0)
+    assert torch.isfinite(out.float()).all()
+    err = rel_l2(out, ref)
+    print(f"attention late jump {jump} {dtype}: rel L2 {err:.2e}", flush=True)
+    assert err < 1e-2
+
+
 def test_attention_folded_heads_and_scale_one(gpu):
     g = torch.Generator().manual_seed(5)
     q, k, v = (rnd(g, 6, 96, 128, std=0.2) for _ in range(3))

@@ -214,3 +214,149 @@ def test_masked_text_keys_equal_the_trimmed_prompt():
     # a fully valid prompt is the unmasked block
     _, h_f = oqwen.block(w, hidden, context, temb, cos, sin, SMALL, text_valid_len=9)
     assert torch.allclose(h_f, h_u, atol=1e-5, rtol=1e-5)
+
+
+# ------------------------------------- step level: time embedding, text embedding, final layer
+# The model-level functions reduced to torch primitives and closed forms (identity linears,
+# distinct scale / shift vectors), each paired with a planted mistake that fails it. The laws:
+# diffusers' QwenTimestepProjEmbeddings (the model casts t / 1000 to its dtype, the sinusoid of
+# 256 channels, cos first, shift 0, scales its argument by 1000), txt_norm = RMSNorm (eps 1e-6)
+# before txt_in, and AdaLN-Continuous (difflet/layers/normalization.py:150-190: emb =
+# linear(SiLU(temb)), chunk scale first, LayerNorm without affine).
+STEP = oqwen.QwenShape(hidden=256, heads=2, head_dim=128, mlp=512, n_blocks=0,
+                       in_channels=256, out_channels=256, txt_dim=256)
+T_FRAC = torch.tensor([0.0, 0.7137, 0.4219])  # t / 1000; 1000 * bf16(0.7137) is not a bf16 value
+
+
+def _sinusoid64(arg, dim=256):
+    """cos / sin halves of exp(-ln(10000) i / 128) * arg, i < 128, in float64."""
+    import math
+
+    import numpy as np
+
+    half = dim // 2
+    f = np.exp(-math.log(10000.0) * np.arange(half) / half)
+    a = np.outer(np.asarray(arg, dtype=np.float64), f)
+    return torch.from_numpy(np.concatenate([np.cos(a), np.sin(a)], axis=1))
+
+
+def _identity_embedders(seed=8):
+    d = STEP.hidden
+    ew = oqwen.embed_weights(STEP, seed, dtype=torch.float32)
+    te = "time_text_embed.timestep_embedder."
+    for n in ("linear_1", "linear_2"):
+        ew[f"{te}{n}.weight"], ew[f"{te}{n}.bias"] = torch.eye(d), torch.zeros(d)
+    ew["txt_in.weight"], ew["txt_in.bias"] = torch.eye(d), torch.zeros(d)
+    ew["img_in.weight"], ew["img_in.bias"] = torch.eye(d), torch.zeros(d)
+    ew["proj_out.weight"], ew["proj_out.bias"] = torch.eye(d), torch.zeros(d)
+    g = torch.Generator().manual_seed(seed)
+    ew["txt_norm.weight"] = 0.5 + torch.rand(d, generator=g)
+    return ew
+
+
+def _check_time_embed(ew, model_dtype):
+    """time_embed with identity linears is silu(sinusoid(1000 * t')), t' = t / 1000 in the model
+    dtype."""
+    import torch.nn.functional as F
+
+    temb = oqwen.time_embed(ew, T_FRAC, model_dtype)
+    arg = T_FRAC.to(model_dtype).double() * 1000.0
+    return torch.allclose(temb.double(), F.silu(_sinusoid64(arg)), atol=3e-4, rtol=0)
+
+
+def test_time_embed_reduces_to_silu_of_the_sinusoid_of_1000_t():
+    ew = _identity_embedders()
+    assert _check_time_embed(ew, torch.float32)
+    assert _check_time_embed(ew, torch.bfloat16)
+    temb = oqwen.time_embed(ew, torch.zeros(1))  # t = 0: cos 0 = 1, sin 0 = 0
+    assert torch.allclose(temb[0, :128], torch.nn.functional.silu(torch.ones(128)))
+    assert torch.equal(temb[0, 128:], torch.zeros(128))
+
+
+def test_planted_timestep_cast_after_the_1000_scale_is_seen(monkeypatch):
+    """Rounding 1000 t' to bf16 (a cast after the scale, not of t / 1000 before it) fails."""
+    ew = _identity_embedders()
+    real = ops.timestep_embedding
+    monkeypatch.setattr(ops, "timestep_embedding",
+                        lambda t, dim, **kw: real(t.to(torch.bfloat16).float(), dim, **kw))
+    assert not _check_time_embed(ew, torch.bfloat16)
+
+
+def test_planted_sin_first_time_embedding_is_seen(monkeypatch):
+    ew = _identity_embedders()
+    real = ops.timestep_embedding
+    monkeypatch.setattr(ops, "timestep_embedding",
+                        lambda t, dim, **kw: real(t, dim, **{**kw, "flip_sin_to_cos": False}))
+    assert not _check_time_embed(ew, torch.float32)
+
+
+def _text_case(seed=9):
+    return torch.randn(1, 6, STEP.txt_dim, generator=torch.Generator().manual_seed(seed)) * 3 + 1
+
+
+def test_text_embedding_is_rms_norm_then_txt_in():
+    ew = _identity_embedders()
+    text = _text_case()
+    ref = torch.nn.functional.rms_norm(text, (STEP.txt_dim,), ew["txt_norm.weight"], 1e-6)
+    assert torch.allclose(oqwen.embed_text(ew, text), ref, atol=1e-5, rtol=1e-5)
+
+
+def test_planted_layer_norm_for_txt_norm_is_seen(monkeypatch):
+    """A LayerNorm (mean removed) in place of the RMSNorm fails the check."""
+    ew = _identity_embedders()
+    text = _text_case()
+    ref = torch.nn.functional.rms_norm(text, (STEP.txt_dim,), ew["txt_norm.weight"], 1e-6)
+    monkeypatch.setattr(ops, "rms_norm_fp32", lambda x, w, eps: torch.nn.functional.layer_norm(
+        x, (x.shape[-1],), w, None, eps))
+    assert not torch.allclose(oqwen.embed_text(ew, text), ref, atol=1e-3)
+
+
+def _final_case(seed=10):
+    d = STEP.hidden
+    ew = _identity_embedders(seed)
+    g = torch.Generator().manual_seed(seed)
+    a, b = 0.75, -1.25
+    ew["norm_out.linear.weight"] = torch.cat([a * torch.eye(d), b * torch.eye(d)])
+    ew["norm_out.linear.bias"] = torch.randn(2 * d, generator=g)
+    hidden = torch.randn(1, 9, d, generator=g) * 2 - 0.5
+    temb = torch.randn(1, d, generator=g)
+    silu = torch.nn.functional.silu(temb)
+    scale = a * silu + ew["norm_out.linear.bias"][:d]
+    shift = b * silu + ew["norm_out.linear.bias"][d:]
+    ref = torch.nn.functional.layer_norm(hidden, (d,), eps=1e-6) * (1 + scale[:, None]) \
+        + shift[:, None]
+    return ew, hidden, temb, ref
+
+
+def test_final_layer_is_ada_layer_norm_continuous_scale_first():
+    ew, hidden, temb, ref = _final_case()
+    assert torch.allclose(oqwen.final_layer(ew, hidden, temb), ref, atol=1e-5, rtol=1e-5)
+
+
+def test_planted_shift_first_final_layer_is_seen():
+    """An oracle reading the AdaLN-Continuous chunks as (shift, scale) fails the check: the
+    same as this oracle with the two halves of the linear exchanged."""
+    ew, hidden, temb, ref = _final_case()
+    d = STEP.hidden
+    swapped = dict(ew)
+    for n in ("weight", "bias"):
+        t = ew[f"norm_out.linear.{n}"]
+        swapped[f"norm_out.linear.{n}"] = torch.cat([t[d:], t[:d]])
+    assert not torch.allclose(oqwen.final_layer(swapped, hidden, temb), ref, atol=1e-3)
+
+
+def test_step_without_blocks_is_img_in_then_the_final_layer():
+    """forward() with no blocks: img_in, the time embedding of t / 1000, the final layer (the
+    text path and the RoPE table are built and unused)."""
+    ew, _, _, _ = _final_case(11)
+    g = torch.Generator().manual_seed(12)
+    lat = torch.randn(1, 12, STEP.in_channels, generator=g)
+    text = _text_case(13)
+    t = torch.tensor([0.4219])
+    out = oqwen.forward(STEP, 0, lat, text, t, (3, 4), weights=(ew, []))
+    temb = oqwen.time_embed(ew, t)
+    d = STEP.hidden
+    emb = torch.nn.functional.silu(temb) @ ew["norm_out.linear.weight"].T + ew["norm_out.linear.bias"]
+    ref = torch.nn.functional.layer_norm(lat, (d,), eps=1e-6) * (1 + emb[:, None, :d]) \
+        + emb[:, None, d:]
+    assert torch.allclose(out, ref, atol=1e-5, rtol=1e-5)

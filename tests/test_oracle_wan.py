@@ -186,3 +186,151 @@ def test_planted_per_head_rope_table_offset_is_seen():
     ref = _plain_wan_block(w, hidden, text, cos, sin)
     out = owan.block(w, hidden, text, tproj, cos.roll(1, 0), sin.roll(1, 0), SMALL)
     assert not torch.allclose(out, ref, atol=1e-4)
+
+
+# ------------------------------------- step level: conditioning and the final layer, pinned
+# Reductions of the step-level functions to torch primitives and closed forms: identity
+# linears make the time embedder silu(sinusoid) and the text projection GELU(tanh); distinct
+# shift / scale vectors and an identity proj_out make the final layer one F.layer_norm
+# expression. Each check is paired with a planted mistake that fails it.
+COND = owan.WanShape(hidden=256, heads=2, head_dim=128, ffn=384, n_blocks=0, text_dim=256)
+T_STEPS = torch.tensor([0.0, 999.7, 317.25])  # 999.7 is not a bf16 value (bf16 rounds it to 1000)
+
+
+def _sinusoid64(t, dim=256):
+    """get_timestep_embedding(t, 256, flip_sin_to_cos=True, downscale_freq_shift=0) as the
+    reference parameterises it (modeling_wan.py:341-343), in float64: frequencies
+    exp(-ln(10000) i / 128) for i < 128, cos half first."""
+    import math
+
+    import numpy as np
+
+    half = dim // 2
+    f = np.exp(-math.log(10000.0) * np.arange(half) / half)
+    a = np.outer(np.asarray(t, dtype=np.float64), f)
+    return torch.from_numpy(np.concatenate([np.cos(a), np.sin(a)], axis=1))
+
+
+def _identity_condition(seed=3):
+    d = COND.hidden
+    ew = owan.embed_weights(COND, seed, dtype=torch.float32)
+    p = "condition_embedder."
+    eye = torch.eye(d)
+    for n in ("time_embedder.linear_1", "time_embedder.linear_2", "text_embedder.linear_1",
+              "text_embedder.linear_2"):
+        ew[f"{p}{n}.weight"], ew[f"{p}{n}.bias"] = eye.clone(), torch.zeros(d)
+    c = torch.tensor([0.5, -1.0, 2.0, 0.25, -0.75, 1.5])
+    ew[p + "time_proj.weight"] = torch.cat([ci * eye for ci in c])
+    ew[p + "time_proj.bias"] = torch.linspace(-1.0, 1.0, 6 * d)
+    text = torch.randn(1, 5, d, generator=torch.Generator().manual_seed(seed)) * 1.5
+    return ew, c, text
+
+
+def _check_condition(ew, c, text, model_dtype=torch.float32):
+    """True when condition() equals the closed forms: temb = silu(sinusoid(t)), timestep_proj
+    chunk i = c_i silu(temb) + b_i, text = GELU_tanh(text)."""
+    import torch.nn.functional as F
+
+    d = COND.hidden
+    temb, tproj, txt = owan.condition(ew, T_STEPS, text, model_dtype)
+    tp = _sinusoid64(T_STEPS)
+    if model_dtype == torch.float32:
+        ref_temb, tol = F.silu(tp), 3e-4  # fp32 arguments up to 1000 rad: ~1e-4
+    else:  # the sinusoid and temb rounded to the model dtype (two roundings: 2 ulp)
+        ref_temb, tol = F.silu(tp.to(model_dtype).double()).to(model_dtype).double(), 8e-3
+    ok = torch.allclose(temb.double(), ref_temb, atol=tol, rtol=0)
+    b = ew["condition_embedder.time_proj.bias"].view(6, d).double()
+    ref_proj = c.double()[:, None] * F.silu(ref_temb)[:, None, :] + b
+    ok &= torch.allclose(tproj.double(), ref_proj, atol=3 * tol, rtol=2 * tol)
+    ok &= torch.allclose(txt, F.gelu(text, approximate="tanh"), atol=1e-6, rtol=1e-6)
+    return bool(ok)
+
+
+def test_condition_reduces_to_silu_sinusoid_and_gelu_tanh():
+    ew, c, text = _identity_condition()
+    assert _check_condition(ew, c, text)
+    assert _check_condition(ew, c, text, torch.bfloat16)
+    # t = 0: the sinusoid is cos 0 = 1 on the first half and sin 0 = 0 on the second
+    temb, _, _ = owan.condition(ew, torch.zeros(1), text)
+    assert torch.allclose(temb[0, :128], torch.nn.functional.silu(torch.ones(128)))
+    assert torch.equal(temb[0, 128:], torch.zeros(128))
+
+
+def test_planted_exact_gelu_in_the_text_projection_is_seen(monkeypatch):
+    ew, c, text = _identity_condition()
+    monkeypatch.setattr(ops, "gelu_tanh", lambda x: torch.nn.functional.gelu(x))
+    assert not _check_condition(ew, c, text)
+
+
+def test_planted_sin_first_sinusoid_is_seen(monkeypatch):
+    ew, c, text = _identity_condition()
+    real = ops.timestep_embedding
+    monkeypatch.setattr(ops, "timestep_embedding",
+                        lambda t, dim, **kw: real(t, dim, **{**kw, "flip_sin_to_cos": False}))
+    assert not _check_condition(ew, c, text)
+
+
+def test_planted_timestep_cast_before_the_sinusoid_is_seen(monkeypatch):
+    """Wan takes the sinusoid of the fp32 timestep and casts its output to the model dtype
+    (modeling_wan.py:356-361); an oracle that casts t itself to bf16 first (FLUX's order)
+    fails at t = 999.7."""
+    ew, c, text = _identity_condition()
+    real = ops.timestep_embedding
+    monkeypatch.setattr(ops, "timestep_embedding",
+                        lambda t, dim, **kw: real(t.to(torch.bfloat16).float(), dim, **kw))
+    assert not _check_condition(ew, c, text, torch.bfloat16)
+
+
+FINAL = owan.WanShape(hidden=64, heads=1, head_dim=64, ffn=128, n_blocks=0, text_dim=64)
+
+
+def _final_case(seed=4):
+    g = torch.Generator().manual_seed(seed)
+    ew = owan.embed_weights(FINAL, seed, dtype=torch.float32)
+    ew["proj_out.weight"], ew["proj_out.bias"] = torch.eye(64), torch.zeros(64)
+    ew["scale_shift_table"] = torch.randn(1, 2, 64, generator=g)
+    hidden = torch.randn(1, 7, 64, generator=g) * 2 + 0.5
+    temb = torch.randn(1, 64, generator=g) * 0.3
+    return ew, hidden, temb
+
+
+def _final_reference(ew, hidden, temb):
+    shift = ew["scale_shift_table"][:, 0] + temb
+    scale = ew["scale_shift_table"][:, 1] + temb
+    return torch.nn.functional.layer_norm(hidden, (64,), eps=1e-6) * (1 + scale[:, None]) \
+        + shift[:, None]
+
+
+def test_final_layer_is_layer_norm_scale_then_shift_from_the_table():
+    """norm_out (:1031-1044): (shift, scale) = scale_shift_table + temb in that order, a
+    LayerNorm without affine; proj_out identity here."""
+    ew, hidden, temb = _final_case()
+    assert torch.allclose(owan.final_layer(ew, hidden, temb), _final_reference(ew, hidden, temb),
+                          atol=1e-5, rtol=1e-5)
+
+
+def test_planted_swapped_shift_and_scale_in_the_final_layer_is_seen():
+    ew, hidden, temb = _final_case()
+    ref = _final_reference(ew, hidden, temb)
+    swapped = dict(ew, scale_shift_table=ew["scale_shift_table"].flip(1))
+    assert not torch.allclose(owan.final_layer(swapped, hidden, temb), ref, atol=1e-3)
+
+
+def test_step_without_blocks_is_patch_embed_final_layer_unpatchify():
+    """forward() with no blocks: the patch Conv3d, the conditioning's temb, the final layer and
+    the unpatchify reshape, composed in that order (:932-1068)."""
+    from difflet_amd.dit.wan import unpatchify
+
+    ew, _, _ = _final_case(5)
+    g = torch.Generator().manual_seed(6)
+    lat = torch.randn(1, 16, 2, 4, 6, generator=g)
+    t = torch.tensor([421.5])
+    text = torch.randn(1, 3, 64, generator=g)
+    out = owan.forward(FINAL, 0, lat, t, text, weights=(ew, []))
+    tokens = torch.nn.functional.conv3d(lat, ew["patch_embedding.weight"],
+                                        ew["patch_embedding.bias"], stride=(1, 2, 2))
+    tokens = tokens.flatten(2).transpose(1, 2)
+    temb, _, _ = owan.condition(ew, t, text)
+    ref = unpatchify(_final_reference(ew, tokens, temb)[0], (2, 2, 3), (1, 2, 2))
+    assert out.shape == lat.shape
+    assert torch.allclose(out, ref, atol=1e-5, rtol=1e-5)
