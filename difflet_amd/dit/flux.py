@@ -212,12 +212,24 @@ class FluxDiT(JointDiT):
 
     def forward(self, latents, text, pooled, timestep, guidance, img_hw):
         """latents [1, S_img, in_ch], text [1, S_txt, txt_dim], pooled [1, pooled_dim],
-        timestep / guidance [1] (timestep in [0, 1]) -> [1, S_img, out_ch] bf16."""
+        timestep / guidance [1] (timestep in [0, 1]) -> [1, S_img, out_ch] bf16. The RoPE
+        table is FluxPosEmbed's over ids (0, 0, 0) for text and (0, i, j) for the img_hw grid."""
+        cos, sin = self.rope_tables(text.shape[1], img_hw)
+        return self.forward_rope(latents, text, pooled, timestep, guidance, cos, sin)
+
+    def forward_rope(self, latents, text, pooled, timestep, guidance, cos, sin):
+        """forward() with the RoPE table given: fp32 cos / sin [S_txt + S_img, head_dim] on the
+        device, text rows first (the caller's ids, as the reference adapter builds them)."""
         if latents.shape[0] != 1:
             raise NotImplementedError("the fused FLUX step runs batch 1 (one request per call)")
         st, si = text.shape[1], latents.shape[1]
+        shape = (st + si, self.cfg.head_dim)
+        for name, t in (("cos", cos), ("sin", sin)):
+            if (tuple(t.shape) != shape or t.dtype != torch.float32 or not t.is_contiguous()
+                    or t.device != self.device):
+                raise ValueError(f"forward_rope: {name} must be a contiguous fp32 {list(shape)} "
+                                 f"on {self.device}")
         bufs = self._buffers(st, si)
-        cos, sin = self.rope_tables(st, img_hw)
         h = bufs["h"]
         dt = torch.bfloat16
         self.ctx_emb(text[0].to(dt).contiguous(), out=h[:st])

@@ -284,12 +284,15 @@ def time_text_embed(ew: dict, timestep, guidance, pooled, shape: FluxShape):
 
 def forward(shape: FluxShape, seed: int, latents, text, pooled, timestep, guidance, img_hw,
             weights=None, rms_law=ops.rms_norm_cpu_law, dtype=torch.bfloat16,
-            model_dtype=torch.float32, quant=None):
+            model_dtype=torch.float32, quant=None, rope_dtype=None):
     """One denoise step (modeling_flux.py:364-613). Block weights are drawn block by block
-    (never all held) unless `weights` = (embed, [double...], [single...]) is given.
+    (never all held) unless `weights` = (embed, double, single) is given, double / single
+    being lists of block weights or callables returning block i's (fetched one at a time).
     `dtype` is the weights' storage dtype; `model_dtype` the model's torch dtype, which the
     reference casts timestep and guidance to and scales by 1000 in (:453-456,477-479); the
-    compute itself is fp32."""
+    compute itself is fp32. `rope_dtype` rounds the RoPE table to that dtype, as the
+    reference's GPU adapter does when it stacks the table and casts it to the model dtype
+    (difflet/backends/cuda/flux/transformer.py:184-188)."""
     ew = weights[0] if weights else embed_weights(shape, seed, dtype=dtype)
     L = ops.linear
     hidden = L(latents, ew["x_embedder.weight"], ew["x_embedder.bias"])
@@ -299,18 +302,25 @@ def forward(shape: FluxShape, seed: int, latents, text, pooled, timestep, guidan
     context = L(text, ew["context_embedder.weight"], ew["context_embedder.bias"])
     ids = ops.flux_ids(text.shape[1], *img_hw)
     cos, sin = ops.flux_pos_embed(ids, shape.axes)
+    if rope_dtype is not None:
+        cos, sin = cos.to(rope_dtype).float(), sin.to(rope_dtype).float()
     for i in range(shape.n_double):
-        w = weights[1][i] if weights else double_block_weights(shape, seed, i, dtype=dtype)
+        w = _block(weights, 1, i) if weights else double_block_weights(shape, seed, i, dtype=dtype)
         context, hidden = double_block(w, hidden, context, temb, cos, sin, shape, rms_law, quant)
     hidden = torch.cat([context, hidden], dim=1)
     for i in range(shape.n_single):
-        w = weights[2][i] if weights else single_block_weights(shape, seed, i, dtype=dtype)
+        w = _block(weights, 2, i) if weights else single_block_weights(shape, seed, i, dtype=dtype)
         hidden = single_block(w, hidden, temb, cos, sin, shape, rms_law, quant)
     hidden = hidden[:, text.shape[1]:]
     emb = L(torch.nn.functional.silu(temb), ew["norm_out.linear.weight"], ew["norm_out.linear.bias"])
     scale, shift = emb.chunk(2, dim=1)  # AdaLN-Continuous: scale first (normalization.py:188)
     hidden = ops.layer_norm(hidden) * (1 + scale)[:, None] + shift[:, None]
     return L(hidden, ew["proj_out.weight"], ew["proj_out.bias"])
+
+
+def _block(weights, part: int, i: int) -> dict:
+    src = weights[part]
+    return src(i) if callable(src) else src[i]
 
 
 def synthetic_inputs(shape: FluxShape, seed: int, img_hw, txt_len, batch: int = 1):

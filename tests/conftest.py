@@ -32,3 +32,31 @@ def gpu():
 
     _lib.load()
     return torch.device("cuda", 0)
+
+
+# ------------------------------------------------------------------ parity margins on record
+# Tests hand each measured error and its bound to the `parity` fixture; with DIFFLET_PARITY_LOG
+# set, the session writes them (test, quantity, error, bound, bound / error) as a markdown
+# table to that path, so the margin under every tolerance is kept, not only pass / fail.
+_PARITY: list = []
+
+
+@pytest.fixture
+def parity(request):
+    def record(quantity: str, value: float, bound: float) -> None:
+        _PARITY.append((request.node.nodeid, quantity, float(value), float(bound)))
+
+    return record
+
+
+def pytest_sessionfinish(session, exitstatus):
+    path = os.environ.get("DIFFLET_PARITY_LOG")
+    if not path or not _PARITY:
+        return
+    lines = ["| test | quantity | measured | bound | bound / measured |",
+             "|---|---|---:|---:|---:|"]
+    for node, q, v, b in _PARITY:
+        ratio = f"{b / v:.1f}" if v > 0 else "inf"
+        lines.append(f"| `{node}` | {q} | {v:.3e} | {b:.1e} | {ratio} |")
+    with open(path, "w") as f:
+        f.write("\n".join(lines) + "\n")

@@ -187,7 +187,7 @@ class FluxSingleOnOps(nn.Module):
 
 
 @pytest.mark.parametrize("kind", ["bf16", "fp8"])
-def test_compiled_flux_single_block_matches_the_oracle(gpu, kind):
+def test_compiled_flux_single_block_matches_the_oracle(gpu, kind, parity):
     """The compiled op-module block at FLUX width (3072, 24 heads, MLP 12288) on 128 + 16 x 16
     tokens against oracle.flux.single_block on the same weights: rel L2 <= 1e-2 against the
     fp32 block (bf16), <= 3e-2 against the oracle of the per-channel fp8 law with bf16
@@ -223,6 +223,7 @@ def test_compiled_flux_single_block_matches_the_oracle(gpu, kind):
     if kind == "bf16":
         e = _rel(y.cpu(), full)
         print(f"compiled bf16 block vs fp32 oracle rel L2 {e:.3e}", flush=True)
+        parity("compiled op-module single block, rel L2 vs fp32 oracle", e, 1e-2)
         assert e < 1e-2
         return
     ref = oflux.single_block(w, x, temb, cos, sin, shape, quant="fp8", act_dtype=torch.bfloat16,
@@ -230,5 +231,6 @@ def test_compiled_flux_single_block_matches_the_oracle(gpu, kind):
     e, fmt_dev, fmt_ref = _rel(y.cpu(), ref), _rel(y.cpu(), full), _rel(ref, full)
     print(f"compiled fp8 block vs same-law oracle rel L2 {e:.3e}; format error device "
           f"{fmt_dev:.3e}, oracle {fmt_ref:.3e}", flush=True)
+    parity("compiled op-module single block fp8, rel L2 vs same-law oracle", e, 3e-2)
     assert e < 3e-2
     assert abs(fmt_dev - fmt_ref) < 0.1 * fmt_ref

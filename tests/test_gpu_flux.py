@@ -79,7 +79,7 @@ TOL = {"bf16": 1e-2, "fp8": 3e-2, "mx": 3e-2}
 FORMAT_ERR = 6e-2
 
 
-def _check_double(gpu, kind, quant, st=None, img_hw=None):
+def _check_double(gpu, kind, quant, parity, st=None, img_hw=None):
     shape, w, dit, hidden, context, temb, st, img_hw = _block_setup(gpu, kind, st, img_hw)
     print(f"flux double block {kind}, {st} + {img_hw[0] * img_hw[1]} tokens", flush=True)
     cos, sin = ops.flux_pos_embed(ops.flux_ids(st, *img_hw))
@@ -97,6 +97,8 @@ def _check_double(gpu, kind, quant, st=None, img_hw=None):
     if quant is None:
         e_c, e_h = rel_l2(out_c, f_c[0]), rel_l2(out_h, f_h[0])
         print(f"rel L2 vs fp32 oracle: context {e_c:.3e} hidden {e_h:.3e}", flush=True)
+        parity("double block, text rows, rel L2 vs fp32 oracle", e_c, TOL[kind])
+        parity("double block, image rows, rel L2 vs fp32 oracle", e_h, TOL[kind])
         assert e_c < TOL[kind] and e_h < TOL[kind]
         return
     mods = (_host_mods(dit, mod, ("d", 0, "norm1"), 6),
@@ -108,12 +110,16 @@ def _check_double(gpu, kind, quant, st=None, img_hw=None):
     o_c, o_h = rel_l2(ref_c, f_c), rel_l2(ref_h, f_h)
     print(f"rel L2 vs same-law oracle: context {e_c:.3e} hidden {e_h:.3e}; {kind} format "
           f"error vs fp32: device {q_c:.3e} / {q_h:.3e}, oracle {o_c:.3e} / {o_h:.3e}", flush=True)
+    parity(f"double block {kind}, text rows, rel L2 vs same-law oracle", e_c, TOL[kind])
+    parity(f"double block {kind}, image rows, rel L2 vs same-law oracle", e_h, TOL[kind])
+    parity(f"double block {kind}, image rows, format error vs fp32 (oracle's {o_h:.3e})", q_h,
+           FORMAT_ERR)
     assert e_c < TOL[kind] and e_h < TOL[kind]
     assert abs(q_c - o_c) < 0.1 * o_c and abs(q_h - o_h) < 0.1 * o_h
     assert q_c < FORMAT_ERR and q_h < FORMAT_ERR
 
 
-def _check_single(gpu, kind, quant, st=None, img_hw=None):
+def _check_single(gpu, kind, quant, parity, st=None, img_hw=None):
     shape, w, dit, hidden, context, temb, st, img_hw = _block_setup(gpu, kind, st, img_hw)
     print(f"flux single block {kind}, {st} + {img_hw[0] * img_hw[1]} tokens", flush=True)
     cos, sin = ops.flux_pos_embed(ops.flux_ids(st, *img_hw))
@@ -131,6 +137,7 @@ def _check_single(gpu, kind, quant, st=None, img_hw=None):
     if quant is None:
         e = rel_l2(out, full[0])
         print(f"rel L2 vs fp32 oracle {e:.3e}", flush=True)
+        parity("single block, rel L2 vs fp32 oracle", e, TOL[kind])
         assert e < TOL[kind]
         return
     ref = oflux.single_block(bw, x, temb, cos, sin, shape, quant=quant, act_dtype=torch.bfloat16,
@@ -139,34 +146,36 @@ def _check_single(gpu, kind, quant, st=None, img_hw=None):
     q, o = rel_l2(out, full[0]), rel_l2(ref, full)
     print(f"rel L2 vs same-law oracle {e:.3e}; {kind} format error vs fp32: device {q:.3e}, "
           f"oracle {o:.3e}", flush=True)
+    parity(f"single block {kind}, rel L2 vs same-law oracle", e, TOL[kind])
+    parity(f"single block {kind}, format error vs fp32 (oracle's {o:.3e})", q, FORMAT_ERR)
     assert e < TOL[kind]
     assert abs(q - o) < 0.1 * o
     assert q < FORMAT_ERR
 
 
 @pytest.mark.parametrize("kind,quant", CASES)
-def test_double_block_matches_fp32_oracle(gpu, kind, quant):
-    _check_double(gpu, kind, quant)
+def test_double_block_matches_fp32_oracle(gpu, kind, quant, parity):
+    _check_double(gpu, kind, quant, parity)
 
 
 @pytest.mark.parametrize("kind,quant", CASES)
-def test_single_block_matches_fp32_oracle(gpu, kind, quant):
-    _check_single(gpu, kind, quant)
+def test_single_block_matches_fp32_oracle(gpu, kind, quant, parity):
+    _check_single(gpu, kind, quant, parity)
 
 
 # The FLUX.1-dev 1024^2 step's own block shape: 512 text + 64 x 64 image tokens (4608 rows),
 # attention over 4608 keys on the split schedule, every GEMM at its step size.
 @pytest.mark.parametrize("kind,quant", [("bf16", None), ("fp8", "fp8")])
-def test_double_block_at_the_flux_1024_step_shape(gpu, kind, quant):
-    _check_double(gpu, kind, quant, st=512, img_hw=(64, 64))
+def test_double_block_at_the_flux_1024_step_shape(gpu, kind, quant, parity):
+    _check_double(gpu, kind, quant, parity, st=512, img_hw=(64, 64))
 
 
 @pytest.mark.parametrize("kind,quant", [("bf16", None), ("fp8", "fp8")])
-def test_single_block_at_the_flux_1024_step_shape(gpu, kind, quant):
-    _check_single(gpu, kind, quant, st=512, img_hw=(64, 64))
+def test_single_block_at_the_flux_1024_step_shape(gpu, kind, quant, parity):
+    _check_single(gpu, kind, quant, parity, st=512, img_hw=(64, 64))
 
 
-def test_reduced_depth_step_matches_fp32_oracle(gpu):
+def test_reduced_depth_step_matches_fp32_oracle(gpu, parity):
     """Embedders + 2 double + 2 single blocks + norm_out / proj_out at FLUX width, a 32 x 32
     patch grid and 256 text tokens: the whole step's wiring against the oracle's forward."""
     shape = oflux.FluxShape(n_double=2, n_single=2)
@@ -185,5 +194,6 @@ def test_reduced_depth_step_matches_fp32_oracle(gpu):
     torch.cuda.synchronize()
     e = rel_l2(out, ref)
     print(f"step rel L2 {e:.3e}", flush=True)
+    parity("2 + 2 block step, rel L2 vs fp32 oracle", e, 1e-2)
     assert out.shape == (1, 1024, 64)
     assert e < 1e-2

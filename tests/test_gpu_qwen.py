@@ -28,7 +28,7 @@ def _source(shape, n_blocks, seed=SEED):
     return w
 
 
-def _check_block(gpu, kind, st, img_hw, tol):
+def _check_block(gpu, kind, st, img_hw, tol, parity):
     """One joint block: bf16 against the fp32 oracle; MX against the oracle of the same law
     with the device's bf16 rounding points and modulation vectors (see test_gpu_flux.py)."""
     print(f"qwen block {kind}, {st} + {img_hw[0] * img_hw[1]} tokens", flush=True)
@@ -55,6 +55,8 @@ def _check_block(gpu, kind, st, img_hw, tol):
     if kind == "bf16":
         e_c, e_h = rel_l2(out_c, f_c[0]), rel_l2(out_h, f_h[0])
         print(f"rel L2 vs fp32 oracle: text {e_c:.3e} image {e_h:.3e}", flush=True)
+        parity("joint block, text rows, rel L2 vs fp32 oracle", e_c, tol)
+        parity("joint block, image rows, rel L2 vs fp32 oracle", e_h, tol)
         assert e_c < tol and e_h < tol
         return
     d = shape.hidden
@@ -67,25 +69,29 @@ def _check_block(gpu, kind, st, img_hw, tol):
     o_c, o_h = rel_l2(ref_c, f_c), rel_l2(ref_h, f_h)
     print(f"rel L2 vs same-law oracle: text {e_c:.3e} image {e_h:.3e}; mx format error vs "
           f"fp32: device {q_c:.3e} / {q_h:.3e}, oracle {o_c:.3e} / {o_h:.3e}", flush=True)
+    parity("joint block mx, text rows, rel L2 vs same-law oracle", e_c, tol)
+    parity("joint block mx, image rows, rel L2 vs same-law oracle", e_h, tol)
+    parity(f"joint block mx, image rows, format error vs fp32 (oracle's {o_h:.3e})", q_h,
+           FORMAT_ERR)
     assert e_c < tol and e_h < tol
     assert abs(q_c - o_c) < 0.1 * o_c and abs(q_h - o_h) < 0.1 * o_h
     assert q_c < FORMAT_ERR and q_h < FORMAT_ERR
 
 
 @pytest.mark.parametrize("kind,tol", [("bf16", 1e-2), ("mx", 3e-2)])
-def test_qwen_block_matches_fp32_oracle(gpu, kind, tol):
+def test_qwen_block_matches_fp32_oracle(gpu, kind, tol, parity):
     st, img_hw = (256, (32, 32)) if kind == "bf16" else (128, (16, 16))
-    _check_block(gpu, kind, st, img_hw, tol)
+    _check_block(gpu, kind, st, img_hw, tol, parity)
 
 
-def test_qwen_block_at_the_1328_step_shape_mx(gpu):
+def test_qwen_block_at_the_1328_step_shape_mx(gpu, parity):
     """The Qwen-Image 1328^2 step's own block shape: 256 text + 83 x 83 image tokens (7145
     rows, attention over 7145 keys on the split schedule), MXFP8 targets."""
-    _check_block(gpu, "mx", 256, (83, 83), 3e-2)
+    _check_block(gpu, "mx", 256, (83, 83), 3e-2, parity)
 
 
 @pytest.mark.parametrize("kind,tol", [("bf16", 1e-2), ("mx", 3e-2)])
-def test_qwen_reduced_depth_step_matches_fp32_oracle(gpu, kind, tol):
+def test_qwen_reduced_depth_step_matches_fp32_oracle(gpu, kind, tol, parity):
     """img_in, txt_norm + txt_in, the timestep embedder, 2 joint blocks and norm_out / proj_out
     at Qwen-Image width on an odd 15 x 17 patch grid (centred RoPE positions) + 64 text tokens."""
     print(f"qwen reduced step {kind}", flush=True)
@@ -106,12 +112,13 @@ def test_qwen_reduced_depth_step_matches_fp32_oracle(gpu, kind, tol):
     torch.cuda.synchronize()
     e = rel_l2(out, ref)
     print(f"step rel L2 {e:.3e}", flush=True)
+    parity(f"2-block step {kind}, rel L2 vs {'same-law' if quant else 'fp32'} oracle", e, tol)
     assert out.shape == (1, 255, 64)
     assert e < tol
 
 
 @pytest.mark.parametrize("valid", [40, 0])
-def test_qwen_padded_prompt_matches_the_masked_oracle(gpu, valid):
+def test_qwen_padded_prompt_matches_the_masked_oracle(gpu, valid, parity):
     """A prompt right-padded to 64 rows with `valid` real ones: the step with text_valid_len
     against the oracle running the reference's masked joint attention (text keys from `valid`
     on masked in every block, modeling_qwen_image.py:493-552) over the padded prompt."""
@@ -134,6 +141,7 @@ def test_qwen_padded_prompt_matches_the_masked_oracle(gpu, valid):
     e, gap = rel_l2(out, ref), rel_l2(unmasked, ref)
     print(f"padded step rel L2 vs masked oracle {e:.3e} (masking moves the oracle {gap:.3e})",
           flush=True)
+    parity(f"padded prompt ({valid} of 64 rows), rel L2 vs masked fp32 oracle", e, 1e-2)
     assert out.shape == (1, 255, 64)
     assert e < 1e-2 and gap > 2 * e
 

@@ -26,7 +26,7 @@ def _source(shape, n_blocks, seed=SEED):
     return w
 
 
-def test_wan_block_matches_fp32_oracle(gpu):
+def test_wan_block_matches_fp32_oracle(gpu, parity):
     """One block at Wan-14B width (5120, 40 heads, FFN 13824) on a 3 x 10 x 12 patch grid
     (360 video tokens) with 96 text tokens."""
     print("wan block", flush=True)
@@ -52,10 +52,11 @@ def test_wan_block_matches_fp32_oracle(gpu):
     torch.cuda.synchronize()
     e = rel_l2(bufs["h"], ref[0])
     print(f"block rel L2 {e:.3e}", flush=True)
+    parity("block at Wan-14B width, rel L2 vs fp32 oracle", e, 1e-2)
     assert e < 1e-2
 
 
-def test_wan_reduced_depth_step_matches_fp32_oracle(gpu):
+def test_wan_reduced_depth_step_matches_fp32_oracle(gpu, parity):
     """Patch embedding, time / text conditioning, 2 blocks, norm_out, proj_out and unpatchify on
     latents [1, 16, 3, 12, 10] (3 x 6 x 5 patches) with 48 text tokens of 4096."""
     print("wan reduced step", flush=True)
@@ -72,11 +73,12 @@ def test_wan_reduced_depth_step_matches_fp32_oracle(gpu):
     torch.cuda.synchronize()
     e = rel_l2(out, ref)
     print(f"step rel L2 {e:.3e}", flush=True)
+    parity("2-block step, rel L2 vs fp32 oracle", e, 1e-2)
     assert out.shape == (1, 16, 3, 12, 10)
     assert e < 1e-2
 
 
-def test_wan_block_mx_matches_the_oracle_of_the_same_law(gpu):
+def test_wan_block_mx_matches_the_oracle_of_the_same_law(gpu, parity):
     """The reference's MXFP8 Wan targets (cross-attention q/k/v, both FFN linears) on the MX
     GEMM, against the oracle block with the MX law on the same linears and the device's bf16
     rounding points (rel L2 <= 3e-2), at width 1024 (8 heads), FFN 2816, a 2 x 8 x 8 grid and
@@ -112,6 +114,8 @@ def test_wan_block_mx_matches_the_oracle_of_the_same_law(gpu):
     fmt_dev, fmt_ref = rel_l2(bufs["h"], ref_bf16[0]), rel_l2(ref, ref_bf16)
     print(f"mx block rel L2 vs the MX oracle {e:.3e}; format error device {fmt_dev:.3e}, "
           f"oracle {fmt_ref:.3e}", flush=True)
+    parity("mx block, rel L2 vs same-law oracle", e, 3e-2)
+    parity(f"mx block, format error vs fp32 (oracle's {fmt_ref:.3e})", fmt_dev, 6e-2)
     assert e < 3e-2
     assert abs(fmt_dev - fmt_ref) <= 0.1 * fmt_ref
 
