@@ -111,12 +111,13 @@ def _properties(name, a, b, shape):
     assert a.float().std() > 0
 
 
-# Full-depth FLUX bounds. bf16: the device against the fp32 oracle. fp8: the per-token fp8
-# step's error against the same fp32 oracle is the e4m3 format's own (the fp8 blocks hold the
-# same-law oracle to 3e-2 and the format error to within 10 % of the oracle's, in
-# test_gpu_flux.py); its bound is the measured full-depth figure with a margin.
+# Full-depth FLUX bounds, from measured figures with a margin of about 1.45. bf16 against the
+# fp32 oracle: 8.7e-3 over 2 + 2 blocks (test_gpu_flux.py), 1.37e-2 over the 57 (bf16 roundings
+# of the residual stream and the modulation vectors, not a random walk: sqrt(57 / 4) would give
+# 3.3e-2). fp8 against the same fp32 oracle is the e4m3 format's own error (per block 4.5-4.9e-2,
+# equal to the same-law oracle's within 10 %, test_gpu_flux.py): 8.35e-2 over the 57 blocks.
 FULL_BF16_TOL = 2e-2
-FULL_FP8_TOL = 0.25
+FULL_FP8_TOL = 0.12
 
 
 @pytest.mark.timeout(900)
@@ -152,8 +153,13 @@ def test_flux_full_depth_step_matches_the_oracle(gpu, parity):
     host = lambda n: get(n).cpu().float()  # noqa: E731
 
     def blocks(prefix):
-        keys = [n[len(prefix) + 2:] for n in names if n.startswith(prefix + ".0.")]
-        return lambda i: {k: host(f"{prefix}.{i}.{k}") for k in keys}
+        keys = [n[len(prefix) + 3:] for n in names if n.startswith(prefix + ".0.")]
+
+        def fetch(i):
+            print(f"  oracle {prefix} {i}", flush=True)  # progress: ~1.2 s of CPU per block
+            return {k: host(f"{prefix}.{i}.{k}") for k in keys}
+
+        return fetch
 
     ew = {n: host(n) for n in names if not n.startswith(("transformer_blocks.",
                                                         "single_transformer_blocks."))}
