@@ -93,6 +93,9 @@ SIGNATURES: dict[str, tuple] = {
     "difflet_rocm_layernorm_modulate_fp8": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _i64, _i64,
                                                    _vp, _vp, _i32, _i64, _i64, _i64, _i32, _f32,
                                                    _vp]),
+    "difflet_rocm_layernorm_modulate_mx": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i32, _i64,
+                                                  _i64, _vp, _vp, _i32, _i64, _i64, _i64, _i32,
+                                                  _f32, _vp]),
     "difflet_rocm_rms_norm": (_i32, [_vp, _i64, _vp, _i64, _i32, _i64, _i64, _vp, _i32, _f32,
                                      _vp]),
     "difflet_rocm_qk_norm_rope": (_i32, [_vp, _i64, _i32, _i64, _i64, _i64, _i64, _i64, _i32,

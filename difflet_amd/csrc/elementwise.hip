@@ -268,6 +268,74 @@ __global__ __launch_bounds__(256) void layernorm_modulate_fp8_kernel(
   }
 }
 
+// layernorm_modulate rounded to bf16, then quantized to MXFP8 in the GEMM's swizzled layout:
+// the output equals quantize_mxfp8(swizzled) of layernorm_modulate's bf16 result, codes and
+// E8M0 scales. dim is a multiple of 512 (whole swizzle tiles), so chunk j of lane L (columns
+// (L + 64 j) * 8 .. + 8) is run L / 16 of block L % 16 of tile j: the four runs of a block sit in
+// lanes b, b + 16, b + 32, b + 48 of one register, and the block's exponent maximum is two
+// cross-lane steps. The codes go to the wave's LDS row at their swizzled bytes ((8 b + r) * 4 +
+// run for element r of a run), then out to HBM in whole 16-byte pieces; the scales likewise.
+template <typename TX, typename TM, int NV>
+__global__ __launch_bounds__(256) void layernorm_modulate_mx_kernel(
+    const TX* __restrict__ x, int64_t ldx, uint8_t* __restrict__ q, int64_t ldq,
+    uint8_t* __restrict__ scale, int64_t ld_scale, int64_t rows, int dim,
+    const TM* __restrict__ mul, const TM* __restrict__ add, int64_t mod_stride,
+    int64_t rows_per_batch, int64_t split, int one_plus, float eps) {
+  constexpr int ROW = NV * 512;  // codes of one row (dim == ROW)
+  __shared__ __attribute__((aligned(16))) uint8_t stage[4][ROW + ROW / 32];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t row = (int64_t)blockIdx.x * 4 + w;
+  if (row >= rows) return;  // whole waves: the LDS rows are per wave, no barrier is needed
+  const int64_t b = split > 0 ? (row >= split ? 1 : 0) : row / rows_per_batch;
+  LnRow<TX, TM, NV, true> r;
+  r.load(x + row * ldx, dim, mul ? mul + b * mod_stride : nullptr,
+         add ? add + b * mod_stride : nullptr, one_plus, eps, lane);
+  uint8_t* st = stage[w];
+  const int run = lane >> 4, blk = lane & 15;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    float o[8];
+    r.out(j, o);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // the bf16 output, as layernorm_modulate stores it
+      const uint32_t p = pack_bf16x2(o[2 * i], o[2 * i + 1]);
+      o[2 * i] = bf16bits_to_f32(p & 0xffffu);
+      o[2 * i + 1] = bf16bits_to_f32(p >> 16);
+    }
+    uint32_t emax = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t e = (__builtin_bit_cast(uint32_t, o[i]) >> 23) & 0xffu;
+      emax = e > emax ? e : emax;
+    }
+    emax = max(emax, (uint32_t)__shfl_xor((int)emax, 16, kWave));
+    emax = max(emax, (uint32_t)__shfl_xor((int)emax, 32, kWave));
+    const int su = (int)emax - 7 < 0 ? 0 : (int)emax - 7;  // clamp(e_max - 7, 0, 255)
+    const float m = __builtin_bit_cast(float, (uint32_t)(254 - su) << 23);  // 2^(127 - su)
+    float c[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[i] = clamp448(__fmul_rn(o[i], m));
+    const uint32_t lo = e4m3x4(c[0], c[1], c[2], c[3]), hi = e4m3x4(c[4], c[5], c[6], c[7]);
+    uint8_t* tile = st + j * 512 + blk * 32 + run;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      tile[4 * i] = (uint8_t)(lo >> (8 * i));
+      tile[4 * (4 + i)] = (uint8_t)(hi >> (8 * i));
+    }
+    if (run == 0) st[ROW + j * 16 + blk] = (uint8_t)su;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  uint8_t* qr = q + row * ldq;
+#pragma unroll
+  for (int i = lane; i < ROW / 16; i += 64)
+    *reinterpret_cast<u32x4*>(qr + 16 * i) = *reinterpret_cast<const u32x4*>(st + 16 * i);
+  if (lane < ROW / 512)
+    *reinterpret_cast<u32x4*>(scale + row * ld_scale + 16 * lane) =
+        *reinterpret_cast<const u32x4*>(st + ROW + 16 * lane);
+}
+
 // ------------------------------------------------------------------ RMSNorm (fp32 law)
 template <typename T, typename TW, int NV>
 __global__ __launch_bounds__(256) void rms_norm_kernel(const T* __restrict__ x, int64_t ldx,
@@ -883,6 +951,65 @@ extern "C" int difflet_rocm_layernorm_modulate_fp8(const void* x, int64_t ldx, u
       return launch_ln_fp8<TX, TM>(x, ldx, q, ldq, scale, rows, dim, mul, add, mod_stride,
                                    rows_per_batch, split, one_plus, eps, s)));
   return DIFFLET_OK;
+}
+
+template <typename TM>
+static int launch_ln_mx(const void* x, int64_t ldx, uint8_t* q, int64_t ldq, uint8_t* scale,
+                        int64_t ld_scale, int64_t rows, int64_t dim, const void* mul,
+                        const void* add, int64_t mod_stride, int64_t rpb, int64_t split,
+                        int one_plus, float eps, hipStream_t s) {
+  dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+#define DLT_LNMX(NV)                                                                          \
+  case NV:                                                                                     \
+    hipLaunchKernelGGL((layernorm_modulate_mx_kernel<bf16, TM, NV>), grid, block, 0, s,       \
+                       (const bf16*)x, ldx, q, ldq, scale, ld_scale, rows, (int)dim,          \
+                       (const TM*)mul, (const TM*)add, mod_stride, rpb, split, one_plus, eps); \
+    break;
+  switch ((int)(dim / 512)) {
+    DLT_LNMX(1) DLT_LNMX(2) DLT_LNMX(3) DLT_LNMX(4) DLT_LNMX(5) DLT_LNMX(6) DLT_LNMX(7)
+    DLT_LNMX(8) DLT_LNMX(9) DLT_LNMX(10) DLT_LNMX(11) DLT_LNMX(12) DLT_LNMX(13) DLT_LNMX(14)
+    DLT_LNMX(15) DLT_LNMX(16)
+    default:
+      dlt_set_error("layernorm_modulate_mx: dim %lld exceeds 8192", (long long)dim);
+      return DIFFLET_EUNSUPPORTED;
+  }
+#undef DLT_LNMX
+  return dlt_check_launch("layernorm_modulate_mx");
+}
+
+extern "C" int difflet_rocm_layernorm_modulate_mx(const void* x, int64_t ldx, uint8_t* q,
+                                                  int64_t ldq, uint8_t* scale, int64_t ld_scale,
+                                                  int dtype, int64_t rows, int64_t dim,
+                                                  const void* mul, const void* add,
+                                                  int mod_dtype, int64_t mod_stride,
+                                                  int64_t rows_per_batch, int64_t split,
+                                                  int one_plus, float eps,
+                                                  difflet_stream_t stream) {
+  DLT_REQUIRE(x && q && scale, DIFFLET_EINVAL, "layernorm_modulate_mx: null pointer");
+  DLT_REQUIRE(dtype == DIFFLET_BF16, DIFFLET_EUNSUPPORTED,
+              "layernorm_modulate_mx: x must be bf16");
+  DLT_REQUIRE(mod_dtype == DIFFLET_BF16 || mod_dtype == DIFFLET_F32, DIFFLET_EUNSUPPORTED,
+              "layernorm_modulate_mx: modulation vectors must be bf16 or fp32");
+  DLT_REQUIRE(split >= 0, DIFFLET_EINVAL, "layernorm_modulate_mx: split must be >= 0");
+  DLT_REQUIRE(rows >= 0 && dim > 0 && dim % 512 == 0, DIFFLET_EINVAL,
+              "layernorm_modulate_mx: dim %lld must be a positive multiple of 512 (whole "
+              "swizzle tiles)", (long long)dim);
+  DLT_REQUIRE(ldx % 8 == 0 && ldq % 16 == 0 && ld_scale % 16 == 0 &&
+                  (mod_stride % 8 == 0 || (!mul && !add)),
+              DIFFLET_EINVAL,
+              "layernorm_modulate_mx: ldx and mod_stride must be multiples of 8 elements, "
+              "ldq and ld_scale multiples of 16 bytes");
+  DLT_REQUIRE(aligned16(x) && aligned16(q) && aligned16(scale) && (!mul || aligned16(mul)) &&
+                  (!add || aligned16(add)),
+              DIFFLET_EINVAL, "layernorm_modulate_mx: pointers must be 16-byte aligned");
+  if (rows == 0) return DIFFLET_OK;
+  if (rows_per_batch <= 0) rows_per_batch = rows;
+  hipStream_t s = (hipStream_t)stream;
+  if (mod_dtype == DIFFLET_BF16)
+    return launch_ln_mx<bf16>(x, ldx, q, ldq, scale, ld_scale, rows, dim, mul, add, mod_stride,
+                              rows_per_batch, split, one_plus, eps, s);
+  return launch_ln_mx<float>(x, ldx, q, ldq, scale, ld_scale, rows, dim, mul, add, mod_stride,
+                             rows_per_batch, split, one_plus, eps, s);
 }
 
 template <typename T, typename TW>

@@ -10,7 +10,8 @@ and image row ranges of one [S, ...] buffer).
 
 Buffers (batch 1, S = S_txt + S_img, D = hidden, text rows first):
   h [S, D] residual stream, n [S, D] modulated LayerNorm output, qkv [S, 3D], ff [S, mlp];
-  fp8 steps add nq [S, D] e4m3 codes and ns [S] scales written by the fused LayerNorm.
+  fp8 steps add nq [S, D] e4m3 codes and ns [S] scales written by the fused LayerNorm; MXFP8
+  steps add nq [S, D] codes in the GEMM's swizzled order and nsx [S, D / 32] E8M0 scales.
 """
 
 from __future__ import annotations
@@ -45,31 +46,48 @@ class JointDiT:
         if self.kind == "fp8":  # LayerNorm output straight to per-token e4m3 + scales
             bufs["nq"] = torch.empty((s, d), dtype=torch.float8_e4m3fn, device=dev)
             bufs["ns"] = torch.empty((s,), dtype=torch.float32, device=dev)
+        if self.kind == "mx" and self._ln_mx_fusable():  # LayerNorm output straight to MXFP8
+            bufs["nq"] = torch.empty((s, d), dtype=torch.float8_e4m3fn, device=dev)
+            bufs["nsx"] = torch.empty((s, d // 32), dtype=torch.uint8, device=dev)
         for k, shape in (extra or {}).items():
             bufs[k] = e(*shape)
         return bufs
 
-    def _ln(self, bufs, rows: slice, sc, sh, fused: bool = True):
-        """adaLN of h[rows] into the next GEMM's A operand: bf16 into n, or (fp8 step) per-token
-        e4m3 codes and scales in one pass. Returns the `prepared` operand (None for bf16)."""
+    def _ln_mx_fusable(self) -> bool:
+        """The LayerNorm -> MXFP8 kernel covers whole 512-wide swizzle tiles."""
+        return self.cfg.hidden % 512 == 0
+
+    def _ln(self, bufs, rows: slice, sc, sh, kind: str = "bf16"):
+        """adaLN of h[rows] into the next GEMM's A operand, for a GEMM of `kind`: bf16 into n,
+        or per-token e4m3 codes and scales (fp8) / swizzled MXFP8 codes and E8M0 scales (mx) in
+        one pass. Returns the `prepared` operand (None for bf16)."""
         h = bufs["h"]
-        if fused and self.kind == "fp8":
+        if kind == "fp8" and "ns" in bufs:
             nq, ns = bufs["nq"][rows], bufs["ns"][rows]
             kernels.layernorm_modulate_fp8(h[rows], sc, sh, eps=EPS, out=(nq, ns))
+            return nq, ns
+        if kind == "mx" and "nsx" in bufs:
+            nq, ns = bufs["nq"][rows], bufs["nsx"][rows]
+            kernels.layernorm_modulate_mx(h[rows], sc, sh, eps=EPS, out=(nq, ns))
             return nq, ns
         kernels.layernorm_modulate(h[rows], sc, sh, eps=EPS, out=bufs["n"][rows])
         return None
 
-    def _ln_joint(self, bufs, st: int, txt_sc, txt_sh, img_sc, img_sh, fused: bool = True):
+    def _ln_joint(self, bufs, st: int, txt_sc, txt_sh, img_sc, img_sh, kind: str = "bf16"):
         """adaLN of all rows of h in one launch, text rows [0, st) with the text vectors and the
-        image rows with the image ones. Returns the text and image `prepared` operands."""
+        image rows with the image ones, into the A operands of a GEMM pair of `kind` (as _ln).
+        Returns the text and image `prepared` operands."""
         h, s = bufs["h"], bufs["h"].shape[0]
         T, I = slice(0, st), slice(st, s)
         kw = dict(eps=EPS, split=st, mul2=img_sc, add2=img_sh) if st else dict(eps=EPS)
         sc, sh = (txt_sc, txt_sh) if st else (img_sc, img_sh)
-        if fused and self.kind == "fp8":
+        if kind == "fp8" and "ns" in bufs:
             nq, ns = bufs["nq"], bufs["ns"]
             kernels.layernorm_modulate_fp8(h, sc, sh, out=(nq, ns), **kw)
+            return (nq[T], ns[T]), (nq[I], ns[I])
+        if kind == "mx" and "nsx" in bufs:
+            nq, ns = bufs["nq"], bufs["nsx"]
+            kernels.layernorm_modulate_mx(h, sc, sh, out=(nq, ns), **kw)
             return (nq[T], ns[T]), (nq[I], ns[I])
         kernels.layernorm_modulate(h, sc, sh, out=bufs["n"], **kw)
         return None, None
@@ -117,8 +135,7 @@ class JointDiT:
         c_sh, c_sc, c_g, c_sh2, c_sc2, c_g2 = txt_mods
         # every elementwise step runs once over all rows: the text and image rows of each
         # launch differ only in their modulation vectors or norm weights
-        fq = blk.qkv_img.kind == "fp8"
-        pt, pi = self._ln_joint(bufs, st, c_sc, c_sh, x_sc, x_sh, fq)
+        pt, pi = self._ln_joint(bufs, st, c_sc, c_sh, x_sc, x_sh, blk.qkv_img.kind)
         # q/k RMSNorm (text rows with the added-stream weights) and RoPE in the GEMM epilogue
         self._gemm(f"gemm.{tag}.qkv",
                    [blk.qkv_txt.problem(n[T], qkv[T], prepared=pt, norm_q=blk.naq,
@@ -133,8 +150,7 @@ class JointDiT:
                    [blk.out_txt.problem(o[T], h[T], gate=c_g, residual=h[T], prepared=pt),
                     blk.out_img.problem(o[I], h[I], gate=x_g, residual=h[I], prepared=pi)],
                    blk.out_img.kind, _lib.EPI_GATE_RESIDUAL)
-        fq = blk.ff1_img.kind == "fp8"
-        pt, pi = self._ln_joint(bufs, st, c_sc2, c_sh2, x_sc2, x_sh2, fq)
+        pt, pi = self._ln_joint(bufs, st, c_sc2, c_sh2, x_sc2, x_sh2, blk.ff1_img.kind)
         self._gemm(f"gemm.{tag}.ff1", [blk.ff1_txt.problem(n[T], ff[T], prepared=pt),
                                        blk.ff1_img.problem(n[I], ff[I], prepared=pi)],
                    blk.ff1_img.kind, _lib.EPI_GELU)

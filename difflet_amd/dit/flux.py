@@ -176,7 +176,7 @@ class FluxDiT(JointDiT):
         d = c.hidden
         h, n, big = bufs["h"], bufs["n"], bufs["big"]
         sh, sc, g = self._mods(mod, self.mod_off[("s", i)], 3)
-        p = self._ln(bufs, slice(0, h.shape[0]), sc, sh, blk.w1.kind == "fp8")
+        p = self._ln(bufs, slice(0, h.shape[0]), sc, sh, blk.w1.kind)
         # [k | v | q | mlp]: GELU on the MLP columns, q/k RMSNorm + RoPE in the same epilogue or
         # in one launch after it (self.fuse_single_qk)
         fuse = self.fuse_single_qk[blk.w1.kind]

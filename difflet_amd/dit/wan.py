@@ -142,10 +142,23 @@ class WanDiT:
             c, dev = self.cfg, self.device
             e = lambda *shape: torch.empty(shape, dtype=torch.bfloat16, device=dev)  # noqa: E731
             d = c.hidden
-            self._bufs = {key: {"h": e(s, d), "n": e(s, d), "qkv": e(s, 3 * d),
-                                "kv_txt": e(st, 2 * d), "ff": e(s, c.ffn), "txt": e(st, d),
-                                "txt_tmp": e(st, d)}}
+            bufs = {"h": e(s, d), "n": e(s, d), "qkv": e(s, 3 * d), "kv_txt": e(st, 2 * d),
+                    "ff": e(s, c.ffn), "txt": e(st, d), "txt_tmp": e(st, d)}
+            if self.kind == "mx" and d % 512 == 0:  # LayerNorm output straight to MXFP8
+                bufs["nq"] = torch.empty((s, d), dtype=torch.float8_e4m3fn, device=dev)
+                bufs["nsx"] = torch.empty((s, d // 32), dtype=torch.uint8, device=dev)
+            self._bufs = {key: bufs}
         return self._bufs[key]
+
+    def _ln(self, bufs, lin, mul, add, one_plus: bool = True):
+        """LayerNorm (+ modulation or affine) of h into the A operand of linear `lin`: swizzled
+        MXFP8 codes and scales in one pass for an MX linear, else bf16 into n."""
+        if lin.kind == "mx" and "nsx" in bufs:
+            out = (bufs["nq"], bufs["nsx"])
+            kernels.layernorm_modulate_mx(bufs["h"], mul, add, eps=EPS, one_plus=one_plus, out=out)
+            return out
+        kernels.layernorm_modulate(bufs["h"], mul, add, eps=EPS, one_plus=one_plus, out=bufs["n"])
+        return None
 
     def rope_tables(self, grid):
         key = tuple(grid)
@@ -181,9 +194,9 @@ class WanDiT:
         self._attention(qkv, 0, qkv, d, qkv, 2 * d)
         self._gemm("gemm.out1", [blk.out1.problem(qkv[:, :d], h, gate=gates[0:1], residual=h)],
                    _lib.EPI_GATE_RESIDUAL, kind=blk.out1.kind)
-        kernels.layernorm_modulate(h, blk.norm2_w, blk.norm2_b, eps=EPS, one_plus=False, out=n)
+        p = self._ln(bufs, blk.q2, blk.norm2_w, blk.norm2_b, one_plus=False)
         q2 = qkv[:, :d]
-        self._gemm("gemm.q2", [blk.q2.problem(n, q2)], kind=blk.q2.kind)
+        self._gemm("gemm.q2", [blk.q2.problem(n, q2, prepared=p)], kind=blk.q2.kind)
         self._gemm("gemm.kv2", [blk.kv2.problem(txt, kvt)], kind=blk.kv2.kind)
         kernels.qk_norm_rope(qkv, heads=c.heads, head_dim=c.head_dim, q_off=0, k_off=-1,
                              wq=blk.nq2, wk=None, eps=EPS, cos=None, sin=None, do_norm=2)
@@ -192,8 +205,9 @@ class WanDiT:
         self._attention(qkv, 0, kvt, 0, kvt, d)
         self._gemm("gemm.out2", [blk.out2.problem(q2, h, gate=self.ones, residual=h)],
                    _lib.EPI_GATE_RESIDUAL, kind=blk.out2.kind)
-        kernels.layernorm_modulate(h, c_sc, c_sh, eps=EPS, out=n)
-        self._gemm("gemm.ffn_in", [blk.ffn_in.problem(n, ff)], _lib.EPI_GELU, kind=blk.ffn_in.kind)
+        p = self._ln(bufs, blk.ffn_in, c_sc, c_sh)
+        self._gemm("gemm.ffn_in", [blk.ffn_in.problem(n, ff, prepared=p)], _lib.EPI_GELU,
+                   kind=blk.ffn_in.kind)
         self._gemm("gemm.ffn_out", [blk.ffn_out.problem(ff, h, gate=gates[1:2], residual=h)],
                    _lib.EPI_GATE_RESIDUAL, kind=blk.ffn_out.kind)
 

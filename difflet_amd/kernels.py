@@ -502,6 +502,40 @@ def layernorm_modulate_fp8(x: torch.Tensor, mul: torch.Tensor | None,
     return q, sc
 
 
+def layernorm_modulate_mx(x: torch.Tensor, mul: torch.Tensor | None,
+                          add: torch.Tensor | None, *, eps: float, one_plus: bool = True,
+                          rows_per_batch: int | None = None, split: int = 0,
+                          mul2: torch.Tensor | None = None, add2: torch.Tensor | None = None,
+                          out: tuple[torch.Tensor, torch.Tensor] | None = None):
+    """layernorm_modulate rounded to bf16 and quantized to MXFP8 in the GEMM's swizzled layout in
+    one pass: (codes float8_e4m3fn [rows, dim], E8M0 scales uint8 [rows, dim / 32]), equal to
+    quantize_mxfp8(swizzled=True) of the bf16 layernorm_modulate output. x bf16, dim a multiple
+    of 512."""
+    dev = _on_gpu(x)
+    x2 = _rows2d(x, "layernorm_modulate_mx")
+    rows, dim = x2.shape
+    if x2.dtype != torch.bfloat16 or dim % 512:
+        raise ValueError(f"layernorm_modulate_mx: x must be bf16 with a width that is a "
+                         f"multiple of 512, got {x2.dtype} [{rows}, {dim}]")
+    if out is None:
+        q = torch.empty((rows, dim), dtype=torch.float8_e4m3fn, device=dev)
+        sc = torch.empty((rows, dim // 32), dtype=torch.uint8, device=dev)
+    else:
+        q, sc = out
+        if q.element_size() != 1 or sc.dtype != torch.uint8 or q.shape[0] != rows or \
+                sc.shape[0] != rows or q.shape[-1] < dim or sc.shape[-1] < dim // 32 or \
+                q.stride(-1) != 1 or sc.stride(-1) != 1:
+            raise ValueError("layernorm_modulate_mx: out must be (8-bit [rows, >=dim], "
+                             "uint8 [rows, >=dim / 32]), unit column stride")
+    mul, add, mod_dt, mod_stride, split = _mod_args(mul, add, mul2, add2, dim, split)
+    rpb = rows_per_batch or rows
+    check(lib().difflet_rocm_layernorm_modulate_mx(
+        _ptr(x2), x2.stride(0), _ptr(q), q.stride(0), _ptr(sc), sc.stride(0), _dt(x2), rows, dim,
+        _ptr(mul), _ptr(add), mod_dt, mod_stride, rpb, split, int(one_plus), float(eps),
+        _stream(dev)), "layernorm_modulate_mx")
+    return q, sc
+
+
 def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float) -> torch.Tensor:
     dev = _on_gpu(x)
     x2 = _rows2d(x, "rms_norm")

@@ -258,6 +258,23 @@ int difflet_rocm_layernorm_modulate_fp8(const void* x, int64_t ldx, uint8_t* q, 
                                         int64_t split, int one_plus, float eps,
                                         difflet_stream_t stream);
 
+/* difflet_rocm_layernorm_modulate's output rounded to bf16 and quantized to MXFP8 in one pass,
+ * in the layout the MXFP8 GEMM reads: the result equals difflet_rocm_quantize_mxfp8 (swizzled)
+ * of the bf16 LayerNorm + modulation output, bit for bit: codes q [rows, dim] in swizzle order
+ * (row stride ldq bytes) and E8M0 scales [rows, dim / 32] (row stride ld_scale bytes), the block
+ * law of difflet/quant/mx.py:85-108. It feeds the MXFP8 linears that follow an adaLN (the
+ * q/k/v and MLP-in projections of difflet/models/qwen_image/modeling_qwen.py:241-281, Wan's
+ * cross-attention q and FFN-in, difflet/models/wan/modeling_wan.py:735-763), which quantize
+ * their activations per call (difflet/backends/neuron/ops_impl/fp8_kernels.py:46-58).
+ * x bf16; mul / add bf16 or fp32; dim a multiple of 512 (whole swizzle tiles), at most 8192;
+ * ldq and ld_scale multiples of 16; every pointer 16-byte aligned. */
+int difflet_rocm_layernorm_modulate_mx(const void* x, int64_t ldx, uint8_t* q, int64_t ldq,
+                                       uint8_t* scale, int64_t ld_scale, int dtype, int64_t rows,
+                                       int64_t dim, const void* mul, const void* add,
+                                       int mod_dtype, int64_t mod_stride, int64_t rows_per_batch,
+                                       int64_t split, int one_plus, float eps,
+                                       difflet_stream_t stream);
+
 /* RMSNorm with fp32 statistics, normalisation and affine and one cast back to dtype: the
  * law of rms_norm_fp32 (difflet/backends/_torch_megatron/norm.py:35-45) and of the CUDA
  * backend's RMSNorm (difflet/backends/cuda/ops_impl/norm.py:24-44). weight may be NULL. */

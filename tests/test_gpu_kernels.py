@@ -255,6 +255,54 @@ def test_layernorm_modulate_fp8_equals_layernorm_then_quantize(gpu, rows, dim):
     assert rel_l2(y, ref) < 4e-3
 
 
+# (rows, dim, split, mod dtype, one_plus): a joint launch (text rows below `split` with their own
+# vectors) at FLUX / Qwen width, Wan's fp32 vectors and its affine norm2 (one_plus off), and
+# the narrowest / widest dims (one and sixteen swizzle tiles)
+@pytest.mark.parametrize("rows,dim,split,mdt,one_plus", [
+    (700, 3072, 100, torch.bfloat16, True), (333, 5120, 0, torch.float32, True),
+    (129, 5120, 0, torch.bfloat16, False), (64, 512, 0, torch.bfloat16, True),
+    (40, 8192, 7, torch.float32, True)])
+def test_layernorm_modulate_mx_equals_layernorm_then_quantize(gpu, rows, dim, split, mdt,
+                                                              one_plus):
+    """The fused LayerNorm -> MXFP8 kernel against the bf16 LayerNorm followed by the swizzled
+    MX quantizer (codes and E8M0 scales bit for bit) and the oracle's MX law on the same bf16
+    rows."""
+    print(f"layernorm_modulate_mx rows={rows} dim={dim} split={split} {mdt}", flush=True)
+    g = torch.Generator().manual_seed(rows + dim)
+    x = (rnd(g, rows, dim, std=2.0).float() * torch.exp(torch.randn(rows, 1, generator=g) * 3)
+         + 0.5).bfloat16()
+    x[1] = 0.25  # a constant row: LN output is the shift alone
+    mods = (torch.randn(4, dim, generator=g) * 0.3).to(mdt).to(gpu)
+    mods[2, :dim // 2] = 0  # a zero half: blocks of shift alone
+    kw = dict(eps=1e-6, one_plus=one_plus)
+    if split:
+        kw.update(split=split, mul2=mods[2], add2=mods[3])
+    xd = x.to(gpu)
+    q, s = kernels.layernorm_modulate_mx(xd, mods[0], mods[1], **kw)
+    y = kernels.layernorm_modulate(xd, mods[0], mods[1], **kw)
+    q2, s2 = kernels.quantize_mxfp8(y, swizzled=True)
+    torch.cuda.synchronize()
+    assert q.dtype == torch.float8_e4m3fn and s.shape == (rows, dim // 32)
+    assert torch.equal(q.view(torch.uint8), q2.view(torch.uint8)) and torch.equal(s, s2)
+    q_ref, s_ref = omx.quantize_mx(y.float().cpu().numpy(), swizzled_out=True)
+    assert np.array_equal(s.cpu().numpy(), s_ref)
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), q_ref)
+    # into strided outputs (the step's buffers are views of wider rows)
+    qb = torch.zeros(rows, dim + 512, dtype=torch.uint8, device=gpu)
+    sb = torch.zeros(rows, dim // 32 + 16, dtype=torch.uint8, device=gpu)
+    kernels.layernorm_modulate_mx(xd, mods[0], mods[1], out=(qb[:, :dim].view(torch.float8_e4m3fn),
+                                                             sb[:, :dim // 32]), **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(qb[:, :dim], q.view(torch.uint8)) and torch.equal(sb[:, :dim // 32], s)
+    assert int(qb[:, dim:].count_nonzero()) == 0 and int(sb[:, dim // 32:].count_nonzero()) == 0
+
+
+def test_layernorm_modulate_mx_refuses_partial_tiles(gpu):
+    x = torch.zeros(4, 640, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError):
+        kernels.layernorm_modulate_mx(x, None, None, eps=1e-6)
+
+
 @pytest.mark.parametrize("cols", [128, 384, 512, 896, 3072, 3456, 13824])
 @pytest.mark.parametrize("swizzled", [False, True])
 def test_quantize_mxfp8_bit_exact(gpu, cols, swizzled):
