@@ -25,7 +25,7 @@ F32, BF16, F16, U8, BOOL, I32 = 0, 1, 2, 3, 4, 5
 # enum difflet_status
 OK, EINVAL, EUNSUPPORTED, ELAUNCH = 0, 1, 2, 3
 # enum difflet_epilogue
-EPI_NONE, EPI_GELU, EPI_GATE_RESIDUAL = 0, 1, 2
+EPI_NONE, EPI_GELU, EPI_GATE_RESIDUAL, EPI_GELU_MX = 0, 1, 2, 3
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -47,6 +47,7 @@ class GemmProblem(ctypes.Structure):
         ("a_scale", _vp), ("w_scale", _vp),
         ("m", _i64), ("rows_per_batch", _i64),
         ("norm_q", _vp), ("norm_k", _vp), ("rope_row0", _i64),
+        ("c_scale", _vp), ("ld_c_scale", _i64),
     ]
 
 

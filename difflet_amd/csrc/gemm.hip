@@ -59,6 +59,8 @@ struct GemmProblemDev {
   const bf16* nq;     // fused q/k norm: RMSNorm weights of q and k heads (NULL: 1)
   const bf16* nk;
   int64_t rope_row0;  // RoPE table row of row 0
+  uint8_t* cs;        // EPI_GELU_MX: E8M0 scales of C, row stride ldcs
+  int64_t ldcs;
 };
 
 // Split schedule. Tiles [0, dp) run one per workgroup. The other S < cus tiles (the last,
@@ -614,6 +616,8 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
       if (n0 >= args.act_col_start) stage(std::integral_constant<int, 1>{});
       else if (n0 + BN > args.act_col_start) stage(std::integral_constant<int, 2>{});
       else stage(std::integral_constant<int, 0>{});
+    } else if constexpr (EPI == DIFFLET_EPI_GELU_MX) {
+      stage(std::integral_constant<int, 1>{});
     } else {
       stage(std::integral_constant<int, 0>{});
     }
@@ -692,6 +696,44 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
             }
           }
         }
+      }
+      continue;  // this tile is stored
+    }
+    if constexpr (EPI == DIFFLET_EPI_GELU_MX) {
+      // the staged bf16 GELU output quantized to MXFP8 in blocks of 32 consecutive columns:
+      // each half-wave takes one row, lanes 4 b .. 4 b + 3 hold block b's 32 values (8 each);
+      // their exponent maximum meets over two xor shuffles inside the quad, then each lane
+      // stores its 8 codes and the block's first lane its E8M0 scale (N % 32 == 0: a block is
+      // wholly in or out, and the quad takes one branch)
+      const int ch = lane & 31, half = lane >> 5;
+      const int64_t n = n0 + ch * 8;
+      for (int r = wave * 2 + half; r < BM; r += 2 * NWAVES) {
+        const int64_t m = m0 + r;
+        if (m >= M) break;  // rows only grow
+        if (n >= N) continue;
+        const u32x4 raw = *reinterpret_cast<const u32x4*>(tile + r * 512 + ((ch ^ (r & 31)) << 4));
+        float v[8];
+        uint32_t emax = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[2 * e] = bf16bits_to_f32(raw[e] & 0xffffu);
+          v[2 * e + 1] = bf16bits_to_f32(raw[e] >> 16);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t x = (__builtin_bit_cast(uint32_t, v[e]) >> 23) & 0xffu;
+          emax = x > emax ? x : emax;
+        }
+        emax = max(emax, (uint32_t)__shfl_xor((int)emax, 1, 64));
+        emax = max(emax, (uint32_t)__shfl_xor((int)emax, 2, 64));
+        const int su = (int)emax - 7 < 0 ? 0 : (int)emax - 7;  // clamp(e_max - 7, 0, 255)
+        const float mul = __builtin_bit_cast(float, (uint32_t)(254 - su) << 23);  // 2^(127 - su)
+        float c[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) c[e] = clamp448(__fmul_rn(v[e], mul));
+        *reinterpret_cast<u32x2*>(P.c + m * P.ldc + n) =
+            u32x2{e4m3x4(c[0], c[1], c[2], c[3]), e4m3x4(c[4], c[5], c[6], c[7])};
+        if ((ch & 3) == 0) P.cs[m * P.ldcs + (n >> 5)] = (uint8_t)su;
       }
       continue;  // this tile is stored
     }
@@ -857,8 +899,14 @@ static int gemm_launch(const char* name, int nproblems, const difflet_gemm_probl
   DLT_REQUIRE(n < (1LL << 30) && k < (1LL << 30), DIFFLET_EINVAL, "%s: n or k too large", name);
   DLT_REQUIRE(n % 4 == 0, DIFFLET_EINVAL, "%s: n = %lld must be a multiple of 4", name,
               (long long)n);
-  DLT_REQUIRE(epilogue >= DIFFLET_EPI_NONE && epilogue <= DIFFLET_EPI_GATE_RESIDUAL,
+  DLT_REQUIRE(epilogue >= DIFFLET_EPI_NONE && epilogue <= DIFFLET_EPI_GELU_MX,
               DIFFLET_EINVAL, "%s: unknown epilogue %d", name, epilogue);
+  const bool mx_out = epilogue == DIFFLET_EPI_GELU_MX;
+  DLT_REQUIRE(!mx_out || E == Elem::MX, DIFFLET_EUNSUPPORTED,
+              "%s: the GELU -> MXFP8 epilogue runs on the MXFP8 GEMM only", name);
+  DLT_REQUIRE(!mx_out || (n % 32 == 0 && act_col_start == 0 && !qk), DIFFLET_EINVAL,
+              "%s: the GELU -> MXFP8 epilogue needs n %% 32 == 0, act_col_start 0 and no "
+              "fused q/k norm", name);
   GemmArgs args = {};
   args.nprob = nproblems;
   args.n = (int)n;
@@ -887,6 +935,11 @@ static int gemm_launch(const char* name, int nproblems, const difflet_gemm_probl
     }
     DLT_REQUIRE(((uintptr_t)q.bias & 7) == 0, DIFFLET_EINVAL, "%s: bias must be 8-byte aligned",
                 name);
+    if (mx_out)
+      DLT_REQUIRE(q.c_scale && q.ldc % 8 == 0 && q.ld_c_scale >= n / 32,
+                  DIFFLET_EINVAL,
+                  "%s: the GELU -> MXFP8 epilogue needs c_scale [m, n / 32] and ldc %% 8 == 0 "
+                  "in problem %d", name, i);
     if (E == Elem::FP8)
       DLT_REQUIRE(((uintptr_t)q.w_scale & 15) == 0, DIFFLET_EINVAL,
                   "%s: w_scale must be 16-byte aligned", name);
@@ -919,6 +972,8 @@ static int gemm_launch(const char* name, int nproblems, const difflet_gemm_probl
     d.nq = (const bf16*)q.norm_q;
     d.nk = (const bf16*)q.norm_k;
     d.rope_row0 = q.rope_row0;
+    d.cs = (uint8_t*)q.c_scale;
+    d.ldcs = q.ld_c_scale;
     DLT_REQUIRE(!qk || (q.rope_row0 >= 0 && ((uintptr_t)q.norm_q & 7) == 0 &&
                         ((uintptr_t)q.norm_k & 7) == 0),
                 DIFFLET_EINVAL, "%s: q/k norm weights must be 8-byte aligned, rope_row0 >= 0",
@@ -992,6 +1047,10 @@ static int gemm_launch(const char* name, int nproblems, const difflet_gemm_probl
       break;
     case 2 * DIFFLET_EPI_GELU + 1:
       go(integral_constant<int, DIFFLET_EPI_GELU>{}, std::true_type{});
+      break;
+    case 2 * DIFFLET_EPI_GELU_MX:
+      if constexpr (E == Elem::MX)
+        go(integral_constant<int, DIFFLET_EPI_GELU_MX>{}, std::false_type{});
       break;
     default:
       go(integral_constant<int, DIFFLET_EPI_GATE_RESIDUAL>{}, std::false_type{});

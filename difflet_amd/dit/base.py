@@ -49,9 +49,23 @@ class JointDiT:
         if self.kind == "mx" and self._ln_mx_fusable():  # LayerNorm output straight to MXFP8
             bufs["nq"] = torch.empty((s, d), dtype=torch.float8_e4m3fn, device=dev)
             bufs["nsx"] = torch.empty((s, d // 32), dtype=torch.uint8, device=dev)
+        if self.kind == "mx":  # the MLP hidden activation as MXFP8 codes from FF1's epilogue
+            f = self.cfg.mlp
+            bufs["ffq"] = torch.empty((s, f), dtype=torch.float8_e4m3fn, device=dev)
+            bufs["ffs"] = torch.empty((s, f // 32), dtype=torch.uint8, device=dev)
         for k, shape in (extra or {}).items():
             bufs[k] = e(*shape)
         return bufs
+
+    @staticmethod
+    def _mx_mlp(blk) -> None:
+        """An MXFP8 MLP pair: FF1's output rows go to swizzle order (FF1 then writes FF2's A
+        operand in its epilogue); blk.ff_mx marks the block."""
+        pairs = ((blk.ff1_txt, blk.ff2_txt), (blk.ff1_img, blk.ff2_img))
+        blk.ff_mx = all(a.kind == "mx" and b.kind == "mx" and a.n % 32 == 0 for a, b in pairs)
+        if blk.ff_mx:
+            blk.ff1_txt = blk.ff1_txt.rows_in_swizzle_order()
+            blk.ff1_img = blk.ff1_img.rows_in_swizzle_order()
 
     def _ln_mx_fusable(self) -> bool:
         """The LayerNorm -> MXFP8 kernel covers whole 512-wide swizzle tiles."""
@@ -151,10 +165,20 @@ class JointDiT:
                     blk.out_img.problem(o[I], h[I], gate=x_g, residual=h[I], prepared=pi)],
                    blk.out_img.kind, _lib.EPI_GATE_RESIDUAL)
         pt, pi = self._ln_joint(bufs, st, c_sc2, c_sh2, x_sc2, x_sh2, blk.ff1_img.kind)
-        self._gemm(f"gemm.{tag}.ff1", [blk.ff1_txt.problem(n[T], ff[T], prepared=pt),
-                                       blk.ff1_img.problem(n[I], ff[I], prepared=pi)],
-                   blk.ff1_img.kind, _lib.EPI_GELU)
-        pt, pi = self._prep_joint(blk.ff2_txt, blk.ff2_img, ff, st)
+        if getattr(blk, "ff_mx", False) and "ffq" in bufs:
+            # FF1's epilogue writes GELU(x) as MXFP8 codes and scales, FF2's A operand: FF1's
+            # weight rows are in swizzle order, so its output columns are FF2's swizzled K
+            fq, fs = bufs["ffq"], bufs["ffs"]
+            self._gemm(f"gemm.{tag}.ff1",
+                       [blk.ff1_txt.problem(n[T], fq[T], prepared=pt, c_scale=fs[T]),
+                        blk.ff1_img.problem(n[I], fq[I], prepared=pi, c_scale=fs[I])],
+                       "mx", _lib.EPI_GELU_MX)
+            pt, pi = (fq[T], fs[T]), (fq[I], fs[I])
+        else:
+            self._gemm(f"gemm.{tag}.ff1", [blk.ff1_txt.problem(n[T], ff[T], prepared=pt),
+                                           blk.ff1_img.problem(n[I], ff[I], prepared=pi)],
+                       blk.ff1_img.kind, _lib.EPI_GELU)
+            pt, pi = self._prep_joint(blk.ff2_txt, blk.ff2_img, ff, st)
         self._gemm(f"gemm.{tag}.ff2",
                    [blk.ff2_txt.problem(ff[T], h[T], gate=c_g2, residual=h[T], prepared=pt),
                     blk.ff2_img.problem(ff[I], h[I], gate=x_g2, residual=h[I], prepared=pi)],

@@ -60,6 +60,7 @@ class _Double:
         self.ff2_img = L("ff.net.2")
         self.ff1_txt = L("ff_context.net.0.proj")
         self.ff2_txt = L("ff_context.net.2")
+        JointDiT._mx_mlp(self)
         bf = lambda n: W(n).to(torch.bfloat16).contiguous()  # noqa: E731
         self.nq, self.nk = bf(a + "norm_q.weight"), bf(a + "norm_k.weight")
         self.naq, self.nak = bf(a + "norm_added_q.weight"), bf(a + "norm_added_k.weight")

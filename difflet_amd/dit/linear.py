@@ -62,6 +62,23 @@ class DeviceLinear:
         self.bias = None if bias is None else bias.to(device=codes.device, dtype=torch.bfloat16).contiguous()
         return self
 
+    def rows_in_swizzle_order(self) -> "DeviceLinear":
+        """This linear with its output rows (weight rows, scales, bias) gathered into the MXFP8
+        swizzle order over N (difflet/quant/mx.py:65-76): its GEMM then writes output column p
+        as logical column perm[p], the layout in which the GELU -> MXFP8 epilogue's codes are
+        the next MXFP8 GEMM's A operand."""
+        from difflet_amd.quant.linear import _swizzle_index
+
+        if self.kind != "mx" or self.n % 32:
+            raise ValueError("rows in swizzle order: an MXFP8 linear with N % 32 == 0")
+        idx = _swizzle_index(self.n, self.w.device)
+        out = DeviceLinear.__new__(DeviceLinear)
+        out.kind, out.n, out.k = self.kind, self.n, self.k
+        out.w = self.w.view(torch.uint8)[idx].view(self.w.dtype).contiguous()
+        out.ws = self.ws[idx].contiguous()
+        out.bias = None if self.bias is None else self.bias[idx].contiguous()
+        return out
+
     def prep(self, a: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor | None]:
         """The GEMM's A operand for activations a [M, K] (quantized for the fp8 kinds)."""
         if self.kind == "bf16":
@@ -71,10 +88,11 @@ class DeviceLinear:
         return kernels.quantize_mxfp8(a, swizzled=True)
 
     def problem(self, a: torch.Tensor, c: torch.Tensor, *, gate=None, residual=None,
-                prepared=None, norm_q=None, norm_k=None, rope_row0: int = 0) -> Problem:
+                prepared=None, norm_q=None, norm_k=None, rope_row0: int = 0,
+                c_scale=None) -> Problem:
         aq, asc = prepared if prepared is not None else self.prep(a)
         return Problem(aq, self.w, c, self.bias, gate, residual, asc, self.ws,
-                       norm_q=norm_q, norm_k=norm_k, rope_row0=rope_row0)
+                       norm_q=norm_q, norm_k=norm_k, rope_row0=rope_row0, c_scale=c_scale)
 
     def __call__(self, a: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         c = out if out is not None else torch.empty((a.shape[0], self.n), dtype=torch.bfloat16,

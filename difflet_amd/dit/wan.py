@@ -86,6 +86,12 @@ class _Block:
         self.out2 = L("bf16", "attn2.to_out.0")
         self.ffn_in = L(kind, "ffn.net_in")
         self.ffn_out = L(kind, "ffn.net_out")
+        # an MXFP8 FFN: ffn_in's output rows in swizzle order, so its GELU -> MXFP8 epilogue
+        # writes ffn_out's A operand
+        self.ff_mx = (self.ffn_in.kind == "mx" and self.ffn_out.kind == "mx"
+                      and self.ffn_in.n % 32 == 0)
+        if self.ff_mx:
+            self.ffn_in = self.ffn_in.rows_in_swizzle_order()
         bf = lambda n: W(n).to(torch.bfloat16).contiguous()  # noqa: E731
         self.nq1, self.nk1 = bf("attn1.norm_q.weight"), bf("attn1.norm_k.weight")
         self.nq2, self.nk2 = bf("attn2.norm_q.weight"), bf("attn2.norm_k.weight")
@@ -147,6 +153,9 @@ class WanDiT:
             if self.kind == "mx" and d % 512 == 0:  # LayerNorm output straight to MXFP8
                 bufs["nq"] = torch.empty((s, d), dtype=torch.float8_e4m3fn, device=dev)
                 bufs["nsx"] = torch.empty((s, d // 32), dtype=torch.uint8, device=dev)
+            if self.kind == "mx":  # the FFN hidden activation as MXFP8 from ffn_in's epilogue
+                bufs["ffq"] = torch.empty((s, c.ffn), dtype=torch.float8_e4m3fn, device=dev)
+                bufs["ffs"] = torch.empty((s, c.ffn // 32), dtype=torch.uint8, device=dev)
             self._bufs = {key: bufs}
         return self._bufs[key]
 
@@ -206,9 +215,16 @@ class WanDiT:
         self._gemm("gemm.out2", [blk.out2.problem(q2, h, gate=self.ones, residual=h)],
                    _lib.EPI_GATE_RESIDUAL, kind=blk.out2.kind)
         p = self._ln(bufs, blk.ffn_in, c_sc, c_sh)
-        self._gemm("gemm.ffn_in", [blk.ffn_in.problem(n, ff, prepared=p)], _lib.EPI_GELU,
-                   kind=blk.ffn_in.kind)
-        self._gemm("gemm.ffn_out", [blk.ffn_out.problem(ff, h, gate=gates[1:2], residual=h)],
+        if blk.ff_mx and "ffq" in bufs:
+            fq = (bufs["ffq"], bufs["ffs"])
+            self._gemm("gemm.ffn_in", [blk.ffn_in.problem(n, fq[0], prepared=p, c_scale=fq[1])],
+                       _lib.EPI_GELU_MX, kind="mx")
+        else:
+            self._gemm("gemm.ffn_in", [blk.ffn_in.problem(n, ff, prepared=p)], _lib.EPI_GELU,
+                       kind=blk.ffn_in.kind)
+            fq = None
+        self._gemm("gemm.ffn_out", [blk.ffn_out.problem(ff, h, gate=gates[1:2], residual=h,
+                                                        prepared=fq)],
                    _lib.EPI_GATE_RESIDUAL, kind=blk.ffn_out.kind)
 
     def condition(self, timestep, text, bufs):

@@ -156,10 +156,11 @@ class Problem:
     """One problem of a grouped GEMM: C = epilogue(A W^T + bias)."""
 
     __slots__ = ("a", "w", "c", "bias", "gate", "residual", "a_scale", "w_scale",
-                 "rows_per_batch", "norm_q", "norm_k", "rope_row0")
+                 "rows_per_batch", "norm_q", "norm_k", "rope_row0", "c_scale")
 
     def __init__(self, a, w, c, bias=None, gate=None, residual=None, a_scale=None,
-                 w_scale=None, rows_per_batch=None, norm_q=None, norm_k=None, rope_row0=0):
+                 w_scale=None, rows_per_batch=None, norm_q=None, norm_k=None, rope_row0=0,
+                 c_scale=None):
         self.a, self.w, self.c = a, w, c
         self.bias, self.gate, self.residual = bias, gate, residual
         self.a_scale, self.w_scale = a_scale, w_scale
@@ -167,6 +168,8 @@ class Problem:
         # fused q/k norm (gemm_grouped(..., qk=QkNormRope)): this problem's [128] bf16 RMSNorm
         # weights and the RoPE table row of its row 0
         self.norm_q, self.norm_k, self.rope_row0 = norm_q, norm_k, rope_row0
+        # EPI_GELU_MX: c holds e4m3 codes and c_scale the E8M0 scales [m, n / 32]
+        self.c_scale = c_scale
 
 
 class QkNormRope:
@@ -316,7 +319,17 @@ def gemm_grouped(problems: Sequence[Problem], *, kind: str = "bf16",
             raise TypeError("bf16 GEMM takes bf16 operands")
         if kind != "bf16" and (p.a.element_size() != 1 or p.w.element_size() != 1):
             raise TypeError("fp8 GEMMs take e4m3 codes (uint8 or float8_e4m3fn)")
-        if p.c.dtype != torch.bfloat16:
+        if epilogue == _lib.EPI_GELU_MX:
+            if kind != "mx":
+                raise ValueError("the GELU -> MXFP8 epilogue runs on the MXFP8 GEMM only")
+            cs = p.c_scale
+            if p.c.element_size() != 1 or cs is None or cs.dtype != torch.uint8 or \
+                    cs.dim() != 2 or cs.stride(1) != 1 or cs.shape[0] != p.a.shape[0] or \
+                    cs.shape[1] < n // 32 or n % 32 or p.c.stride(0) % 8:
+                raise ValueError("the GELU -> MXFP8 epilogue writes e4m3 codes [m, n] (row "
+                                 "stride a multiple of 8) and uint8 scales [m, n / 32]; n % 32 "
+                                 "== 0")
+        elif p.c.dtype != torch.bfloat16:
             raise TypeError("GEMM output is bf16")
         _check_epilogue_operands(p, i, kind, n, k, epilogue)
     if qk is not None:
@@ -338,6 +351,8 @@ def gemm_grouped(problems: Sequence[Problem], *, kind: str = "bf16",
         q.w_scale = p.w_scale.data_ptr() if p.w_scale is not None else None
         q.m = p.a.shape[0]
         q.rows_per_batch = p.rows_per_batch or p.a.shape[0]
+        if p.c_scale is not None and epilogue == _lib.EPI_GELU_MX:
+            q.c_scale, q.ld_c_scale = p.c_scale.data_ptr(), p.c_scale.stride(0)
         if qk is not None:
             q.norm_q = p.norm_q.data_ptr() if p.norm_q is not None else None
             q.norm_k = p.norm_k.data_ptr() if p.norm_k is not None else None

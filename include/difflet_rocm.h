@@ -112,9 +112,20 @@ int difflet_rocm_attention_noalloc(const void* q, const void* k, const void* v, 
  * All problems of one call share n, k and the epilogue; each has its own A, W, C, M.
  * ---------------------------------------------------------------------------------------- */
 enum difflet_epilogue {
-  DIFFLET_EPI_NONE = 0,          /* C = acc + bias */
-  DIFFLET_EPI_GELU = 1,          /* C = gelu_tanh(acc + bias) for columns >= act_col_start */
-  DIFFLET_EPI_GATE_RESIDUAL = 2  /* C = residual + gate[batch] * (acc + bias) */
+  DIFFLET_EPI_NONE = 0,           /* C = acc + bias */
+  DIFFLET_EPI_GELU = 1,           /* C = gelu_tanh(acc + bias) for columns >= act_col_start */
+  DIFFLET_EPI_GATE_RESIDUAL = 2,  /* C = residual + gate[batch] * (acc + bias) */
+  /* MXFP8 GEMM only: y = gelu_tanh(acc + bias) on every column, rounded to bf16, then
+   * quantized to MXFP8 in blocks of 32 consecutive columns (the block law of
+   * difflet/quant/mx.py:85-108): C receives the e4m3 codes (one byte per element, row stride
+   * ldc bytes) and c_scale the E8M0 scales [m, n / 32] (row stride ld_c_scale bytes). With W's
+   * rows (and the bias) in the swizzle order of difflet/quant/mx.py:65-76 over n, C and c_scale
+   * are difflet_rocm_quantize_mxfp8 (swizzled) of the bf16 GELU output in logical order: the
+   * next MXFP8 GEMM's A operand (a feed-forward's hidden activation), written once. n % 32 == 0,
+   * act_col_start 0, no fused q/k norm; ldc and ld_c_scale multiples of 8. The reference's
+   * device MX linear quantizes its activations inside the matmul kernel
+   * (difflet/backends/neuron/ops_impl/fp8_kernels.py:46-58). */
+  DIFFLET_EPI_GELU_MX = 3
 };
 
 typedef struct difflet_gemm_problem {
@@ -136,6 +147,8 @@ typedef struct difflet_gemm_problem {
   const void* norm_q;   /* fused q/k norm (difflet_gemm_qk): [128] bf16 RMSNorm weights of q */
   const void* norm_k;   /*   and of k for this problem's rows (NULL: weight 1) */
   int64_t rope_row0;    /*   RoPE table row of this problem's row 0 */
+  void* c_scale;        /* EPI_GELU_MX: E8M0 scales of C [m, n / 32], row stride ld_c_scale */
+  int64_t ld_c_scale;
 } difflet_gemm_problem;
 
 /* Optional fused q/k RMSNorm + RoPE epilogue (EPI_NONE or EPI_GELU), for attention

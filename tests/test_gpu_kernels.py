@@ -384,6 +384,60 @@ def test_gemm_mxfp8_matches_fake_quant_linear(gpu, m, n, k):
     assert rel_l2(c, torch.from_numpy(ref)) < 4e-3
 
 
+# (m, n, k, split rows, workspace): a two-problem launch (text / image rows), FLUX-Qwen's MLP
+# width, a width with a 128-wide last swizzle tile, and 336 tiles on the split schedule
+@pytest.mark.parametrize("m,n,k,split,ws", [(300, 1024, 512, 0, None), (900, 12288, 3072, 256, None),
+                                            (500, 640, 256, 77, None),
+                                            (7168, 3072, 3072, 0, "shared")])
+def test_gemm_gelu_mx_epilogue_equals_gelu_then_quantize(gpu, m, n, k, split, ws):
+    """The GELU -> MXFP8 epilogue of an MXFP8 GEMM whose weight rows are in swizzle order: its
+    codes and E8M0 scales equal the swizzled MX quantizer applied to the bf16 GELU output of the
+    same GEMM on the weights in logical order, bit for bit (the next GEMM's A operand)."""
+    from difflet_amd.dit.linear import DeviceLinear
+
+    print(f"gemm_mx gelu->mx m={m} n={n} k={k} split={split} ws={ws}", flush=True)
+    g = torch.Generator().manual_seed(m + n + k)
+    a, w, b = rnd(g, m, k), rnd(g, n, k, std=0.05), rnd(g, n, std=0.1)
+    w[5] *= 40  # one output column with large values (its blocks scale alone)
+    lin = DeviceLinear(w.to(gpu), b.to(gpu), "mx")
+    aq, as_ = kernels.quantize_mxfp8(a.to(gpu), swizzled=True)
+    rows = [slice(0, split), slice(split, m)] if split else [slice(0, m)]
+    c = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+    kernels.gemm_grouped([lin.problem(None, c[r], prepared=(aq[r], as_[r])) for r in rows],
+                         kind="mx", epilogue=_lib.EPI_GELU, workspace=ws)
+    q_ref, s_ref = kernels.quantize_mxfp8(c, swizzled=True)
+    perm = lin.rows_in_swizzle_order()
+    q = torch.full((m, n), 0x7f, dtype=torch.uint8, device=gpu).view(torch.float8_e4m3fn)
+    s = torch.full((m, n // 32), 0xee, dtype=torch.uint8, device=gpu)
+    kernels.gemm_grouped([perm.problem(None, q[r], prepared=(aq[r], as_[r]), c_scale=s[r])
+                          for r in rows], kind="mx", epilogue=_lib.EPI_GELU_MX, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(s, s_ref)
+    assert torch.equal(q.view(torch.uint8), q_ref.view(torch.uint8))
+
+
+def test_gemm_gelu_mx_epilogue_refusals(gpu):
+    a = torch.zeros(64, 256, dtype=torch.bfloat16, device=gpu)
+    w = torch.zeros(96, 256, dtype=torch.bfloat16, device=gpu)
+    q = torch.zeros(64, 96, dtype=torch.uint8, device=gpu)
+    s = torch.zeros(64, 3, dtype=torch.uint8, device=gpu)
+    with pytest.raises(ValueError):  # bf16 GEMM
+        kernels.gemm_grouped([kernels.Problem(a, w, q, c_scale=s)], kind="bf16",
+                             epilogue=_lib.EPI_GELU_MX)
+    aq, as_ = kernels.quantize_mxfp8(a, swizzled=True)
+    wq, ws = kernels.quantize_mxfp8(w, swizzled=True)
+    with pytest.raises(ValueError):  # no scale output
+        kernels.gemm_grouped([kernels.Problem(aq, wq, q, a_scale=as_, w_scale=ws)], kind="mx",
+                             epilogue=_lib.EPI_GELU_MX)
+    w2, = kernels.quantize_mxfp8(torch.zeros(80, 256, dtype=torch.bfloat16, device=gpu),
+                                 swizzled=True)[:1]
+    with pytest.raises(ValueError):  # n % 32 != 0
+        kernels.gemm_grouped([kernels.Problem(aq, w2, q[:, :80], a_scale=as_,
+                                              w_scale=torch.zeros(80, 8, dtype=torch.uint8,
+                                                                  device=gpu),
+                                              c_scale=s)], kind="mx", epilogue=_lib.EPI_GELU_MX)
+
+
 # ------------------------------------------------------------------------------- attention
 def _attn_case(g, b, h, sq, sk, d=128, dtype=torch.bfloat16):
     q, k, v = rnd(g, b, h, sq, d, dtype=dtype), rnd(g, b, h, sk, d, dtype=dtype), rnd(g, b, h, sk, d, dtype=dtype)
