@@ -86,6 +86,8 @@ SIGNATURES: dict[str, tuple] = {
                                                 ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
     "difflet_rocm_quantize_fp8_rowwise": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _vp,
                                                  _vp]),
+    "difflet_rocm_quantize_fp8_rowwise_gelu": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64,
+                                                      _vp, _i64, _vp]),
     "difflet_rocm_quantize_mxfp8": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _vp, _i64,
                                            _i32, _vp]),
     "difflet_rocm_layernorm_modulate": (_i32, [_vp, _i64, _vp, _i64, _i32, _i32, _i64, _i64,

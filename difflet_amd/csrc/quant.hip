@@ -8,6 +8,8 @@
 // positions of the swizzle order; inside a K tile of width `tile` (512, or the remainder) with
 // sub = tile / 4, swizzled position r * 4 + j is logical k = k0 + j * sub + r, so block b of the
 // tile is the four runs k0 + j * sub + 8 b + [0, 8), j = 0..3: four 16-byte loads of bf16.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace dlt {
@@ -89,13 +91,16 @@ __global__ __launch_bounds__(256) void quant_rowwise_kernel(const T* __restrict_
 }
 
 // Single pass for 16-bit rows up to 2048 NCH elements: one workgroup per row, each thread keeps
-// its NCH chunks of 8 as raw 16-byte vectors, so the row is read from memory once.
-template <typename T, int NCH>
+// its NCH chunks of 8 as raw 16-byte vectors, so the row is read from memory once. GELU (bf16
+// rows): columns >= act_col_start (a multiple of 8) first become gelu_tanh(x) rounded to bf16,
+// the values a GELU epilogue would have stored, and are quantized as such.
+template <typename T, int NCH, bool GELU = false>
 __global__ __launch_bounds__(256) void quant_rowwise_wg_kernel(const T* __restrict__ x,
                                                                int64_t cols, int64_t ldx,
                                                                uint8_t* __restrict__ q,
                                                                int64_t ldq,
-                                                               float* __restrict__ scale) {
+                                                               float* __restrict__ scale,
+                                                               int64_t act_col_start = 0) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
@@ -106,6 +111,19 @@ __global__ __launch_bounds__(256) void quant_rowwise_wg_kernel(const T* __restri
   for (int c = 0; c < NCH; ++c) {
     const int64_t col = ((int64_t)c * 256 + tid) * 8;
     raw[c] = col < cols ? *reinterpret_cast<const u32x4*>(xr + col) : u32x4{0u, 0u, 0u, 0u};
+  }
+  if constexpr (GELU) {
+    static_assert(std::is_same<T, bf16>::value, "the GELU quantizer takes bf16 rows");
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int64_t col = ((int64_t)c * 256 + tid) * 8;
+      if (col >= act_col_start && col < cols) {
+        float v[8];
+        decode8<T>(raw[c], v);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) raw[c][i] = pack_bf16x2(gelu_tanh(v[2 * i]), gelu_tanh(v[2 * i + 1]));
+      }
+    }
   }
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
@@ -216,6 +234,37 @@ __global__ __launch_bounds__(256) void quant_mx_kernel(const T* __restrict__ x, 
 }  // namespace dlt
 
 using namespace dlt;
+
+extern "C" int difflet_rocm_quantize_fp8_rowwise_gelu(const void* x, int dtype, int64_t rows,
+                                                      int64_t cols, int64_t ldx, uint8_t* q,
+                                                      int64_t ldq, float* scale,
+                                                      int64_t act_col_start,
+                                                      difflet_stream_t stream) {
+  DLT_REQUIRE(x && q && scale, DIFFLET_EINVAL, "quantize_fp8_rowwise_gelu: null pointer");
+  DLT_REQUIRE(dtype == DIFFLET_BF16, DIFFLET_EUNSUPPORTED,
+              "quantize_fp8_rowwise_gelu: rows must be bf16");
+  DLT_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols <= 16384 && ldx % 8 == 0 &&
+                  ldq % 8 == 0 && act_col_start >= 0 && act_col_start % 8 == 0,
+              DIFFLET_EINVAL,
+              "quantize_fp8_rowwise_gelu: cols (at most 16384), strides and act_col_start must "
+              "be multiples of 8");
+  DLT_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 7) == 0, DIFFLET_EINVAL,
+              "quantize_fp8_rowwise_gelu: misaligned pointers");
+  if (rows == 0) return DIFFLET_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t nch = (cols + 2047) / 2048;
+  const dim3 grid((unsigned)rows), block(256);
+#define DLT_QWGG(N)                                                                            \
+  hipLaunchKernelGGL((quant_rowwise_wg_kernel<bf16, N, true>), grid, block, 0, s,              \
+                     (const bf16*)x, cols, ldx, q, ldq, scale, act_col_start)
+  if (nch <= 1) DLT_QWGG(1);
+  else if (nch <= 2) DLT_QWGG(2);
+  else if (nch <= 4) DLT_QWGG(4);
+  else if (nch <= 6) DLT_QWGG(6);
+  else DLT_QWGG(8);
+#undef DLT_QWGG
+  return dlt_check_launch("quantize_fp8_rowwise_gelu");
+}
 
 extern "C" int difflet_rocm_quantize_fp8_rowwise(const void* x, int dtype, int64_t rows,
                                                  int64_t cols, int64_t ldx, uint8_t* q,

@@ -106,15 +106,24 @@ class JointDiT:
         kernels.layernorm_modulate(h, sc, sh, out=bufs["n"], **kw)
         return None, None
 
-    def _prep_joint(self, lin_txt, lin_img, a, st: int):
+    def _prep_joint(self, lin_txt, lin_img, a, st: int, gelu_from: int | None = None):
         """The A operands of a text / image GEMM pair from one activation buffer a [S, K],
-        quantized (fp8 kinds) in one launch over all rows."""
+        quantized (fp8 kinds) in one launch over all rows (gelu_from: see DeviceLinear.prep)."""
         if lin_txt.kind != lin_img.kind:
             raise ValueError("a joint GEMM pair shares one kind")
         if lin_img.kind == "bf16":
             return None, None
-        q, sc = lin_img.prep(a)
+        q, sc = lin_img.prep(a, gelu_from=gelu_from)
         return (q[:st], sc[:st]), (q[st:], sc[st:])
+
+    #: per-token fp8 steps apply the MLP's GELU where its bf16 pre-activation is quantized for
+    #: the next GEMM (quantize_fp8_rowwise(gelu_from=...)), not in the producing GEMM's epilogue:
+    #: the quantizer is bound by HBM and absorbs the GELU's VALU work, which in a GEMM epilogue
+    #: runs while the matrix cores idle
+    fp8_gelu_at_quant = True
+
+    def _gelu_at_quant(self, lin) -> bool:
+        return lin.kind == "fp8" and self.fp8_gelu_at_quant
 
     def _attn(self, buf, q_off: int, k_off: int, v_off: int):
         """Joint attention over all rows of `buf` [S, ld]; output written over q."""
@@ -175,10 +184,12 @@ class JointDiT:
                        "mx", _lib.EPI_GELU_MX)
             pt, pi = (fq[T], fs[T]), (fq[I], fs[I])
         else:
+            late = self._gelu_at_quant(blk.ff2_img)  # fp8: FF1 stores the pre-activation
             self._gemm(f"gemm.{tag}.ff1", [blk.ff1_txt.problem(n[T], ff[T], prepared=pt),
                                            blk.ff1_img.problem(n[I], ff[I], prepared=pi)],
-                       blk.ff1_img.kind, _lib.EPI_GELU)
-            pt, pi = self._prep_joint(blk.ff2_txt, blk.ff2_img, ff, st)
+                       blk.ff1_img.kind, _lib.EPI_NONE if late else _lib.EPI_GELU)
+            pt, pi = self._prep_joint(blk.ff2_txt, blk.ff2_img, ff, st,
+                                      gelu_from=0 if late else None)
         self._gemm(f"gemm.{tag}.ff2",
                    [blk.ff2_txt.problem(ff[T], h[T], gate=c_g2, residual=h[T], prepared=pt),
                     blk.ff2_img.problem(ff[I], h[I], gate=x_g2, residual=h[I], prepared=pi)],

@@ -181,15 +181,21 @@ class FluxDiT(JointDiT):
         # [k | v | q | mlp]: GELU on the MLP columns, q/k RMSNorm + RoPE in the same epilogue or
         # in one launch after it (self.fuse_single_qk)
         fuse = self.fuse_single_qk[blk.w1.kind]
+        # per-token fp8: W1 stores the MLP pre-activation and W2's activation quantizer applies
+        # the GELU (see JointDiT.fp8_gelu_at_quant)
+        late = self._gelu_at_quant(blk.w2)
         self._gemm("gemm.single.w1",
                    [blk.w1.problem(n, big, prepared=p, norm_q=blk.nq, norm_k=blk.nk)],
-                   blk.w1.kind, _lib.EPI_GELU, 3 * d,
+                   blk.w1.kind, _lib.EPI_NONE if late else _lib.EPI_GELU, 0 if late else 3 * d,
                    qk=self._qk_epilogue(2 * d, 0, cos, sin) if fuse else None)
         if not fuse:
             kernels.qk_norm_rope(big, heads=c.heads, head_dim=c.head_dim, q_off=2 * d, k_off=0,
                                  wq=blk.nq, wk=blk.nk, eps=EPS, cos=cos, sin=sin, law=0)
         self._attn(big, 2 * d, 0, d)
-        self._gemm("gemm.single.w2", [blk.w2.problem(big[:, 2 * d:], h, gate=g, residual=h)],
+        a2 = big[:, 2 * d:]
+        self._gemm("gemm.single.w2",
+                   [blk.w2.problem(a2, h, gate=g, residual=h,
+                                   prepared=blk.w2.prep(a2, gelu_from=d) if late else None)],
                    blk.w2.kind, _lib.EPI_GATE_RESIDUAL)
 
     # -------------------------------------------------------------------------- step

@@ -79,12 +79,17 @@ class DeviceLinear:
         out.bias = None if self.bias is None else self.bias[idx].contiguous()
         return out
 
-    def prep(self, a: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor | None]:
-        """The GEMM's A operand for activations a [M, K] (quantized for the fp8 kinds)."""
+    def prep(self, a: torch.Tensor, gelu_from: int | None = None
+             ) -> tuple[torch.Tensor, torch.Tensor | None]:
+        """The GEMM's A operand for activations a [M, K] (quantized for the fp8 kinds).
+        gelu_from (fp8 only): a's columns from there on are an MLP pre-activation, quantized as
+        bf16(gelu_tanh(a)) (the per-token fp8 law's GELU point)."""
         if self.kind == "bf16":
             return a, None
         if self.kind == "fp8":
-            return kernels.quantize_fp8_rowwise(a)
+            return kernels.quantize_fp8_rowwise(a, gelu_from=gelu_from)
+        if gelu_from is not None:
+            raise ValueError("the GELU-at-quantization point is part of the per-token fp8 law")
         return kernels.quantize_mxfp8(a, swizzled=True)
 
     def problem(self, a: torch.Tensor, c: torch.Tensor, *, gate=None, residual=None,

@@ -391,16 +391,25 @@ def linear(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, *
 
 
 # ------------------------------------------------------------------------------- quantizers
-def quantize_fp8_rowwise(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Per-row e4m3 codes (float8_e4m3fn [rows, K]) and fp32 scales [rows]."""
+def quantize_fp8_rowwise(x: torch.Tensor, *, gelu_from: int | None = None
+                         ) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row e4m3 codes (float8_e4m3fn [rows, K]) and fp32 scales [rows]. gelu_from (bf16 x,
+    a multiple of 8): columns from there on are quantized as bf16(gelu_tanh(x)), the MLP
+    activation applied where its pre-activation is quantized."""
     dev = _on_gpu(x)
     x2 = _rows2d(x, "quantize_fp8_rowwise")
     rows, cols = x2.shape
     q = torch.empty((rows, cols), dtype=torch.float8_e4m3fn, device=dev)
     s = torch.empty((rows,), dtype=torch.float32, device=dev)
-    check(lib().difflet_rocm_quantize_fp8_rowwise(_ptr(x2), _dt(x2), rows, cols, x2.stride(0),
-                                                  _ptr(q), cols, _ptr(s), _stream(dev)),
-          "quantize_fp8_rowwise")
+    if gelu_from is None:
+        check(lib().difflet_rocm_quantize_fp8_rowwise(_ptr(x2), _dt(x2), rows, cols,
+                                                      x2.stride(0), _ptr(q), cols, _ptr(s),
+                                                      _stream(dev)), "quantize_fp8_rowwise")
+    else:
+        check(lib().difflet_rocm_quantize_fp8_rowwise_gelu(_ptr(x2), _dt(x2), rows, cols,
+                                                           x2.stride(0), _ptr(q), cols, _ptr(s),
+                                                           int(gelu_from), _stream(dev)),
+              "quantize_fp8_rowwise_gelu")
     return q, s
 
 

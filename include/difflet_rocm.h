@@ -231,6 +231,16 @@ int difflet_rocm_quantize_fp8_rowwise(const void* x, int dtype, int64_t rows, in
                                       int64_t ldx, uint8_t* q, int64_t ldq, float* scale,
                                       difflet_stream_t stream);
 
+/* difflet_rocm_quantize_fp8_rowwise of y, where y = x on columns below act_col_start and
+ * y = bf16(gelu_tanh(x)) from act_col_start on (difflet/layers/activations.py:59-65): the GELU
+ * of an MLP's bf16 pre-activation applied where the per-token fp8 activation is quantized, so the
+ * producing GEMM stores the pre-activation with a plain epilogue. x bf16, cols <= 16384,
+ * act_col_start a multiple of 8. Part of this library's per-token fp8 law (no reference
+ * counterpart, like difflet_rocm_quantize_fp8_rowwise). */
+int difflet_rocm_quantize_fp8_rowwise_gelu(const void* x, int dtype, int64_t rows, int64_t cols,
+                                           int64_t ldx, uint8_t* q, int64_t ldq, float* scale,
+                                           int64_t act_col_start, difflet_stream_t stream);
+
 /* MXFP8 block law of difflet/quant/mx.py:46-108 (`swizzle_perm`, `_block_scales`,
  * `quantize_mx`): blocks are consecutive 32 values in swizzle order, scale_u8 =
  * clamp(max exponent field - 7, 0, 255), q = e4m3_rne(clamp(x / 2^(scale_u8 - 127), +-448)).

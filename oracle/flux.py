@@ -160,6 +160,14 @@ def qlinear(quant, act_dtype=None):
     return lin
 
 
+def gelu_input_rounder(quant, store):
+    """Where the MLP's GELU reads its input. Under the per-token fp8 law the producing GEMM
+    stores the pre-activation (rounded to `store`) and the next GEMM's activation quantizer
+    applies the GELU (difflet_rocm_quantize_fp8_rowwise_gelu); otherwise the GELU takes the
+    fp32 GEMM output (a GELU epilogue)."""
+    return ops.rounder(store) if quant == "fp8" else (lambda x: x)
+
+
 def _heads(x, shape: FluxShape):
     b, s, _ = x.shape
     return x.view(b, s, shape.heads, shape.head_dim).transpose(1, 2)
@@ -211,14 +219,15 @@ def double_block(w: dict, hidden, context, temb, cos, sin, shape: FluxShape,
 
     hidden = R(hidden + g_msa[:, None] * x_attn)
     nx2 = R(ops.ada_modulate(hidden, sh_mlp, sc_mlp))
-    ff = Q(R(ops.gelu_tanh(Q(nx2, w["ff.net.0.proj.weight"], w["ff.net.0.proj.bias"]))),
+    P = gelu_input_rounder(quant, store)
+    ff = Q(R(ops.gelu_tanh(P(Q(nx2, w["ff.net.0.proj.weight"], w["ff.net.0.proj.bias"])))),
            w["ff.net.2.weight"], w["ff.net.2.bias"])
     hidden = R(hidden + g_mlp[:, None] * ff)
 
     context = R(context + c_g_msa[:, None] * c_attn)
     nc2 = R(ops.ada_modulate(context, c_sh_mlp, c_sc_mlp))
-    cff = Q(R(ops.gelu_tanh(Q(nc2, w["ff_context.net.0.proj.weight"],
-                              w["ff_context.net.0.proj.bias"]))),
+    cff = Q(R(ops.gelu_tanh(P(Q(nc2, w["ff_context.net.0.proj.weight"],
+                                w["ff_context.net.0.proj.bias"])))),
             w["ff_context.net.2.weight"], w["ff_context.net.2.bias"])
     context = R(context + c_g_mlp[:, None] * cff)
     return context, hidden
@@ -248,7 +257,8 @@ def single_block(w: dict, hidden, temb, cos, sin, shape: FluxShape, rms_law=ops.
         mods = L(torch.nn.functional.silu(temb), w["norm.linear.weight"], w["norm.linear.bias"])
     shift, scale, gate = R(mods).chunk(3, dim=1)
     nh = R(ops.ada_modulate(hidden, shift, scale))
-    mlp = R(ops.gelu_tanh(Q(nh, w["proj_mlp.weight"], w["proj_mlp.bias"])))
+    mlp = R(ops.gelu_tanh(gelu_input_rounder(quant, store)(
+        Q(nh, w["proj_mlp.weight"], w["proj_mlp.bias"]))))
     a = lambda n: R(Q(nh, w[f"attn.{n}.weight"], w[f"attn.{n}.bias"]))  # noqa: E731
     q, k, v = _heads(a("to_q"), shape), _heads(a("to_k"), shape), _heads(a("to_v"), shape)
     q = rms_law(q, w["attn.norm_q.weight"], 1e-6)

@@ -38,7 +38,7 @@ import math
 import torch
 
 from oracle import ops
-from oracle.flux import _draw, qlinear
+from oracle.flux import _draw, gelu_input_rounder, qlinear
 
 
 @dataclasses.dataclass(frozen=True)
@@ -220,12 +220,13 @@ def block(w: dict, hidden, context, temb, cos, sin, shape: QwenShape, quant=None
 
     hidden = R(hidden + i_g1[:, None] * x_attn)
     context = R(context + t_g1[:, None] * c_attn)
+    P = gelu_input_rounder(quant, store)  # the per-token fp8 law's GELU point
     nx2 = R(ops.ada_modulate(hidden, i_sh2, i_sc2))
     hidden = R(hidden + i_g2[:, None] * lin("img_mlp.net.2",
-                                            R(ops.gelu_tanh(lin("img_mlp.net.0.proj", nx2)))))
+                                            R(ops.gelu_tanh(P(lin("img_mlp.net.0.proj", nx2))))))
     nc2 = R(ops.ada_modulate(context, t_sh2, t_sc2))
     context = R(context + t_g2[:, None] * lin("txt_mlp.net.2",
-                                              R(ops.gelu_tanh(lin("txt_mlp.net.0.proj", nc2)))))
+                                              R(ops.gelu_tanh(P(lin("txt_mlp.net.0.proj", nc2))))))
     return context, hidden
 
 

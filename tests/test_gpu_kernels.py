@@ -255,6 +255,30 @@ def test_layernorm_modulate_fp8_equals_layernorm_then_quantize(gpu, rows, dim):
     assert rel_l2(y, ref) < 4e-3
 
 
+@pytest.mark.parametrize("rows,cols,gelu_from", [(37, 15360, 3072), (300, 12288, 0),
+                                                  (5, 640, 8), (9, 16384, 16376)])
+def test_quantize_fp8_rowwise_gelu_equals_gelu_then_quantize(gpu, rows, cols, gelu_from):
+    """The per-token fp8 quantizer that applies the MLP's GELU from gelu_from on: codes and
+    scales equal the GELU kernel's bf16 output (the values a GELU epilogue stores) quantized by
+    the plain row quantizer, bit for bit."""
+    g = torch.Generator().manual_seed(rows + cols)
+    x = (rnd(g, rows, cols, std=2.0).float() * torch.exp(torch.randn(rows, 1, generator=g))).bfloat16()
+    x[1, gelu_from:] = -30.0  # GELU of large negatives: zeros (and -0.0)
+    xd = x.to(gpu)
+    q, s = kernels.quantize_fp8_rowwise(xd, gelu_from=gelu_from)
+    y = xd.clone()
+    y[:, gelu_from:] = kernels.gelu_tanh(xd[:, gelu_from:])
+    q2, s2 = kernels.quantize_fp8_rowwise(y)
+    torch.cuda.synchronize()
+    assert torch.equal(q.view(torch.uint8), q2.view(torch.uint8)) and torch.equal(s, s2)
+    # strided input (W2's A operand is a column window of the single block's buffer)
+    wide = torch.zeros(rows, cols + 64, dtype=torch.bfloat16, device=gpu)
+    wide[:, 64:] = xd
+    q3, s3 = kernels.quantize_fp8_rowwise(wide[:, 64:], gelu_from=gelu_from)
+    torch.cuda.synchronize()
+    assert torch.equal(q3.view(torch.uint8), q.view(torch.uint8)) and torch.equal(s3, s)
+
+
 # (rows, dim, split, mod dtype, one_plus): a joint launch (text rows below `split` with their own
 # vectors) at FLUX / Qwen width, Wan's fp32 vectors and its affine norm2 (one_plus off), and
 # the narrowest / widest dims (one and sixteen swizzle tiles)
