@@ -34,12 +34,15 @@ encoders and the decoder draw their weights with their initializations' scales.
 Each step starts with its inputs resident in HBM. W untimed warmup steps, then K steps
 bracketed by torch.cuda.synchronize(); per-step times from HIP events on the step stream.
 
-roofline: the dominant kernel of the workload (flux: the single-block input GEMM, M 4608, N 7 x
-3072, K 3072, GELU on the MLP columns, 2 M N K = 608.8 GFLOP per launch, 38 per step; qwen: the
-joint attention, 24 heads x 7145^2 keys x 128, 4 H S^2 d = 627.3 GFLOP per launch, 60 per step).
-Its average duration comes from HIP events recorded around each of its launches inside the timed
-steps, on the stream it runs on. traffic: HBM bytes per launch of that kernel from rocprofv3
-read / write request counters (null when not measured for this kernel and shape).
+roofline: the dominant kernel of each kind's step, the attention or GEMM launch name with the
+largest summed time in a fully probed step run before the timed ones (flux bf16: the single-block
+input GEMM, M 4608, N 7 x 3072, K 3072, 2 M N K = 608.8 GFLOP per launch, 38 per step; flux fp8:
+the joint attention, 24 heads x 4608^2 keys x 128, 4 H S^2 d = 260.9 GFLOP per launch, 57 per
+step; qwen: the joint attention, 24 heads x 7145^2 keys x 128, 627.3 GFLOP per launch, 60 per
+step). Its average duration comes from HIP events recorded around each of its launches inside
+the timed steps, on the stream it runs on. traffic: bytes per launch of that kernel between L2
+and the memory fabric from rocprofv3 read / write request counters (null when not measured for
+that kernel, kind and shape).
 attn_gemm: one extra probed step times every GEMM and attention launch; the fraction is the
 roofline time of their algorithmic FLOPs at MFMA peak over their summed measured time.
 cpu_baseline (flux, N = 1): the oracle (fp32 torch restatement of the reference's CPU path) on
@@ -64,13 +67,23 @@ COPY_BYTES = 256 << 20
 # two rocprofv3 --pmc runs of this script: TCC_EA0_RDREQ_{32B,64B,128B} and TCC_EA0_WRREQ{,_64B}
 # request counts times their sizes (the same counters read exactly 256 MiB each way for the
 # --calibrate-copy 256 MiB copy). MALL hits are counted too, so this bounds HBM bytes from above.
-# Keyed by (workload, kind); absent -> null.
+# Keyed by (workload, probe name, kind); absent -> null.
 TRAFFIC: dict = {
-    # 4608 x 21504 x 3072 GEMM (GELU, fused q/k norm): 1195.8 MB read (A + W = 160 MB once, plus
+    # 4608 x 21504 x 3072 GEMM (GELU, fused q/k norm): 1178.9 MB read (A + W = 160 MB once, plus
     # the RoPE tables) + 198.2 MB written (C)
-    ("flux", "bf16"): 1_394_000_000,
-    # same GEMM, e4m3 operands: 654.7 MB read (80 MB once) + 198.2 MB written
-    ("flux", "fp8"): 852_900_000,
+    ("flux", "gemm.single.w1", "bf16"): 1_377_100_000,
+    # the joint attention, 24 heads x 4608 x 4608 x 128 bf16 on the split schedule (the same
+    # kernel in both steps): 834.2 MB read (q, k, v 84.9 MB once) + 93.2 MB written (the output
+    # 28.3 MB and the cut query tiles' fp32 partials)
+    ("flux", "attn", "fp8"): 927_400_000,
+    ("flux", "attn", "bf16"): 927_400_000,
+    # Qwen-Image's joint attention, 24 heads x 7145 x 7145 x 128: 1976.8 MB read + 104.5 written
+    ("qwen", "attn", "mx"): 2_081_300_000,
+    ("qwen", "attn", "bf16"): 2_081_300_000,
+    # Wan's self-attention, 40 heads x 32760 x 32760 x 128 (one query tile per workgroup, 20
+    # waves of workgroups): 3019.7 MB read + 335.5 MB written
+    ("wan", "attn.self", "bf16"): 3_355_200_000,
+    ("wan", "attn.self", "mx"): 3_355_200_000,
 }
 
 
@@ -130,8 +143,9 @@ class Flux:
     name = "flux"
     kinds = ("bf16", "fp8")
     img_hw, txt = (64, 64), 512
-    dominant = "gemm.single.w1"
-    dominant_desc = "single-block input GEMM (4608 x 21504 x 3072, GELU epilogue)"
+    desc = {"gemm.single.w1": "single-block input GEMM (4608 x 21504 x 3072; bf16: GELU epilogue)",
+            "gemm.single.w2": "single-block output GEMM (4608 x 3072 x 15360, gated residual)",
+            "attn": "joint attention (24 heads x 4608 queries x 4608 keys x 128, bf16)"}
     config = {"workload": "FLUX.1-dev-shaped DiT denoise step, 1024x1024 image (64x64 patches "
                           "= 4096 tokens) + 512 text tokens, 19 double + 38 single blocks, "
                           "hidden 3072, 24 x 128 heads",
@@ -184,8 +198,7 @@ class Qwen:
     name = "qwen"
     kinds = ("mx", "bf16")
     img_hw, txt = (83, 83), 256
-    dominant = "attn"
-    dominant_desc = "joint attention (24 heads x 7145 queries x 7145 keys x 128, bf16)"
+    desc = {"attn": "joint attention (24 heads x 7145 queries x 7145 keys x 128, bf16)"}
     config = {"workload": "Qwen-Image-shaped MMDiT denoise step, 1328x1328 image (83x83 patches "
                           "= 6889 tokens) + 256 text tokens, 60 joint blocks, hidden 3072, "
                           "24 x 128 heads, MLP 12288",
@@ -233,8 +246,7 @@ class Wan:
     name = "wan"
     kinds = ("bf16", "mx")
     latent_fhw, txt = (21, 60, 104), 512
-    dominant = "attn.self"
-    dominant_desc = "self-attention (40 heads x 32760 queries x 32760 keys x 128, bf16)"
+    desc = {"attn.self": "self-attention (40 heads x 32760 queries x 32760 keys x 128, bf16)"}
     config = {"workload": "Wan-2.2-14B-shaped video DiT denoise step, 480x832x81 frames -> "
                           "latent 21x60x104, patch (1, 2, 2) = 32760 video tokens + 512 text "
                           "tokens, 40 blocks, hidden 5120, 40 x 128 heads, FFN 13824",
@@ -301,7 +313,17 @@ def run_kind(wl, kind, steps, warmup, torch, log):
         raise RuntimeError(f"[{wl.name}/{kind}] non-finite output")
     log(f"[{wl.name}/{kind}] warmup done")
 
-    probe = Probe(only={wl.dominant})
+    # one step with every GEMM / attention launch probed: per-kernel times (attn_gemm) and the
+    # dominant kernel, the launch name with the largest summed time
+    full = Probe()
+    model.probe = full
+    step()
+    torch.cuda.synchronize()
+    model.probe = None
+    by_name = full.times_ms()
+    dominant = max(by_name, key=lambda n: sum(by_name[n]))
+
+    probe = Probe(only={dominant})
     model.probe = probe
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(steps)]
@@ -315,20 +337,13 @@ def run_kind(wl, kind, steps, warmup, torch, log):
     wall_ms = (time.perf_counter() - t_wall) * 1e3 / steps
     model.probe = None
     per_step = sorted(s.elapsed_time(e) for s, e in evs)
-    dom = probe.times_ms()[wl.dominant]
+    dom = probe.times_ms()[dominant]
     log(f"[{wl.name}/{kind}] {steps} steps: mean {sum(per_step) / steps:.2f} ms, "
-        f"wall {wall_ms:.2f} ms")
-
-    # one more step with every GEMM / attention launch probed
-    full = Probe()
-    model.probe = full
-    step()
-    torch.cuda.synchronize()
-    model.probe = None
-    by_name = full.times_ms()
+        f"wall {wall_ms:.2f} ms; dominant kernel {dominant}")
     del model
     torch.cuda.empty_cache()
-    return {"per_step": per_step, "wall_ms": wall_ms, "dominant_ms": dom, "by_name": by_name}
+    return {"per_step": per_step, "wall_ms": wall_ms, "dominant": dominant, "dominant_ms": dom,
+            "by_name": by_name}
 
 
 def summarize(wl, kind, r):
@@ -337,10 +352,10 @@ def summarize(wl, kind, r):
     # attn+GEMM: roofline time of their FLOPs at MFMA peak / their measured kernel time
     t_meas = sum(sum(v) for v in r["by_name"].values()) * 1e-3
     t_roof = sum(fl[n] * len(v) / wl.peak(n, kind) for n, v in r["by_name"].items())
-    dom = r["dominant_ms"]
+    dom, dname = r["dominant_ms"], r["dominant"]
     dom_avg = sum(dom) / len(dom)
-    peak = wl.peak(wl.dominant, kind)
-    achieved = fl[wl.dominant] / (dom_avg * 1e-3) / 1e12
+    peak = wl.peak(dname, kind)
+    achieved = fl[dname] / (dom_avg * 1e-3) / 1e12
     per_kernel = {n: {"launches": len(v), "avg_ms": round(sum(v) / len(v), 4),
                       "tflops": round(fl[n] / (sum(v) / len(v) * 1e-3) / 1e12, 1)}
                   for n, v in sorted(r["by_name"].items())}
@@ -354,7 +369,8 @@ def summarize(wl, kind, r):
         "attn_gemm_kernel_ms": round(t_meas * 1e3, 3),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak / 1e12,
                      "unit": "TFLOP/s", "frac": round(achieved * 1e12 / peak, 4),
-                     "traffic": TRAFFIC.get((wl.name, kind)), "kernel": wl.dominant_desc,
+                     "traffic": TRAFFIC.get((wl.name, dname, kind)),
+                     "kernel": wl.desc.get(dname, dname),
                      "avg_ms": round(dom_avg, 4), "launches_timed": len(dom)},
         "kernels": per_kernel,
     }
