@@ -54,7 +54,8 @@ int difflet_rocm_device_count(void);
  * semantics are the CPU oracle's, difflet/backends/cpu/ops_impl/attention.py:8-48:
  *   out = softmax(q k^T * scale [+ mask]) v, softmax in fp32, output in v's dtype.
  * q: [batch, heads, seq_q, head_dim] addressed by strides {b, h, s}; k, v: [.., seq_k, ..];
- * o: like q. head_dim must be 128; dtype BF16 or F16.
+ * o: like q. head_dim 64 or 128; dtype BF16 or F16 (matrix-core kernels) or F32 (a VALU
+ * kernel, one query per lane).
  * causal: key j > query i is masked. mask: optional, [batch, heads, seq_q, seq_k] through
  * strides (0 broadcasts); BOOL (nonzero attends) or F32/BF16/F16 additive. bound_min /
  * bound_max: optional int32 [batch, heads, seq_q] through strides; keys in [min, max) attend
