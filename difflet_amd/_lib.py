@@ -84,6 +84,9 @@ SIGNATURES: dict[str, tuple] = {
                                        _i64, _vp, _i64, ctypes.POINTER(GemmQk), _vp]),
     "difflet_rocm_gemm_schedule_check": (_i32, [_i32, _i32, _i32, _i32, _i64,
                                                 ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
+    "difflet_rocm_attention_schedule_check": (_i32, [_i64, _i32, _i32, _i64,
+                                                     ctypes.POINTER(_i32),
+                                                     ctypes.POINTER(_i32)]),
     "difflet_rocm_quantize_fp8_rowwise": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _vp,
                                                  _vp]),
     "difflet_rocm_quantize_fp8_rowwise_gelu": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64,

@@ -63,10 +63,11 @@ int difflet_rocm_device_count(void);
  * finite value, so a fully masked row averages v exactly as the reference does.
  * workspace / workspace_bytes: optional device memory for the split schedule of unmasked
  * attention over more than 1024 keys. When the launch's 256-query tiles would leave the last
- * wave of workgroups under 90 % full, one workgroup per compute unit takes an equal range of
- * (query tile, key tile) units and query tiles cut between workgroups are merged, in a fixed
- * order, by the last contributor (a deterministic result; the summation order differs from the
- * unsplit one by fp32 rounding). With workspace NULL or too small every query tile runs whole.
+ * wave of workgroups under 90 % full, one workgroup per compute unit runs the last round's
+ * query tiles cut along the keys over lockstep sets of workgroups (the workgroups of a set read
+ * the same key tiles together), then the full rounds of whole tiles; query tiles cut
+ * between sets are merged, in a fixed order, by the last contributor (a deterministic result;
+ * the summation order differs from the unsplit one by fp32 rounding). With workspace NULL or too small every query tile runs whole.
  * The workspace must be zero-filled once when allocated (the kernels leave it zeroed), and
  * launches that may overlap in time must not share one.
  * ---------------------------------------------------------------------------------------- */
@@ -83,6 +84,14 @@ int difflet_rocm_attention(const void* q, const void* k, const void* v, void* o,
  * counters + 2 x 132 KiB per compute unit (0 without a device). No counterpart in the
  * reference, whose attention calls torch's SDPA (difflet/backends/cuda/ops_impl/attention.py:41-86). */
 int64_t difflet_rocm_attention_workspace_bytes(void);
+
+/* Host-side check of the attention's split schedule for `tiles` query tiles of `key_tiles` key
+ * tiles on `cus` compute units with `workspace_bytes` of workspace: each (query tile, key tile)
+ * runs on exactly one workgroup, and cut tiles are merged from the right contributors and
+ * slots. Returns 0 or the number of the failed check; *dp / *w receive the whole-tile count and
+ * the workgroups per lockstep set (0 and 0: no split). Runs on the CPU only (for tests). */
+int difflet_rocm_attention_schedule_check(int64_t tiles, int key_tiles, int cus,
+                                          int64_t workspace_bytes, int* dp, int* w);
 
 /* difflet_rocm_attention with no workspace argument, allocating nothing: no counterpart in the
  * reference. It is for callers that cannot allocate device memory (code under HIP graph

@@ -113,3 +113,58 @@ def test_gemm_split_plan_at_the_step_shapes():
     assert lib.difflet_rocm_gemm_schedule_check(336, 48, 1, 256, 1 << 20, ctypes.byref(dp),
                                                 ctypes.byref(groups)) == 0
     assert (dp.value, groups.value) == (336, 0)
+
+
+@pytest.mark.parametrize("cus", [256, 304, 80, 32])
+def test_attention_split_schedule_covers_every_unit_once(cus):
+    """The attention's split schedule (whole rounds, then lockstep sets over the cut tiles),
+    walked on the host with the kernel's own functions: every (query tile, key tile) runs
+    exactly once, a cut tile is merged from the sets that hold its key tiles, and no two parts
+    share a workspace slot."""
+    import ctypes
+
+    from difflet_amd import _lib
+
+    lib = _lib.load()
+    ws = 16384 + 2 * cus * (8 * 16 * 1024 + 8 * 64 * 8)
+    dp, w = ctypes.c_int(), ctypes.c_int()
+    split = 0
+    for tiles in list(range(1, 12)) + [cus - 1, cus, cus + 1, cus + 7, 2 * cus - 3, 432, 672,
+                                       1000, 5120, 7 * cus + 5]:
+        for key_tiles in (1, 2, 3, 17, 64, 72, 112, 512):
+            r = lib.difflet_rocm_attention_schedule_check(tiles, key_tiles, cus, ws,
+                                                          ctypes.byref(dp), ctypes.byref(w))
+            assert r == 0, (tiles, key_tiles, r)
+            if w.value:
+                split += 1
+                assert dp.value % cus == 0 and 0 < tiles - dp.value < cus
+                assert (cus // 8) % w.value == 0
+            else:
+                assert dp.value == 0
+    assert split > 20  # the split path is exercised
+
+
+def test_attention_split_plan_at_the_step_shapes():
+    import ctypes
+
+    from difflet_amd import _lib
+
+    lib = _lib.load()
+    ws = 16384 + 2 * 256 * (8 * 16 * 1024 + 8 * 64 * 8)
+    dp, w = ctypes.c_int(), ctypes.c_int()
+    # FLUX 24 heads x 18 query tiles, 72 key tiles: a round of 256 whole tiles, then 176 cut
+    # over 16 sets of 16 (11 groups: 49.5 key tiles per set; sets of 32 would take 54)
+    assert lib.difflet_rocm_attention_schedule_check(432, 72, 256, ws, ctypes.byref(dp),
+                                                     ctypes.byref(w)) == 0
+    assert (dp.value, w.value) == (256, 16)
+    # Qwen-Image 24 x 28 query tiles, 112 key tiles: 160 cut tiles in 5 groups of 32
+    assert lib.difflet_rocm_attention_schedule_check(672, 112, 256, ws, ctypes.byref(dp),
+                                                     ctypes.byref(w)) == 0
+    assert (dp.value, w.value) == (512, 32)
+    # Wan 40 x 128 query tiles fill 20 rounds exactly: no split; nor without the workspace
+    assert lib.difflet_rocm_attention_schedule_check(5120, 512, 256, ws, ctypes.byref(dp),
+                                                     ctypes.byref(w)) == 0
+    assert (dp.value, w.value) == (0, 0)
+    assert lib.difflet_rocm_attention_schedule_check(432, 72, 256, 1 << 20, ctypes.byref(dp),
+                                                     ctypes.byref(w)) == 0
+    assert (dp.value, w.value) == (0, 0)

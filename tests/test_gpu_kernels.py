@@ -486,8 +486,12 @@ def test_attention_matches_fp32(gpu, b, h, sq, sk, dtype):
 
 
 # more 256-query tiles than compute units with a last wave under 90 % full: the split schedule
-# (query tiles cut between workgroups, merged by the last contributor) runs with the workspace
-@pytest.mark.parametrize("b,h,sq,sk", [(1, 24, 4600, 1100), (2, 20, 2048, 2048)])
+# (a round of whole tiles, then the rest cut along the keys over lockstep sets of workgroups and
+# merged by the last contributor) runs with the workspace. On 256 CUs: 432 tiles of 18 key
+# tiles cut 176 in sets of 16; 320 of 32 cut 64 in sets of 32; 300 of 18 cut 44 in sets of 16,
+# the last group holding 12 tiles.
+@pytest.mark.parametrize("b,h,sq,sk", [(1, 24, 4600, 1100), (2, 20, 2048, 2048),
+                                       (1, 25, 3000, 1100)])
 def test_attention_split_schedule_equals_whole_tiles(gpu, b, h, sq, sk):
     print(f"attention split b={b} h={h} sq={sq} sk={sk}", flush=True)
     g = torch.Generator().manual_seed(sq + sk + h)
