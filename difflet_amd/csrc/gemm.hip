@@ -547,7 +547,6 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
   // is all in or all out). Column vectors (bias, gate, W scales) are read once for the whole
   // tile, and each row block's residual is read before any of its stores: the residual may
   // alias C, so loads left between stores would each wait out a full memory latency.
-  const int act_start = args.act_col_start;
   const float* ws = reinterpret_cast<const float*>(P.w_scale);
   // fused q/k RMSNorm + RoPE: this tile's 256 columns are two heads of q or of k; a head's 128
   // columns are the 64 of waves wn = 2 h and 2 h + 1, whose per-row sums of squares meet in LDS
@@ -756,79 +755,219 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
     }
     continue;  // this tile is stored
   }
-  const bf16* bias = P.bias;
-  u32x2 bias_v[4][4], gate_v[4][4];  // [j < TJ][q]
-  f32x4 ws_v[4][4];
-#pragma unroll
-  for (int j = 0; j < TJ; ++j)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int64_t n = n0 + wn * WTN + j * 32 + q * 8 + fhalf * 4;
-      const bool nok = n < N;
-      bias_v[j][q] = (bias && nok) ? *reinterpret_cast<const u32x2*>(bias + n) : u32x2{0u, 0u};
-      if constexpr (E == Elem::FP8)
-        ws_v[j][q] = nok ? *reinterpret_cast<const f32x4*>(ws + n) : f32x4{};
-      if constexpr (EPI == DIFFLET_EPI_GATE_RESIDUAL) {
-        // one gate row per batch element: a wave's 128 rows lie in one batch element, since
-        // the host requires rows_per_batch % 128 == 0 when a problem holds several. A wave whose
-        // rows all lie past M stores nothing; its row is clamped to M - 1 so the gate read stays
-        // within the ceil(M / rows_per_batch) rows the gate holds.
-        const int64_t b0 = min(m0 + wm * 128, (int64_t)M - 1) / P.rows_per_batch;
-        gate_v[j][q] = nok ? *reinterpret_cast<const u32x2*>(P.gate + b0 * P.gate_stride + n)
-                           : u32x2{0u, 0u};
-      }
-    }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t m = m0 + wm * 128 + i * 32 + frow;
-    const bool mok = m < M;
-    const int64_t mc = mok ? m : 0;  // clamped row for address formation
-    float sa = 1.f;
-    if constexpr (E == Elem::FP8) sa = mok ? reinterpret_cast<const float*>(P.a_scale)[mc] : 0.f;
-    bf16* crow = reinterpret_cast<bf16*>(P.c) + mc * P.ldc;
-    u32x2 res_v[4][4];
-    if constexpr (EPI == DIFFLET_EPI_GATE_RESIDUAL) {
-      const bf16* rrow = P.res + mc * P.ldr;
-#pragma unroll
-      for (int j = 0; j < TJ; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int64_t n = n0 + wn * WTN + j * 32 + q * 8 + fhalf * 4;
-          res_v[j][q] = (mok && n < N) ? *reinterpret_cast<const u32x2*>(rrow + n) : u32x2{0u, 0u};
-        }
-    }
-#pragma unroll
+  if constexpr (SPLIT) {
+    // the split schedule's kernels (whose cut-tile state stays live) store straight from the
+    // accumulators: staged through the ring they spilled 140-250 bytes per lane
+    const bf16* bias = P.bias;
+    u32x2 bias_v[4][4], gate_v[4][4];  // [j < TJ][q]
+    f32x4 ws_v[4][4];
+  #pragma unroll
     for (int j = 0; j < TJ; ++j)
-#pragma unroll
+  #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int64_t n = n0 + wn * WTN + j * 32 + q * 8 + fhalf * 4;
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v[e] = acc[i][j][q * 4 + e];
-          if constexpr (E == Elem::FP8) v[e] = v[e] * (sa * ws_v[j][q][e]);
-          v[e] += bf16bits_to_f32(e & 1 ? bias_v[j][q][e >> 1] >> 16
-                                        : bias_v[j][q][e >> 1] & 0xffffu);
-        }
-        if constexpr (EPI == DIFFLET_EPI_GELU) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (n + e >= act_start) v[e] = gelu_tanh(v[e]);
-        } else if constexpr (EPI == DIFFLET_EPI_GATE_RESIDUAL) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t rw_ = res_v[j][q][e >> 1], gw_ = gate_v[j][q][e >> 1];
-            v[e] = bf16bits_to_f32(e & 1 ? rw_ >> 16 : rw_ & 0xffffu) +
-                   bf16bits_to_f32(e & 1 ? gw_ >> 16 : gw_ & 0xffffu) * v[e];
-          }
-        }
-        if (mok && n < N) {
-          u32x2 o;
-          o[0] = pack_bf16x2(v[0], v[1]);
-          o[1] = pack_bf16x2(v[2], v[3]);
-          *reinterpret_cast<u32x2*>(crow + n) = o;
+        const bool nok = n < N;
+        bias_v[j][q] = (bias && nok) ? *reinterpret_cast<const u32x2*>(bias + n) : u32x2{0u, 0u};
+        if constexpr (E == Elem::FP8)
+          ws_v[j][q] = nok ? *reinterpret_cast<const f32x4*>(ws + n) : f32x4{};
+        if constexpr (EPI == DIFFLET_EPI_GATE_RESIDUAL) {
+          // one gate row per batch element: a wave's 128 rows lie in one batch element, since
+          // the host requires rows_per_batch % 128 == 0 when a problem holds several. A wave whose
+          // rows all lie past M stores nothing; its row is clamped to M - 1 so the gate read stays
+          // within the ceil(M / rows_per_batch) rows the gate holds.
+          const int64_t b0 = min(m0 + wm * 128, (int64_t)M - 1) / P.rows_per_batch;
+          gate_v[j][q] = nok ? *reinterpret_cast<const u32x2*>(P.gate + b0 * P.gate_stride + n)
+                             : u32x2{0u, 0u};
         }
       }
+  #pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t m = m0 + wm * 128 + i * 32 + frow;
+      const bool mok = m < M;
+      const int64_t mc = mok ? m : 0;  // clamped row for address formation
+      float sa = 1.f;
+      if constexpr (E == Elem::FP8) sa = mok ? reinterpret_cast<const float*>(P.a_scale)[mc] : 0.f;
+      bf16* crow = reinterpret_cast<bf16*>(P.c) + mc * P.ldc;
+      u32x2 res_v[4][4];
+      if constexpr (EPI == DIFFLET_EPI_GATE_RESIDUAL) {
+        const bf16* rrow = P.res + mc * P.ldr;
+  #pragma unroll
+        for (int j = 0; j < TJ; ++j)
+  #pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int64_t n = n0 + wn * WTN + j * 32 + q * 8 + fhalf * 4;
+            res_v[j][q] = (mok && n < N) ? *reinterpret_cast<const u32x2*>(rrow + n) : u32x2{0u, 0u};
+          }
+      }
+  #pragma unroll
+      for (int j = 0; j < TJ; ++j)
+  #pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t n = n0 + wn * WTN + j * 32 + q * 8 + fhalf * 4;
+          float v[4];
+  #pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[e] = acc[i][j][q * 4 + e];
+            if constexpr (E == Elem::FP8) v[e] = v[e] * (sa * ws_v[j][q][e]);
+            v[e] += bf16bits_to_f32(e & 1 ? bias_v[j][q][e >> 1] >> 16
+                                          : bias_v[j][q][e >> 1] & 0xffffu);
+          }
+          {
+  #pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t rw_ = res_v[j][q][e >> 1], gw_ = gate_v[j][q][e >> 1];
+              v[e] = bf16bits_to_f32(e & 1 ? rw_ >> 16 : rw_ & 0xffffu) +
+                     bf16bits_to_f32(e & 1 ? gw_ >> 16 : gw_ & 0xffffu) * v[e];
+            }
+          }
+          if (mok && n < N) {
+            u32x2 o;
+            o[0] = pack_bf16x2(v[0], v[1]);
+            o[1] = pack_bf16x2(v[2], v[3]);
+            *reinterpret_cast<u32x2*>(crow + n) = o;
+          }
+        }
+    }
+    continue;  // this tile is stored
+  }
+  // ---- gate * (acc + bias) + residual (EPI_GATE_RESIDUAL) through the LDS ring, one row half
+  // (128 rows) at a time: the fp32 values of a 128 x 256 half tile fill the 128 KB ring. The 4
+  // waves of row half p write y = acc (* a_scale * w_scale) + bias in fp32 as [128 rows][64
+  // chunks of 16 bytes], chunk c of row r at c ^ (r & 63) (conflict-free both ways), then each
+  // of their half-waves takes 16 rows of the half, reads 8 columns per lane and stores 16 bytes
+  // per lane, 512 contiguous bytes per row; the other half's waves wait (their accumulators
+  // stay live, the writers' are dead once staged, which leaves registers for the residual
+  // rows). The math is the direct store's: fp32 y, fp32 res + gate * y, one bf16 rounding. A
+  // half-wave loads its residual rows before it stores any of them (the residual may alias C;
+  // each row is read and written by the same half-wave), the first RB of them before the
+  // staging so that their latency overlaps it. Stored straight from the accumulators, each wave
+  // instruction touched 32 rows x 8 bytes, and this epilogue cost 10-15 us per launch at
+  // 4608 x 3072.
+  {
+    float* yt = reinterpret_cast<float*>(lds);
+    const int ch = lane & 31, half = lane >> 5;  // 8-column chunk of a row, which row of two
+    const int64_t n = n0 + ch * 8;
+    const bool nin = n < N, nfull = n + 8 <= N;  // N % 4 == 0: a chunk is full or half full
+    const bool wide_c = (((uintptr_t)P.c & 15) == 0) && (P.ldc % 8 == 0);
+    const bool wide_r = (((uintptr_t)P.res & 15) == 0) && (P.ldr % 8 == 0);
+    constexpr int RPH = 128 / (2 * WN_WAVES), RB = 4;  // rows per half-wave of the half
+    const int hr = wn * 2 + half;                         // this half-wave's first row
+    const int64_t mh = m0 + wm * 128;                     // first row of this wave's half
+    auto load8 = [&](const bf16* src, bool wide) {  // 8 bf16 (4 when only half the chunk is in)
+      if (wide && nfull) return *reinterpret_cast<const u32x4*>(src);
+      u32x4 v = {0u, 0u, 0u, 0u};
+      const u32x2 lo = *reinterpret_cast<const u32x2*>(src);
+      v[0] = lo[0];
+      v[1] = lo[1];
+      if (nfull) {
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 4);
+        v[2] = hi[0];
+        v[3] = hi[1];
+      }
+      return v;
+    };
+    auto load_res = [&](int t) {  // residual row t of this half-wave (t < RPH)
+      const int64_t m = mh + hr + t * 2 * WN_WAVES;
+      return (m < M && nin) ? load8(P.res + m * P.ldr + n, wide_r) : u32x4{0u, 0u, 0u, 0u};
+    };
+    auto stage = [&]() {
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        u32x2 bv[4];
+        f32x4 wv[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t nc = n0 + wn * WTN + j * 32 + q * 8 + fhalf * 4;
+          const bool nok = nc < N;
+          bv[q] = (P.bias && nok) ? *reinterpret_cast<const u32x2*>(P.bias + nc) : u32x2{0u, 0u};
+          if constexpr (E == Elem::FP8)
+            wv[q] = nok ? *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(P.w_scale) + nc)
+                        : f32x4{};
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = i * 32 + frow;  // row within the half
+          float sa = 1.f;
+          if constexpr (E == Elem::FP8)
+            sa = mh + r < M ? reinterpret_cast<const float*>(P.a_scale)[mh + r] : 0.f;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int cl = wn * WTN + j * 32 + q * 8 + fhalf * 4;  // tile column of the 4 values
+            f32x4 y;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float v = acc[i][j][q * 4 + e];
+              if constexpr (E == Elem::FP8) v = v * (sa * wv[q][e]);
+              y[e] = v + bf16bits_to_f32(e & 1 ? bv[q][e >> 1] >> 16 : bv[q][e >> 1] & 0xffffu);
+            }
+            *reinterpret_cast<f32x4*>(yt + r * 256 + (((cl >> 2) ^ (r & 63)) << 2)) = y;
+          }
+        }
+      }
+    };
+    // rows in batches of RB, the next batch's residual loads issued before this batch's math
+    // (the first batch's before the staging)
+    u32x4 cur[RB];
+#pragma unroll
+    for (int t = 0; t < RB; ++t) cur[t] = load_res(t);
+    auto emit = [&]() {
+      // one gate row per batch element: 128 rows lie in one (rows_per_batch % 128 == 0 when a
+      // problem holds several); a half past M stores nothing and reads row M - 1's gate
+      const int64_t b0 = min(mh, (int64_t)M - 1) / P.rows_per_batch;
+      const u32x4 gv = nin ? load8(P.gate + b0 * P.gate_stride + n, false) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll 1
+      for (int t0 = 0; t0 < RPH; t0 += RB) {
+        u32x4 nxt[RB];
+        if (t0 + RB < RPH) {
+#pragma unroll
+          for (int t = 0; t < RB; ++t) nxt[t] = load_res(t0 + RB + t);
+        }
+#pragma unroll
+        for (int t = 0; t < RB; ++t) {
+          const int r = hr + (t0 + t) * 2 * WN_WAVES;  // row within the half
+          const int64_t m = mh + r;
+          if (m >= M || !nin) continue;
+          const f32x4 y0 = *reinterpret_cast<const f32x4*>(yt + r * 256 + (((2 * ch) ^ (r & 63)) << 2));
+          const f32x4 y1 = *reinterpret_cast<const f32x4*>(yt + r * 256 + (((2 * ch + 1) ^ (r & 63)) << 2));
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float y = e < 4 ? y0[e] : y1[e - 4];
+            const uint32_t rw_ = cur[t][e >> 1], gw_ = gv[e >> 1];
+            v[e] = bf16bits_to_f32(e & 1 ? rw_ >> 16 : rw_ & 0xffffu) +
+                   bf16bits_to_f32(e & 1 ? gw_ >> 16 : gw_ & 0xffffu) * y;
+          }
+          u32x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+          bf16* dst = reinterpret_cast<bf16*>(P.c) + m * P.ldc + n;
+          if (wide_c && nfull) {
+            *reinterpret_cast<u32x4*>(dst) = o;
+          } else {
+            *reinterpret_cast<u32x2*>(dst) = u32x2{o[0], o[1]};
+            if (nfull) *reinterpret_cast<u32x2*>(dst + 4) = u32x2{o[2], o[3]};
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < RB; ++t) cur[t] = nxt[t];
+      }
+    };
+    // the same four barriers on both sides: ring free, half 0 staged, half 0 read, half 1 staged
+    if (wm == 0) {
+      __syncthreads();
+      stage();
+      __syncthreads();
+      emit();
+      __syncthreads();
+      __syncthreads();
+    } else {
+      __syncthreads();
+      __syncthreads();
+      __syncthreads();
+      stage();
+      __syncthreads();
+      emit();
+    }
   }
   }  // tiles of this workgroup
 }
