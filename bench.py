@@ -69,17 +69,17 @@ COPY_BYTES = 256 << 20
 # --calibrate-copy 256 MiB copy). MALL hits are counted too, so this bounds HBM bytes from above.
 # Keyed by (workload, probe name, kind); absent -> null.
 TRAFFIC: dict = {
-    # 4608 x 21504 x 3072 GEMM (GELU, fused q/k norm): 1178.9 MB read (A + W = 160 MB once, plus
+    # 4608 x 21504 x 3072 GEMM (GELU, fused q/k norm): 1186.5 MB read (A + W = 160 MB once, plus
     # the RoPE tables) + 198.2 MB written (C)
-    ("flux", "gemm.single.w1", "bf16"): 1_377_100_000,
+    ("flux", "gemm.single.w1", "bf16"): 1_384_700_000,
     # the joint attention, 24 heads x 4608 x 4608 x 128 bf16 on the split schedule (the same
-    # kernel in both steps): 834.2 MB read (q, k, v 84.9 MB once) + 93.2 MB written (the output
-    # 28.3 MB and the cut query tiles' fp32 partials)
-    ("flux", "attn", "fp8"): 927_400_000,
-    ("flux", "attn", "bf16"): 927_400_000,
-    # Qwen-Image's joint attention, 24 heads x 7145 x 7145 x 128: 1976.8 MB read + 104.5 written
-    ("qwen", "attn", "mx"): 2_081_300_000,
-    ("qwen", "attn", "bf16"): 2_081_300_000,
+    # kernel in both steps; cut tiles in lockstep sets of 16 workgroups): 190.8 MB read (q, k, v
+    # 84.9 MB once) + 84.6 MB written (the output 28.3 MB and the cut query tiles' fp32 partials)
+    ("flux", "attn", "fp8"): 275_400_000,
+    ("flux", "attn", "bf16"): 275_400_000,
+    # Qwen-Image's joint attention, 24 heads x 7145 x 7145 x 128: 266.2 MB read + 95.8 written
+    ("qwen", "attn", "mx"): 362_000_000,
+    ("qwen", "attn", "bf16"): 362_000_000,
     # Wan's self-attention, 40 heads x 32760 x 32760 x 128 (one query tile per workgroup, 20
     # waves of workgroups): 3019.7 MB read + 335.5 MB written
     ("wan", "attn.self", "bf16"): 3_355_200_000,
