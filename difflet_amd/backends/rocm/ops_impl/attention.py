@@ -14,8 +14,11 @@ attention.py:8-48; the CUDA twin difflet/backends/cuda/ops_impl/attention.py:41-
 
 The kernels run bf16 and fp16 on the matrix cores and fp32 on the vector ALUs (an fp32 model
 computes in fp32, as the reference's CPU op does), at head_dim 128 (the DiTs) or 64 (the T5 /
-UMT5 text encoders); other dtypes / head dims raise NotImplementedError (no silent fallback to
-another implementation).
+UMT5 text encoders). Any other head_dim up to 128 runs on the same kernels with q, k and v
+zero-padded to the next of those two: the padded dimensions add exact zeros to every score and
+give zero output columns, which are cut off, so the result is the unpadded attention's (the
+scale is the caller's, never derived from the padded width). Other dtypes and head_dim above
+128 raise NotImplementedError (no silent fallback to another implementation).
 
 The context-parallel forms run their cp = 1 degenerate case (plain attention over the local,
 here whole, sequence: difflet/backends/cpu/ops_impl/attention.py:55-143); cp > 1 raises.
@@ -28,7 +31,22 @@ import torch
 from difflet_amd.backends.rocm.ops_impl import library
 
 _SUPPORTED = (torch.bfloat16, torch.float16, torch.float32)
-_HEAD_DIMS = (64, 128)
+_HEAD_DIMS = (64, 128)  # the kernels' own; others up to 128 are zero-padded to one of them
+
+
+def kernel_head_dim(d: int) -> int:
+    """The kernel head_dim that head_dim d runs at: d itself for 64 and 128, else the next of
+    the two (d <= 128); NotImplementedError above 128."""
+    if d in _HEAD_DIMS:
+        return d
+    if 0 < d <= 128:
+        return 64 if d < 64 else 128
+    raise NotImplementedError(f"rocm attention supports head_dim up to 128, got {d}")
+
+
+def pad_head_dim(t: torch.Tensor, width: int) -> torch.Tensor:
+    """t with its last dimension zero-padded to `width` (a new contiguous tensor)."""
+    return torch.nn.functional.pad(t, (0, width - t.shape[-1])).contiguous()
 
 
 def _check(q, k, v):
@@ -38,8 +56,9 @@ def _check(q, k, v):
     if q.dtype not in _SUPPORTED:
         raise NotImplementedError(
             f"rocm attention runs bf16 / fp16 / fp32 on the HIP kernels; got {q.dtype}")
-    if q.shape[-1] not in _HEAD_DIMS:
-        raise NotImplementedError(f"rocm attention supports head_dim 64 and 128, got {q.shape[-1]}")
+    if not (q.shape[-1] == k.shape[-1] == v.shape[-1]):
+        raise ValueError(f"q, k, v head dims differ: {q.shape[-1]}, {k.shape[-1]}, {v.shape[-1]}")
+    kernel_head_dim(q.shape[-1])
 
 
 def attention(q, k, v, *, scale: float | None = None, causal: bool = False,
@@ -54,6 +73,12 @@ def attention(q, k, v, *, scale: float | None = None, causal: bool = False,
     scale = 1.0 if scale is None else float(scale)
     if attention_mask is not None and attention_mask.dtype not in (torch.bool,) + _SUPPORTED:
         attention_mask = attention_mask.to(q.dtype)
+    d = q.shape[-1]
+    dk = kernel_head_dim(d)
+    if dk != d:
+        q, k, v = (pad_head_dim(t, dk) for t in (q, k, v))
+        out = library.attention(q, k, v, scale, bool(causal), attention_mask, bound_min, bound_max)
+        return out[..., :d]
     return library.attention(q, k, v, scale, bool(causal), attention_mask, bound_min, bound_max)
 
 

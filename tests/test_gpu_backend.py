@@ -53,6 +53,38 @@ def test_ops_attention_forms(gpu):
         A.attention(q.double().to(gpu), k.double().to(gpu), v.double().to(gpu))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("d", [32, 40, 80, 96, 120])
+def test_ops_attention_other_head_dims(gpu, dtype, d):
+    """head_dim other than 64 / 128 (the reference op takes any): q, k, v zero-padded to the
+    kernel's width, the output cut back, against the fp32 attention of the oracle, with a bool
+    mask, per-query bounds and causal masking too; the scale is the caller's."""
+    from difflet_amd.backends.rocm.ops_impl import attention as A
+
+    print(f"attention head_dim {d} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(d)
+    q, k, v = (torch.randn(2, 3, 150, d, generator=g).to(dtype) for _ in range(3))
+    qf, kf, vf = q.float(), k.float(), v.float()
+    sc = 1 / math.sqrt(d)
+    tol = 1e-4 if dtype == torch.float32 else 1e-2
+    G = lambda t: t.to(gpu)  # noqa: E731
+    out = A.attention(G(q), G(k), G(v), scale=sc)
+    assert out.shape == q.shape and out.dtype == dtype
+    assert rel_l2(out, ops.attention(qf, kf, vf, scale=sc)) < tol
+    mask = torch.rand(2, 1, 150, 150, generator=g) > 0.3
+    assert rel_l2(A.attention(G(q), G(k), G(v), scale=sc, attention_mask=G(mask)),
+                  ops.attention(qf, kf, vf, scale=sc, attention_mask=mask)) < tol
+    lo = torch.randint(0, 40, (2, 3, 150, 1), generator=g)
+    hi = lo + torch.randint(1, 110, (2, 3, 150, 1), generator=g)
+    assert rel_l2(A.attention(G(q), G(k), G(v), scale=sc, bound_min=G(lo.int()), bound_max=G(hi.int())),
+                  ops.attention(qf, kf, vf, scale=sc, bound_min=lo, bound_max=hi)) < tol
+    assert rel_l2(A.attention(G(q), G(k), G(v), scale=sc, causal=True),
+                  ops.attention(qf, kf, vf, scale=sc, causal=True)) < tol
+    with pytest.raises(NotImplementedError):
+        A.attention(G(q.new_zeros(1, 1, 4, 160)), G(q.new_zeros(1, 1, 4, 160)),
+                    G(q.new_zeros(1, 1, 4, 160)))
+
+
 @pytest.mark.parametrize("m,k,n", [(3, 3072, 500), (300, 256, 128), (77, 100, 30)])
 def test_ops_linear_modules(gpu, m, k, n):
     from difflet_amd.backends.rocm.ops_impl import linear as L

@@ -164,3 +164,26 @@ def test_model_output_has_sample_and_indexes_like_a_tuple():
     t = torch.ones(2)
     out = model_output(t)
     assert out.sample is t and out[0] is t
+
+
+def test_attention_head_dim_padding_law():
+    """Other head dims run the 64 / 128 kernels on zero-padded q, k, v: the padded dimensions
+    add exact zeros to every score and give zero output columns, so padding then cutting the
+    output back is the unpadded attention (checked here with the fp32 oracle on the CPU)."""
+    from difflet_amd.backends.rocm.ops_impl.attention import kernel_head_dim, pad_head_dim
+    from oracle import ops
+
+    assert [kernel_head_dim(d) for d in (8, 40, 63, 64, 65, 96, 127, 128)] == \
+        [64, 64, 64, 64, 128, 128, 128, 128]
+    for bad in (0, 129, 256):
+        with pytest.raises(NotImplementedError):
+            kernel_head_dim(bad)
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(1, 2, 33, 40, generator=g) for _ in range(3))
+    sc = 40 ** -0.5
+    ref = ops.attention(q, k, v, scale=sc)
+    qp, kp, vp = (pad_head_dim(t, 64) for t in (q, k, v))
+    assert qp.shape[-1] == 64 and torch.equal(qp[..., 40:], torch.zeros_like(qp[..., 40:]))
+    out = ops.attention(qp, kp, vp, scale=sc)
+    assert torch.equal(out[..., 40:], torch.zeros_like(out[..., 40:]))
+    assert torch.allclose(out[..., :40], ref, atol=1e-6, rtol=1e-6)
