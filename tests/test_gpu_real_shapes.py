@@ -231,6 +231,63 @@ def test_wan_gemms_at_32760_rows(gpu, parity, name, n, k, kind, epi):
     assert e < 4e-3  # one bf16 rounding of the output
 
 
+# Full-depth Qwen-Image bounds, from the measured figures with a margin of about 1.45 (as for FLUX
+# above): bf16 against the fp32 oracle 2.05e-2 over the 60 blocks (5.6e-3 over 2, test_gpu_qwen.py:
+# the bf16 roundings of the residual stream and the modulation vectors, again not a random walk,
+# which would give 3.1e-2); MXFP8 against the same fp32 oracle is the format's own error (per
+# block 4.6e-2, equal to the same-law oracle's, test_gpu_qwen.py), 1.00e-1 over the 60 blocks.
+QWEN_FULL_BF16_TOL, QWEN_FULL_MX_TOL = 3e-2, 0.15
+
+
+@pytest.mark.timeout(900)
+def test_qwen_full_depth_step_matches_the_oracle(gpu, parity):
+    """Qwen-Image 1328^2 (6889 image + 256 text tokens, 60 joint blocks) with random-init weights
+    drawn on the device: bf16 and MXFP8 steps, each finite and bit-identical on a rerun, against
+    the oracle's fp32 forward over the same weights (fetched to the host one block at a time)
+    and the same bf16-rounded inputs."""
+    from difflet_amd.dit.qwen import QwenConfig, QwenImageDiT, qwen_param_shapes, random_param_source
+    from oracle import qwen as oqwen
+
+    torch.set_num_threads(16)
+    cfg = QwenConfig()
+    get = random_param_source(cfg, SEED, gpu)
+    g = torch.Generator().manual_seed(SEED)
+    lat = torch.randn(1, 6889, 64, generator=g).bfloat16().float()
+    text = torch.randn(1, 256, 3584, generator=g).bfloat16().float()
+    t = torch.rand(1, generator=g)
+    outs = {}
+    for kind in ("bf16", "mx"):
+        print(f"qwen full step {kind}", flush=True)
+        model = QwenImageDiT(cfg, get, kind=kind, device=gpu)
+        a, b = _twice(lambda: model.forward(lat.to(gpu), text.to(gpu), t.to(gpu), (83, 83)))
+        _properties(f"qwen {kind}", a, b, (1, 6889, 64))
+        outs[kind] = a.float().cpu()
+        del model, a, b
+        torch.cuda.empty_cache()
+    print("qwen full step: fp32 oracle forward, 60 blocks on the host", flush=True)
+    names = qwen_param_shapes(cfg)
+    host = lambda n: get(n).cpu().float()  # noqa: E731
+    pre = "transformer_blocks."
+    keys = [n[len(pre) + 2:] for n in names if n.startswith(pre + "0.")]
+
+    class Blocks:
+        def __getitem__(self, i):
+            print(f"  oracle block {i}", flush=True)  # progress: a few s of CPU per block
+            return {k: host(f"{pre}{i}.{k}") for k in keys}
+
+    ew = {n: host(n) for n in names if not n.startswith(pre)}
+    ref = oqwen.forward(oqwen.QwenShape(), SEED, lat, text, t, (83, 83), weights=(ew, Blocks()),
+                        model_dtype=torch.bfloat16)
+    e_bf16, e_mx = rel_l2(outs["bf16"], ref), rel_l2(outs["mx"], ref)
+    print(f"qwen 60-block step rel L2 vs fp32 oracle: bf16 {e_bf16:.3e}, mx {e_mx:.3e} "
+          f"(mx vs bf16 {rel_l2(outs['mx'], outs['bf16']):.3e})", flush=True)
+    parity("60-block Qwen-Image 1328^2 step bf16, rel L2 vs fp32 oracle", e_bf16, QWEN_FULL_BF16_TOL)
+    parity("60-block Qwen-Image 1328^2 step MXFP8, format error vs fp32 oracle", e_mx,
+           QWEN_FULL_MX_TOL)
+    assert e_bf16 < QWEN_FULL_BF16_TOL
+    assert e_mx < QWEN_FULL_MX_TOL
+
+
 def test_qwen_full_step_60_blocks_mxfp8(gpu):
     """Qwen-Image 1328^2 (6889 + 256 tokens, 60 joint blocks) on the MXFP8 targets."""
     from difflet_amd.dit.qwen import QwenConfig, QwenImageDiT, random_param_source
