@@ -49,6 +49,23 @@ def parity(request):
     return record
 
 
+# Long GPU tests (the full-depth steps against the host oracle, minutes of CPU work) report
+# their progress through `progress`, which writes past pytest's output capture, so a quiet
+# (-q) run still shows them advancing.
+@pytest.fixture
+def progress(request):
+    capman = request.config.pluginmanager.getplugin("capturemanager")
+
+    def emit(msg: str) -> None:
+        if capman is None:
+            print(msg, flush=True)
+            return
+        with capman.global_and_fixture_disabled():
+            print(msg, flush=True)
+
+    return emit
+
+
 def pytest_sessionfinish(session, exitstatus):
     path = os.environ.get("DIFFLET_PARITY_LOG")
     if not path or not _PARITY:

@@ -121,7 +121,7 @@ FULL_FP8_TOL = 0.12
 
 
 @pytest.mark.timeout(900)
-def test_flux_full_depth_step_matches_the_oracle(gpu, parity):
+def test_flux_full_depth_step_matches_the_oracle(gpu, parity, progress):
     """FLUX.1-dev 1024^2 (4096 + 512 tokens, 19 double + 38 single blocks) with random-init
     weights drawn on the device: bf16 and per-token fp8 steps, each finite and bit-identical
     on a rerun, against the oracle's fp32 forward over the same weights (fetched to the host one
@@ -140,7 +140,7 @@ def test_flux_full_depth_step_matches_the_oracle(gpu, parity):
     guid = torch.full((1,), 3.5)
     outs = {}
     for kind in ("bf16", "fp8"):
-        print(f"flux full step {kind}", flush=True)
+        progress(f"flux full step {kind}")
         model = FluxDiT(cfg, get, kind=kind, device=gpu)
         a, b = _twice(lambda: model.forward(lat.to(gpu), text.to(gpu), pooled.to(gpu),
                                             t.to(gpu), guid.to(gpu), (64, 64)))
@@ -148,7 +148,7 @@ def test_flux_full_depth_step_matches_the_oracle(gpu, parity):
         outs[kind] = a.float().cpu()
         del model, a, b
         torch.cuda.empty_cache()
-    print("flux full step: fp32 oracle forward, 57 blocks on the host", flush=True)
+    progress("flux full step: fp32 oracle forward, 57 blocks on the host")
     names = flux_param_shapes(cfg)
     host = lambda n: get(n).cpu().float()  # noqa: E731
 
@@ -156,7 +156,7 @@ def test_flux_full_depth_step_matches_the_oracle(gpu, parity):
         keys = [n[len(prefix) + 3:] for n in names if n.startswith(prefix + ".0.")]
 
         def fetch(i):
-            print(f"  oracle {prefix} {i}", flush=True)  # progress: ~1.2 s of CPU per block
+            progress(f"  oracle {prefix} {i}")  # ~1.2 s of CPU per block
             return {k: host(f"{prefix}.{i}.{k}") for k in keys}
 
         return fetch
@@ -240,7 +240,7 @@ QWEN_FULL_BF16_TOL, QWEN_FULL_MX_TOL = 3e-2, 0.15
 
 
 @pytest.mark.timeout(900)
-def test_qwen_full_depth_step_matches_the_oracle(gpu, parity):
+def test_qwen_full_depth_step_matches_the_oracle(gpu, parity, progress):
     """Qwen-Image 1328^2 (6889 image + 256 text tokens, 60 joint blocks) with random-init weights
     drawn on the device: bf16 and MXFP8 steps, each finite and bit-identical on a rerun, against
     the oracle's fp32 forward over the same weights (fetched to the host one block at a time)
@@ -257,14 +257,14 @@ def test_qwen_full_depth_step_matches_the_oracle(gpu, parity):
     t = torch.rand(1, generator=g)
     outs = {}
     for kind in ("bf16", "mx"):
-        print(f"qwen full step {kind}", flush=True)
+        progress(f"qwen full step {kind}")
         model = QwenImageDiT(cfg, get, kind=kind, device=gpu)
         a, b = _twice(lambda: model.forward(lat.to(gpu), text.to(gpu), t.to(gpu), (83, 83)))
         _properties(f"qwen {kind}", a, b, (1, 6889, 64))
         outs[kind] = a.float().cpu()
         del model, a, b
         torch.cuda.empty_cache()
-    print("qwen full step: fp32 oracle forward, 60 blocks on the host", flush=True)
+    progress("qwen full step: fp32 oracle forward, 60 blocks on the host")
     names = qwen_param_shapes(cfg)
     host = lambda n: get(n).cpu().float()  # noqa: E731
     pre = "transformer_blocks."
@@ -272,7 +272,7 @@ def test_qwen_full_depth_step_matches_the_oracle(gpu, parity):
 
     class Blocks:
         def __getitem__(self, i):
-            print(f"  oracle block {i}", flush=True)  # progress: a few s of CPU per block
+            progress(f"  oracle block {i}")  # ~2 s of CPU per block
             return {k: host(f"{pre}{i}.{k}") for k in keys}
 
     ew = {n: host(n) for n in names if not n.startswith(pre)}
