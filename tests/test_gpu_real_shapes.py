@@ -288,6 +288,63 @@ def test_qwen_full_depth_step_matches_the_oracle(gpu, parity, progress):
     assert e_mx < QWEN_FULL_MX_TOL
 
 
+# Full-depth Wan bounds (40 blocks at width 5120 on a 5 x 24 x 26 latent: 780 video tokens, so
+# the host oracle finishes in seconds; the GEMMs at the real 32760 rows are checked above), from
+# the measured figures with a margin of about 1.45: bf16 against the fp32 oracle 1.33e-2 (4.9e-3
+# over 2 blocks, test_gpu_wan.py), MXFP8 against the same oracle 3.29e-2, the format's error on
+# the reference's Wan targets (a block's 1.5e-2, test_gpu_wan.py).
+WAN_FULL_BF16_TOL, WAN_FULL_MX_TOL = 2e-2, 5e-2
+
+
+@pytest.mark.timeout(900)
+def test_wan_full_depth_step_matches_the_oracle(gpu, parity, progress):
+    """Wan 2.2 14B's 40 blocks at full width (5120, 40 x 128 heads, FFN 13824) with random-init
+    weights drawn on the device, on a 5 x 24 x 26 latent (780 video tokens) and 512 text tokens:
+    bf16 and MXFP8 steps, each finite and bit-identical on a rerun, against the oracle's fp32
+    forward over the same weights (fetched one block at a time) and the same bf16 inputs."""
+    from difflet_amd.dit.wan import WanConfig, WanDiT, random_param_source, wan_param_shapes
+    from oracle import wan as owan
+
+    torch.set_num_threads(16)
+    cfg = WanConfig()
+    get = random_param_source(cfg, SEED, gpu)
+    g = torch.Generator().manual_seed(SEED)
+    lat = torch.randn(1, 16, 5, 24, 26, generator=g).bfloat16().float()
+    text = torch.randn(1, 512, 4096, generator=g).bfloat16().float()
+    t = torch.rand(1, generator=g) * 1000
+    outs = {}
+    for kind in ("bf16", "mx"):
+        progress(f"wan full-depth step {kind}")
+        model = WanDiT(cfg, get, device=gpu, kind=kind)
+        a, b = _twice(lambda: model.forward(lat.to(gpu), t.to(gpu), text.to(gpu)))
+        _properties(f"wan {kind}", a, b, (1, 16, 5, 24, 26))
+        outs[kind] = a.float().cpu()
+        del model, a, b
+        torch.cuda.empty_cache()
+    progress("wan full-depth step: fp32 oracle forward, 40 blocks on the host")
+    names = wan_param_shapes(cfg)
+    host = lambda n: get(n).cpu().float()  # noqa: E731
+    pre = "blocks."
+    keys = [n[len(pre) + 2:] for n in names if n.startswith(pre + "0.")]
+
+    class Blocks:
+        def __getitem__(self, i):
+            progress(f"  oracle block {i}")
+            return {k: host(f"{pre}{i}.{k}") for k in keys}
+
+    ew = {n: host(n) for n in names if not n.startswith(pre)}
+    ref = owan.forward(owan.WanShape(), SEED, lat, t, text, weights=(ew, Blocks()),
+                       model_dtype=torch.bfloat16)
+    e_bf16, e_mx = rel_l2(outs["bf16"], ref), rel_l2(outs["mx"], ref)
+    progress(f"wan 40-block step rel L2 vs fp32 oracle: bf16 {e_bf16:.3e}, mx {e_mx:.3e} "
+             f"(mx vs bf16 {rel_l2(outs['mx'], outs['bf16']):.3e})")
+    parity("40-block Wan step (780 tokens) bf16, rel L2 vs fp32 oracle", e_bf16, WAN_FULL_BF16_TOL)
+    parity("40-block Wan step (780 tokens) MXFP8, format error vs fp32 oracle", e_mx,
+           WAN_FULL_MX_TOL)
+    assert e_bf16 < WAN_FULL_BF16_TOL
+    assert e_mx < WAN_FULL_MX_TOL
+
+
 def test_qwen_full_step_60_blocks_mxfp8(gpu):
     """Qwen-Image 1328^2 (6889 + 256 tokens, 60 joint blocks) on the MXFP8 targets."""
     from difflet_amd.dit.qwen import QwenConfig, QwenImageDiT, random_param_source
