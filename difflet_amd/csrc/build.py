@@ -23,7 +23,7 @@ LIB_NAME = "libdifflet_rocm.so"
 LIB_PATH = PKG / LIB_NAME
 OBJ_DIR = REPO / "_build" / "difflet_rocm"
 SOURCES = ("runtime.hip", "elementwise.hip", "gemm.hip", "gemm_f32.hip", "attention.hip",
-           "quant.hip", "vae.hip")
+           "quant.hip", "vae.hip", "conv.hip")
 ARCH = "gfx950"
 
 # -packed-fp32-ops off: hipcc must not form v_pk_{add,mul,fma}_f32 on its own.

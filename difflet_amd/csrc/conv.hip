@@ -1,0 +1,394 @@
+// The Wan VAE decoder's causal convolutions as implicit GEMMs on the bf16 matrix cores: the GEMM
+// of the im2col rows with the packed weight, where each K stage gathers its 64 columns of the
+// im2col rows straight from the channels-last frames into the LDS, so the rows (27 C columns
+// per output pixel) are never written to memory.
+//
+// The convolution is WanCausalConv3d (difflet/models/wan/vae/modeling_vae.py:95-134: kernel
+// (kt, ks, ks), kt - 1 frames of zero or cached padding in front, ks / 2 pixels around) and the
+// resampler's per-frame nn.Conv2d(3, padding=1) after a nearest 2x upsampling (:163-226). Column
+// k of an output pixel's row is tap (dt, ky, kx) = k / C and channel k % C, taps in (dt, ky, kx)
+// order, the weight's layout [Cout][kt][ks][ks][C] (zero past kt ks^2 C).
+//
+// Tiles: 8 waves, WMW along the output pixels and 8 / WMW along the output channels, each wave 64
+// pixels x 32 NJ channels (2 x NJ MFMA 32x32x16 tiles). Cout <= 96 runs one channel tile of
+// 32 NJ with 512 pixels (the 96-channel full-resolution stage: no MFMA column wasted); wider
+// convolutions run 256 x 192 tiles. A stage is 64 K elements (128 bytes) of every row, staged
+// by direct-to-LDS buffer loads in two LDS slots, 8 rows x 128 B per load instruction, chunk c
+// of row r at c ^ swz8(r) as in the GEMM kernel. Each lane's 16-byte chunk of an A row is 8
+// channels of one tap of one pixel (C is a multiple of 8), so its address is the pixel's shifted
+// position in its frame: out-of-frame taps, padding columns and rows past the end take an
+// offset past the buffer, which the load's range check turns into zeros.
+
+#include "common.hpp"
+
+namespace dlt {
+namespace {
+
+// q = n / d and r = n % d for n < 2^32 from m = min(floor(2^32 / d), 2^32 - 1): the high word of
+// n m is floor(n / d) or one less (n (2^32 mod d) / (d 2^32) < 1), which one compare fixes.
+__device__ __forceinline__ uint32_t udiv(uint32_t n, uint32_t d, uint32_t m, uint32_t& r) {
+  uint32_t q = __umulhi(n, m);
+  r = n - q * d;
+  if (r >= d) {
+    ++q;
+    r -= d;
+  }
+  return q;
+}
+
+__device__ __forceinline__ int swz8(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+__device__ __forceinline__ int lds_off8(int row, int chunk) {
+  return row * 128 + ((chunk ^ swz8(row)) << 4);
+}
+
+}  // namespace
+
+struct ConvArgs {
+  const uint8_t* x;  // the input frames, x_bytes long
+  const uint8_t* w;  // [n][kpad] bf16
+  const bf16* bias;  // [n] or null
+  const bf16* res;   // [rows][ldr] or null
+  bf16* out;         // [rows][ldo]
+  uint32_t x_bytes;
+  uint32_t rows;                 // output pixels: frames x ho x wo
+  uint32_t fstride_b, sub_b, ld_b;  // frame-block, sub-frame and pixel strides of x, bytes
+  int lfpb;                      // log2 of frames per block
+  int fbase;                     // buffer frame of output frame t's tap dt: t + dt + fbase
+  int w_in, ho, wo, up, half, ks;
+  uint32_t po, po_m, wo_m;       // pixels per output frame; magic numbers of po and wo
+  uint32_t cin, cin_m;
+  int ktot, nk;                  // kt ks^2 C; K stages (kpad / 64)
+  int n;                         // output channels (weight rows)
+  uint32_t ldw_b;                // weight row bytes
+  int64_t ldr, ldo;
+  int tiles_n, tiles;
+};
+
+constexpr uint32_t kOutside = 0x80000000u;  // an offset past every buffer (x_bytes < 2^31)
+
+template <int WMW, int NJ>
+__global__ __launch_bounds__(512, 1) void conv_igemm_kernel(const ConvArgs a) {
+  constexpr int WNW = 8 / WMW;
+  constexpr int BM = 64 * WMW, BN = 32 * NJ * WNW;
+  constexpr int SA = BM / 64;  // A slabs (8 rows x 128 B) per wave and stage
+  constexpr int SW = BN / 8;   // W slabs per stage, wave w taking w, w + 8, ...
+  constexpr int NWJ = (SW + 7) / 8;
+  constexpr int SLOT = (BM + BN) * 128;
+  static_assert(SA % 2 == 0 && SA <= 8 && NWJ <= 3 && NJ <= 3 && 2 * SLOT <= 160 * 1024,
+                "tile does not fit the LDS");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * SLOT];
+  typedef __attribute__((address_space(3))) void lds_void;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % WMW, wn = wave / WMW;
+
+  // workgroups go round-robin over the 8 XCDs: give each XCD a contiguous run of tiles, so the
+  // pixels it convolves at once (and their neighbours the taps read) share its L2
+  int tile;
+  {
+    const int bid = blockIdx.x, per = a.tiles >> 3, rem = a.tiles & 7, xc = bid & 7, i = bid >> 3;
+    tile = xc < rem ? xc * (per + 1) + i : rem * (per + 1) + (xc - rem) * per + i;
+  }
+  const int tm = tile / a.tiles_n, tn = tile - tm * a.tiles_n;
+  const uint32_t m0 = (uint32_t)tm * BM;
+  const int n0 = tn * BN;
+
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes);
+  const __amdgpu_buffer_rsrc_t rw =
+      make_rsrc(a.w + (int64_t)n0 * a.ldw_b, (uint32_t)(a.n - n0) * a.ldw_b);
+
+  // A load i of this lane fills row (wave SA + i) 8 + lane / 8 of the stage, physical chunk
+  // lane % 8, i.e. logical chunk lc0 ^ (i & 1): its output pixel (frame, y, x), y far outside
+  // the frame past the last row
+  const int lc0 = (lane & 7) ^ (lane >> 3);
+  // arrays whose elements reach target builtins are sized for the largest tile, not by SA, NWJ
+  // or NJ: with a template-dependent size the host pass drops the kernel's launch stub
+  int rt[8], ry[8], rxp[8];
+#pragma unroll
+  for (int i = 0; i < SA; ++i) {
+    const uint32_t R = m0 + (uint32_t)((wave * SA + i) * 8 + (lane >> 3));
+    uint32_t p, xx;
+    const uint32_t t = udiv(R, a.po, a.po_m, p);
+    const uint32_t y = udiv(p, (uint32_t)a.wo, a.wo_m, xx);
+    const bool in = R < a.rows;
+    rt[i] = (int)t;
+    ry[i] = in ? (int)y : -(1 << 24);
+    rxp[i] = (int)xx;
+  }
+  uint32_t w_off[3];
+#pragma unroll
+  for (int j = 0; j < NWJ; ++j) {
+    const int s = wave + 8 * j;
+    const int r = s * 8 + (lane >> 3);
+    w_off[j] = (uint32_t)r * a.ldw_b + (uint32_t)(((lane & 7) ^ swz8(r)) << 4);
+  }
+
+  // column chunk lc of stage kt: its tap as a frame offset and a pixel shift, and its channel
+  // byte offset (padding columns: a shift that leaves every frame)
+  struct Tap {
+    int fo, dy, dx;
+    uint32_t cb;
+  };
+  auto tap_of = [&](int kt, int lc) {
+    const uint32_t kk = (uint32_t)(kt * 64 + lc * 8);
+    uint32_t c;
+    const int tap = (int)udiv(kk, a.cin, a.cin_m, c);
+    int dt = tap, ky = 0, kx = 0;
+    if (a.ks == 3) {  // tap = 9 dt + 3 ky + kx, tap < 27 on real columns
+      dt = (tap * 57) >> 9;
+      const int rr = tap - 9 * dt;
+      ky = (rr * 11) >> 5;
+      kx = rr - 3 * ky;
+    }
+    Tap o;
+    o.fo = dt + a.fbase;
+    o.dy = (int)kk < a.ktot ? ky - a.half : -(1 << 24);
+    o.dx = kx - a.half;
+    o.cb = c * 2;
+    return o;
+  };
+  auto a_off = [&](int i, const Tap& tp) {
+    const int f = rt[i] + tp.fo, yy = ry[i] + tp.dy, xs = rxp[i] + tp.dx;
+    const bool ok = (uint32_t)yy < (uint32_t)a.ho && (uint32_t)xs < (uint32_t)a.wo && f >= 0;
+    const uint32_t pix = (uint32_t)(yy >> a.up) * (uint32_t)a.w_in + (uint32_t)(xs >> a.up);
+    const uint32_t off = (uint32_t)(f >> a.lfpb) * a.fstride_b +
+                         (uint32_t)(f & ((1 << a.lfpb) - 1)) * a.sub_b + pix * a.ld_b + tp.cb;
+    return ok ? off : kOutside;
+  };
+  // part p (of 2) of stage kt's loads into slot st: A loads [p SA / 2, (p + 1) SA / 2), and with
+  // part 1 this wave's W slabs
+  Tap tp0, tp1;
+  auto issue_part = [&](int kt, int st, int p) {
+    uint8_t* sl = lds + st * SLOT;
+    if (p == 0) {
+      tp0 = tap_of(kt, lc0);
+      tp1 = tap_of(kt, lc0 ^ 1);
+    }
+#pragma unroll
+    for (int i = p * SA / 2; i < (p + 1) * SA / 2; ++i) {
+      // a named offset: with the call inside the builtin's arguments the host pass drops the
+      // launch stub
+      const uint32_t off = a_off(i, (i & 1) ? tp1 : tp0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)(sl + (wave * SA + i) * 1024), 16,
+                                               off, 0, 0, 0);
+    }
+    if (p == 1) {
+#pragma unroll
+      for (int j = 0; j < NWJ; ++j)
+        if (wave + 8 * j < SW)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rw, (lds_void*)(sl + BM * 128 + (wave + 8 * j) * 1024), 16, w_off[j],
+              (uint32_t)kt * 128, 0, 0);
+    }
+  };
+
+  f32x16 acc[2][3];  // columns j < NJ used (fixed sizes: see rt above)
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x16{};
+
+  const int frow = lane & 31, fhalf = lane >> 5;
+  i32x4 fa[2], fw[2][3];
+  auto read_a = [&](int st, int ks, int i) {
+    const uint8_t* sA = lds + st * SLOT;
+    fa[i] = *reinterpret_cast<const i32x4*>(sA + lds_off8(wm * 64 + i * 32 + frow, 2 * ks + fhalf));
+  };
+  auto read_w = [&](int st, int ks, int set) {
+    const uint8_t* sW = lds + st * SLOT + BM * 128;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      fw[set][j] = *reinterpret_cast<const i32x4*>(
+          sW + lds_off8(wn * 32 * NJ + j * 32 + frow, 2 * ks + fhalf));
+  };
+  // D[channel][pixel]: the weight fragment is the first operand, as in the GEMM kernel, so the
+  // products and their order match the im2col GEMM's
+  auto mma_tile = [&](int set, int i) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fw[set][j]),
+                                                          __builtin_bit_cast(bf16x8, fa[i]),
+                                                          acc[i][j], 0, 0, 0);
+  };
+
+  // Stage 0 lands before the loop; stage kt + 1 is in flight while stage kt computes. Before the
+  // last K step of stage kt every wave waits for its loads (stage kt + 1's, the only ones in
+  // flight) and its LDS reads, and one barrier publishes stage kt + 1 and frees slot kt & 1 for
+  // stage kt + 2, whose loads go out with the last K step's MFMAs.
+  const int nk = a.nk;
+  issue_part(0, 0, 0);
+  issue_part(0, 0, 1);
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+  __syncthreads();
+  if (nk > 1) {
+    issue_part(1, 1, 0);
+    issue_part(1, 1, 1);
+  }
+  read_w(0, 0, 0);
+  read_a(0, 0, 0);
+  read_a(0, 0, 1);
+  for (int kt = 0; kt < nk; ++kt) {
+    const int st = kt & 1;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int set = ks & 1;
+      const bool last = ks == 3;
+      const int nst = last ? (st ^ 1) : st, nks = last ? 0 : ks + 1;
+      const bool loads = last && kt + 2 < nk;
+      if (last) {
+        __builtin_amdgcn_s_waitcnt(0x0070);
+        asm volatile("s_barrier" ::: "memory");
+      }
+      read_w(nst, nks, set ^ 1);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        mma_tile(set, i);
+        read_a(nst, nks, i);
+        if (loads) issue_part(kt + 2, st, i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+
+  // ---- epilogue: lane holds pixel m0 + wm 64 + 32 i + (lane & 31) and, per group g, the four
+  // channels 8 g + 4 (lane >> 5) .. + 3 of each 32-channel tile: + bias (+ residual), rounded once
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t R = m0 + (uint32_t)(wm * 64 + i * 32 + frow);
+    if (R >= a.rows) continue;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c = n0 + wn * 32 * NJ + j * 32 + g * 8 + fhalf * 4;
+        if (c >= a.n) continue;
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = acc[i][j][g * 4 + q];
+        if (a.bias) {
+          const u32x2 b = *reinterpret_cast<const u32x2*>(a.bias + c);
+          v[0] += bf16bits_to_f32(b[0] & 0xffffu);
+          v[1] += bf16bits_to_f32(b[0] >> 16);
+          v[2] += bf16bits_to_f32(b[1] & 0xffffu);
+          v[3] += bf16bits_to_f32(b[1] >> 16);
+        }
+        if (a.res) {
+          const u32x2 r = *reinterpret_cast<const u32x2*>(a.res + (int64_t)R * a.ldr + c);
+          v[0] += bf16bits_to_f32(r[0] & 0xffffu);
+          v[1] += bf16bits_to_f32(r[0] >> 16);
+          v[2] += bf16bits_to_f32(r[1] & 0xffffu);
+          v[3] += bf16bits_to_f32(r[1] >> 16);
+        }
+        const u32x2 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        *reinterpret_cast<u32x2*>(a.out + (int64_t)R * a.ldo + c) = o;
+      }
+    }
+  }
+}
+
+namespace {
+
+uint32_t magic_of(uint32_t d) {
+  const uint64_t m = (1ULL << 32) / d;
+  return m > 0xffffffffULL ? 0xffffffffu : (uint32_t)m;
+}
+
+template <int WMW, int NJ>
+void launch_conv(ConvArgs a, hipStream_t s) {
+  constexpr int BM = 64 * WMW, BN = 32 * NJ * (8 / WMW);
+  a.tiles_n = (a.n + BN - 1) / BN;
+  const int64_t tiles = (((int64_t)a.rows + BM - 1) / BM) * a.tiles_n;
+  a.tiles = (int)tiles;
+  hipLaunchKernelGGL((conv_igemm_kernel<WMW, NJ>), dim3((unsigned)tiles), dim3(512), 0, s, a);
+}
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+}  // namespace
+}  // namespace dlt
+
+using namespace dlt;
+
+extern "C" int difflet_rocm_conv_causal(const void* x, int64_t x_elems, int64_t frame_stride,
+                                        int64_t frames_per_block, int64_t sub_stride,
+                                        int64_t pixel_stride, int64_t lead_frames, int dtype,
+                                        int64_t height, int64_t width, int64_t channels,
+                                        int64_t kt, int64_t ks, int upsample, int64_t frames,
+                                        const void* w, int64_t n, int64_t kpad, const void* bias,
+                                        const void* residual, int64_t ldr, void* out,
+                                        int64_t ldo, difflet_stream_t stream) {
+  DLT_REQUIRE(dtype == DIFFLET_BF16, DIFFLET_EUNSUPPORTED, "conv_causal: bf16 only");
+  DLT_REQUIRE(height > 0 && width > 0 && channels > 0 && frames >= 0 && n > 0 &&
+                  (upsample == 0 || upsample == 1) && (kt == 1 || kt == 3) &&
+                  (ks == 1 || ks == 3) && (frames_per_block == 1 || frames_per_block == 2) &&
+                  lead_frames >= 0 && lead_frames <= 2,
+              DIFFLET_EINVAL, "conv_causal: bad sizes or taps (kt, ks in {1, 3})");
+  DLT_REQUIRE(x && w && out, DIFFLET_EINVAL, "conv_causal: null pointer");
+  const int64_t k = kt * ks * ks * channels;
+  DLT_REQUIRE(channels % 8 == 0 && pixel_stride >= channels && pixel_stride % 8 == 0 &&
+                  sub_stride % 8 == 0 && frame_stride % 8 == 0 && kpad % 64 == 0 && kpad >= k &&
+                  n % 4 == 0 && ldo >= n && ldo % 4 == 0 &&
+                  (!residual || (ldr >= n && ldr % 4 == 0 && aligned(residual, 8))) &&
+                  (!bias || aligned(bias, 8)) && aligned(x, 16) && aligned(w, 16) &&
+                  aligned(out, 8),
+              DIFFLET_EINVAL,
+              "conv_causal: channels and strides multiples of 8, kpad a multiple of 64 >= "
+              "kt ks^2 C, n, ldo, ldr multiples of 4, pointers aligned");
+  const int64_t ho = height << upsample, wo = width << upsample, po = ho * wo;
+  const int64_t rows = frames * po;
+  DLT_REQUIRE(rows < (1LL << 31) && x_elems * 2 < (1LL << 31) && n * kpad * 2 < (1LL << 32) &&
+                  k < (1LL << 24),
+              DIFFLET_EUNSUPPORTED,
+              "conv_causal: the frames must span under 2 GiB and the output under 2^31 pixels");
+  if (rows == 0) return DIFFLET_OK;
+  {  // every frame the taps read lies inside x
+    const int64_t last = frames - 1 + lead_frames;
+    const int64_t end = (last / frames_per_block) * frame_stride +
+                        (last % frames_per_block) * sub_stride +
+                        (height * width - 1) * pixel_stride + channels;
+    DLT_REQUIRE(end <= x_elems, DIFFLET_EINVAL,
+                "conv_causal: frames 0..%lld of the input overrun x (%lld elements)",
+                (long long)last, (long long)x_elems);
+  }
+  ConvArgs a;
+  a.x = (const uint8_t*)x;
+  a.w = (const uint8_t*)w;
+  a.bias = (const bf16*)bias;
+  a.res = (const bf16*)residual;
+  a.out = (bf16*)out;
+  a.x_bytes = (uint32_t)(x_elems * 2);
+  a.rows = (uint32_t)rows;
+  a.fstride_b = (uint32_t)(frame_stride * 2);
+  a.sub_b = (uint32_t)(sub_stride * 2);
+  a.ld_b = (uint32_t)(pixel_stride * 2);
+  a.lfpb = frames_per_block == 2 ? 1 : 0;
+  a.fbase = (int)(lead_frames - (kt - 1));
+  a.w_in = (int)width;
+  a.ho = (int)ho;
+  a.wo = (int)wo;
+  a.up = upsample;
+  a.half = (int)(ks / 2);
+  a.ks = (int)ks;
+  a.po = (uint32_t)po;
+  a.po_m = magic_of((uint32_t)po);
+  a.wo_m = magic_of((uint32_t)wo);
+  a.cin = (uint32_t)channels;
+  a.cin_m = magic_of((uint32_t)channels);
+  a.ktot = (int)k;
+  a.nk = (int)(kpad / 64);
+  a.n = (int)n;
+  a.ldw_b = (uint32_t)(kpad * 2);
+  a.ldr = ldr;
+  a.ldo = ldo;
+  hipStream_t s = (hipStream_t)stream;
+  if (n <= 32)
+    launch_conv<8, 1>(a, s);
+  else if (n <= 64)
+    launch_conv<8, 2>(a, s);
+  else if (n <= 96)
+    launch_conv<8, 3>(a, s);
+  else
+    launch_conv<4, 3>(a, s);
+  return dlt_check_launch("conv_causal");
+}

@@ -839,6 +839,55 @@ def softmax_rows(s: torch.Tensor, scale: float, *, dtype: torch.dtype = torch.fl
 
 
 # ------------------------------------------------------------------------ Wan's 3D VAE decoder
+def conv_causal(x: torch.Tensor, hw: tuple[int, int], channels: int, frames: int, w: torch.Tensor,
+                bias: torch.Tensor | None = None, *, kt: int, ks: int, upsample: bool = False,
+                lead_frames: int = 0, frames_per_block: int = 1, frame_stride: int | None = None,
+                sub_stride: int = 0, pixel_stride: int | None = None,
+                residual: torch.Tensor | None = None,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """The causal (kt, ks, ks) convolution of `frames` chunk frames as one implicit GEMM (bf16):
+    [frames * Ho * Wo, n] = the im2col rows of im2col_causal times w [n, kpad] (+ bias, +
+    residual), without writing the rows. x holds the frames (contiguous; buffer frame b at
+    element (b // frames_per_block) * frame_stride + (b % frames_per_block) * sub_stride, pixels
+    pixel_stride apart); chunk frame f is buffer frame f + lead_frames, so a causal convolution
+    passes [cache frame -2, cache frame -1, frames...] with lead_frames 2."""
+    h, wd = hw
+    if not x.is_contiguous():
+        raise ValueError("conv_causal: x must be contiguous")
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise ValueError("conv_causal: bf16 frames and weight only")
+    pix = h * wd
+    ld = channels if pixel_stride is None else pixel_stride
+    fs = pix * ld if frame_stride is None else frame_stride
+    up = int(bool(upsample))
+    rows = frames * (h << up) * (wd << up)
+    n, kpad = w.shape
+    if w.stride(1) != 1 or w.stride(0) != kpad:
+        raise ValueError("conv_causal: w must be a contiguous [n, kpad]")
+    if frames > 0:
+        last = frames - 1 + lead_frames
+        end = ((last // frames_per_block) * fs + (last % frames_per_block) * sub_stride
+               + (pix - 1) * ld + channels)
+        if end > x.numel() or channels > ld:
+            raise ValueError(f"conv_causal: buffer frames 0..{last} of {h}x{wd}x{channels} "
+                             f"overrun x ({x.numel()} elements)")
+    dev = _on_gpu(x, w, bias, residual, out)
+    y = out if out is not None else torch.empty((rows, n), dtype=x.dtype, device=dev)
+    if y.dtype != x.dtype or y.shape[0] != rows or y.shape[1] < n or y.stride(1) != 1:
+        raise ValueError(f"conv_causal: out must be [{rows}, >= {n}] of x's dtype")
+    if residual is not None and (residual.dtype != x.dtype or residual.shape[0] != rows
+                                 or residual.shape[1] < n or residual.stride(1) != 1):
+        raise ValueError(f"conv_causal: residual must be [{rows}, >= {n}] of x's dtype")
+    if bias is not None and (bias.dtype != x.dtype or bias.numel() < n or not bias.is_contiguous()):
+        raise ValueError(f"conv_causal: bias must hold {n} values of x's dtype")
+    check(lib().difflet_rocm_conv_causal(
+        _ptr(x), x.numel(), fs, frames_per_block, sub_stride, ld, lead_frames, _dt(x), h, wd,
+        channels, kt, ks, up, frames, _ptr(w), n, kpad, _ptr(bias), _ptr(residual),
+        0 if residual is None else residual.stride(0), _ptr(y), y.stride(0), _stream(dev)),
+        "conv_causal")
+    return y
+
+
 def im2col_causal(x: torch.Tensor, hw: tuple[int, int], channels: int, *, kt: int, ks: int,
                   kpad: int, upsample: bool = False, cache: torch.Tensor | None = None,
                   frames_per_block: int = 1, frame_stride: int | None = None,

@@ -201,12 +201,13 @@ def pack_conv(w: torch.Tensor, b: torch.Tensor, kq: int, dtype: torch.dtype) -> 
 
 class _Chunk:
     """Frames of one chunk at one level: data [frames, pixels, ld] (channels in the first C
-    columns of each row), (h, w), C."""
+    columns of each row), (h, w), C; full: None, or a [2 + frames, pixels, C] buffer whose
+    frames 2.. are data, its first two left for a causal convolution's cache."""
 
-    __slots__ = ("data", "frames", "hw", "c")
+    __slots__ = ("data", "frames", "hw", "c", "full")
 
-    def __init__(self, data, frames, hw, c):
-        self.data, self.frames, self.hw, self.c = data, frames, hw, c
+    def __init__(self, data, frames, hw, c, full=None):
+        self.data, self.frames, self.hw, self.c, self.full = data, frames, hw, c, full
 
     @property
     def rows(self) -> torch.Tensor:
@@ -285,6 +286,21 @@ class WanVaeDecoder:
             fs, sub, pstride = h * w * ld, 0, ld
         if cv.kt == 1 and cv.ks == 1 and not up and cv.kpad == cv.cin and ld == cv.cin:
             self._gemm(x.rows, cv.w, cv.b, y, residual)   # a 1x1x1 convolution is the GEMM itself
+        elif self.dtype == torch.bfloat16:
+            # one implicit GEMM; a causal convolution reads its cache as the two frames in front
+            if cache is not None:
+                if x.full is not None:
+                    full = x.full
+                    full[:2].copy_(cache)
+                else:
+                    full = torch.cat([cache, data[:, :, : x.c]])
+                kernels.conv_causal(full, (h, w), cv.cin, frames, cv.w, cv.b, kt=cv.kt, ks=cv.ks,
+                                    upsample=upsample, lead_frames=2, residual=residual, out=y)
+            else:
+                kernels.conv_causal(data, (h, w), cv.cin, frames, cv.w, cv.b, kt=cv.kt, ks=cv.ks,
+                                    upsample=upsample, frames_per_block=frames_per_block,
+                                    frame_stride=fs, sub_stride=sub, pixel_stride=pstride,
+                                    residual=residual, out=y)
         else:
             step = max(1, IM2COL_BYTES // (cv.kpad * cv.w.element_size()))
             for r0 in range(0, total, step):
@@ -319,19 +335,23 @@ class WanVaeDecoder:
         self._roll(cache, x)
         return y
 
-    def _norm(self, name: str, x: _Chunk, silu: bool) -> _Chunk:
+    def _norm(self, name: str, x: _Chunk, silu: bool, causal: bool = False) -> _Chunk:
+        """causal: the output feeds a causal convolution, which on the bf16 path reads it with
+        its cache in front (frames allocated with two leading ones)."""
+        pix = x.hw[0] * x.hw[1]
+        lead = 2 if causal and self.dtype == torch.bfloat16 else 0
+        full = torch.empty(lead + x.frames, pix, x.c, dtype=self.dtype, device=self.device)
         y = kernels.rms_norm_channels(x.rows[:, : x.c], self.gamma[name], eps=EPS, silu=silu,
-                                      out=torch.empty(x.rows.shape[0], x.c, dtype=self.dtype,
-                                                      device=self.device))
-        return _Chunk(y.view(x.frames, -1, x.c), x.frames, x.hw, x.c)
+                                      out=full[lead:].view(-1, x.c))
+        return _Chunk(full[lead:], x.frames, x.hw, x.c, full if lead else None)
 
     def _resnet(self, state: dict, pre: str, x: _Chunk) -> _Chunk:
         sc = x
         if f"{pre}.conv_shortcut" in self.conv:
             sc = self._conv(f"{pre}.conv_shortcut", x)
-        h = self._norm(f"{pre}.norm1", x, True)
+        h = self._norm(f"{pre}.norm1", x, True, causal=True)
         h = self._causal(state, f"{pre}.conv1", h)
-        h = self._norm(f"{pre}.norm2", h, True)
+        h = self._norm(f"{pre}.norm2", h, True, causal=True)
         res = sc.rows
         return self._causal(state, f"{pre}.conv2", h, residual=res,
                             out=res if sc is not x else None)
@@ -430,5 +450,5 @@ class WanVaeDecoder:
                 x = self._resnet(state, f"decoder.up_blocks.{i}.resnets.{j}", x)
             if mode is not None:
                 x = self._resample(state, f"decoder.up_blocks.{i}.upsamplers.0", mode, x)
-        x = self._norm("decoder.norm_out", x, True)
+        x = self._norm("decoder.norm_out", x, True, causal=True)
         return self._causal(state, "decoder.conv_out", x)

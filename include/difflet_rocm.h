@@ -469,6 +469,28 @@ int difflet_rocm_im2col_causal(const void* x, int64_t frame_stride, int64_t fram
                                int64_t kt, int64_t ks, int upsample, int64_t row0, int64_t rows,
                                void* out, int64_t ldo, int64_t kpad, difflet_stream_t stream);
 
+/* The causal convolution whose rows difflet_rocm_im2col_causal writes, times its packed weight,
+ * as one implicit GEMM on the bf16 matrix cores (the rows are gathered into the LDS stage by
+ * stage, never written): out[r][o] = bias[o] + sum_k row_r[k] w[o][k] (+ residual[r][o]) for the
+ * frames * Ho * Wo output pixels r of the chunk and o < n, rounded to bf16 once; the products
+ * and their order are those of the im2col rows' GEMM (difflet_rocm_gemm, whole tiles), so the
+ * two agree bit for bit. It replaces WanCausalConv3d.forward and the resampler's Conv2d
+ * (modeling_vae.py:121-134, 163-226) in the decoder's bf16 path. Chunk frame f (f >= -2) lies
+ * at buffer frame b = f + lead_frames of x (x_elems elements): at x + (b / frames_per_block) *
+ * frame_stride + (b % frames_per_block) * sub_stride, pixel stride pixel_stride; b < 0 reads
+ * zero. A causal convolution passes its two-frame cache as buffer frames 0 and 1 (lead_frames
+ * 2); lead_frames 0 with kt = 3 is the first chunk's zero padding. w [n][kpad], the weight
+ * [Cout][kt][ks][ks][C] zero-padded to kpad (a multiple of 64) columns and n (a multiple of 4)
+ * rows; bias [n] or null; residual [rows][ldr] or null, may equal out [rows][ldo]. bf16 only;
+ * channels and strides multiples of 8 elements; the frames span under 2 GiB. */
+int difflet_rocm_conv_causal(const void* x, int64_t x_elems, int64_t frame_stride,
+                             int64_t frames_per_block, int64_t sub_stride, int64_t pixel_stride,
+                             int64_t lead_frames, int dtype, int64_t height, int64_t width,
+                             int64_t channels, int64_t kt, int64_t ks, int upsample,
+                             int64_t frames, const void* w, int64_t n, int64_t kpad,
+                             const void* bias, const void* residual, int64_t ldr, void* out,
+                             int64_t ldo, difflet_stream_t stream);
+
 /* WanRMSNorm over the channels of each row (pixel), then SiLU when act == 1
  * (modeling_vae.py:137-160, F.normalize in fp32): y = x sqrt(C) / max(||x||_2, eps) * gamma
  * (fp32 gamma [C]), bf16 or fp32 rows of stride ldx / ldy; channels a multiple of 8, <= 2048; y

@@ -8,7 +8,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from difflet_amd import kernels
+from difflet_amd import _lib, kernels
 from difflet_amd.vae import wan as dwan
 from oracle import wan_vae as ow
 from tests.test_wan_vae_host import _cfg, _im2col_causal
@@ -65,6 +65,117 @@ def test_im2col_causal_refuses_an_overrun(gpu):
     x = torch.zeros(2, 12, 16, dtype=torch.bfloat16, device=gpu)
     with pytest.raises(ValueError, match="overrun"):
         kernels.im2col_causal(x, (3, 4), 16, kt=3, ks=3, kpad=448, row0=0, rows=3 * 12)
+
+
+# (kt, ks, up, fpb, lead, frames, h, w, cin, cout, residual): every tile shape (cout <= 32, 64,
+# 96 in one channel tile of 512 pixels; wider in 256 x 192 tiles, 2 and 4 of them across), taps
+# that straddle the 64-column stages (C = 96, 8, 16), pixel counts that end mid-tile
+CONV_CASES = [
+    (3, 3, False, 1, 2, 2, 5, 7, 16, 4, False),      # conv_out-like, a 2-frame cache
+    (3, 3, False, 1, 0, 1, 4, 6, 96, 96, True),      # the first chunk: zero padding in front
+    (3, 3, False, 1, 2, 4, 12, 20, 96, 96, True),    # the full-resolution stage's widths
+    (3, 3, False, 1, 2, 1, 9, 13, 8, 64, False),
+    (3, 3, False, 1, 2, 2, 12, 20, 192, 192, False),
+    (3, 3, False, 1, 2, 1, 6, 10, 384, 384, True),
+    (3, 3, False, 1, 2, 3, 6, 10, 16, 384, False),   # conv_in
+    (3, 1, False, 1, 2, 1, 6, 10, 384, 768, False),  # a time convolution
+    (1, 3, True, 1, 0, 1, 6, 10, 384, 192, False),   # the resampler's conv after chunk 0
+    (1, 3, True, 2, 0, 4, 3, 4, 8, 32, False),       # ... reading the interleaved time-conv output
+    (1, 3, True, 2, 0, 2, 12, 20, 192, 96, False),
+    (1, 1, False, 1, 0, 3, 2, 9, 24, 24, False),     # post_quant_conv-like 1x1
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES)
+def test_conv_causal_equals_the_im2col_gemm(gpu, case):
+    """The implicit GEMM against im2col rows times the weight on the whole-tile GEMM kernel: the
+    same products in the same order, so bit-identical (and the residual may be the output);
+    both within bf16 rounding of the fp32 convolution of the rows."""
+    kt, ks, up, fpb, lead, frames, h, w, cin, cout, with_res = case
+    print(f"conv_causal {case}", flush=True)
+    g = torch.Generator().manual_seed(cin * 7 + cout + frames)
+    pix = h * w
+    bf = torch.bfloat16
+    if fpb == 2:
+        x = torch.randn(frames // 2, pix, 2 * cin, generator=g).to(bf)
+        kw = dict(frames_per_block=2, frame_stride=pix * 2 * cin, sub_stride=cin,
+                  pixel_stride=2 * cin)
+        cache = None
+    else:
+        x = torch.randn(lead + frames, pix, cin, generator=g).to(bf)
+        kw = {}
+        cache = x[:2] if lead else None
+    k = kt * ks * ks * cin
+    kpad = -(-k // 64) * 64
+    n = -(-cout // 4) * 4
+    wt = torch.zeros(n, kpad)
+    wt[:cout, :k] = torch.randn(cout, k, generator=g) * k ** -0.5
+    wt = wt.to(bf)
+    bias = (torch.randn(n, generator=g) * 0.1).to(bf)
+    rows = frames * pix * (4 if up else 1)
+    res = (torch.randn(rows, n, generator=g)).to(bf) if with_res else None
+    xg, wg, bg = x.to(gpu), wt.to(gpu), bias.to(gpu)
+    out = kernels.conv_causal(xg, (h, w), cin, frames, wg, bg, kt=kt, ks=ks, upsample=up,
+                              lead_frames=lead, residual=None if res is None else res.to(gpu),
+                              **kw)
+    src = xg[lead:] if fpb == 1 else xg
+    cols = kernels.im2col_causal(src.contiguous(), (h, w), cin, kt=kt, ks=ks, kpad=kpad,
+                                 upsample=up, cache=None if cache is None else cache.to(gpu),
+                                 rows=rows, **kw)
+    ref = torch.empty(rows, n, dtype=bf, device=gpu)
+    if res is None:
+        kernels.gemm_grouped([kernels.Problem(cols, wg, ref, bg)], kind="bf16")
+    else:
+        ones = torch.ones(1, n, dtype=bf, device=gpu)
+        kernels.gemm_grouped([kernels.Problem(cols, wg, ref, bg, gate=ones,
+                                              residual=res.to(gpu))],
+                             kind="bf16", epilogue=_lib.EPI_GATE_RESIDUAL)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    f32 = cols.float().cpu() @ wt.float().t() + bias.float()
+    if res is not None:
+        f32 = f32 + res.float()
+        inplace = res.to(gpu)
+        kernels.conv_causal(xg, (h, w), cin, frames, wg, bg, kt=kt, ks=ks, upsample=up,
+                            lead_frames=lead, residual=inplace, out=inplace, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(inplace.view(torch.int16), ref.view(torch.int16))
+    assert rel_l2(out, f32) < 4e-3
+
+
+def test_conv_causal_full_resolution_stage(gpu):
+    """A 96-channel 3x3x3 convolution of the full-resolution stage (4 frames of 480 x 832 and
+    the 2-frame cache, 1.6 M output pixels, 3120 tiles) bit-identical to the im2col GEMM."""
+    print("conv_causal 480x832x4 C=96", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(5)
+    bf, h, w, c = torch.bfloat16, 480, 832, 96
+    x = torch.randn(6, h * w, c, generator=g, device=gpu).to(bf)
+    wt = torch.zeros(c, 2624, device=gpu)
+    wt[:, :2592] = torch.randn(c, 2592, generator=g, device=gpu) * 2592 ** -0.5
+    wt = wt.to(bf)
+    bias = (torch.randn(c, generator=g, device=gpu) * 0.1).to(bf)
+    out = kernels.conv_causal(x, (h, w), c, 4, wt, bias, kt=3, ks=3, lead_frames=2)
+    ref = torch.empty_like(out)
+    po = h * w
+    for f in range(4):  # a frame's rows at a time: the GEMM's operands stay under 4 GiB
+        cols = kernels.im2col_causal(x[2:].contiguous(), (h, w), c, kt=3, ks=3, kpad=2624,
+                                     cache=x[:2].contiguous(), row0=f * po, rows=po)
+        kernels.gemm_grouped([kernels.Problem(cols, wt, ref[f * po:(f + 1) * po], bias)],
+                             kind="bf16")
+        del cols
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
+def test_conv_causal_refuses_what_it_cannot_run(gpu):
+    x = torch.zeros(2, 12, 16, dtype=torch.bfloat16, device=gpu)
+    wt = torch.zeros(16, 448, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError, match="overrun"):
+        kernels.conv_causal(x, (3, 4), 16, 3, wt, kt=3, ks=3)
+    with pytest.raises(ValueError, match="bf16"):
+        kernels.conv_causal(x.float(), (3, 4), 16, 2, wt, kt=3, ks=3)
+    with pytest.raises(ValueError, match="multiple of 64"):
+        kernels.conv_causal(x, (3, 4), 16, 2, wt[:, :440].contiguous(), kt=3, ks=3)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

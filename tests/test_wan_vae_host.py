@@ -51,6 +51,35 @@ def _im2col_causal(x, hw, channels, *, kt, ks, kpad, upsample=False, cache=None,
     return F.pad(a, (0, kpad - a.shape[1])).to(x.dtype)
 
 
+def _conv_causal(x, hw, channels, frames, w, bias=None, *, kt, ks, upsample=False,
+                 lead_frames=0, frames_per_block=1, frame_stride=None, sub_stride=0,
+                 pixel_stride=None, residual=None, out=None):
+    """The contract of kernels.conv_causal: the im2col rows of the chunk's frames (buffer frames
+    lead_frames.. of x; the ones in front are frames -lead_frames..-1, zeros before) times w."""
+    h, wd = hw
+    pix = h * wd
+    ld = channels if pixel_stride is None else pixel_stride
+    fs = pix * ld if frame_stride is None else frame_stride
+    flat = x.reshape(-1)
+
+    def frame(b):
+        base = (b // frames_per_block) * fs + (b % frames_per_block) * sub_stride
+        return flat[base + torch.arange(pix)[:, None] * ld + torch.arange(channels)[None]]
+
+    seq = torch.stack([frame(b) for b in range(lead_frames + frames)])
+    cache = torch.cat([torch.zeros(2 - lead_frames, pix, channels, dtype=x.dtype),
+                       seq[:lead_frames]])
+    cols = _im2col_causal(seq[lead_frames:].contiguous(), hw, channels, kt=kt, ks=ks,
+                          kpad=w.shape[1], upsample=upsample, cache=cache)
+    acc = cols.float() @ w.float().t()
+    acc = acc + (0 if bias is None else bias.float())
+    acc = acc + (0 if residual is None else residual[:, : w.shape[0]].float())
+    if out is None:
+        return acc.to(x.dtype)
+    out[:, : w.shape[0]].copy_(acc)
+    return out
+
+
 def _rms(x, gamma, *, eps=1e-12, silu=False, out=None):
     c = x.shape[1]
     y = x.float() * (c ** 0.5) / x.float().norm(dim=1, keepdim=True).clamp_min(eps) * gamma
@@ -99,6 +128,7 @@ def _softmax(s, scale, *, dtype=torch.float32, out=None):
 @pytest.fixture
 def cpu_kernels(monkeypatch):
     monkeypatch.setattr(kernels, "im2col_causal", _im2col_causal)
+    monkeypatch.setattr(kernels, "conv_causal", _conv_causal)
     monkeypatch.setattr(kernels, "rms_norm_channels", _rms)
     monkeypatch.setattr(kernels, "rows_to_planes", _planes)
     monkeypatch.setattr(kernels, "gemm_grouped", _gemm_grouped)
@@ -119,7 +149,8 @@ def _cfg(shape):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_host_walk_equals_the_oracle(cpu_kernels, monkeypatch, dtype):
     """Three latent frames (two temporal upsamplings), a 3 x 5 latent; the im2col chunk cut
-    small so every convolution runs in several row ranges."""
+    small so every fp32 convolution runs in several row ranges (bf16: one implicit GEMM each,
+    its cache passed as the two frames in front)."""
     monkeypatch.setattr(dwan, "IM2COL_BYTES", 1 << 16)
     store = None if dtype == torch.float32 else dtype
     w = ow.weights(SMALL, 5, store)
