@@ -133,7 +133,8 @@ SIGNATURES: dict[str, tuple] = {
                                           _vp]),
     "difflet_rocm_conv_causal": (_i32, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i64,
                                         _i64, _i64, _i64, _i64, _i32, _i64, _vp, _i64, _i64, _vp,
-                                        _vp, _i64, _vp, _i64, _vp]),
+                                        _vp, _i64, _vp, _i64, _vp, _i64, _vp]),
+    "difflet_rocm_conv_causal_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "difflet_rocm_rms_norm_channels": (_i32, [_vp, _i64, _vp, _i64, _i32, _i64, _i64, _vp, _f32,
                                               _i32, _vp]),
     "difflet_rocm_rows_to_planes": (_i32, [_vp, _i64, _i32, _i64, _i64, _vp, _f32, _f32, _vp]),

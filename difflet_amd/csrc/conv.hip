@@ -12,7 +12,7 @@
 // Tiles: 8 waves, WMW along the output pixels and 8 / WMW along the output channels, each wave 64
 // pixels x 32 NJ channels (2 x NJ MFMA 32x32x16 tiles). Cout <= 96 runs one channel tile of
 // 32 NJ with 512 pixels (the 96-channel full-resolution stage: no MFMA column wasted); wider
-// convolutions run 256 x 192 tiles. A stage is 64 K elements (128 bytes) of every row, staged
+// convolutions run 256 x 192 or 256 x 128 tiles. A stage is 64 K elements (128 bytes) of every row, staged
 // by direct-to-LDS buffer loads in two LDS slots, 8 rows x 128 B per load instruction, chunk c
 // of row r at c ^ swz8(r) as in the GEMM kernel. Each lane's 16-byte chunk of an A row is 8
 // channels of one tap of one pixel (C is a multiple of 8), so its address is the pixel's shifted
@@ -61,7 +61,9 @@ struct ConvArgs {
   int n;                         // output channels (weight rows)
   uint32_t ldw_b;                // weight row bytes
   int64_t ldr, ldo;
-  int tiles_n, tiles;
+  int tiles_n, tiles;  // channel tiles across; workgroups (tiles x ksplit)
+  int ksplit;          // K ranges per tile: > 1 writes fp32 partial sums to ws
+  float* ws;           // [ksplit][rows][n]
 };
 
 constexpr uint32_t kOutside = 0x80000000u;  // an offset past every buffer (x_bytes < 2^31)
@@ -90,6 +92,10 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_kernel(const ConvArgs a) {
     const int bid = blockIdx.x, per = a.tiles >> 3, rem = a.tiles & 7, xc = bid & 7, i = bid >> 3;
     tile = xc < rem ? xc * (per + 1) + i : rem * (per + 1) + (xc - rem) * per + i;
   }
+  // a tile's K stages [kbeg, kend): all of them, or range `piece` of ksplit
+  const int piece = tile % a.ksplit;
+  tile /= a.ksplit;
+  const int kbeg = piece * a.nk / a.ksplit, kend = (piece + 1) * a.nk / a.ksplit;
   const int tm = tile / a.tiles_n, tn = tile - tm * a.tiles_n;
   const uint32_t m0 = (uint32_t)tm * BM;
   const int n0 = tn * BN;
@@ -216,26 +222,25 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_kernel(const ConvArgs a) {
   // last K step of stage kt every wave waits for its loads (stage kt + 1's, the only ones in
   // flight) and its LDS reads, and one barrier publishes stage kt + 1 and frees slot kt & 1 for
   // stage kt + 2, whose loads go out with the last K step's MFMAs.
-  const int nk = a.nk;
-  issue_part(0, 0, 0);
-  issue_part(0, 0, 1);
+  issue_part(kbeg, 0, 0);
+  issue_part(kbeg, 0, 1);
   __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
   __syncthreads();
-  if (nk > 1) {
-    issue_part(1, 1, 0);
-    issue_part(1, 1, 1);
+  if (kend - kbeg > 1) {
+    issue_part(kbeg + 1, 1, 0);
+    issue_part(kbeg + 1, 1, 1);
   }
   read_w(0, 0, 0);
   read_a(0, 0, 0);
   read_a(0, 0, 1);
-  for (int kt = 0; kt < nk; ++kt) {
-    const int st = kt & 1;
+  for (int kt = kbeg; kt < kend; ++kt) {
+    const int st = (kt - kbeg) & 1;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int set = ks & 1;
       const bool last = ks == 3;
       const int nst = last ? (st ^ 1) : st, nks = last ? 0 : ks + 1;
-      const bool loads = last && kt + 2 < nk;
+      const bool loads = last && kt + 2 < kend;
       if (last) {
         __builtin_amdgcn_s_waitcnt(0x0070);
         asm volatile("s_barrier" ::: "memory");
@@ -253,10 +258,24 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_kernel(const ConvArgs a) {
 
   // ---- epilogue: lane holds pixel m0 + wm 64 + 32 i + (lane & 31) and, per group g, the four
   // channels 8 g + 4 (lane >> 5) .. + 3 of each 32-channel tile: + bias (+ residual), rounded once
+  // (a K range: the fp32 partial sums, which conv_split_reduce_kernel adds up)
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const uint32_t R = m0 + (uint32_t)(wm * 64 + i * 32 + frow);
     if (R >= a.rows) continue;
+    if (a.ksplit > 1) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int c = n0 + wn * 32 * NJ + j * 32 + g * 8 + fhalf * 4;
+          if (c >= a.n) continue;
+          const f32x4 v = {acc[i][j][g * 4], acc[i][j][g * 4 + 1], acc[i][j][g * 4 + 2],
+                           acc[i][j][g * 4 + 3]};
+          *reinterpret_cast<f32x4*>(a.ws + ((int64_t)piece * a.rows + R) * a.n + c) = v;
+        }
+      continue;
+    }
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
 #pragma unroll
@@ -287,6 +306,39 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_kernel(const ConvArgs a) {
   }
 }
 
+// out[r][c..c+3] = sum over the K ranges in order of ws[p][r][c..c+3] + bias (+ residual),
+// rounded once: one thread per 4 channels of a row
+__global__ __launch_bounds__(256) void conv_split_reduce_kernel(const float* __restrict__ ws,
+                                                                int ksplit, uint32_t rows, int n,
+                                                                const bf16* __restrict__ bias,
+                                                                const bf16* res, int64_t ldr,
+                                                                bf16* out, int64_t ldo) {
+  const int ng = n >> 2;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)rows * ng) return;
+  const int64_t r = i / ng;
+  const int c = (int)(i - r * ng) * 4;
+  f32x4 v = *reinterpret_cast<const f32x4*>(ws + r * n + c);
+  for (int p = 1; p < ksplit; ++p) v += *reinterpret_cast<const f32x4*>(ws + ((int64_t)p * rows + r) * n + c);
+  float o[4] = {v[0], v[1], v[2], v[3]};
+  if (bias) {
+    const u32x2 b = *reinterpret_cast<const u32x2*>(bias + c);
+    o[0] += bf16bits_to_f32(b[0] & 0xffffu);
+    o[1] += bf16bits_to_f32(b[0] >> 16);
+    o[2] += bf16bits_to_f32(b[1] & 0xffffu);
+    o[3] += bf16bits_to_f32(b[1] >> 16);
+  }
+  if (res) {
+    const u32x2 q = *reinterpret_cast<const u32x2*>(res + r * ldr + c);
+    o[0] += bf16bits_to_f32(q[0] & 0xffffu);
+    o[1] += bf16bits_to_f32(q[0] >> 16);
+    o[2] += bf16bits_to_f32(q[1] & 0xffffu);
+    o[3] += bf16bits_to_f32(q[1] >> 16);
+  }
+  const u32x2 w = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+  *reinterpret_cast<u32x2*>(out + r * ldo + c) = w;
+}
+
 namespace {
 
 uint32_t magic_of(uint32_t d) {
@@ -294,13 +346,63 @@ uint32_t magic_of(uint32_t d) {
   return m > 0xffffffffULL ? 0xffffffffu : (uint32_t)m;
 }
 
-template <int WMW, int NJ>
-void launch_conv(ConvArgs a, hipStream_t s) {
-  constexpr int BM = 64 * WMW, BN = 32 * NJ * (8 / WMW);
-  a.tiles_n = (a.n + BN - 1) / BN;
-  const int64_t tiles = (((int64_t)a.rows + BM - 1) / BM) * a.tiles_n;
-  a.tiles = (int)tiles;
-  hipLaunchKernelGGL((conv_igemm_kernel<WMW, NJ>), dim3((unsigned)tiles), dim3(512), 0, s, a);
+// The tile for n output channels, as (WMW, NJ): the widest that wastes little, 512 x 32 NJ up to
+// 96 channels, 256 x 128 up to 128, then 256 x 192 unless rounding up to 192 adds over an eighth
+// (256 channels: two 256 x 128).
+void conv_tile(int64_t n, int& wmw, int& nj) {
+  if (n <= 96) {
+    wmw = 8;
+    nj = (int)((n + 31) / 32);
+  } else if (n <= 128 || (n + 191) / 192 * 192 * 8 > 9 * n) {
+    wmw = 4;
+    nj = 2;
+  } else {
+    wmw = 4;
+    nj = 3;
+  }
+}
+
+// Compute units of the current device (0 without one: then nothing is split).
+int conv_device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    cached[dev] = v;
+  }
+  return cached[dev];
+}
+
+struct ConvPlan {
+  int wmw, nj, tiles_n, ksplit;
+  int64_t tiles;  // whole tiles
+};
+
+// A launch of under half a wave of tiles (the 60 x 104 latent-resolution convolutions: 50
+// tiles, K = 10368) cuts each tile's K stages into up to 8 ranges of at least 8 stages, so about
+// one wave of workgroups runs; the ranges' fp32 partial sums meet in a second kernel.
+ConvPlan conv_plan(int64_t rows, int64_t n, int64_t kpad, int cus) {
+  ConvPlan p;
+  conv_tile(n, p.wmw, p.nj);
+  const int bm = 64 * p.wmw, bn = 32 * p.nj * (8 / p.wmw);
+  p.tiles_n = (int)((n + bn - 1) / bn);
+  p.tiles = (rows + bm - 1) / bm * p.tiles_n;
+  p.ksplit = 1;
+  const int64_t nk = kpad / 64;
+  if (p.tiles > 0 && 2 * p.tiles < cus) {
+    int64_t k = cus / p.tiles;
+    if (k > 8) k = 8;
+    if (k > nk / 8) k = nk / 8;
+    if (k > 1) p.ksplit = (int)k;
+  }
+  return p;
+}
+
+int64_t conv_ws_bytes(const ConvPlan& p, int64_t rows, int64_t n) {
+  return p.ksplit > 1 ? (int64_t)p.ksplit * rows * n * 4 : 0;
 }
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
@@ -317,7 +419,8 @@ extern "C" int difflet_rocm_conv_causal(const void* x, int64_t x_elems, int64_t 
                                         int64_t kt, int64_t ks, int upsample, int64_t frames,
                                         const void* w, int64_t n, int64_t kpad, const void* bias,
                                         const void* residual, int64_t ldr, void* out,
-                                        int64_t ldo, difflet_stream_t stream) {
+                                        int64_t ldo, void* workspace, int64_t workspace_bytes,
+                                        difflet_stream_t stream) {
   DLT_REQUIRE(dtype == DIFFLET_BF16, DIFFLET_EUNSUPPORTED, "conv_causal: bf16 only");
   DLT_REQUIRE(height > 0 && width > 0 && channels > 0 && frames >= 0 && n > 0 &&
                   (upsample == 0 || upsample == 1) && (kt == 1 || kt == 3) &&
@@ -382,13 +485,34 @@ extern "C" int difflet_rocm_conv_causal(const void* x, int64_t x_elems, int64_t 
   a.ldr = ldr;
   a.ldo = ldo;
   hipStream_t s = (hipStream_t)stream;
-  if (n <= 32)
-    launch_conv<8, 1>(a, s);
-  else if (n <= 64)
-    launch_conv<8, 2>(a, s);
-  else if (n <= 96)
-    launch_conv<8, 3>(a, s);
+  ConvPlan plan = conv_plan(rows, n, kpad, conv_device_cus());
+  if (conv_ws_bytes(plan, rows, n) > workspace_bytes || !aligned(workspace, 16)) plan.ksplit = 1;
+  a.tiles_n = plan.tiles_n;
+  a.ksplit = plan.ksplit;
+  a.ws = (float*)workspace;
+  a.tiles = (int)(plan.tiles * plan.ksplit);
+  const dim3 grid((unsigned)a.tiles), block(512);
+  if (plan.wmw == 8 && plan.nj == 1)
+    hipLaunchKernelGGL((conv_igemm_kernel<8, 1>), grid, block, 0, s, a);
+  else if (plan.wmw == 8 && plan.nj == 2)
+    hipLaunchKernelGGL((conv_igemm_kernel<8, 2>), grid, block, 0, s, a);
+  else if (plan.wmw == 8)
+    hipLaunchKernelGGL((conv_igemm_kernel<8, 3>), grid, block, 0, s, a);
+  else if (plan.nj == 2)
+    hipLaunchKernelGGL((conv_igemm_kernel<4, 2>), grid, block, 0, s, a);
   else
-    launch_conv<4, 3>(a, s);
+    hipLaunchKernelGGL((conv_igemm_kernel<4, 3>), grid, block, 0, s, a);
+  if (plan.ksplit > 1) {
+    const int64_t items = rows * (n / 4);
+    hipLaunchKernelGGL(conv_split_reduce_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256),
+                       0, s, (const float*)workspace, plan.ksplit, (uint32_t)rows, (int)n,
+                       (const bf16*)bias, (const bf16*)residual, ldr, (bf16*)out, ldo);
+  }
   return dlt_check_launch("conv_causal");
+}
+
+extern "C" int64_t difflet_rocm_conv_causal_workspace_bytes(int64_t rows, int64_t n,
+                                                            int64_t kpad) {
+  if (rows <= 0 || n <= 0 || kpad <= 0) return 0;
+  return conv_ws_bytes(conv_plan(rows, n, kpad, conv_device_cus()), rows, n);
 }

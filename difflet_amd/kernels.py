@@ -843,14 +843,16 @@ def conv_causal(x: torch.Tensor, hw: tuple[int, int], channels: int, frames: int
                 bias: torch.Tensor | None = None, *, kt: int, ks: int, upsample: bool = False,
                 lead_frames: int = 0, frames_per_block: int = 1, frame_stride: int | None = None,
                 sub_stride: int = 0, pixel_stride: int | None = None,
-                residual: torch.Tensor | None = None,
-                out: torch.Tensor | None = None) -> torch.Tensor:
+                residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                split: bool = True) -> torch.Tensor:
     """The causal (kt, ks, ks) convolution of `frames` chunk frames as one implicit GEMM (bf16):
     [frames * Ho * Wo, n] = the im2col rows of im2col_causal times w [n, kpad] (+ bias, +
     residual), without writing the rows. x holds the frames (contiguous; buffer frame b at
     element (b // frames_per_block) * frame_stride + (b % frames_per_block) * sub_stride, pixels
     pixel_stride apart); chunk frame f is buffer frame f + lead_frames, so a causal convolution
-    passes [cache frame -2, cache frame -1, frames...] with lead_frames 2."""
+    passes [cache frame -2, cache frame -1, frames...] with lead_frames 2. split: a convolution
+    too small to fill the device may cut its K stages (fp32 partial sums through a per-stream
+    workspace); False runs whole tiles, bit-identical to the im2col rows' GEMM."""
     h, wd = hw
     if not x.is_contiguous():
         raise ValueError("conv_causal: x must be contiguous")
@@ -880,12 +882,26 @@ def conv_causal(x: torch.Tensor, hw: tuple[int, int], channels: int, frames: int
         raise ValueError(f"conv_causal: residual must be [{rows}, >= {n}] of x's dtype")
     if bias is not None and (bias.dtype != x.dtype or bias.numel() < n or not bias.is_contiguous()):
         raise ValueError(f"conv_causal: bias must hold {n} values of x's dtype")
+    ws = None
+    if split and rows:
+        i = dev.index if dev.index is not None else torch.cuda.current_device()
+        with torch.cuda.device(i):
+            need = int(lib().difflet_rocm_conv_causal_workspace_bytes(rows, n, kpad))
+        if need:  # per (device, stream), as the group-norm workspace
+            key = (i, torch.cuda.current_stream(torch.device("cuda", i)).cuda_stream)
+            ws = _CONV_WORKSPACE.get(key)
+            if ws is None or ws.numel() < need:
+                ws = torch.empty(need, dtype=torch.uint8, device=torch.device("cuda", i))
+                _CONV_WORKSPACE[key] = ws
     check(lib().difflet_rocm_conv_causal(
         _ptr(x), x.numel(), fs, frames_per_block, sub_stride, ld, lead_frames, _dt(x), h, wd,
         channels, kt, ks, up, frames, _ptr(w), n, kpad, _ptr(bias), _ptr(residual),
-        0 if residual is None else residual.stride(0), _ptr(y), y.stride(0), _stream(dev)),
-        "conv_causal")
+        0 if residual is None else residual.stride(0), _ptr(y), y.stride(0), _ptr(ws),
+        0 if ws is None else ws.numel(), _stream(dev)), "conv_causal")
     return y
+
+
+_CONV_WORKSPACE: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def im2col_causal(x: torch.Tensor, hw: tuple[int, int], channels: int, *, kt: int, ks: int,

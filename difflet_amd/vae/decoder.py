@@ -3,15 +3,16 @@
 decode of unscaled latents, difflet/backends/neuron/flux/vae.py:25-36,78-80), bf16 or fp32 (the
 reference runs fp32 by default, GroupNorm in fp32 either way: modeling_vae.py:39-68).
 
-Activations stay channels-last, [pixels][channels] per image, so every 3x3 convolution is an
-im2col gather (the nearest 2x upsampling of Upsample2D folded into its addressing) followed by a
-GEMM with the weight repacked [Cout][ky][kx][Cin] once at load, bias and any residual added in
-the GEMM's epilogue. GroupNorm (+ SiLU) is its own two-pass kernel. The mid block's attention
+Activations stay channels-last, [pixels][channels] per image, so a 3x3 convolution is the GEMM
+of its im2col rows (the nearest 2x upsampling of Upsample2D folded into their addressing) with
+the weight repacked [Cout][ky][kx][Cin] once at load, bias and any residual added in the GEMM's
+epilogue: in bf16 one implicit GEMM that gathers the rows into the LDS stage by stage
+(kernels.conv_causal on one frame), in fp32 an im2col gather and the fp32 GEMM. GroupNorm (+ SiLU) is its own two-pass kernel. The mid block's attention
 (one head of 512 channels over the latent's pixels) runs as GEMMs: fp32 scores S = Q K^T, the
 row softmax kernel, P V, then the output projection with the residual.
 
-Per resnet: GroupNorm+SiLU -> im2col -> GEMM (conv1) -> GroupNorm+SiLU -> im2col -> GEMM (conv2
-+ bias + shortcut), the shortcut a 1x1 GEMM where the channel count changes.
+Per resnet: GroupNorm+SiLU -> conv1 -> GroupNorm+SiLU -> conv2 (+ bias + shortcut), the shortcut
+a 1x1 GEMM where the channel count changes.
 """
 
 from __future__ import annotations
@@ -217,13 +218,17 @@ class VaeDecoder:
         return t
 
     def _conv3x3(self, x, hw, name, *, upsample=False, residual=None, out=None):
-        """x [H * W, Cin] -> [Ho * Wo, Cout padded to 4], in chunks of output pixels whose im2col
-        rows take at most IM2COL_BYTES (the GEMM's operands stay under 4 GiB)."""
+        """x [H * W, Cin] -> [Ho * Wo, Cout padded to 4]; fp32 in chunks of output pixels whose
+        im2col rows take at most IM2COL_BYTES (the GEMM's operands stay under 4 GiB)."""
         w, b, _, kp = self.conv[name]
         h, wd = hw
         total = (h * wd) << (2 * int(upsample))
         y = out if out is not None else torch.empty(total, w.shape[0], dtype=self.dtype,
                                                      device=self.device)
+        if self.dtype == torch.bfloat16:  # one implicit GEMM: a one-frame (1, 3, 3) convolution
+            kernels.conv_causal(x.contiguous(), hw, x.shape[1], 1, w, b, kt=1, ks=3,
+                                upsample=upsample, residual=residual, out=y)
+            return y
         step = max(1, IM2COL_BYTES // (kp * self.conv[name][0].element_size()))
         img = x.view(h, wd, -1)
         for r0 in range(0, total, step):

@@ -474,8 +474,12 @@ int difflet_rocm_im2col_causal(const void* x, int64_t frame_stride, int64_t fram
  * stage, never written): out[r][o] = bias[o] + sum_k row_r[k] w[o][k] (+ residual[r][o]) for the
  * frames * Ho * Wo output pixels r of the chunk and o < n, rounded to bf16 once; the products
  * and their order are those of the im2col rows' GEMM (difflet_rocm_gemm, whole tiles), so the
- * two agree bit for bit. It replaces WanCausalConv3d.forward and the resampler's Conv2d
- * (modeling_vae.py:121-134, 163-226) in the decoder's bf16 path. Chunk frame f (f >= -2) lies
+ * two agree bit for bit, unless the workspace (difflet_rocm_conv_causal_workspace_bytes; null
+ * and 0 always run whole tiles) lets a small convolution cut its K stages. It replaces
+ * WanCausalConv3d.forward and the resampler's Conv2d (modeling_vae.py:121-134, 163-226) in the
+ * Wan decoder's bf16 path, and with kt = 1 and one frame the FLUX decoder's 3x3 convolutions
+ * (diffusers' Decoder, difflet/models/flux/vae/modeling_vae.py:107-117). Calls on one stream
+ * may share a workspace; calls that overlap may not. Chunk frame f (f >= -2) lies
  * at buffer frame b = f + lead_frames of x (x_elems elements): at x + (b / frames_per_block) *
  * frame_stride + (b % frames_per_block) * sub_stride, pixel stride pixel_stride; b < 0 reads
  * zero. A causal convolution passes its two-frame cache as buffer frames 0 and 1 (lead_frames
@@ -489,7 +493,16 @@ int difflet_rocm_conv_causal(const void* x, int64_t x_elems, int64_t frame_strid
                              int64_t channels, int64_t kt, int64_t ks, int upsample,
                              int64_t frames, const void* w, int64_t n, int64_t kpad,
                              const void* bias, const void* residual, int64_t ldr, void* out,
-                             int64_t ldo, difflet_stream_t stream);
+                             int64_t ldo, void* workspace, int64_t workspace_bytes,
+                             difflet_stream_t stream);
+
+/* Workspace bytes difflet_rocm_conv_causal uses for rows = frames * Ho * Wo output pixels, n
+ * weight rows and kpad columns on the current device: nonzero when the convolution is too
+ * small to fill the compute units (under half a wave of tiles) and its K stages are then cut
+ * into ranges whose fp32 partial sums are added in order by a second kernel (the result then
+ * differs from the whole-tile GEMM's by fp32 summation order). A smaller workspace runs whole
+ * tiles. */
+int64_t difflet_rocm_conv_causal_workspace_bytes(int64_t rows, int64_t n, int64_t kpad);
 
 /* WanRMSNorm over the channels of each row (pixel), then SiLU when act == 1
  * (modeling_vae.py:137-160, F.normalize in fp32): y = x sqrt(C) / max(||x||_2, eps) * gamma

@@ -68,8 +68,8 @@ def test_im2col_causal_refuses_an_overrun(gpu):
 
 
 # (kt, ks, up, fpb, lead, frames, h, w, cin, cout, residual): every tile shape (cout <= 32, 64,
-# 96 in one channel tile of 512 pixels; wider in 256 x 192 tiles, 2 and 4 of them across), taps
-# that straddle the 64-column stages (C = 96, 8, 16), pixel counts that end mid-tile
+# 96 in one channel tile of 512 pixels; wider in 256 x 128 or 256 x 192 tiles, up to 4 across),
+# taps that straddle the 64-column stages (C = 96, 8, 16), pixel counts that end mid-tile
 CONV_CASES = [
     (3, 3, False, 1, 2, 2, 5, 7, 16, 4, False),      # conv_out-like, a 2-frame cache
     (3, 3, False, 1, 0, 1, 4, 6, 96, 96, True),      # the first chunk: zero padding in front
@@ -83,6 +83,9 @@ CONV_CASES = [
     (1, 3, True, 2, 0, 4, 3, 4, 8, 32, False),       # ... reading the interleaved time-conv output
     (1, 3, True, 2, 0, 2, 12, 20, 192, 96, False),
     (1, 1, False, 1, 0, 3, 2, 9, 24, 24, False),     # post_quant_conv-like 1x1
+    (1, 3, False, 1, 0, 1, 20, 24, 128, 128, True),  # FLUX's 2D decoder: 256 x 128 tiles
+    (1, 3, True, 1, 0, 1, 10, 12, 512, 256, False),  # ... two of them across
+    (1, 3, False, 1, 0, 1, 8, 9, 512, 512, True),    # ... three 256 x 192 tiles
 ]
 
 
@@ -117,7 +120,7 @@ def test_conv_causal_equals_the_im2col_gemm(gpu, case):
     xg, wg, bg = x.to(gpu), wt.to(gpu), bias.to(gpu)
     out = kernels.conv_causal(xg, (h, w), cin, frames, wg, bg, kt=kt, ks=ks, upsample=up,
                               lead_frames=lead, residual=None if res is None else res.to(gpu),
-                              **kw)
+                              split=False, **kw)
     src = xg[lead:] if fpb == 1 else xg
     cols = kernels.im2col_causal(src.contiguous(), (h, w), cin, kt=kt, ks=ks, kpad=kpad,
                                  upsample=up, cache=None if cache is None else cache.to(gpu),
@@ -137,10 +140,50 @@ def test_conv_causal_equals_the_im2col_gemm(gpu, case):
         f32 = f32 + res.float()
         inplace = res.to(gpu)
         kernels.conv_causal(xg, (h, w), cin, frames, wg, bg, kt=kt, ks=ks, upsample=up,
-                            lead_frames=lead, residual=inplace, out=inplace, **kw)
+                            lead_frames=lead, residual=inplace, out=inplace, split=False, **kw)
         torch.cuda.synchronize()
         assert torch.equal(inplace.view(torch.int16), ref.view(torch.int16))
     assert rel_l2(out, f32) < 4e-3
+
+
+@pytest.mark.parametrize("case", [
+    (3, 3, 1, 60, 104, 384, 384, True),   # the latent-resolution resnet convolution: 50 tiles
+    (3, 1, 1, 60, 104, 384, 768, False),  # the time convolution there (K = 1152)
+    (3, 3, 2, 9, 13, 96, 96, True),       # 3 tiles of 512 x 96
+    (3, 3, 1, 5, 7, 96, 4, False),        # 41 stages, 1 tile of 512 x 32: cut in 5
+])
+def test_conv_causal_split_k_matches_whole_tiles(gpu, case):
+    """Convolutions under half a wave of tiles cut their K stages into ranges (up to 8, at
+    least 8 stages each) whose fp32 partial sums a second kernel adds in order with the bias
+    and the residual: within fp32 summation order of whole tiles (bf16 outputs at most one
+    rounding step apart where no sum cancels), bit-identical on a rerun; whole tiles without a
+    workspace."""
+    kt, ks, frames, h, w, cin, cout, with_res = case
+    print(f"conv_causal split {case}", flush=True)
+    g = torch.Generator().manual_seed(cin + cout + h)
+    bf, pix = torch.bfloat16, h * w
+    x = torch.randn(2 + frames, pix, cin, generator=g).to(bf).to(gpu)
+    k = kt * ks * ks * cin
+    kpad = -(-k // 64) * 64
+    n = -(-cout // 4) * 4
+    wt = torch.zeros(n, kpad)
+    wt[:cout, :k] = torch.randn(cout, k, generator=g) * k ** -0.5
+    wt = wt.to(bf).to(gpu)
+    bias = (torch.randn(n, generator=g) * 0.1).to(bf).to(gpu)
+    rows = frames * pix
+    res = torch.randn(rows, n, generator=g).to(bf).to(gpu) if with_res else None
+    assert kernels.lib().difflet_rocm_conv_causal_workspace_bytes(rows, n, kpad) > 0
+    run = lambda split: kernels.conv_causal(x, (h, w), cin, frames, wt, bias, kt=kt, ks=ks,
+                                            lead_frames=2, residual=res, split=split)
+    a, b, whole = run(True), run(True), run(False)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    d = (a.float() - whole.float()).abs()
+    assert (d <= whole.float().abs() * 2 ** -7 + 1e-3).all() and rel_l2(a, whole) < 2e-3
+    cols = kernels.im2col_causal(x[2:].contiguous(), (h, w), cin, kt=kt, ks=ks, kpad=kpad,
+                                 cache=x[:2].contiguous())
+    f32 = cols.float() @ wt.float().t() + bias.float() + (0 if res is None else res.float())
+    assert rel_l2(a, f32.cpu()) < 4e-3
 
 
 def test_conv_causal_full_resolution_stage(gpu):
@@ -154,7 +197,7 @@ def test_conv_causal_full_resolution_stage(gpu):
     wt[:, :2592] = torch.randn(c, 2592, generator=g, device=gpu) * 2592 ** -0.5
     wt = wt.to(bf)
     bias = (torch.randn(c, generator=g, device=gpu) * 0.1).to(bf)
-    out = kernels.conv_causal(x, (h, w), c, 4, wt, bias, kt=3, ks=3, lead_frames=2)
+    out = kernels.conv_causal(x, (h, w), c, 4, wt, bias, kt=3, ks=3, lead_frames=2, split=False)
     ref = torch.empty_like(out)
     po = h * w
     for f in range(4):  # a frame's rows at a time: the GEMM's operands stay under 4 GiB
