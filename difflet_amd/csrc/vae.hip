@@ -257,8 +257,9 @@ __global__ __launch_bounds__(256) void im2col_rows_kernel(
 
 // WanRMSNorm over the channels of each pixel, then SiLU when act == 1 (modeling_vae.py:154-160):
 // y = x * sqrt(C) / max(||x||_2, eps) * gamma, in fp32, rounded once. LPR lanes share a pixel
-// row, each holding NV vectors of 8 channels (channels <= 8 * LPR * NV).
-template <typename T, int LPR, int NV>
+// row, each holding NV vectors of 8 channels (channels <= 8 * LPR * NV); a lane group takes RB
+// rows at a time, their loads issued together, and each lane holds its gamma values throughout.
+template <typename T, int LPR, int NV, int RB>
 __global__ __launch_bounds__(256) void rms_channels_kernel(const T* __restrict__ x, int64_t ldx,
                                                            T* __restrict__ y, int64_t ldy,
                                                            int64_t rows, int channels,
@@ -267,33 +268,60 @@ __global__ __launch_bounds__(256) void rms_channels_kernel(const T* __restrict__
   const int lane = threadIdx.x % LPR;
   const int nvec = channels / 8;
   const float root = __builtin_sqrtf((float)channels);
-  for (int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LPR; row < rows;
-       row += (int64_t)gridDim.x * (256 / LPR)) {
-    float v[NV][8];
-    float ss = 0.f;
+  float g[NV][8];
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const int vi = lane + j * LPR;
-      if (vi < nvec) {
-        Vec8<T>::load(x + row * ldx + vi * 8, v[j]);
+  for (int j = 0; j < NV; ++j) {
+    const int vi = lane + j * LPR;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) ss = __builtin_fmaf(v[j][k], v[j][k], ss);
+    for (int k = 0; k < 8; ++k) g[j][k] = vi < nvec ? gamma[vi * 8 + k] : 0.f;
+  }
+  const int64_t stride = (int64_t)gridDim.x * (256 / LPR);
+  for (int64_t row0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LPR; row0 < rows;
+       row0 += stride * RB) {
+    float v[RB][NV][8];
+    float ss[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const int64_t row = row0 + r * stride;
+      ss[r] = 0.f;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int vi = lane + j * LPR;
+        if (row < rows && vi < nvec) Vec8<T>::load(x + row * ldx + vi * 8, v[r][j]);
       }
     }
 #pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, LPR);
-    const float scale = root / fmaxf(__builtin_sqrtf(ss), eps);
+    for (int r = 0; r < RB; ++r) {
+      const int64_t row = row0 + r * stride;
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const int vi = lane + j * LPR;
-      if (vi < nvec) {
+      for (int j = 0; j < NV; ++j) {
+        const int vi = lane + j * LPR;
+        if (row < rows && vi < nvec) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          float o = v[j][k] * scale * gamma[vi * 8 + k];
-          if (act == 1) o = o / (1.0f + __expf(-o));
-          v[j][k] = o;
+          for (int k = 0; k < 8; ++k) ss[r] = __builtin_fmaf(v[r][j][k], v[r][j][k], ss[r]);
         }
-        Vec8<T>::store(y + row * ldy + vi * 8, v[j]);
+      }
+#pragma unroll
+      for (int o = LPR / 2; o > 0; o >>= 1) ss[r] += __shfl_xor(ss[r], o, LPR);
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const int64_t row = row0 + r * stride;
+      const float scale = root / fmaxf(__builtin_sqrtf(ss[r]), eps);
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int vi = lane + j * LPR;
+        if (row < rows && vi < nvec) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            float o = v[r][j][k] * scale * g[j][k];
+            // SiLU with the hardware reciprocal (1 ulp) in place of the IEEE divide, which
+            // costs more than the rest of the row's arithmetic
+            if (act == 1) o = o * __builtin_amdgcn_rcpf(1.0f + __expf(-o));
+            v[r][j][k] = o;
+          }
+          Vec8<T>::store(y + row * ldy + vi * 8, v[r][j]);
+        }
       }
     }
   }
@@ -477,14 +505,14 @@ extern "C" int difflet_rocm_im2col_causal(const void* x, int64_t frame_stride,
   return dlt_check_launch("im2col_causal");
 }
 
-template <typename T, int LPR, int NV>
+template <typename T, int LPR, int NV, int RB>
 static void launch_rms_channels(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
                                 int channels, const float* gamma, float eps, int act,
                                 hipStream_t s) {
-  int64_t blocks = (rows * LPR + 255) / 256;
+  int64_t blocks = (rows * LPR + 256 * RB - 1) / (256 * RB);
   if (blocks > 16384) blocks = 16384;
-  hipLaunchKernelGGL((rms_channels_kernel<T, LPR, NV>), dim3((unsigned)blocks), dim3(256), 0, s,
-                     (const T*)x, ldx, (T*)y, ldy, rows, channels, gamma, eps, act);
+  hipLaunchKernelGGL((rms_channels_kernel<T, LPR, NV, RB>), dim3((unsigned)blocks), dim3(256), 0,
+                     s, (const T*)x, ldx, (T*)y, ldy, rows, channels, gamma, eps, act);
 }
 
 extern "C" int difflet_rocm_rms_norm_channels(const void* x, int64_t ldx, void* y, int64_t ldy,
@@ -504,10 +532,10 @@ extern "C" int difflet_rocm_rms_norm_channels(const void* x, int64_t ldx, void* 
   hipStream_t s = (hipStream_t)stream;
   const int nvec = (int)(channels / 8);
   DLT_DISPATCH_BF16_F32(dtype, T,
-    if (nvec <= 16) launch_rms_channels<T, 16, 1>(x, ldx, y, ldy, rows, (int)channels, gamma, eps, act, s);
-    else if (nvec <= 32) launch_rms_channels<T, 32, 1>(x, ldx, y, ldy, rows, (int)channels, gamma, eps, act, s);
-    else if (nvec <= 64) launch_rms_channels<T, 64, 1>(x, ldx, y, ldy, rows, (int)channels, gamma, eps, act, s);
-    else launch_rms_channels<T, 64, 4>(x, ldx, y, ldy, rows, (int)channels, gamma, eps, act, s));
+    if (nvec <= 16) launch_rms_channels<T, 16, 1, 4>(x, ldx, y, ldy, rows, (int)channels, gamma, eps, act, s);
+    else if (nvec <= 32) launch_rms_channels<T, 32, 1, 4>(x, ldx, y, ldy, rows, (int)channels, gamma, eps, act, s);
+    else if (nvec <= 64) launch_rms_channels<T, 64, 1, 4>(x, ldx, y, ldy, rows, (int)channels, gamma, eps, act, s);
+    else launch_rms_channels<T, 64, 4, 1>(x, ldx, y, ldy, rows, (int)channels, gamma, eps, act, s));
   return dlt_check_launch("rms_norm_channels");
 }
 
