@@ -200,6 +200,50 @@ __device__ __forceinline__ u32x2 buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t of
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
 }
 
+// Where a causal convolution's im2col rows come from (the frames of difflet_rocm_conv_causal),
+// for the kernels that gather them instead of reading materialized rows: output pixel r =
+// (t, y, x) of an ho x wo frame, column k = tap (dt, ky, kx) x C + c, read from buffer frame b =
+// t + dt + fbase (zero when b < 0) at element (b >> lfpb) fstride + (b & (2^lfpb - 1)) sub +
+// ((y + ky - half) >> up) w + ((x + kx - half) >> up)) ld + c, zero outside the frame.
+struct ConvGeo {
+  int64_t fstride, sub, ld;  // elements
+  int lfpb, fbase;
+  int w, ho, wo, up, half, ks;
+  uint32_t po, po_m, wo_m, cin, cin_m;  // divisors and their magic numbers (conv_magic)
+  int ktot;                             // kt ks^2 C
+};
+
+// q = n / d, r = n % d for n < 2^32, m = conv_magic(d): the high word of n m is floor(n / d) or
+// one less (n (2^32 mod d) / (d 2^32) < 1), which one compare fixes.
+__device__ __forceinline__ uint32_t conv_udiv(uint32_t n, uint32_t d, uint32_t m, uint32_t& r) {
+  uint32_t q = __umulhi(n, m);
+  r = n - q * d;
+  if (r >= d) {
+    ++q;
+    r -= d;
+  }
+  return q;
+}
+inline uint32_t conv_magic(uint32_t d) {
+  const uint64_t m = (1ULL << 32) / d;
+  return m > 0xffffffffULL ? 0xffffffffu : (uint32_t)m;
+}
+// tap -> (dt, ky, kx) for ks in {1, 3} (tap = (dt ks + ky) ks + kx; exact for tap < 27)
+__device__ __forceinline__ void conv_tap(int tap, int ks, int& dt, int& ky, int& kx) {
+  dt = tap, ky = 0, kx = 0;
+  if (ks == 3) {
+    dt = (tap * 57) >> 9;
+    const int rr = tap - 9 * dt;
+    ky = (rr * 11) >> 5;
+    kx = rr - 3 * ky;
+  }
+}
+
+// The fp32 convolution on the fp32 matrix-core GEMM with its A rows gathered (gemm_f32.hip).
+int launch_conv_f32(const float* x, const ConvGeo& g, int64_t rows, const float* w, int64_t n,
+                    int64_t kpad, const float* bias, const float* res, int64_t ldr, float* out,
+                    int64_t ldo, hipStream_t s);
+
 }  // namespace dlt
 
 // Error plumbing shared by every entry point: a status code plus a message readable through

@@ -24,18 +24,6 @@
 namespace dlt {
 namespace {
 
-// q = n / d and r = n % d for n < 2^32 from m = min(floor(2^32 / d), 2^32 - 1): the high word of
-// n m is floor(n / d) or one less (n (2^32 mod d) / (d 2^32) < 1), which one compare fixes.
-__device__ __forceinline__ uint32_t udiv(uint32_t n, uint32_t d, uint32_t m, uint32_t& r) {
-  uint32_t q = __umulhi(n, m);
-  r = n - q * d;
-  if (r >= d) {
-    ++q;
-    r -= d;
-  }
-  return q;
-}
-
 __device__ __forceinline__ int swz8(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 __device__ __forceinline__ int lds_off8(int row, int chunk) {
   return row * 128 + ((chunk ^ swz8(row)) << 4);
@@ -115,8 +103,8 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_kernel(const ConvArgs a) {
   for (int i = 0; i < SA; ++i) {
     const uint32_t R = m0 + (uint32_t)((wave * SA + i) * 8 + (lane >> 3));
     uint32_t p, xx;
-    const uint32_t t = udiv(R, a.po, a.po_m, p);
-    const uint32_t y = udiv(p, (uint32_t)a.wo, a.wo_m, xx);
+    const uint32_t t = conv_udiv(R, a.po, a.po_m, p);
+    const uint32_t y = conv_udiv(p, (uint32_t)a.wo, a.wo_m, xx);
     const bool in = R < a.rows;
     rt[i] = (int)t;
     ry[i] = in ? (int)y : -(1 << 24);
@@ -139,14 +127,9 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_kernel(const ConvArgs a) {
   auto tap_of = [&](int kt, int lc) {
     const uint32_t kk = (uint32_t)(kt * 64 + lc * 8);
     uint32_t c;
-    const int tap = (int)udiv(kk, a.cin, a.cin_m, c);
-    int dt = tap, ky = 0, kx = 0;
-    if (a.ks == 3) {  // tap = 9 dt + 3 ky + kx, tap < 27 on real columns
-      dt = (tap * 57) >> 9;
-      const int rr = tap - 9 * dt;
-      ky = (rr * 11) >> 5;
-      kx = rr - 3 * ky;
-    }
+    const int tap = (int)conv_udiv(kk, a.cin, a.cin_m, c);
+    int dt, ky, kx;
+    conv_tap(tap, a.ks, dt, ky, kx);
     Tap o;
     o.fo = dt + a.fbase;
     o.dy = (int)kk < a.ktot ? ky - a.half : -(1 << 24);
@@ -341,11 +324,6 @@ __global__ __launch_bounds__(256) void conv_split_reduce_kernel(const float* __r
 
 namespace {
 
-uint32_t magic_of(uint32_t d) {
-  const uint64_t m = (1ULL << 32) / d;
-  return m > 0xffffffffULL ? 0xffffffffu : (uint32_t)m;
-}
-
 // The tile for n output channels, as (WMW, NJ): the widest that wastes little, 512 x 32 NJ up to
 // 96 channels, 256 x 128 up to 128, then 256 x 192 unless rounding up to 192 adds over an eighth
 // (256 channels: two 256 x 128).
@@ -421,29 +399,34 @@ extern "C" int difflet_rocm_conv_causal(const void* x, int64_t x_elems, int64_t 
                                         const void* residual, int64_t ldr, void* out,
                                         int64_t ldo, void* workspace, int64_t workspace_bytes,
                                         difflet_stream_t stream) {
-  DLT_REQUIRE(dtype == DIFFLET_BF16, DIFFLET_EUNSUPPORTED, "conv_causal: bf16 only");
+  DLT_REQUIRE(dtype == DIFFLET_BF16 || dtype == DIFFLET_F32, DIFFLET_EUNSUPPORTED,
+              "conv_causal: bf16 or fp32");
   DLT_REQUIRE(height > 0 && width > 0 && channels > 0 && frames >= 0 && n > 0 &&
                   (upsample == 0 || upsample == 1) && (kt == 1 || kt == 3) &&
                   (ks == 1 || ks == 3) && (frames_per_block == 1 || frames_per_block == 2) &&
                   lead_frames >= 0 && lead_frames <= 2,
               DIFFLET_EINVAL, "conv_causal: bad sizes or taps (kt, ks in {1, 3})");
   DLT_REQUIRE(x && w && out, DIFFLET_EINVAL, "conv_causal: null pointer");
+  const bool f32 = dtype == DIFFLET_F32;
+  const int ev = f32 ? 4 : 8, kq = f32 ? 4 : 64;  // elements per 16 bytes; the K stage multiple
   const int64_t k = kt * ks * ks * channels;
-  DLT_REQUIRE(channels % 8 == 0 && pixel_stride >= channels && pixel_stride % 8 == 0 &&
-                  sub_stride % 8 == 0 && frame_stride % 8 == 0 && kpad % 64 == 0 && kpad >= k &&
+  DLT_REQUIRE(channels % ev == 0 && pixel_stride >= channels && pixel_stride % ev == 0 &&
+                  sub_stride % ev == 0 && frame_stride % ev == 0 && kpad % kq == 0 && kpad >= k &&
                   n % 4 == 0 && ldo >= n && ldo % 4 == 0 &&
-                  (!residual || (ldr >= n && ldr % 4 == 0 && aligned(residual, 8))) &&
-                  (!bias || aligned(bias, 8)) && aligned(x, 16) && aligned(w, 16) &&
-                  aligned(out, 8),
+                  (!residual || (ldr >= n && ldr % 4 == 0 && aligned(residual, 2 * ev))) &&
+                  (!bias || aligned(bias, 2 * ev)) && aligned(x, 16) && aligned(w, 16) &&
+                  aligned(out, 2 * ev),
               DIFFLET_EINVAL,
-              "conv_causal: channels and strides multiples of 8, kpad a multiple of 64 >= "
-              "kt ks^2 C, n, ldo, ldr multiples of 4, pointers aligned");
+              "conv_causal: channels and strides multiples of 16 bytes, kpad a multiple of %d "
+              ">= kt ks^2 C, n, ldo, ldr multiples of 4, pointers aligned (x, w: 16 bytes; "
+              "bias, residual, out: 4 elements)", kq);
   const int64_t ho = height << upsample, wo = width << upsample, po = ho * wo;
   const int64_t rows = frames * po;
-  DLT_REQUIRE(rows < (1LL << 31) && x_elems * 2 < (1LL << 31) && n * kpad * 2 < (1LL << 32) &&
-                  k < (1LL << 24),
+  DLT_REQUIRE(rows < (1LL << 31) && k < (1LL << 24) &&
+                  (f32 || (x_elems * 2 < (1LL << 31) && n * kpad * 2 < (1LL << 32))),
               DIFFLET_EUNSUPPORTED,
-              "conv_causal: the frames must span under 2 GiB and the output under 2^31 pixels");
+              "conv_causal: the output must hold under 2^31 pixels (bf16: the frames span under "
+              "2 GiB)");
   if (rows == 0) return DIFFLET_OK;
   {  // every frame the taps read lies inside x
     const int64_t last = frames - 1 + lead_frames;
@@ -453,6 +436,29 @@ extern "C" int difflet_rocm_conv_causal(const void* x, int64_t x_elems, int64_t 
     DLT_REQUIRE(end <= x_elems, DIFFLET_EINVAL,
                 "conv_causal: frames 0..%lld of the input overrun x (%lld elements)",
                 (long long)last, (long long)x_elems);
+  }
+  hipStream_t s = (hipStream_t)stream;
+  if (f32) {
+    ConvGeo g;
+    g.fstride = frame_stride;
+    g.sub = sub_stride;
+    g.ld = pixel_stride;
+    g.lfpb = frames_per_block == 2 ? 1 : 0;
+    g.fbase = (int)(lead_frames - (kt - 1));
+    g.w = (int)width;
+    g.ho = (int)ho;
+    g.wo = (int)wo;
+    g.up = upsample;
+    g.half = (int)(ks / 2);
+    g.ks = (int)ks;
+    g.po = (uint32_t)po;
+    g.po_m = conv_magic((uint32_t)po);
+    g.wo_m = conv_magic((uint32_t)wo);
+    g.cin = (uint32_t)channels;
+    g.cin_m = conv_magic((uint32_t)channels);
+    g.ktot = (int)k;
+    return launch_conv_f32((const float*)x, g, rows, (const float*)w, n, kpad,
+                           (const float*)bias, (const float*)residual, ldr, (float*)out, ldo, s);
   }
   ConvArgs a;
   a.x = (const uint8_t*)x;
@@ -474,17 +480,16 @@ extern "C" int difflet_rocm_conv_causal(const void* x, int64_t x_elems, int64_t 
   a.half = (int)(ks / 2);
   a.ks = (int)ks;
   a.po = (uint32_t)po;
-  a.po_m = magic_of((uint32_t)po);
-  a.wo_m = magic_of((uint32_t)wo);
+  a.po_m = conv_magic((uint32_t)po);
+  a.wo_m = conv_magic((uint32_t)wo);
   a.cin = (uint32_t)channels;
-  a.cin_m = magic_of((uint32_t)channels);
+  a.cin_m = conv_magic((uint32_t)channels);
   a.ktot = (int)k;
   a.nk = (int)(kpad / 64);
   a.n = (int)n;
   a.ldw_b = (uint32_t)(kpad * 2);
   a.ldr = ldr;
   a.ldo = ldo;
-  hipStream_t s = (hipStream_t)stream;
   ConvPlan plan = conv_plan(rows, n, kpad, conv_device_cus());
   if (conv_ws_bytes(plan, rows, n) > workspace_bytes || !aligned(workspace, 16)) plan.ksplit = 1;
   a.tiles_n = plan.tiles_n;

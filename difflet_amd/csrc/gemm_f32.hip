@@ -8,6 +8,9 @@
 // the stage's 32 indices onto the 16 MFMA steps x 2 halves), so each lane reads its 16 values
 // of a row with four 16-byte LDS reads.
 //
+// The same kernel runs the fp32 causal convolutions of the VAE decoders as implicit GEMMs: the A
+// loader gathers each row's 4-float runs from the frames (difflet_rocm_conv_causal).
+//
 // Workgroup tile 64 (M) x 128 (N), 4 waves of 32 x 64 (two 32 x 32 MFMA tiles); A and W stages
 // of 32 floats per row in LDS, double-buffered (55 KB: two workgroups per compute unit), the
 // next stage loaded into registers while the current one is multiplied. As in the bf16 GEMM the
@@ -28,7 +31,8 @@ constexpr int F32_BM = 64, F32_BN = 128, F32_BK = 32;
 constexpr int F32_LDS_STRIDE = F32_BK + 4;  // floats per LDS row: 16-byte pad against conflicts
 
 struct GemmF32Args {
-  const float* a;
+  const float* a;  // [m][lda], or (CONV) the frames the rows are gathered from by g
+  ConvGeo g;
   const float* w;
   const float* bias;
   const float* res;
@@ -38,6 +42,8 @@ struct GemmF32Args {
   int tiles_m, tiles, xcd_chunk;
 };
 
+// CONV: A is the im2col rows of a causal convolution, gathered from the frames (p.a) by p.g
+template <bool CONV>
 __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(const GemmF32Args p) {
   __shared__ __attribute__((aligned(16))) float sa[2][F32_BM * F32_LDS_STRIDE];
   __shared__ __attribute__((aligned(16))) float sw[2][F32_BN * F32_LDS_STRIDE];
@@ -53,14 +59,47 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(const GemmF32Args p) {
   // thread i of a 256-wide pass takes row i / 8, floats (i % 8) * 4 .. + 4
   f32x4 ra[2], rw[4];
   const int lr = tid >> 3, lc = (tid & 7) * 4;
-  auto load = [&](int64_t k0) {
-    const int64_t kk = k0 + lc;
-    const bool kok = kk < p.k;  // K % 4 == 0: a run of 4 is all in or all out
+  // CONV: the output pixel (frame, y, x) of this thread's two A rows (y far outside past m)
+  int rt[2] = {0, 0}, ry[2] = {0, 0}, rx[2] = {0, 0};
+  if constexpr (CONV) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int64_t m = m0 + lr + 32 * j;
-      ra[j] = (kok && m < p.m) ? *reinterpret_cast<const f32x4*>(p.a + m * p.lda + kk)
-                               : f32x4{0.f, 0.f, 0.f, 0.f};
+      uint32_t pp, xx;
+      const uint32_t t = conv_udiv((uint32_t)m, p.g.po, p.g.po_m, pp);
+      const uint32_t y = conv_udiv(pp, (uint32_t)p.g.wo, p.g.wo_m, xx);
+      rt[j] = (int)t;
+      ry[j] = m < p.m ? (int)y : -(1 << 24);
+      rx[j] = (int)xx;
+    }
+  }
+  auto load = [&](int64_t k0) {
+    const int64_t kk = k0 + lc;
+    const bool kok = kk < p.k;  // K % 4 == 0: a run of 4 is all in or all out
+    if constexpr (CONV) {  // the run is channels c .. c + 3 of one tap (C % 4 == 0)
+      uint32_t c;
+      const int tap = (int)conv_udiv((uint32_t)kk, p.g.cin, p.g.cin_m, c);
+      int dt, ky, kx;
+      conv_tap(tap, p.g.ks, dt, ky, kx);
+      const bool col = kk < p.g.ktot;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int f = rt[j] + dt + p.g.fbase;
+        const int yy = ry[j] + ky - p.g.half, xs = rx[j] + kx - p.g.half;
+        const bool ok = col && f >= 0 && (uint32_t)yy < (uint32_t)p.g.ho &&
+                        (uint32_t)xs < (uint32_t)p.g.wo;
+        const int64_t off = (int64_t)(f >> p.g.lfpb) * p.g.fstride +
+                            (int64_t)(f & ((1 << p.g.lfpb) - 1)) * p.g.sub +
+                            ((int64_t)(yy >> p.g.up) * p.g.w + (xs >> p.g.up)) * p.g.ld + c;
+        ra[j] = ok ? *reinterpret_cast<const f32x4*>(p.a + off) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int64_t m = m0 + lr + 32 * j;
+        ra[j] = (kok && m < p.m) ? *reinterpret_cast<const f32x4*>(p.a + m * p.lda + kk)
+                                 : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -170,7 +209,7 @@ extern "C" int difflet_rocm_gemm_f32(const float* a, int64_t lda, const float* w
                 "gemm_f32: pointers must be 16-byte aligned");
   const int64_t tiles_m = (m + F32_BM - 1) / F32_BM, tiles_n = (n + F32_BN - 1) / F32_BN;
   DLT_REQUIRE(tiles_m * tiles_n < (1LL << 31), DIFFLET_EUNSUPPORTED, "gemm_f32: too many tiles");
-  GemmF32Args args;
+  GemmF32Args args{};
   args.a = a;
   args.w = w;
   args.bias = bias;
@@ -186,7 +225,38 @@ extern "C" int difflet_rocm_gemm_f32(const float* a, int64_t lda, const float* w
   args.tiles_m = (int)tiles_m;
   args.tiles = (int)(tiles_m * tiles_n);
   args.xcd_chunk = args.tiles % 8 == 0 ? args.tiles / 8 : 0;
-  hipLaunchKernelGGL(gemm_f32_kernel, dim3((unsigned)args.tiles), dim3(256), 0,
+  hipLaunchKernelGGL((gemm_f32_kernel<false>), dim3((unsigned)args.tiles), dim3(256), 0,
                      (hipStream_t)stream, args);
   return dlt_check_launch("gemm_f32");
 }
+
+namespace dlt {
+
+// The implicit-GEMM form of the fp32 convolution (difflet_rocm_conv_causal with dtype F32): the
+// same tiles and K order as the fp32 GEMM of the im2col rows, so the same results bit for bit.
+int launch_conv_f32(const float* x, const ConvGeo& g, int64_t rows, const float* w, int64_t n,
+                    int64_t kpad, const float* bias, const float* res, int64_t ldr, float* out,
+                    int64_t ldo, hipStream_t s) {
+  const int64_t tiles_m = (rows + F32_BM - 1) / F32_BM, tiles_n = (n + F32_BN - 1) / F32_BN;
+  GemmF32Args args{};
+  args.a = x;
+  args.g = g;
+  args.w = w;
+  args.bias = bias;
+  args.res = res;
+  args.c = out;
+  args.lda = 0;
+  args.ldw = kpad;
+  args.ldr = ldr;
+  args.ldc = ldo;
+  args.m = rows;
+  args.n = n;
+  args.k = kpad;
+  args.tiles_m = (int)tiles_m;
+  args.tiles = (int)(tiles_m * tiles_n);
+  args.xcd_chunk = args.tiles % 8 == 0 ? args.tiles / 8 : 0;
+  hipLaunchKernelGGL((gemm_f32_kernel<true>), dim3((unsigned)args.tiles), dim3(256), 0, s, args);
+  return dlt_check_launch("conv_causal");
+}
+
+}  // namespace dlt

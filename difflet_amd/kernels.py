@@ -845,7 +845,8 @@ def conv_causal(x: torch.Tensor, hw: tuple[int, int], channels: int, frames: int
                 sub_stride: int = 0, pixel_stride: int | None = None,
                 residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
                 split: bool = True) -> torch.Tensor:
-    """The causal (kt, ks, ks) convolution of `frames` chunk frames as one implicit GEMM (bf16):
+    """The causal (kt, ks, ks) convolution of `frames` chunk frames as one implicit GEMM (bf16
+    on the bf16 matrix cores, fp32 on the fp32 GEMM):
     [frames * Ho * Wo, n] = the im2col rows of im2col_causal times w [n, kpad] (+ bias, +
     residual), without writing the rows. x holds the frames (contiguous; buffer frame b at
     element (b // frames_per_block) * frame_stride + (b % frames_per_block) * sub_stride, pixels
@@ -856,8 +857,8 @@ def conv_causal(x: torch.Tensor, hw: tuple[int, int], channels: int, frames: int
     h, wd = hw
     if not x.is_contiguous():
         raise ValueError("conv_causal: x must be contiguous")
-    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
-        raise ValueError("conv_causal: bf16 frames and weight only")
+    if x.dtype not in (torch.bfloat16, torch.float32) or w.dtype != x.dtype:
+        raise ValueError("conv_causal: bf16 or fp32 frames, and a weight of their dtype")
     pix = h * wd
     ld = channels if pixel_stride is None else pixel_stride
     fs = pix * ld if frame_stride is None else frame_stride
@@ -883,7 +884,7 @@ def conv_causal(x: torch.Tensor, hw: tuple[int, int], channels: int, frames: int
     if bias is not None and (bias.dtype != x.dtype or bias.numel() < n or not bias.is_contiguous()):
         raise ValueError(f"conv_causal: bias must hold {n} values of x's dtype")
     ws = None
-    if split and rows:
+    if split and rows and x.dtype == torch.bfloat16:
         i = dev.index if dev.index is not None else torch.cuda.current_device()
         with torch.cuda.device(i):
             need = int(lib().difflet_rocm_conv_causal_workspace_bytes(rows, n, kpad))

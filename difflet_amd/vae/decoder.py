@@ -6,8 +6,8 @@ reference runs fp32 by default, GroupNorm in fp32 either way: modeling_vae.py:39
 Activations stay channels-last, [pixels][channels] per image, so a 3x3 convolution is the GEMM
 of its im2col rows (the nearest 2x upsampling of Upsample2D folded into their addressing) with
 the weight repacked [Cout][ky][kx][Cin] once at load, bias and any residual added in the GEMM's
-epilogue: in bf16 one implicit GEMM that gathers the rows into the LDS stage by stage
-(kernels.conv_causal on one frame), in fp32 an im2col gather and the fp32 GEMM. GroupNorm (+ SiLU) is its own two-pass kernel. The mid block's attention
+epilogue: one implicit GEMM that gathers the rows stage by stage (kernels.conv_causal on one
+frame; bf16 on the bf16 matrix cores, fp32 on the fp32 GEMM). GroupNorm (+ SiLU) is its own two-pass kernel. The mid block's attention
 (one head of 512 channels over the latent's pixels) runs as GEMMs: fp32 scores S = Q K^T, the
 row softmax kernel, P V, then the output projection with the residual.
 
@@ -65,7 +65,6 @@ class VaeConfig:
 
 FLUX_VAE = VaeConfig()
 EPS = 1e-6  # the decoder's GroupNorm eps (resnets, attention, conv_norm_out)
-IM2COL_BYTES = 1 << 30  # largest im2col chunk a convolution materializes
 
 
 def _plan(cfg: VaeConfig):
@@ -218,24 +217,15 @@ class VaeDecoder:
         return t
 
     def _conv3x3(self, x, hw, name, *, upsample=False, residual=None, out=None):
-        """x [H * W, Cin] -> [Ho * Wo, Cout padded to 4]; fp32 in chunks of output pixels whose
-        im2col rows take at most IM2COL_BYTES (the GEMM's operands stay under 4 GiB)."""
-        w, b, _, kp = self.conv[name]
+        """x [H * W, Cin] -> [Ho * Wo, Cout padded to 4]."""
+        w, b, _, _ = self.conv[name]
         h, wd = hw
         total = (h * wd) << (2 * int(upsample))
         y = out if out is not None else torch.empty(total, w.shape[0], dtype=self.dtype,
                                                      device=self.device)
-        if self.dtype == torch.bfloat16:  # one implicit GEMM: a one-frame (1, 3, 3) convolution
-            kernels.conv_causal(x.contiguous(), hw, x.shape[1], 1, w, b, kt=1, ks=3,
-                                upsample=upsample, residual=residual, out=y)
-            return y
-        step = max(1, IM2COL_BYTES // (kp * self.conv[name][0].element_size()))
-        img = x.view(h, wd, -1)
-        for r0 in range(0, total, step):
-            n = min(step, total - r0)
-            cols = kernels.im2col3x3(img, upsample=upsample, kpad=kp, row0=r0, rows=n)
-            self._gemm(cols, w, b, y[r0:r0 + n],
-                       None if residual is None else residual[r0:r0 + n])
+        # one implicit GEMM: a one-frame (1, 3, 3) convolution
+        kernels.conv_causal(x.contiguous(), hw, x.shape[1], 1, w, b, kt=1, ks=3,
+                            upsample=upsample, residual=residual, out=y)
         return y
 
     def _gn(self, x, name, silu):

@@ -7,14 +7,15 @@ frame (difflet/models/wan/vae/regions.py:3-6). bf16 or fp32.
 
 The decode walks the latent video one frame (a chunk) at a time, as the reference does: chunk 0
 decodes to one frame, every later chunk to 2^u frames (u temporal upsamplings). Activations are
-channels-last frames, [frames][pixels][channels]. Each causal 3x3x3 convolution is an im2col
-gather over the chunk's frames and a two-frame cache of the convolution's own input from the
-chunks before (zeros at the start, the reference's front padding), followed by a GEMM with the
-weight repacked [Cout][dt][ky][kx][Cin] once at load; the cache then takes the last two frames
-of (cache, chunk). The time convolution of an upsample3d resampler is a (3, 1, 1) causal
+channels-last frames, [frames][pixels][channels]. Each causal 3x3x3 convolution is one implicit
+GEMM (kernels.conv_causal: the im2col rows gathered into the matrix kernel's LDS, never written)
+over the chunk's frames and a two-frame cache of the convolution's own input from the chunks
+before (zeros at the start, the reference's front padding), passed as two frames in front of
+the chunk's, with the weight repacked [Cout][dt][ky][kx][Cin] once at load; the cache then takes
+the last two frames of (cache, chunk). The time convolution of an upsample3d resampler is a (3, 1, 1) causal
 convolution that skips chunk 0 (the reference's "Rep"); its [t][pixels][2C] output is read as
-the interleaved frames 2t, 2t + 1 by the resampler's im2col, with the nearest 2x upsampling of
-the following 3x3 Conv2d folded into its addressing. WanRMSNorm (+ SiLU) is one row kernel.
+the interleaved frames 2t, 2t + 1 by the resampler's convolution, with the nearest 2x upsampling
+of that 3x3 Conv2d folded into its addressing. WanRMSNorm (+ SiLU) is one row kernel.
 The mid block's attention (one head over a frame's pixels with all channels) runs as GEMMs:
 fp32 scores, the row softmax kernel, P V, then the output projection with the residual.
 """
@@ -30,7 +31,6 @@ import torch
 
 from difflet_amd import _lib, kernels
 
-IM2COL_BYTES = 1 << 30  # largest im2col chunk a convolution materializes
 EPS = 1e-12             # F.normalize's eps in WanRMSNorm
 
 
@@ -267,9 +267,8 @@ class WanVaeDecoder:
     def _conv(self, name: str, x: _Chunk, *, cache: Optional[torch.Tensor] = None,
               upsample: bool = False, frames_per_block: int = 1, residual=None,
               out=None) -> _Chunk:
-        """The convolution `name` over the chunk's frames (cache: the two frames before them),
-        in row ranges whose im2col takes at most IM2COL_BYTES; the output's rows are padded to
-        Cout rounded up to 4."""
+        """The convolution `name` over the chunk's frames (cache: the two frames before them) as
+        one implicit GEMM; the output's rows are padded to Cout rounded up to 4."""
         cv = self.conv[name]
         h, w = x.hw
         up = int(upsample)
@@ -286,31 +285,20 @@ class WanVaeDecoder:
             fs, sub, pstride = h * w * ld, 0, ld
         if cv.kt == 1 and cv.ks == 1 and not up and cv.kpad == cv.cin and ld == cv.cin:
             self._gemm(x.rows, cv.w, cv.b, y, residual)   # a 1x1x1 convolution is the GEMM itself
-        elif self.dtype == torch.bfloat16:
+        elif cache is not None:
             # one implicit GEMM; a causal convolution reads its cache as the two frames in front
-            if cache is not None:
-                if x.full is not None:
-                    full = x.full
-                    full[:2].copy_(cache)
-                else:
-                    full = torch.cat([cache, data[:, :, : x.c]])
-                kernels.conv_causal(full, (h, w), cv.cin, frames, cv.w, cv.b, kt=cv.kt, ks=cv.ks,
-                                    upsample=upsample, lead_frames=2, residual=residual, out=y)
+            if x.full is not None:
+                full = x.full
+                full[:2].copy_(cache)
             else:
-                kernels.conv_causal(data, (h, w), cv.cin, frames, cv.w, cv.b, kt=cv.kt, ks=cv.ks,
-                                    upsample=upsample, frames_per_block=frames_per_block,
-                                    frame_stride=fs, sub_stride=sub, pixel_stride=pstride,
-                                    residual=residual, out=y)
+                full = torch.cat([cache, data[:, :, : x.c]])
+            kernels.conv_causal(full, (h, w), cv.cin, frames, cv.w, cv.b, kt=cv.kt, ks=cv.ks,
+                                upsample=upsample, lead_frames=2, residual=residual, out=y)
         else:
-            step = max(1, IM2COL_BYTES // (cv.kpad * cv.w.element_size()))
-            for r0 in range(0, total, step):
-                n = min(step, total - r0)
-                cols = kernels.im2col_causal(data, (h, w), cv.cin, kt=cv.kt, ks=cv.ks, kpad=cv.kpad,
-                                             upsample=upsample, cache=cache,
-                                             frames_per_block=frames_per_block, frame_stride=fs,
-                                             sub_stride=sub, pixel_stride=pstride, row0=r0, rows=n)
-                self._gemm(cols, cv.w, cv.b, y[r0:r0 + n],
-                           None if residual is None else residual[r0:r0 + n])
+            kernels.conv_causal(data, (h, w), cv.cin, frames, cv.w, cv.b, kt=cv.kt, ks=cv.ks,
+                                upsample=upsample, frames_per_block=frames_per_block,
+                                frame_stride=fs, sub_stride=sub, pixel_stride=pstride,
+                                residual=residual, out=y)
         return _Chunk(y.view(frames, ho * wo, np_), frames, (ho, wo), cv.cout)
 
     def _cache(self, state: dict, name: str, x: _Chunk) -> torch.Tensor:
@@ -336,10 +324,10 @@ class WanVaeDecoder:
         return y
 
     def _norm(self, name: str, x: _Chunk, silu: bool, causal: bool = False) -> _Chunk:
-        """causal: the output feeds a causal convolution, which on the bf16 path reads it with
-        its cache in front (frames allocated with two leading ones)."""
+        """causal: the output feeds a causal convolution, which reads it with its cache in front
+        (frames allocated with two leading ones)."""
         pix = x.hw[0] * x.hw[1]
-        lead = 2 if causal and self.dtype == torch.bfloat16 else 0
+        lead = 2 if causal else 0
         full = torch.empty(lead + x.frames, pix, x.c, dtype=self.dtype, device=self.device)
         y = kernels.rms_norm_channels(x.rows[:, : x.c], self.gamma[name], eps=EPS, silu=silu,
                                       out=full[lead:].view(-1, x.c))

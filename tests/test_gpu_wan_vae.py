@@ -89,23 +89,25 @@ CONV_CASES = [
 ]
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("case", CONV_CASES)
-def test_conv_causal_equals_the_im2col_gemm(gpu, case):
-    """The implicit GEMM against im2col rows times the weight on the whole-tile GEMM kernel: the
-    same products in the same order, so bit-identical (and the residual may be the output);
-    both within bf16 rounding of the fp32 convolution of the rows."""
+def test_conv_causal_equals_the_im2col_gemm(gpu, case, dtype):
+    """The implicit GEMM against im2col rows times the weight on the whole-tile GEMM kernel of
+    its dtype (bf16 matrix cores; fp32: the fp32 GEMM): the same products in the same order, so
+    bit-identical (and the residual may be the output); both within output rounding of the
+    fp32 convolution of the rows."""
     kt, ks, up, fpb, lead, frames, h, w, cin, cout, with_res = case
-    print(f"conv_causal {case}", flush=True)
+    print(f"conv_causal {case} {dtype}", flush=True)
     g = torch.Generator().manual_seed(cin * 7 + cout + frames)
     pix = h * w
-    bf = torch.bfloat16
+    dt = dtype
     if fpb == 2:
-        x = torch.randn(frames // 2, pix, 2 * cin, generator=g).to(bf)
+        x = torch.randn(frames // 2, pix, 2 * cin, generator=g).to(dt)
         kw = dict(frames_per_block=2, frame_stride=pix * 2 * cin, sub_stride=cin,
                   pixel_stride=2 * cin)
         cache = None
     else:
-        x = torch.randn(lead + frames, pix, cin, generator=g).to(bf)
+        x = torch.randn(lead + frames, pix, cin, generator=g).to(dt)
         kw = {}
         cache = x[:2] if lead else None
     k = kt * ks * ks * cin
@@ -113,10 +115,10 @@ def test_conv_causal_equals_the_im2col_gemm(gpu, case):
     n = -(-cout // 4) * 4
     wt = torch.zeros(n, kpad)
     wt[:cout, :k] = torch.randn(cout, k, generator=g) * k ** -0.5
-    wt = wt.to(bf)
-    bias = (torch.randn(n, generator=g) * 0.1).to(bf)
+    wt = wt.to(dt)
+    bias = (torch.randn(n, generator=g) * 0.1).to(dt)
     rows = frames * pix * (4 if up else 1)
-    res = (torch.randn(rows, n, generator=g)).to(bf) if with_res else None
+    res = (torch.randn(rows, n, generator=g)).to(dt) if with_res else None
     xg, wg, bg = x.to(gpu), wt.to(gpu), bias.to(gpu)
     out = kernels.conv_causal(xg, (h, w), cin, frames, wg, bg, kt=kt, ks=ks, upsample=up,
                               lead_frames=lead, residual=None if res is None else res.to(gpu),
@@ -125,16 +127,19 @@ def test_conv_causal_equals_the_im2col_gemm(gpu, case):
     cols = kernels.im2col_causal(src.contiguous(), (h, w), cin, kt=kt, ks=ks, kpad=kpad,
                                  upsample=up, cache=None if cache is None else cache.to(gpu),
                                  rows=rows, **kw)
-    ref = torch.empty(rows, n, dtype=bf, device=gpu)
-    if res is None:
+    ref = torch.empty(rows, n, dtype=dt, device=gpu)
+    if dt == torch.float32:
+        kernels.gemm_f32(cols, wg, bg, residual=None if res is None else res.to(gpu), out=ref)
+    elif res is None:
         kernels.gemm_grouped([kernels.Problem(cols, wg, ref, bg)], kind="bf16")
     else:
-        ones = torch.ones(1, n, dtype=bf, device=gpu)
+        ones = torch.ones(1, n, dtype=dt, device=gpu)
         kernels.gemm_grouped([kernels.Problem(cols, wg, ref, bg, gate=ones,
                                               residual=res.to(gpu))],
                              kind="bf16", epilogue=_lib.EPI_GATE_RESIDUAL)
     torch.cuda.synchronize()
-    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    bits = torch.int16 if dt == torch.bfloat16 else torch.int32
+    assert torch.equal(out.view(bits), ref.view(bits))
     f32 = cols.float().cpu() @ wt.float().t() + bias.float()
     if res is not None:
         f32 = f32 + res.float()
@@ -142,8 +147,8 @@ def test_conv_causal_equals_the_im2col_gemm(gpu, case):
         kernels.conv_causal(xg, (h, w), cin, frames, wg, bg, kt=kt, ks=ks, upsample=up,
                             lead_frames=lead, residual=inplace, out=inplace, split=False, **kw)
         torch.cuda.synchronize()
-        assert torch.equal(inplace.view(torch.int16), ref.view(torch.int16))
-    assert rel_l2(out, f32) < 4e-3
+        assert torch.equal(inplace.view(bits), ref.view(bits))
+    assert rel_l2(out, f32) < (4e-3 if dt == torch.bfloat16 else 1e-5)
 
 
 @pytest.mark.parametrize("case", [
@@ -215,7 +220,9 @@ def test_conv_causal_refuses_what_it_cannot_run(gpu):
     wt = torch.zeros(16, 448, dtype=torch.bfloat16, device=gpu)
     with pytest.raises(ValueError, match="overrun"):
         kernels.conv_causal(x, (3, 4), 16, 3, wt, kt=3, ks=3)
-    with pytest.raises(ValueError, match="bf16"):
+    with pytest.raises(ValueError, match="bf16 or fp32"):
+        kernels.conv_causal(x.half(), (3, 4), 16, 2, wt.half(), kt=3, ks=3)
+    with pytest.raises(ValueError, match="dtype"):
         kernels.conv_causal(x.float(), (3, 4), 16, 2, wt, kt=3, ks=3)
     with pytest.raises(ValueError, match="multiple of 64"):
         kernels.conv_causal(x, (3, 4), 16, 2, wt[:, :440].contiguous(), kt=3, ks=3)

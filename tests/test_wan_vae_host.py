@@ -148,10 +148,8 @@ def _cfg(shape):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_host_walk_equals_the_oracle(cpu_kernels, monkeypatch, dtype):
-    """Three latent frames (two temporal upsamplings), a 3 x 5 latent; the im2col chunk cut
-    small so every fp32 convolution runs in several row ranges (bf16: one implicit GEMM each,
-    its cache passed as the two frames in front)."""
-    monkeypatch.setattr(dwan, "IM2COL_BYTES", 1 << 16)
+    """Three latent frames (two temporal upsamplings), a 3 x 5 latent; every convolution one
+    implicit GEMM, a causal one's cache passed as the two frames in front of the chunk's."""
     store = None if dtype == torch.float32 else dtype
     w = ow.weights(SMALL, 5, store)
     dec = dwan.WanVaeDecoder(_cfg(SMALL), lambda n: w[n], dtype=dtype, device="cpu")
