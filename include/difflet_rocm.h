@@ -470,11 +470,12 @@ int difflet_rocm_im2col_causal(const void* x, int64_t frame_stride, int64_t fram
                                void* out, int64_t ldo, int64_t kpad, difflet_stream_t stream);
 
 /* The causal convolution whose rows difflet_rocm_im2col_causal writes, times its packed weight,
- * as one implicit GEMM on the bf16 matrix cores (the rows are gathered into the LDS stage by
- * stage, never written): out[r][o] = bias[o] + sum_k row_r[k] w[o][k] (+ residual[r][o]) for the
- * frames * Ho * Wo output pixels r of the chunk and o < n, rounded to bf16 once; the products
- * and their order are those of the im2col rows' GEMM (difflet_rocm_gemm, whole tiles), so the
- * two agree bit for bit, unless the workspace (difflet_rocm_conv_causal_workspace_bytes; null
+ * as one implicit GEMM (the rows are gathered stage by stage, never written): out[r][o] =
+ * bias[o] + sum_k row_r[k] w[o][k] (+ residual[r][o]) for the frames * Ho * Wo output pixels r
+ * of the chunk and o < n, rounded once. bf16 runs on the bf16 matrix cores (the rows gathered
+ * into the LDS), fp32 on the fp32 GEMM (difflet_rocm_gemm_f32's tiles); the products and their
+ * order are those of the im2col rows' GEMM of the dtype (bf16: difflet_rocm_gemm, whole tiles),
+ * so the two agree bit for bit, unless the workspace (difflet_rocm_conv_causal_workspace_bytes; null
  * and 0 always run whole tiles) lets a small convolution cut its K stages. It replaces
  * WanCausalConv3d.forward and the resampler's Conv2d (modeling_vae.py:121-134, 163-226) in the
  * Wan decoder's bf16 path, and with kt = 1 and one frame the FLUX decoder's 3x3 convolutions
@@ -484,9 +485,10 @@ int difflet_rocm_im2col_causal(const void* x, int64_t frame_stride, int64_t fram
  * frame_stride + (b % frames_per_block) * sub_stride, pixel stride pixel_stride; b < 0 reads
  * zero. A causal convolution passes its two-frame cache as buffer frames 0 and 1 (lead_frames
  * 2); lead_frames 0 with kt = 3 is the first chunk's zero padding. w [n][kpad], the weight
- * [Cout][kt][ks][ks][C] zero-padded to kpad (a multiple of 64) columns and n (a multiple of 4)
- * rows; bias [n] or null; residual [rows][ldr] or null, may equal out [rows][ldo]. bf16 only;
- * channels and strides multiples of 8 elements; the frames span under 2 GiB. */
+ * [Cout][kt][ks][ks][C] zero-padded to kpad (a multiple of 64 for bf16, 4 for fp32) columns
+ * and n (a multiple of 4) rows; bias [n] or null; residual [rows][ldr] or null, may equal out
+ * [rows][ldo]; all of x's dtype. Channels and strides multiples of 16 bytes; bf16 frames span
+ * under 2 GiB. */
 int difflet_rocm_conv_causal(const void* x, int64_t x_elems, int64_t frame_stride,
                              int64_t frames_per_block, int64_t sub_stride, int64_t pixel_stride,
                              int64_t lead_frames, int dtype, int64_t height, int64_t width,
@@ -496,8 +498,8 @@ int difflet_rocm_conv_causal(const void* x, int64_t x_elems, int64_t frame_strid
                              int64_t ldo, void* workspace, int64_t workspace_bytes,
                              difflet_stream_t stream);
 
-/* Workspace bytes difflet_rocm_conv_causal uses for rows = frames * Ho * Wo output pixels, n
- * weight rows and kpad columns on the current device: nonzero when the convolution is too
+/* Workspace bytes difflet_rocm_conv_causal uses (bf16) for rows = frames * Ho * Wo output
+ * pixels, n weight rows and kpad columns on the current device: nonzero when the convolution is too
  * small to fill the compute units (under half a wave of tiles) and its K stages are then cut
  * into ranges whose fp32 partial sums are added in order by a second kernel (the result then
  * differs from the whole-tile GEMM's by fp32 summation order). A smaller workspace runs whole
