@@ -42,7 +42,7 @@ struct ConvArgs {
   uint32_t fstride_b, sub_b, ld_b;  // frame-block, sub-frame and pixel strides of x, bytes
   int lfpb;                      // log2 of frames per block
   int fbase;                     // buffer frame of output frame t's tap dt: t + dt + fbase
-  int w_in, ho, wo, up, half, ks;
+  int w_in, ho, wo, up, half, ks, kt;
   uint32_t po, po_m, wo_m;       // pixels per output frame; magic numbers of po and wo
   uint32_t cin, cin_m;
   int ktot, nk;                  // kt ks^2 C; K stages (kpad / 64)
@@ -56,7 +56,10 @@ struct ConvArgs {
 
 constexpr uint32_t kOutside = 0x80000000u;  // an offset past every buffer (x_bytes < 2^31)
 
-template <int WMW, int NJ>
+// LIN: no upsampling, so a tap moves every pixel by the same offset: each A row keeps its
+// pixel's byte offset and a bit per tap that is inside the frames, and a load is that offset
+// plus the chunk's tap offset when the bit is set (4 VALU operations instead of about 15)
+template <int WMW, int NJ, bool LIN>
 __global__ __launch_bounds__(512, 1) void conv_igemm_kernel(const ConvArgs a) {
   constexpr int WNW = 8 / WMW;
   constexpr int BM = 64 * WMW, BN = 32 * NJ * WNW;
@@ -98,7 +101,8 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_kernel(const ConvArgs a) {
   const int lc0 = (lane & 7) ^ (lane >> 3);
   // arrays whose elements reach target builtins are sized for the largest tile, not by SA, NWJ
   // or NJ: with a template-dependent size the host pass drops the kernel's launch stub
-  int rt[8], ry[8], rxp[8];
+  int rt[8], ry[8], rxp[8];  // LIN: rt = the pixel's byte offset at tap (0, half, half),
+                             // ry = the bits of the taps inside the frames
 #pragma unroll
   for (int i = 0; i < SA; ++i) {
     const uint32_t R = m0 + (uint32_t)((wave * SA + i) * 8 + (lane >> 3));
@@ -106,9 +110,33 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_kernel(const ConvArgs a) {
     const uint32_t t = conv_udiv(R, a.po, a.po_m, p);
     const uint32_t y = conv_udiv(p, (uint32_t)a.wo, a.wo_m, xx);
     const bool in = R < a.rows;
-    rt[i] = (int)t;
-    ry[i] = in ? (int)y : -(1 << 24);
-    rxp[i] = (int)xx;
+    if constexpr (LIN) {
+      // the taps (dt, ky, kx) inside: rows y + ky - half and columns x + kx - half of the
+      // frame, buffer frames t + dt + fbase >= 0; bit (dt ks + ky) ks + kx
+      const int b = (int)t + a.fbase;
+      uint32_t cols = 0, rows = 0, frames = 0;
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        const int d = q - a.half;
+        cols |= (q < a.ks && (uint32_t)((int)xx + d) < (uint32_t)a.wo) ? 1u << q : 0u;
+        rows |= (q < a.ks && (uint32_t)((int)y + d) < (uint32_t)a.ho) ? 1u << q : 0u;
+        frames |= (q < a.kt && b + q >= 0) ? 1u << q : 0u;
+      }
+      uint32_t plane = 0;  // the ks x ks taps of one frame
+#pragma unroll
+      for (int q = 0; q < 3; ++q) plane |= (rows >> q & 1u) ? cols << (q * a.ks) : 0u;
+      uint32_t m = 0;
+#pragma unroll
+      for (int q = 0; q < 3; ++q) m |= (frames >> q & 1u) ? plane << (q * a.ks * a.ks) : 0u;
+      rt[i] = (b >> a.lfpb) * (int)a.fstride_b + (b & ((1 << a.lfpb) - 1)) * (int)a.sub_b +
+              ((int)y * a.w_in + (int)xx) * (int)a.ld_b;
+      ry[i] = in ? (int)m : 0;
+      rxp[i] = 0;
+    } else {
+      rt[i] = (int)t;
+      ry[i] = in ? (int)y : -(1 << 24);
+      rxp[i] = (int)xx;
+    }
   }
   uint32_t w_off[3];
 #pragma unroll
@@ -120,6 +148,7 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_kernel(const ConvArgs a) {
 
   // column chunk lc of stage kt: its tap as a frame offset and a pixel shift, and its channel
   // byte offset (padding columns: a shift that leaves every frame)
+  // (LIN: fo = the tap's bit, 31 past the real columns; cb = its byte offset with the channel's)
   struct Tap {
     int fo, dy, dx;
     uint32_t cb;
@@ -131,13 +160,22 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_kernel(const ConvArgs a) {
     int dt, ky, kx;
     conv_tap(tap, a.ks, dt, ky, kx);
     Tap o;
-    o.fo = dt + a.fbase;
-    o.dy = (int)kk < a.ktot ? ky - a.half : -(1 << 24);
-    o.dx = kx - a.half;
-    o.cb = c * 2;
+    if constexpr (LIN) {
+      o.fo = (int)kk < a.ktot ? tap : 31;
+      o.dy = o.dx = 0;
+      o.cb = (uint32_t)((dt >> a.lfpb) * (int)a.fstride_b +
+                        ((ky - a.half) * a.w_in + (kx - a.half)) * (int)a.ld_b + (int)c * 2);
+    } else {
+      o.fo = dt + a.fbase;
+      o.dy = (int)kk < a.ktot ? ky - a.half : -(1 << 24);
+      o.dx = kx - a.half;
+      o.cb = c * 2;
+    }
     return o;
   };
   auto a_off = [&](int i, const Tap& tp) {
+    if constexpr (LIN)
+      return ((uint32_t)ry[i] >> tp.fo & 1u) ? (uint32_t)rt[i] + tp.cb : kOutside;
     const int f = rt[i] + tp.fo, yy = ry[i] + tp.dy, xs = rxp[i] + tp.dx;
     const bool ok = (uint32_t)yy < (uint32_t)a.ho && (uint32_t)xs < (uint32_t)a.wo && f >= 0;
     const uint32_t pix = (uint32_t)(yy >> a.up) * (uint32_t)a.w_in + (uint32_t)(xs >> a.up);
@@ -479,6 +517,7 @@ extern "C" int difflet_rocm_conv_causal(const void* x, int64_t x_elems, int64_t 
   a.up = upsample;
   a.half = (int)(ks / 2);
   a.ks = (int)ks;
+  a.kt = (int)kt;
   a.po = (uint32_t)po;
   a.po_m = conv_magic((uint32_t)po);
   a.wo_m = conv_magic((uint32_t)wo);
@@ -497,16 +536,27 @@ extern "C" int difflet_rocm_conv_causal(const void* x, int64_t x_elems, int64_t 
   a.ws = (float*)workspace;
   a.tiles = (int)(plan.tiles * plan.ksplit);
   const dim3 grid((unsigned)a.tiles), block(512);
+  // taps at fixed pixel offsets unless the frames are upsampled (or read as interleaved pairs
+  // by a kernel that spans frames)
+  const bool lin = upsample == 0 && (frames_per_block == 1 || kt == 1);
+#define DLT_CONV_LAUNCH(W, J)                                                      \
+  do {                                                                             \
+    if (lin)                                                                       \
+      hipLaunchKernelGGL((conv_igemm_kernel<W, J, true>), grid, block, 0, s, a);  \
+    else                                                                           \
+      hipLaunchKernelGGL((conv_igemm_kernel<W, J, false>), grid, block, 0, s, a); \
+  } while (0)
   if (plan.wmw == 8 && plan.nj == 1)
-    hipLaunchKernelGGL((conv_igemm_kernel<8, 1>), grid, block, 0, s, a);
+    DLT_CONV_LAUNCH(8, 1);
   else if (plan.wmw == 8 && plan.nj == 2)
-    hipLaunchKernelGGL((conv_igemm_kernel<8, 2>), grid, block, 0, s, a);
+    DLT_CONV_LAUNCH(8, 2);
   else if (plan.wmw == 8)
-    hipLaunchKernelGGL((conv_igemm_kernel<8, 3>), grid, block, 0, s, a);
+    DLT_CONV_LAUNCH(8, 3);
   else if (plan.nj == 2)
-    hipLaunchKernelGGL((conv_igemm_kernel<4, 2>), grid, block, 0, s, a);
+    DLT_CONV_LAUNCH(4, 2);
   else
-    hipLaunchKernelGGL((conv_igemm_kernel<4, 3>), grid, block, 0, s, a);
+    DLT_CONV_LAUNCH(4, 3);
+#undef DLT_CONV_LAUNCH
   if (plan.ksplit > 1) {
     const int64_t items = rows * (n / 4);
     hipLaunchKernelGGL(conv_split_reduce_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256),
