@@ -128,8 +128,11 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_kernel(const ConvArgs a) {
       uint32_t m = 0;
 #pragma unroll
       for (int q = 0; q < 3; ++q) m |= (frames >> q & 1u) ? plane << (q * a.ks * a.ks) : 0u;
-      rt[i] = (b >> a.lfpb) * (int)a.fstride_b + (b & ((1 << a.lfpb) - 1)) * (int)a.sub_b +
-              ((int)y * a.w_in + (int)xx) * (int)a.ld_b;
+      // modulo 2^32 (b < 0 before a causal convolution's first frames, t past the last row):
+      // every offset a set bit selects is in range
+      rt[i] = (int)((uint32_t)(b >> a.lfpb) * a.fstride_b +
+                    (uint32_t)(b & ((1 << a.lfpb) - 1)) * a.sub_b +
+                    (y * (uint32_t)a.w_in + xx) * a.ld_b);
       ry[i] = in ? (int)m : 0;
       rxp[i] = 0;
     } else {
@@ -163,8 +166,8 @@ __global__ __launch_bounds__(512, 1) void conv_igemm_kernel(const ConvArgs a) {
     if constexpr (LIN) {
       o.fo = (int)kk < a.ktot ? tap : 31;
       o.dy = o.dx = 0;
-      o.cb = (uint32_t)((dt >> a.lfpb) * (int)a.fstride_b +
-                        ((ky - a.half) * a.w_in + (kx - a.half)) * (int)a.ld_b + (int)c * 2);
+      o.cb = (uint32_t)(dt >> a.lfpb) * a.fstride_b +
+             (uint32_t)((ky - a.half) * a.w_in + (kx - a.half)) * a.ld_b + c * 2;
     } else {
       o.fo = dt + a.fbase;
       o.dy = (int)kk < a.ktot ? ky - a.half : -(1 << 24);
