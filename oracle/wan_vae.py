@@ -159,7 +159,9 @@ def rms_norm(x, gamma, shape: WanVaeShape):
 
 
 def _norm_silu(w, name, x, shape, r):
-    return r(F.silu(r(rms_norm(x, w[name], shape))))
+    """RMS norm then SiLU, stored once (the device computes both in fp32 and rounds the result;
+    storing the norm's output as well moves the bf16 decode by 1.8e-2 on the small decoder)."""
+    return r(F.silu(rms_norm(x, w[name], shape)))
 
 
 def causal_conv(x, wt, b, cache=None):

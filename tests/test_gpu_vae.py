@@ -80,10 +80,12 @@ SMALL = ovae.VaeShape(latent_channels=16, block_out_channels=(32, 32, 64, 64), l
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("hw", [(8, 8), (6, 10)])
-def test_small_decoder_matches_oracle(gpu, dtype, hw):
+def test_small_decoder_matches_oracle(gpu, dtype, hw, parity):
     """Four up blocks of two resnets (one with a 1x1 shortcut, 64 -> 32 channels), three
     upsamplings, the mid-block attention over 64 or 60 latent pixels (60: the P V GEMM's K
-    padded)."""
+    padded). bf16 within 2e-2: this random-weight decoder stored in bf16 moves 1.25e-2 when the
+    oracle itself only sums its convolutions in fp64 instead of fp32 (the rounding flips of
+    one layer change the next layer's), so 1e-2 sits below the oracle's own noise."""
     print(f"vae small {dtype} {hw}", flush=True)
     w = ovae.weights(SMALL, 8, None if dtype == torch.float32 else dtype)
     dec = dvae.VaeDecoder(_cfg(SMALL), lambda n: w[n], dtype=dtype, device=gpu)
@@ -95,7 +97,10 @@ def test_small_decoder_matches_oracle(gpu, dtype, hw):
     assert out.dtype == dtype and tuple(out.shape) == tuple(ref.shape)
     e = rel_l2(out, ref)
     print(f"  rel L2 {e:.3e}", flush=True)
-    assert e < (1e-4 if dtype == torch.float32 else 2e-2)
+    bound = 1e-4 if dtype == torch.float32 else 2e-2
+    parity(f"small FLUX VAE decode {str(dtype)[6:]}, rel L2 vs oracle at the device's rounding "
+           "points", e, bound)
+    assert e < bound
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

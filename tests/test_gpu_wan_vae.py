@@ -1,7 +1,8 @@
 """Wan's 3D causal VAE decoder on the HIP path: its kernels against torch statements of their
 contracts (bit-exact gathers, fp32-law norms), decoders against the fp32 oracle
 (oracle/wan_vae.py: fp32 <= 1e-4, bf16 <= 2e-2 against the oracle with the device's rounding
-points), Wan's real widths on a small latent, and the full 21-frame 480 x 832 decode through
+points: a random-weight decoder stored in bf16 moves 1.5-6.8e-3 when the oracle only sums its
+convolutions in fp64, and 1.3-1.5e-2 from its fp32 form), Wan's real widths on a small latent, and the full 21-frame 480 x 832 decode through
 properties (finite, bit-identical rerun, causal frame by frame, the first frame alone)."""
 
 import pytest
@@ -258,7 +259,7 @@ SMALL = ow.WanVaeShape(base_dim=8, z_dim=16, dim_mult=(1, 2, 4, 4), num_res_bloc
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("t,hw", [(3, (4, 6)), (2, (3, 5))])
-def test_small_decoder_matches_oracle(gpu, dtype, t, hw):
+def test_small_decoder_matches_oracle(gpu, dtype, t, hw, parity):
     """Two temporal upsamplings and one spatial, a resnet with a 1x1 shortcut (16 -> 32
     channels), the mid-block attention over 24 or 15 pixels (15: the scores' key count padded)."""
     print(f"wan vae small {dtype} t={t} {hw}", flush=True)
@@ -272,11 +273,14 @@ def test_small_decoder_matches_oracle(gpu, dtype, t, hw):
     assert out.dtype == dtype and tuple(out.shape) == tuple(ref.shape)
     e = rel_l2(out, ref)
     print(f"  rel L2 {e:.3e}", flush=True)
-    assert e < (1e-4 if dtype == torch.float32 else 2e-2)
+    bound = 1e-4 if dtype == torch.float32 else 2e-2
+    parity(f"small Wan VAE decode {str(dtype)[6:]}, rel L2 vs oracle at the device's rounding "
+           "points", e, bound)
+    assert e < bound
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_wan_widths_on_a_small_latent_match_oracle(gpu, dtype):
+def test_wan_widths_on_a_small_latent_match_oracle(gpu, dtype, parity):
     """Wan 2.2's decoder (384 / 192 / 96 channels) on two 6 x 10 latent frames (5 frames of
     48 x 80); and its mid-block attention alone on a full 60 x 104 latent frame (6240
     pixels, one head of 384 channels)."""
@@ -292,6 +296,7 @@ def test_wan_widths_on_a_small_latent_match_oracle(gpu, dtype):
     assert tuple(out.shape) == (1, 3, 5, 48, 80)
     e = rel_l2(out, ref)
     print(f"  decode rel L2 {e:.3e}", flush=True)
+    parity(f"Wan VAE widths decode {str(dtype)[6:]}, rel L2 vs oracle", e, tol)
     assert e < tol
     r = (lambda x: x) if store is None else (lambda x: x.to(store).float())
     x = r(torch.randn(1, 384, 1, 60, 104, generator=torch.Generator().manual_seed(12)))
