@@ -1,23 +1,25 @@
-// The Wan VAE decoder's causal convolutions as implicit GEMMs on the bf16 matrix cores: the GEMM
-// of the im2col rows with the packed weight, where each K stage gathers its 64 columns of the
-// im2col rows straight from the channels-last frames into the LDS, so the rows (27 C columns
-// per output pixel) are never written to memory.
+// The VAE decoders' convolutions as implicit GEMMs on the bf16 matrix cores: the GEMM of the
+// im2col rows with the packed weight, where each K stage gathers its 64 columns of the im2col
+// rows straight from the channels-last frames into the LDS, so the rows (9 C or 27 C columns per
+// output pixel) are never written to memory. fp32 convolutions take the fp32 GEMM with the same
+// gather in its register-staged loader (launch_conv_f32, gemm_f32.hip).
 //
 // The convolution is WanCausalConv3d (difflet/models/wan/vae/modeling_vae.py:95-134: kernel
-// (kt, ks, ks), kt - 1 frames of zero or cached padding in front, ks / 2 pixels around) and the
-// resampler's per-frame nn.Conv2d(3, padding=1) after a nearest 2x upsampling (:163-226). Column
-// k of an output pixel's row is tap (dt, ky, kx) = k / C and channel k % C, taps in (dt, ky, kx)
-// order, the weight's layout [Cout][kt][ks][ks][C] (zero past kt ks^2 C).
+// (kt, ks, ks), kt - 1 frames of zero or cached padding in front, ks / 2 pixels around), the
+// resampler's per-frame nn.Conv2d(3, padding=1) after a nearest 2x upsampling (:163-226), and
+// with kt = 1 on one frame the FLUX decoder's 3x3 convolutions. Column k of an output pixel's row
+// is tap (dt, ky, kx) = k / C and channel k % C, taps in (dt, ky, kx) order, the weight's layout
+// [Cout][kt][ks][ks][C] (zero past kt ks^2 C).
 //
 // Tiles: 8 waves, WMW along the output pixels and 8 / WMW along the output channels, each wave 64
 // pixels x 32 NJ channels (2 x NJ MFMA 32x32x16 tiles). Cout <= 96 runs one channel tile of
 // 32 NJ with 512 pixels (the 96-channel full-resolution stage: no MFMA column wasted); wider
-// convolutions run 256 x 192 or 256 x 128 tiles. A stage is 64 K elements (128 bytes) of every row, staged
-// by direct-to-LDS buffer loads in two LDS slots, 8 rows x 128 B per load instruction, chunk c
-// of row r at c ^ swz8(r) as in the GEMM kernel. Each lane's 16-byte chunk of an A row is 8
-// channels of one tap of one pixel (C is a multiple of 8), so its address is the pixel's shifted
-// position in its frame: out-of-frame taps, padding columns and rows past the end take an
-// offset past the buffer, which the load's range check turns into zeros.
+// convolutions run 256 x 192 or 256 x 128 tiles. A stage is 64 K elements (128 bytes) of every
+// row, staged by direct-to-LDS buffer loads in two LDS slots, 8 rows x 128 B per load
+// instruction, chunk c of row r at c ^ swz8(r) as in the GEMM kernel. Each lane's 16-byte chunk
+// of an A row is 8 channels of one tap of one pixel (C is a multiple of 8), so its address is the
+// pixel's shifted position in its frame: out-of-frame taps, padding columns and rows past the
+// end take an offset past the buffer, which the load's range check turns into zeros.
 
 #include "common.hpp"
 
