@@ -345,7 +345,8 @@ __global__ __launch_bounds__(256) void conv_split_reduce_kernel(const float* __r
   const int64_t r = i / ng;
   const int c = (int)(i - r * ng) * 4;
   f32x4 v = *reinterpret_cast<const f32x4*>(ws + r * n + c);
-  for (int p = 1; p < ksplit; ++p) v += *reinterpret_cast<const f32x4*>(ws + ((int64_t)p * rows + r) * n + c);
+  for (int p = 1; p < ksplit; ++p)
+    v += *reinterpret_cast<const f32x4*>(ws + ((int64_t)p * rows + r) * n + c);
   float o[4] = {v[0], v[1], v[2], v[3]};
   if (bias) {
     const u32x2 b = *reinterpret_cast<const u32x2*>(bias + c);
