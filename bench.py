@@ -1,7 +1,7 @@
 """Benchmark: one DiT denoise step on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload flux|qwen|wan|weights|compile|t5|umt5|vae|wanvae]
+                    [--workload flux|qwen|wan|weights|compile|t5|umt5|vae|wanvae|qwenvae]
                     [--kinds bf16,fp8] [--no-cpu] [--calibrate-copy]
 
 flux (default): the full FLUX.1-dev-shaped transformer forward of one denoise step, batch 1,
@@ -28,6 +28,8 @@ vae: FLUX's VAE decoder after the loop, a 128 x 128 x 16 latent to a 1024 x 1024
 and fp32; `value` is the bf16 decode in ms.
 wanvae: Wan 2.2's 3D causal VAE decoder after the loop, a 21 x 60 x 104 x 16 latent to 81
 frames of 480 x 832, bf16 and fp32; `value` is the bf16 decode in ms.
+qwenvae: the same decoder on Qwen-Image's one latent frame, 166 x 166 x 16 to one 1328 x 1328
+image, bf16 and fp32; `value` is the bf16 decode in ms.
 Weights are random N(0, 0.02) drawn on the device (norm weights ones); inputs N(0, 1); the
 encoders and the decoder draw their weights with their initializations' scales.
 
@@ -94,7 +96,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="flux",
                     choices=("flux", "qwen", "wan", "weights", "compile", "t5", "umt5", "vae",
-                             "wanvae"))
+                             "wanvae", "qwenvae"))
     ap.add_argument("--kinds", default=None,
                     help="comma list (flux: bf16,fp8 by default; qwen: mx,bf16)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -699,21 +701,24 @@ def run_stage(args, torch, log):
             log(f"[{args.workload}] {dt}: {ms:.2f} ms")
             del enc
             torch.cuda.empty_cache()
-    elif args.workload == "wanvae":
+    elif args.workload in ("wanvae", "qwenvae"):
         from difflet_amd.vae import wan as dwan
 
         cfg = dwan.WAN_VAE
-        z = torch.randn(1, 16, 21, 60, 104, generator=torch.Generator().manual_seed(SEED)).to(dev)
-        flops = wan_vae_flops(cfg, 21, 60, 104)
+        lat = (21, 60, 104) if args.workload == "wanvae" else (1, 166, 166)
+        z = torch.randn(1, 16, *lat, generator=torch.Generator().manual_seed(SEED)).to(dev)
+        flops = wan_vae_flops(cfg, *lat)
         workload = ("Wan 2.2 VAE decoder (3D causal), 21 x 60 x 104 x 16 latent -> 81 frames of "
-                    "480 x 832 RGB")
+                    "480 x 832 RGB" if args.workload == "wanvae" else
+                    "Qwen-Image VAE decoder (Wan's 3D causal decoder on one frame), 166 x 166 x "
+                    "16 latent -> 1328 x 1328 RGB")
         for dt in (torch.bfloat16, torch.float32):
             dec = dwan.WanVaeDecoder(cfg, dwan.random_param_source(cfg, SEED, dev), dtype=dt,
                                      device=dev)
             ms, med = _time(lambda: dec.decode(z), args.steps, args.warmup, torch)
             res[str(dt).split(".")[1]] = {"ms": round(ms, 3), "median_ms": round(med, 3),
                                           "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
-            log(f"[wanvae] {dt}: {ms:.2f} ms")
+            log(f"[{args.workload}] {dt}: {ms:.2f} ms")
             del dec
             torch.cuda.empty_cache()
     else:
@@ -770,7 +775,7 @@ def main():
         return run_weights(args, torch, log)
     if args.workload == "compile":
         return run_compile(args, torch, log)
-    if args.workload in ("t5", "umt5", "vae", "wanvae"):
+    if args.workload in ("t5", "umt5", "vae", "wanvae", "qwenvae"):
         return run_stage(args, torch, log)
     wl = WORKLOADS[args.workload]()
     kinds = [k for k in (args.kinds or ",".join(wl.kinds)).split(",") if k]

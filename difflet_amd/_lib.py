@@ -25,7 +25,7 @@ F32, BF16, F16, U8, BOOL, I32 = 0, 1, 2, 3, 4, 5
 # enum difflet_status
 OK, EINVAL, EUNSUPPORTED, ELAUNCH = 0, 1, 2, 3
 # enum difflet_epilogue
-EPI_NONE, EPI_GELU, EPI_GATE_RESIDUAL, EPI_GELU_MX = 0, 1, 2, 3
+EPI_NONE, EPI_GELU, EPI_GATE_RESIDUAL, EPI_GELU_MX, EPI_F32 = 0, 1, 2, 3, 4
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64

@@ -547,6 +547,35 @@ __global__ __launch_bounds__(128 * WN, 1) void gemm_kernel(const GemmArgs args) 
   // is all in or all out). Column vectors (bias, gate, W scales) are read once for the whole
   // tile, and each row block's residual is read before any of its stores: the residual may
   // alias C, so loads left between stores would each wait out a full memory latency.
+  if constexpr (EPI == DIFFLET_EPI_F32) {
+    // fp32 C = acc (+ bias), straight from the accumulators: 16 bytes per lane and register
+    // group (the scores of the VAE decoders' mid-block attention, which a softmax reads next)
+    float* C = reinterpret_cast<float*>(P.c);
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t n = n0 + wn * WTN + j * 32 + q * 8 + fhalf * 4;
+        if (n >= N) continue;
+        float b[4] = {0.f, 0.f, 0.f, 0.f};
+        if (P.bias) {
+          const u32x2 bv = *reinterpret_cast<const u32x2*>(reinterpret_cast<const bf16*>(P.bias) + n);
+          b[0] = bf16bits_to_f32(bv[0] & 0xffffu);
+          b[1] = bf16bits_to_f32(bv[0] >> 16);
+          b[2] = bf16bits_to_f32(bv[1] & 0xffffu);
+          b[3] = bf16bits_to_f32(bv[1] >> 16);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t m = m0 + wm * 128 + i * 32 + frow;
+          if (m >= M) continue;
+          const f32x4 v = {acc[i][j][4 * q] + b[0], acc[i][j][4 * q + 1] + b[1],
+                           acc[i][j][4 * q + 2] + b[2], acc[i][j][4 * q + 3] + b[3]};
+          *reinterpret_cast<f32x4*>(C + m * P.ldc + n) = v;
+        }
+      }
+    continue;  // the next piece (split workgroups), or the end of the loop
+  }
   const float* ws = reinterpret_cast<const float*>(P.w_scale);
   // fused q/k RMSNorm + RoPE: this tile's 256 columns are two heads of q or of k; a head's 128
   // columns are the 64 of waves wn = 2 h and 2 h + 1, whose per-row sums of squares meet in LDS
@@ -1038,8 +1067,12 @@ static int gemm_launch(const char* name, int nproblems, const difflet_gemm_probl
   DLT_REQUIRE(n < (1LL << 30) && k < (1LL << 30), DIFFLET_EINVAL, "%s: n or k too large", name);
   DLT_REQUIRE(n % 4 == 0, DIFFLET_EINVAL, "%s: n = %lld must be a multiple of 4", name,
               (long long)n);
-  DLT_REQUIRE(epilogue >= DIFFLET_EPI_NONE && epilogue <= DIFFLET_EPI_GELU_MX,
+  DLT_REQUIRE(epilogue >= DIFFLET_EPI_NONE && epilogue <= DIFFLET_EPI_F32,
               DIFFLET_EINVAL, "%s: unknown epilogue %d", name, epilogue);
+  const bool f32_out = epilogue == DIFFLET_EPI_F32;
+  DLT_REQUIRE(!f32_out || (E == Elem::BF16 && !qk), DIFFLET_EUNSUPPORTED,
+              "%s: the fp32-output epilogue runs on the bf16 GEMM without the q/k norm", name);
+  if (f32_out) workspace = nullptr;  // whole tiles
   const bool mx_out = epilogue == DIFFLET_EPI_GELU_MX;
   DLT_REQUIRE(!mx_out || E == Elem::MX, DIFFLET_EUNSUPPORTED,
               "%s: the GELU -> MXFP8 epilogue runs on the MXFP8 GEMM only", name);
@@ -1061,7 +1094,7 @@ static int gemm_launch(const char* name, int nproblems, const difflet_gemm_probl
                 "%s: leading dimensions smaller than the matrix in problem %d", name, i);
     DLT_REQUIRE((q.lda * EB) % 16 == 0 && (q.ldw * EB) % 16 == 0 && q.ldc % 4 == 0 &&
                     ((uintptr_t)q.a & 15) == 0 && ((uintptr_t)q.w & 15) == 0 &&
-                    ((uintptr_t)q.c & 7) == 0,
+                    ((uintptr_t)q.c & (f32_out ? 15 : 7)) == 0,
                 DIFFLET_EINVAL, "%s: operands must be 16-byte aligned row by row", name);
     DLT_REQUIRE((int64_t)q.m * q.lda * EB < (1LL << 32) && n * q.ldw * EB < (1LL << 32),
                 DIFFLET_EUNSUPPORTED, "%s: an operand exceeds 4 GiB", name);
@@ -1190,6 +1223,10 @@ static int gemm_launch(const char* name, int nproblems, const difflet_gemm_probl
     case 2 * DIFFLET_EPI_GELU_MX:
       if constexpr (E == Elem::MX)
         go(integral_constant<int, DIFFLET_EPI_GELU_MX>{}, std::false_type{});
+      break;
+    case 2 * DIFFLET_EPI_F32:
+      if constexpr (E == Elem::BF16)
+        go(integral_constant<int, DIFFLET_EPI_F32>{}, std::false_type{});
       break;
     default:
       go(integral_constant<int, DIFFLET_EPI_GATE_RESIDUAL>{}, std::false_type{});

@@ -174,14 +174,44 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* __restri
   __shared__ float red[4];
   const float* row = s + (int64_t)blockIdx.x * lds;
   T* prow = p + (int64_t)blockIdx.x * ldp;
-  float mx = -INFINITY;
-  for (int64_t c = threadIdx.x; c < cols; c += 256) mx = fmaxf(mx, row[c] * scale);
-  mx = block_max<4>(mx, red);
-  float sum = 0.f;
-  for (int64_t c = threadIdx.x; c < cols; c += 256) sum += __expf(row[c] * scale - mx);
-  sum = block_sum<4>(sum, red);
+  // rows of 16-byte runs when both strides and bases allow (the scores of the decoders); the
+  // rest of a row, or every element otherwise, one at a time
+  const bool vec = (lds & 3) == 0 && ((uintptr_t)s & 15) == 0 && (ldp & 3) == 0 &&
+                   ((uintptr_t)p & (4 * sizeof(T) - 1)) == 0;
+  const int64_t nv = vec ? cols >> 2 : 0;
+  // one read for both statistics: each thread's running max and its sum of exp(x - max),
+  // rescaled when the max moves; then the block's max and the sums rescaled to it
+  float m = -INFINITY, sum = 0.f;
+  for (int64_t v = threadIdx.x; v < nv; v += 256) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(row + 4 * v);
+    const float a = x[0] * scale, b = x[1] * scale, c = x[2] * scale, d = x[3] * scale;
+    const float nm = fmaxf(m, fmaxf(fmaxf(a, b), fmaxf(c, d)));
+    sum = sum * __expf(m - nm) + __expf(a - nm) + __expf(b - nm) + __expf(c - nm) +
+          __expf(d - nm);
+    m = nm;
+  }
+  for (int64_t c = 4 * nv + threadIdx.x; c < cols; c += 256) {
+    const float x = row[c] * scale;
+    const float nm = fmaxf(m, x);
+    sum = sum * __expf(m - nm) + __expf(x - nm);
+    m = nm;
+  }
+  const float mx = block_max<4>(m, red);
+  sum = block_sum<4>(m == -INFINITY ? 0.f : sum * __expf(m - mx), red);
   const float inv = 1.0f / sum;
-  for (int64_t c = threadIdx.x; c < cols; c += 256)
+  for (int64_t v = threadIdx.x; v < nv; v += 256) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(row + 4 * v);
+    float o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = __expf(x[e] * scale - mx) * inv;
+    if constexpr (sizeof(T) == 2) {
+      const u32x2 w = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+      *reinterpret_cast<u32x2*>(prow + 4 * v) = w;
+    } else {
+      *reinterpret_cast<f32x4*>(prow + 4 * v) = f32x4{o[0], o[1], o[2], o[3]};
+    }
+  }
+  for (int64_t c = 4 * nv + threadIdx.x; c < cols; c += 256)
     Elt<T>::store(prow + c, __expf(row[c] * scale - mx) * inv);
 }
 

@@ -329,6 +329,13 @@ def gemm_grouped(problems: Sequence[Problem], *, kind: str = "bf16",
                 raise ValueError("the GELU -> MXFP8 epilogue writes e4m3 codes [m, n] (row "
                                  "stride a multiple of 8) and uint8 scales [m, n / 32]; n % 32 "
                                  "== 0")
+        elif epilogue == _lib.EPI_F32:
+            if kind != "bf16" or qk is not None:
+                raise ValueError("the fp32-output epilogue runs on the bf16 GEMM without the "
+                                 "q/k norm")
+            if p.c.dtype != torch.float32 or p.c.stride(0) % 4 or p.c.data_ptr() % 16:
+                raise ValueError("the fp32-output epilogue writes fp32 C (row stride a multiple "
+                                 "of 4, 16-byte aligned)")
         elif p.c.dtype != torch.bfloat16:
             raise TypeError("GEMM output is bf16")
         _check_epilogue_operands(p, i, kind, n, k, epilogue)
@@ -679,6 +686,22 @@ def timestep_embedding(t: torch.Tensor, dim: int, *, flip_sin_to_cos: bool,
 
 
 # ------------------------------------------------------------------------ text encoders
+def gemm_bf16_f32out(a: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """A W^T for bf16 a [M, K] and w [N, K] (K a multiple of 64) on the bf16 matrix cores, the
+    fp32 accumulators stored as they are: [M, N] fp32 (a view of [M, N rounded up to 4], w's
+    missing rows zero). The VAE decoders' mid-block attention scores."""
+    m, k = a.shape
+    n = w.shape[0]
+    npad = -(-n // 4) * 4
+    if npad != n:
+        w2 = torch.zeros(npad, k, dtype=w.dtype, device=w.device)
+        w2[:n] = w
+        w = w2
+    y = torch.empty(m, npad, dtype=torch.float32, device=a.device)
+    gemm_grouped([Problem(a, w, y)], kind="bf16", epilogue=_lib.EPI_F32)
+    return y[:, :n]
+
+
 def gemm_f32(a: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, *,
              residual: torch.Tensor | None = None, out: torch.Tensor | None = None
              ) -> torch.Tensor:

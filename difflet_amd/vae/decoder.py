@@ -250,9 +250,12 @@ class VaeDecoder:
         wqkv, bqkv = self.lin["qkv"]
         qkv = self._gemm(n, wqkv, bqkv, torch.empty(pix, 3 * c, dtype=self.dtype, device=self.device))
         q, k = qkv[:, :c], qkv[:, c:2 * c]
-        if self.dtype != torch.float32:
-            q, k = q.float(), k.float()
-        s = kernels.gemm_f32(q, k)
+        if self.dtype == torch.bfloat16 and c % 64 == 0:
+            s = kernels.gemm_bf16_f32out(q, k)  # fp32 scores from the bf16 matrix cores
+        else:
+            if self.dtype != torch.float32:
+                q, k = q.float(), k.float()
+            s = kernels.gemm_f32(q, k)
         # P V: K = pixels, zero-padded to the GEMM's K multiple when it is not one
         kp = _ceil(pix, self.kq)
         alloc = torch.empty if kp == pix else torch.zeros

@@ -356,13 +356,16 @@ class WanVaeDecoder:
             rows = slice(f * pix, (f + 1) * pix)
             qkv = self._conv(f"{pre}.to_qkv", _Chunk(n.data[f:f + 1], 1, x.hw, c)).rows
             q, k = qkv[:, :c], qkv[:, c:2 * c]
-            if self.dtype != torch.float32 or pix % 4:
-                # fp32 scores; the fp32 GEMM's N (keys) padded to a multiple of 4 with zero
-                # keys, whose scores the softmax never reads (cols = pix)
-                kf = torch.zeros(_ceil(pix, 4), c, dtype=torch.float32, device=self.device)
-                kf[:pix] = k
-                q, k = q.float(), kf
-            s = kernels.gemm_f32(q, k)
+            if self.dtype == torch.bfloat16 and c % 64 == 0:
+                s = kernels.gemm_bf16_f32out(q, k)  # fp32 scores from the bf16 matrix cores
+            else:
+                if self.dtype != torch.float32 or pix % 4:
+                    # fp32 scores; the fp32 GEMM's N (keys) padded to a multiple of 4 with zero
+                    # keys, whose scores the softmax never reads (cols = pix)
+                    kf = torch.zeros(_ceil(pix, 4), c, dtype=torch.float32, device=self.device)
+                    kf[:pix] = k
+                    q, k = q.float(), kf
+                s = kernels.gemm_f32(q, k)
             p = alloc(pix, kp, dtype=self.dtype, device=self.device)
             kernels.softmax_rows(s[:, :pix], 1.0 / math.sqrt(c), dtype=self.dtype, out=p[:, :pix])
             del s

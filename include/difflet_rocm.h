@@ -135,7 +135,12 @@ enum difflet_epilogue {
    * act_col_start 0, no fused q/k norm; ldc and ld_c_scale multiples of 8. The reference's
    * device MX linear quantizes its activations inside the matmul kernel
    * (difflet/backends/neuron/ops_impl/fp8_kernels.py:46-58). */
-  DIFFLET_EPI_GELU_MX = 3
+  DIFFLET_EPI_GELU_MX = 3,
+  /* bf16 GEMM only: C = acc + bias stored as fp32 (C [m, n] fp32, row stride ldc floats, 16-byte
+   * aligned), no fused q/k norm, never split: the fp32 scores of the VAE decoders' mid-block
+   * attention (one head of all channels, 384 or 512 wide, which the flash kernels do not
+   * take), whose reference (SDPA in the model dtype) keeps them in fp32 before the softmax. */
+  DIFFLET_EPI_F32 = 4
 };
 
 typedef struct difflet_gemm_problem {

@@ -139,3 +139,17 @@ def test_problems_without_rows_are_dropped_before_any_check():
     kernels.gemm_grouped([empty], epilogue=_lib.EPI_GATE_RESIDUAL)
     with pytest.raises(ValueError, match=DEVICE_MSG):
         kernels.gemm_grouped([empty, _gated()], epilogue=_lib.EPI_GATE_RESIDUAL)
+
+
+def test_fp32_output_epilogue_checks():
+    """EPI_F32: fp32 C from the bf16 GEMM only, 16-byte rows, no q/k norm."""
+    f32 = Problem(_bf16(M, K), _bf16(N, K), torch.zeros(M, N))
+    with pytest.raises(ValueError, match=DEVICE_MSG):
+        _run(f32, "bf16", _lib.EPI_F32)
+    with pytest.raises(ValueError, match="fp32 C"):
+        _run(_prob(), "bf16", _lib.EPI_F32)  # bf16 C
+    with pytest.raises(ValueError, match="fp32 C"):
+        _run(Problem(_bf16(M, K), _bf16(N, K), torch.zeros(M, N + 2)[:, :N]), "bf16",
+             _lib.EPI_F32)
+    with pytest.raises(ValueError, match="bf16 GEMM"):
+        _run(_prob("fp8"), "fp8", _lib.EPI_F32)

@@ -67,11 +67,16 @@ def test_im2col_rows_are_exact(gpu, dtype, h, w, c, up):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_softmax_rows(gpu, dtype):
-    g = torch.Generator().manual_seed(5)
-    s = torch.randn(300, 1030, generator=g) * 20
-    out = kernels.softmax_rows(s.to(gpu), 0.044, dtype=dtype)
-    ref = torch.softmax(s * 0.044, dim=-1)
+@pytest.mark.parametrize("cols,ld", [(1030, 1030), (1024, 1024), (6241, 6244), (15, 16)])
+def test_softmax_rows(gpu, dtype, cols, ld):
+    """Rows in 16-byte runs (ld a multiple of 4) and one element at a time (1030), a ragged tail
+    (6241, 15), and a row maximum that moves late (a ramp), against torch.softmax."""
+    g = torch.Generator().manual_seed(5 + cols)
+    s = torch.randn(300, ld, generator=g) * 20
+    s[:, : cols // 2] -= 40.0  # the running maximum jumps halfway along each row
+    out = torch.empty(300, ld, dtype=dtype, device=gpu)[:, :cols]
+    kernels.softmax_rows(s.to(gpu)[:, :cols], 0.044, dtype=dtype, out=out)
+    ref = torch.softmax(s[:, :cols] * 0.044, dim=-1)
     assert rel_l2(out, ref) < (2e-6 if dtype == torch.float32 else 4e-3)
 
 
@@ -150,3 +155,18 @@ def test_flux_vae_full_decode_bf16_and_fp32(gpu):
     e = rel_l2(outs[torch.bfloat16], outs[torch.float32])
     print(f"  bf16 vs fp32 rel L2 {e:.3e}", flush=True)
     assert e < 5e-2
+
+
+@pytest.mark.parametrize("m,n,k", [(1000, 1003, 384), (6240, 6240, 384), (300, 4096, 512)])
+def test_bf16_gemm_with_fp32_output(gpu, m, n, k):
+    """The mid-block attention's scores: bf16 q k^T with the fp32 accumulators stored as they
+    are (the products exact, sums in fp32), keys padded to a multiple of 4."""
+    print(f"bf16 gemm fp32 out {m} x {n} x {k}", flush=True)
+    g = torch.Generator().manual_seed(m + n)
+    a = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    w = torch.randn(n, k, generator=g).to(torch.bfloat16)
+    s = kernels.gemm_bf16_f32out(a.to(gpu), w.to(gpu))
+    torch.cuda.synchronize()
+    assert s.dtype == torch.float32 and tuple(s.shape) == (m, n)
+    ref = a.double() @ w.double().t()
+    assert rel_l2(s, ref) < 1e-6
