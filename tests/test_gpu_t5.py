@@ -130,7 +130,7 @@ SMALL_UMT5 = dataclasses.replace(SMALL, per_layer_bias=True)
 
 @pytest.mark.parametrize("shape", [SMALL, SMALL_UMT5], ids=["t5", "umt5"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_encoder_matches_oracle(gpu, shape, dtype):
+def test_encoder_matches_oracle(gpu, shape, dtype, parity):
     print(f"encoder {'umt5' if shape.per_layer_bias else 't5'} {dtype}", flush=True)
     w = ot5.weights(shape, 21, None if dtype == torch.float32 else dtype)
     enc = T5Encoder(_cfg(shape), lambda n: w[n], dtype=dtype, device=gpu)
@@ -142,11 +142,14 @@ def test_encoder_matches_oracle(gpu, shape, dtype):
     assert out.dtype == dtype and tuple(out.shape) == (2, 150, shape.d_model)
     e = rel_l2(out, ref)
     print(f"  rel L2 {e:.3e}", flush=True)
-    assert e < (1e-5 if dtype == torch.float32 else 1e-2)
+    bound = 1e-5 if dtype == torch.float32 else 1e-2
+    parity(f"{'UMT5' if shape.per_layer_bias else 'T5'} 3-block encoder {str(dtype)[6:]}, rel L2 "
+           "vs oracle", e, bound)
+    assert e < bound
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_umt5_padding_mask_matches_oracle(gpu, dtype):
+def test_umt5_padding_mask_matches_oracle(gpu, dtype, parity):
     """Two prompts, the second right-padded after 97 of 150 tokens, and an all-padding one."""
     w = ot5.weights(SMALL_UMT5, 22, None if dtype == torch.float32 else dtype)
     enc = T5Encoder(_cfg(SMALL_UMT5), lambda n: w[n], dtype=dtype, device=gpu)
@@ -161,12 +164,14 @@ def test_umt5_padding_mask_matches_oracle(gpu, dtype):
     assert torch.isfinite(out.float()).all()
     e = rel_l2(out, ref)
     print(f"  masked rel L2 {e:.3e}", flush=True)
-    assert e < (1e-5 if dtype == torch.float32 else 1e-2)
+    bound = 1e-5 if dtype == torch.float32 else 1e-2
+    parity(f"UMT5 padded prompts {str(dtype)[6:]}, rel L2 vs oracle", e, bound)
+    assert e < bound
     with pytest.raises(ValueError, match="no attention mask"):
         T5Encoder(_cfg(SMALL), lambda n: ot5.weights(SMALL, 1)[n], device=gpu)(ids, mask)
 
 
-def test_umt5_width_two_blocks_fp32_matches_oracle(gpu):
+def test_umt5_width_two_blocks_fp32_matches_oracle(gpu, parity):
     """Two UMT5-XXL blocks at their real width (4096, 64 heads, d_ff 10240) on 512 tokens, fp32
     (the vocabulary cut to 1000 rows: it is a gather, not a dimension of the math)."""
     shape = dataclasses.replace(ot5.UMT5_XXL, vocab=1000, layers=2)
@@ -179,6 +184,7 @@ def test_umt5_width_two_blocks_fp32_matches_oracle(gpu):
     ref = ot5.encode(w, shape, ids, attention_mask=mask)
     e = rel_l2(out, ref)
     print(f"  umt5 width 2 blocks rel L2 {e:.3e}", flush=True)
+    parity("UMT5-XXL width, 2 blocks fp32, rel L2 vs oracle", e, 1e-5)
     assert e < 1e-5
 
 
