@@ -438,8 +438,16 @@ __global__ __launch_bounds__(256) void qk_rms_rows_kernel(
   ss[0] = wave_sum(ss[0]);
   ss[1] = wave_sum(ss[1]);
   const bool second = split > 0 && row >= split;  // rows past split: the second weights
-  const float* cr = cosb ? cosb + (row % rope_rows) * HD : nullptr;
-  const float* sr = sinb ? sinb + (row % rope_rows) * HD : nullptr;
+  // every chunk of a lane sits at the same place in its head ((lane + 64 c) * 8 mod 128 =
+  // lane * 8 mod 128), so the row's cos / sin values are loaded once for all of them
+  float cs[8], sn[8];
+  if (cosb) {
+    const int64_t tr = (row % rope_rows) * HD + (lane * 8) % HD;
+    *reinterpret_cast<f32x4*>(cs) = *reinterpret_cast<const f32x4*>(cosb + tr);
+    *reinterpret_cast<f32x4*>(cs + 4) = *reinterpret_cast<const f32x4*>(cosb + tr + 4);
+    *reinterpret_cast<f32x4*>(sn) = *reinterpret_cast<const f32x4*>(sinb + tr);
+    *reinterpret_cast<f32x4*>(sn + 4) = *reinterpret_cast<const f32x4*>(sinb + tr + 4);
+  }
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     if (!has[t]) continue;
@@ -458,7 +466,7 @@ __global__ __launch_bounds__(256) void qk_rms_rows_kernel(
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = v[i] * r * w8[i];
-      if (cr) rope8(v, cr + (c % HD), sr + (c % HD), law);
+      if (cosb) rope8(v, cs, sn, law);
       V8<T>::store(base[t] + c, v);
     }
   }
