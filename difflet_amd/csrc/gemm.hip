@@ -102,6 +102,7 @@ constexpr int64_t SK_CTR_BYTES = 16384;        // one int counter per split tile
 constexpr int SK_MAX_TILES = (int)(SK_CTR_BYTES / 4);
 constexpr int64_t SK_SLOT_BYTES = 256 * 256 * 4;  // fp32 accumulators of one 256 x 256 tile
 constexpr int SK_MIN_STAGES = 8;               // shortest K range worth a workgroup
+constexpr int SK_MIN_SAVED_STAGES = 24;         // shortest cut off the busiest K walk (below)
 
 struct GemmArgs {
   GemmProblemDev p[MAX_PROBLEMS];
@@ -1023,12 +1024,14 @@ static int64_t sk_workspace_bytes(int groups) {
 // units. Whole tiles while the last wave of workgroups would still be >= 92 % full; otherwise
 // the full waves run whole tiles and the S tiles of the last one are cut over the XCDs (see
 // SkPlan), when each XCD's range is at least SK_MIN_STAGES stages and the cut takes a quarter
-// off the launch's K walk (waves * nu units on the busiest workgroup). The cut tiles' partial
-// sums go through memory: 256 KB out and back per cut, all CUs at once, which at ~6 TB/s costs
-// about as much as 10-20 % of a 3072-deep tile. On MI355X that pays on Qwen-Image's 336-tile
-// launches (FF2 MXFP8 365 -> 316 us, bf16 576 -> 483 us) and loses on FLUX's 216-, 648- and
-// 864-tile ones (out projection bf16 87 -> 101 us, FF1 fp8 169 -> 198 us), which this rule
-// leaves whole.
+// off the launch's K walk (waves * nu units on the busiest workgroup), and at least
+// SK_MIN_SAVED_STAGES stages. The cut tiles' partial sums go through memory: 256 KB out and
+// back per cut, all CUs at once, which at ~6 TB/s costs about as much as 10-20 % of a
+// 3072-deep tile, whatever the K walk saves. On MI355X that pays on Qwen-Image's 336-tile
+// launches (FF2 MXFP8 365 -> 316 us, bf16 576 -> 483 us; 60 and 30 stages saved) and Wan's
+// 80-tile bf16 text k/v projection (93 -> 87 us, 40 saved), and loses on FLUX's 216-, 648-
+// and 864-tile ones (out projection bf16 87 -> 101 us, FF1 fp8 169 -> 198 us) and on the MXFP8
+// twin of that k/v projection (49 -> 66 us, 20 saved), which these rules leave whole.
 static SkPlan sk_plan(int T, int nk, int gran, int cus, int64_t ws_bytes) {
   const int nu = (nk + gran - 1) / gran;
   SkPlan pl = {T, 0, nu, gran, 0, 0, 0, 0};
@@ -1042,7 +1045,7 @@ static SkPlan sk_plan(int T, int nk, int gran, int cus, int64_t ws_bytes) {
   const int64_t span = (units + NX - 1) / NX;
   if (S > SK_MAX_TILES || ws_bytes < sk_workspace_bytes(cus) ||
       units / NX < std::max(1, SK_MIN_STAGES / gran) ||
-      4 * (nu - span) < (int64_t)waves * nu)
+      4 * (nu - span) < (int64_t)waves * nu || (nu - span) * gran < SK_MIN_SAVED_STAGES)
     return pl;
   pl.dp = dp;
   pl.groups = cus;

@@ -300,8 +300,9 @@ def gemm_grouped(problems: Sequence[Problem], *, kind: str = "bf16",
     workspace: None (every tile whole on one workgroup, the default), "shared" (the current
     stream's, see gemm_workspace) or a zero-filled uint8 tensor of
     difflet_rocm_gemm_workspace_bytes() bytes, which lets a launch whose last wave of tiles
-    would be poorly filled cut those tiles along K over the XCDs when that takes a quarter off
-    its time (Qwen-Image's 336-tile projections; FLUX's launches stay whole)."""
+    would be poorly filled cut those tiles along K over the XCDs when that takes a quarter and
+    at least 24 K stages off its time (Qwen-Image's 336-tile projections, Wan's bf16 text k/v
+    projection; FLUX's launches stay whole)."""
     # a problem without rows has nothing to compute (and an empty tensor may have no address)
     problems = [p for p in problems if p.a.shape[0] > 0]
     if not problems:

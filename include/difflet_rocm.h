@@ -190,8 +190,9 @@ typedef struct difflet_gemm_qk {
  * as whole tiles and cuts the last wave's tiles along K over the 8 XCDs: in groups of 32 tiles,
  * each XCD takes a contiguous range of (group, K unit) pairs and its 32 workgroups walk the
  * same K units of 32 neighbouring tiles together (whole-tile L2 sharing is kept). The cut is
- * made only when it takes a quarter off the launch's K walk (Qwen-Image's 336-tile projections
- * qualify; FLUX's 216-tile ones, which would save an eighth, stay whole). The workgroup
+ * made only when it takes a quarter and at least 24 K stages off the launch's K walk
+ * (Qwen-Image's 336-tile projections qualify; FLUX's 216-tile ones, which would save an
+ * eighth, stay whole, and so does an MXFP8 projection of 512 rows at K = 4096). The workgroup
  * finishing a cut tile adds the fp32 partial sums of the others in a fixed order, so results
  * are deterministic for a given device. With workspace NULL (or too small) every tile runs
  * whole on one workgroup. The workspace must be zero-filled once when allocated; the GEMMs

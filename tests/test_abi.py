@@ -100,15 +100,26 @@ def test_gemm_split_plan_at_the_step_shapes():
     assert lib.difflet_rocm_gemm_schedule_check(1512, 96, 1, 256, ws, ctypes.byref(dp),
                                                 ctypes.byref(groups)) == 0
     assert (dp.value, groups.value) == (1512, 0)
-    # MXFP8 (units of 4 K stages of 128) with a shorter last unit: K = 2816 (22 stages, the last
+    # MXFP8 (units of 4 K stages of 128) with a shorter last unit: K = 6912 (54 stages, the last
     # unit 2) at Qwen-Image's 336 tiles, K = 7808 (61 stages, the last unit 1) on 15 tiles;
     # both split, as the device tests of these shapes assume
-    assert lib.difflet_rocm_gemm_schedule_check(336, 22, 4, 256, ws, ctypes.byref(dp),
+    assert lib.difflet_rocm_gemm_schedule_check(336, 54, 4, 256, ws, ctypes.byref(dp),
                                                 ctypes.byref(groups)) == 0
     assert (dp.value, groups.value) == (256, 256)
     assert lib.difflet_rocm_gemm_schedule_check(15, 61, 4, 256, ws, ctypes.byref(dp),
                                                 ctypes.byref(groups)) == 0
     assert (dp.value, groups.value) == (0, 256)
+    # a cut that saves under 24 K stages stays whole: Wan's 80-tile text k/v projection
+    # (K = 4096) splits in bf16 (64 stages, 24 per XCD) but not in MXFP8 (8 units of 4, 3 per
+    # XCD: 20 stages saved), nor do fp8 and MXFP8 at 336 tiles and K = 3072
+    for nk, gran, plan in ((64, 1, (0, 256)), (8, 4, (80, 0))):
+        assert lib.difflet_rocm_gemm_schedule_check(80, nk, gran, 256, ws, ctypes.byref(dp),
+                                                    ctypes.byref(groups)) == 0
+        assert (dp.value, groups.value) == plan
+    for nk, gran in ((24, 1), (24, 4)):
+        assert lib.difflet_rocm_gemm_schedule_check(336, nk, gran, 256, ws, ctypes.byref(dp),
+                                                    ctypes.byref(groups)) == 0
+        assert (dp.value, groups.value) == (336, 0)
     # without enough workspace nothing is split
     assert lib.difflet_rocm_gemm_schedule_check(336, 48, 1, 256, 1 << 20, ctypes.byref(dp),
                                                 ctypes.byref(groups)) == 0

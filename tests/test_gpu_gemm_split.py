@@ -45,9 +45,10 @@ def _reference(kind, a, w, b):
 
 
 # (m, n, k): 336 and 360 tiles (a wave of whole tiles, then the last 80 / 104 cut in groups of
-# 32 over the 8 XCDs, one or two XCDs per tile; fp8 at k = 1024 stays whole), 15 tiles of a
-# long K (one group cut over all 8 XCDs: eight contributors per tile)
-SHAPES = [(7168, 3072, 3072), (4608, 5120, 1024), (600, 1280, 8192)]
+# 32 over the 8 XCDs, one or two XCDs per tile; k = 6144 so that every kind's cut saves the
+# planner's minimum of 24 K stages), 15 tiles of a long K (one group cut over all 8 XCDs:
+# eight contributors per tile)
+SHAPES = [(7168, 3072, 6144), (4608, 5120, 6144), (600, 1280, 8192)]
 
 
 @pytest.mark.parametrize("kind", ["bf16", "fp8", "mx"])
@@ -76,9 +77,9 @@ def test_split_gemm_equals_whole_tiles_and_reference(gpu, kind, m, n, k):
 
 
 # MXFP8 cuts K in units of 4 stages (one E8M0 block per row of 128 K); these K leave a shorter
-# last unit: 2816 = 22 stages at 336 tiles (the last unit 2 stages), 7808 = 61 stages on 15
+# last unit: 6912 = 54 stages at 336 tiles (the last unit 2 stages), 7808 = 61 stages on 15
 # tiles (the last unit 1 stage, eight contributors per tile). Both plans split (test_abi.py).
-@pytest.mark.parametrize("m,n,k", [(7168, 3072, 2816), (600, 1280, 7808)])
+@pytest.mark.parametrize("m,n,k", [(7168, 3072, 6912), (600, 1280, 7808)])
 def test_split_gemm_mx_with_a_short_last_unit(gpu, m, n, k):
     test_split_gemm_equals_whole_tiles_and_reference(gpu, "mx", m, n, k)
 
@@ -87,9 +88,10 @@ def test_split_gemm_mx_with_a_short_last_unit(gpu, m, n, k):
 def test_split_gemm_gate_residual_in_place_grouped(gpu, kind):
     """Qwen-Image's output projection shape: text and image problems in one launch (1 + 27
     row tiles x 12 = 336 tiles, the last 80 cut), gate * (acc + bias) + residual written over
-    the residual. MXFP8 runs this epilogue on the split in the Qwen-Image step's FF2."""
+    the residual. MXFP8 runs this epilogue on the split in the Qwen-Image step's FF2. fp8 and
+    MXFP8 take K = 6144: at 3072 their cut saves under the planner's 24 stages."""
     g = torch.Generator().manual_seed(11)
-    n, k = 3072, 3072
+    n, k = 3072, 3072 if kind == "bf16" else 6144
     probs, refs = [], []
     for m in (256, 6889):
         a, w, b = rnd(g, m, k), rnd(g, n, k, std=0.05), rnd(g, n, std=0.1)
